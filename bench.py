@@ -1,0 +1,270 @@
+"""Benchmark: MoE-layer decode on one MI355X (BASELINE.json configs[1] by default).
+
+A step is one token through one MoE layer -- router (scores, top-6 of 384)
+-> gate/up GEMV over the six selected 2-bit g128 experts -> SwiGLU -> down GEMV
+-> route-order combine -> bf16 residual add -- with inputs resident in HBM.
+Steps are chained: the output of step s is the activation of step s+1, and step
+s runs layer s mod L of an L-layer resident bank (L = 16 by default: 16 x 384
+experts, 61.6 GB), so consecutive steps never re-read experts the 256 MB
+Infinity Cache could still hold.
+
+Printed as one JSON line (rank 0): value = token-layers per second; the
+`roofline` object covers the expert GEMV kernel pair (q2_gate_up_kernel +
+q2_down_kernel, timed with HIP events on the launching stream over a run of
+precomputed routes) against the 8 TB/s HBM peak; `cpu_baseline` times the
+NumPy restatement (oracle/) of the reference's CPU dequant+matmul path on a
+small sample of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "MoE-layer decode tok/s + expert-byte HBM GB/s (B=1); prefill grouped-GEMM TFLOPS"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--layers", type=int, default=16, help="resident layers rotated through (MALL defeat)")
+    ap.add_argument("--seed", type=int, default=20260917)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget for the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(seed: int, budget_s: float):
+    """oracle (NumPy) 2-bit decode of whole token-layers on the host: dequant + matvec per expert."""
+    import numpy as np
+
+    from cachalot_amd.storage.index import affine_format
+    from oracle import experts as oexperts
+    from oracle import router as orouter
+    from oracle import synth as osynth
+    from oracle.affine2 import qmv64
+    from oracle.bf16 import bf16_bits_to_f32
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    fmt = affine_format(4096, 2880)
+    specs = osynth.q2_tensor_specs(4096, 2880)
+    done, t_total = 0, 0.0
+    while t_total < budget_s and done < 64:
+        layer = done % 16
+        w_bits, bias = osynth.router_tensors(seed, layer, 384, 4096)
+        x_bits = osynth.activations(seed, 1000 + done, 1, 4096)
+        # expert bytes are generated outside the timed region (they are "resident")
+        xf = bf16_bits_to_f32(x_bits)
+        idx, wts, _ = orouter.route(xf, bf16_bits_to_f32(w_bits), bias, topk=6, route_scale=1.0,
+                                    score=orouter.SCORE_SIGMOID)
+        tens = [osynth.expert_tensors(seed, layer, int(e), specs) for e in idx[0]]
+        t0 = time.perf_counter()
+        idx, wts, _ = orouter.route(xf, bf16_bits_to_f32(w_bits), bias, topk=6, route_scale=1.0,
+                                    score=orouter.SCORE_SIGMOID)
+        mats = []
+        for t in tens:
+            def mm(p, k, t=t):
+                return lambda v: qmv64(v, t[f"{p}.weight"], t[f"{p}.scales"], t[f"{p}.biases"], k=k, group=128)
+            mats.append((mm("w1", 4096), mm("w3", 4096), mm("w2", 2880)))
+        oexperts.affine_decode(xf[0], mats, wts[0], 10.0, xf[0])
+        t_total += time.perf_counter() - t0
+        done += 1
+    per = t_total / max(done, 1)
+    return {
+        "value": round(1.0 / per, 4),
+        "unit": "tok/s (token-layers)",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{done} token-layers of config 1 (router + 6 experts dequant+matvec, NumPy float64, "
+                  f"oracle/), {t_total:.1f} s; host has {os.cpu_count()} CPUs",
+        "ms_per_token_layer": round(per * 1e3, 2),
+        "expert_GBps": round(6 * fmt.algorithmic_bytes / per / 1e9, 4),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X (got --gpus {args.gpus}); "
+              "multi-GPU expert parallelism is a design note only.", file=sys.stderr)
+        return 2
+    import torch
+
+    from cachalot_amd import _lib, synth
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+    from cachalot_amd.moe_decode import decode_experts
+    from cachalot_amd.router import route_topk_fused
+    from cachalot_amd.storage.index import affine_format
+
+    dev = torch.device("cuda:0")
+    _lib.lib()
+    D, F, E, K = 4096, 2880, 384, 6
+    L = args.layers
+    fmt = affine_format(D, F)
+    log(f"filling {L} layers x {E} experts ({L * E * fmt.expert_bytes / 1e9:.1f} GB) in HBM")
+    t0 = time.time()
+    loader = SyntheticLoader(fmt, args.seed)
+    store = ResidentExpertStore(fmt=fmt, n_slots=L * E, n_layers=L, n_experts=E, device=dev)
+    store.preload([(la, e) for la in range(L) for e in range(E)], loader.fill_key)
+    table = store.track_slots()
+    gates = [synth.router_weights(args.seed, la, E, D, dev) for la in range(L)]
+    x0 = synth.activations(args.seed, 0, 1, D, dev)[0]
+    torch.cuda.synchronize()
+    log(f"bank ready in {time.time() - t0:.1f} s")
+
+    pool = store.pool
+
+    def step(x, s):
+        w, b = gates[s % L]
+        route = route_topk_fused(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+        _, out = decode_experts(x, pool, table[s % L], route.indices, route.weights, swiglu_limit=10.0,
+                                addend=x, want_routed=False)
+        return out
+
+    # The chain is captured in a HIP graph of G steps (G a multiple of L) and
+    # replayed, so host launch overhead stays out of the GPU timeline.
+    G = L * max(1, 64 // L)
+    xbuf = x0.clone()
+    warm = xbuf
+    for s in range(G):                       # eager warm-up (and allocator priming)
+        warm = step(warm, s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        xg = xbuf
+        for s in range(G):
+            xg = step(xg, s)
+        xbuf.copy_(xg)
+    replays_w = max(1, args.warmup // G)
+    replays = max(1, args.steps // G)
+    steps = replays * G
+    xbuf.copy_(x0)
+    for _ in range(replays_w):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    xbuf.copy_(x0)
+    t_wall = time.perf_counter()
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms = start.elapsed_time(end)
+    ms_per_step = ms / steps
+    log(f"chained steps: {ms_per_step * 1e3:.2f} us/step (wall {t_wall / steps * 1e6:.2f} us/step)")
+    if not torch.isfinite(xbuf.float()).all():
+        raise RuntimeError("non-finite activations after the chained run")
+    # the graph replays must equal eager execution of the same chain
+    eager = x0
+    for s in range(G):
+        eager = step(eager, s)
+    xbuf.copy_(x0)
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(eager, xbuf):
+        raise RuntimeError("graph replay differs from eager execution")
+
+    # ---- expert GEMV kernel pair alone, over precomputed routes (distinct layers per launch)
+    n_routes = 256
+    xs = synth.activations(args.seed, 7, n_routes, D, dev)
+    routes = []
+    for r in range(n_routes):
+        w, b = gates[r % L]
+        rt = route_topk_fused(xs[r], w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+        routes.append((xs[r], table[r % L], rt.indices, rt.weights))
+    reps = max(1, args.steps // n_routes)
+    routed_buf = torch.empty(D, dtype=torch.float32, device=dev)
+    ws_bytes = _lib.lib().cachalot_moe_decode_q2_workspace_bytes(D, F, K)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    layout = pool.layout()
+    stream = _lib.stream_handle(dev)
+    Lh = _lib.lib()
+
+    def launch(xr, tb, idx, wt):
+        rc = Lh.cachalot_moe_decode_q2(xr.data_ptr(), pool.storage.data_ptr(), layout, tb.data_ptr(), idx.data_ptr(),
+                                       wt.data_ptr(), D, F, E, K, 128, 10.0, None, routed_buf.data_ptr(), None,
+                                       ws.data_ptr(), ws_bytes, stream)
+        if rc:
+            _lib.check(rc)
+
+    for r in range(n_routes):
+        launch(*routes[r])
+    torch.cuda.synchronize()
+    kgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(kgraph):
+        stream = _lib.stream_handle(dev)
+        for r in range(n_routes):
+            launch(*routes[r])
+    kgraph.replay()
+    torch.cuda.synchronize()
+    s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s2.record()
+    for _ in range(reps):
+        kgraph.replay()
+    e2.record()
+    torch.cuda.synchronize()
+    us_kernel = s2.elapsed_time(e2) * 1e3 / (reps * n_routes)
+    alg_bytes = K * fmt.algorithmic_bytes
+    achieved = alg_bytes / (us_kernel * 1e-6) / 1e9
+    log(f"expert kernel pair: {us_kernel:.2f} us/launch, {achieved:.0f} GB/s algorithmic")
+
+    router_bytes = E * D * 2 + E * 4
+    step_bytes = alg_bytes + router_bytes
+    result = {
+        "metric": METRIC,
+        "value": round(1e3 / ms_per_step, 1),
+        "unit": "tok/s (token-layers, B=1)",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded 2-bit affine g128 bank, sigmoid router; BASELINE configs[1])",
+        "config": {
+            "workload": "configs[1]: one MoE layer decode, B=1, d_model 4096, 384 experts top-6, d_ff 2880, "
+                        "2-bit affine g128 bank (bf16 scales/biases), chained over "
+                        f"{L} resident layers",
+            "d_model": D, "d_ff": F, "experts": E, "topk": K, "batch": 1, "resident_layers": L,
+            "parallelism": "single GPU",
+        },
+        "expert_GBps_step": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "hbm_frac_step": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {
+            "kernel": "q2_gate_up_kernel + q2_down_kernel (one decode launch pair)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "us_per_launch": round(us_kernel, 3),
+            "algorithmic_bytes_per_launch": alg_bytes,
+        },
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

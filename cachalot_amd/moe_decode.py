@@ -1,0 +1,116 @@
+"""Device-addressed decode of the top-k routed experts (one token).
+
+``decode_experts`` is the single entry the reference-shaped wrappers below and
+``moe_layer_forward`` share: experts are named by router ids on the device and
+resolved through the store's slot table inside the kernels, so nothing crosses
+to the host between routing and the expert GEMVs.
+
+* ``fused_routed_experts``  -- ``src/cachalot/model/moe_fused_metal.py:189-233`` (FP4 bank)
+* ``affine_routed_experts`` -- ``src/cachalot/model/expert_affine.py:186-206`` (2-bit bank)
+* ``affine_expert_forward`` -- ``expert_affine.py:65-81`` (one expert)
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .cache.slots import HBMSlotPool
+from .storage.index import ExpertFormat
+
+
+def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor, idx: torch.Tensor,
+                   weights: torch.Tensor, *, swiglu_limit: float = 10.0, addend: torch.Tensor | None = None,
+                   want_routed: bool = True, want_out: bool = True):
+    """x [D] bf16; slot_table [E] int32 (device); idx [k] int32; weights [k] fp32.
+
+    Returns (routed fp32 [D] or None, out bf16 [D] or None)."""
+    fmt: ExpertFormat = pool.format
+    if x.ndim != 1:
+        raise ValueError(f"x must be 1D for decode, got {tuple(x.shape)}")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("decode expects bf16 activations")
+    d, f = fmt.d_model, fmt.d_ff
+    if x.shape[0] != d:
+        raise ValueError(f"x has {x.shape[0]} elements, experts expect {d}")
+    k = int(idx.numel())
+    if weights.numel() != k:
+        raise ValueError(f"{weights.numel()} router weights for {k} experts")
+    _lib.require_cuda(x, slot_table, idx, weights, addend)
+    dev = x.device
+    idx = idx.to(torch.int32).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    slot_table = slot_table.to(torch.int32).contiguous()
+    x = x.contiguous()
+    if addend is not None:
+        if addend.dtype != torch.bfloat16 or addend.shape != x.shape:
+            raise ValueError("addend must be a bf16 vector shaped like x")
+        addend = addend.contiguous()
+    routed = torch.empty((d,), dtype=torch.float32, device=dev) if want_routed else None
+    out = torch.empty((d,), dtype=torch.bfloat16, device=dev) if want_out else None
+    L = _lib.lib()
+    layout = pool.layout()
+    stream = _lib.stream_handle(dev)
+    e = int(slot_table.numel())
+    if fmt.kind == "affine":
+        nbytes = L.cachalot_moe_decode_q2_workspace_bytes(d, f, k)
+        ws = torch.empty((max(1, nbytes),), dtype=torch.uint8, device=dev)
+        rc = L.cachalot_moe_decode_q2(x.data_ptr(), pool.storage.data_ptr(), layout, slot_table.data_ptr(),
+                                      idx.data_ptr(), weights.data_ptr(), d, f, e, k, fmt.group_size,
+                                      float(swiglu_limit), _lib.ptr(addend), _lib.ptr(routed), _lib.ptr(out),
+                                      ws.data_ptr(), nbytes, stream)
+        _lib.check(rc, "moe_decode_q2")
+    elif fmt.kind == "fp4":
+        nbytes = L.cachalot_moe_decode_fp4_workspace_bytes(d, f, k)
+        ws = torch.empty((max(1, nbytes),), dtype=torch.uint8, device=dev)
+        rc = L.cachalot_moe_decode_fp4(x.data_ptr(), pool.storage.data_ptr(), layout, slot_table.data_ptr(),
+                                       idx.data_ptr(), weights.data_ptr(), d, f, e, k, float(swiglu_limit),
+                                       _lib.ptr(addend), _lib.ptr(routed), _lib.ptr(out), ws.data_ptr(), nbytes,
+                                       stream)
+        _lib.check(rc, "moe_decode_fp4")
+    else:
+        raise ValueError(f"unknown expert format {fmt.kind!r}")
+    return routed, out
+
+
+def _experts_table(experts):
+    pools = {id(ex.slot.pool) for ex in experts}
+    if len(pools) != 1 or experts[0].slot.pool is None:
+        raise ValueError("experts must live in one HBM slot pool")
+    pool = experts[0].slot.pool
+    dev = pool.device
+    slots = torch.tensor([ex.slot.index for ex in experts], dtype=torch.int32).to(dev)
+    idx = torch.arange(len(experts), dtype=torch.int32).to(dev)
+    return pool, slots, idx
+
+
+def fused_routed_experts(x: torch.Tensor, experts, router_weights: torch.Tensor, *, hidden_size: int = 4096,
+                         intermediate: int = 2880, swiglu_limit: float = 10.0) -> torch.Tensor:
+    """FP4 experts: fp32 [hidden_size] = sum_e w_e * W2_e(silu(W1_e x) * W3_e x) (clamped)."""
+    pool, slots, idx = _experts_table(experts)
+    fmt = pool.format
+    if fmt.kind != "fp4":
+        raise ValueError("fused_routed_experts needs an FP4 bank")
+    if (hidden_size, intermediate) != (fmt.d_model, fmt.d_ff):
+        raise ValueError(f"shape {(hidden_size, intermediate)} != bank {(fmt.d_model, fmt.d_ff)}")
+    w = router_weights.to(device=pool.device, dtype=torch.float32)
+    routed, _ = decode_experts(x.to(torch.bfloat16), pool, slots, idx, w, swiglu_limit=swiglu_limit,
+                               want_out=False)
+    return routed
+
+
+def affine_routed_experts(x: torch.Tensor, experts, fmt: ExpertFormat, weights: torch.Tensor,
+                          swiglu_limit: float = 10.0) -> torch.Tensor:
+    """2-bit experts: fp32 [D] sum over experts in order (bf16 rounding points of the reference)."""
+    pool, slots, idx = _experts_table(experts)
+    if pool.format.kind != "affine" or fmt.kind != "affine":
+        raise ValueError("affine_routed_experts needs an affine bank")
+    w = weights.to(device=pool.device, dtype=torch.float32)
+    routed, _ = decode_experts(x, pool, slots, idx, w, swiglu_limit=swiglu_limit, want_out=False)
+    return routed
+
+
+def affine_expert_forward(x: torch.Tensor, expert, fmt: ExpertFormat, weight: float,
+                          swiglu_limit: float = 10.0) -> torch.Tensor:
+    """One affine expert: fp32 [D] = bf16(W2(bf16(silu(min(W1 x, L)) * clip(W3 x) * weight)))."""
+    w = torch.tensor([float(weight)], dtype=torch.float32)
+    return affine_routed_experts(x, [expert], fmt, w, swiglu_limit)

@@ -1,0 +1,77 @@
+"""Decode MoE layer: router -> top-k routed experts -> combine, one token.
+
+Keeps the call-site signature of ``moe_layer_forward``
+(``src/cachalot/model/moe_layer_metal.py:133-153``) and its return value
+``(out, RouterResult)`` with ``out`` in the activation dtype.
+
+Difference in mechanism, not in result: the reference evaluates the routing,
+reads the ids on the host, asks the store for the experts and launches the
+expert kernels (``moe_layer_metal.py:220-300``).  Here the whole bank is
+resident in HBM and the store's (layer, expert) -> slot table lives on the
+device, so the router's ids go straight into the expert kernels: three
+launches (router scores, top-k, gate/up) plus the down/combine launch, no host
+synchronisation.  When a layer is not fully resident the host path is taken:
+one synchronisation, ``get_many`` (which loads misses), then the same kernels.
+
+The FP8 shared expert the reference adds into the combine
+(``moe_layer_metal.py:381-397``) is not built yet; ``shared_*`` must be None,
+and ``addend`` (bf16 [D], optional) is added before the final cast instead.
+"""
+from __future__ import annotations
+
+import torch
+
+from .cache.resident_store import ResidentExpertStore
+from .moe_decode import decode_experts
+from .router import RouterResult, route_topk, route_topk_fused
+from .storage.index import ExpertEntry
+
+
+def moe_layer_forward(
+    x: torch.Tensor,
+    *,
+    layer_id: int,
+    gate_weight: torch.Tensor,
+    gate_bias: torch.Tensor,
+    expert_index: dict | None,
+    expert_store: ResidentExpertStore,
+    shared_w1=None,
+    shared_w1_scales=None,
+    shared_w2=None,
+    shared_w2_scales=None,
+    shared_w3=None,
+    shared_w3_scales=None,
+    topk: int = 6,
+    gate_temp: float = 1.0,
+    route_scale: float = 1.5,
+    norm_topk_prob: bool = True,
+    swiglu_limit: float = 10.0,
+    fused: bool | None = None,
+    score_fn: str = "sqrt_softplus",
+    order: str = "ascending",
+    addend: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, RouterResult]:
+    if x.ndim != 1:
+        raise ValueError(f"x must be 1D for decode, got {tuple(x.shape)}")
+    if any(t is not None for t in (shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3,
+                                   shared_w3_scales)):
+        raise NotImplementedError("the FP8 shared expert is not part of this build yet")
+    router = route_topk_fused if norm_topk_prob else route_topk
+    route = router(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp, route_scale=route_scale,
+                   norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order)
+    pool = expert_store.pool
+    if not expert_store.layer_fully_resident(layer_id):
+        # host-addressed path: one sync for the ids, then load what is missing
+        ids = route.indices.tolist()
+        entries = []
+        for e in ids:
+            key = (layer_id, int(e))
+            entry = expert_index.get(key) if expert_index is not None else ExpertEntry(*key)
+            if entry is None:
+                raise KeyError(f"Missing routed expert layer={layer_id}, expert={e}")
+            entries.append(entry)
+        expert_store.get_many(entries, priorities=route.weights.tolist())
+    table = expert_store.layer_table(layer_id)
+    _, out = decode_experts(x, pool, table, route.indices, route.weights, swiglu_limit=swiglu_limit,
+                            addend=addend, want_routed=False, want_out=True)
+    return out.to(x.dtype), route

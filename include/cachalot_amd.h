@@ -1,0 +1,134 @@
+/*
+ * cachalot_amd.h -- C ABI of libcachalot_amd.so, the MI355X (gfx950) routed-expert
+ * MoE path.
+ *
+ * Conventions
+ *   - every pointer argument is a device pointer unless the comment says "host";
+ *   - bf16 tensors are passed as uint16_t bit patterns;
+ *   - all work is stream-ordered on `stream` (a hipStream_t; NULL = default
+ *     stream) and asynchronous; nothing allocates device memory -- scratch
+ *     space comes in through `workspace` (size from the *_workspace_bytes
+ *     query);
+ *   - return 0 on success or a negative CACHALOT_E* code; the message is in
+ *     cachalot_last_error() (thread-local).  The Python layer maps EINVAL to
+ *     ValueError, ENOTFOUND to KeyError, EHIP to RuntimeError, the exception
+ *     types the reference raises for the same conditions
+ *     (src/cachalot/model/router_mlx.py:40-66, moe_layer_metal.py:279-283).
+ *
+ * Reference citations are paths relative to the prooshani/cachalot checkout.
+ */
+#ifndef CACHALOT_AMD_H
+#define CACHALOT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* cachalot_stream_t; /* == hipStream_t */
+
+#define CACHALOT_OK 0
+#define CACHALOT_EINVAL (-1)    /* shape / argument contract violated        */
+#define CACHALOT_ENOTFOUND (-2) /* expert not resident (slot table -1)       */
+#define CACHALOT_EHIP (-3)      /* HIP runtime / launch error                */
+#define CACHALOT_ESPACE (-4)    /* workspace too small                       */
+
+/* Router score functions and output orders. */
+#define CACHALOT_SCORE_SQRT_SOFTPLUS 0 /* DeepSeek: router_mlx.py:189-191          */
+#define CACHALOT_SCORE_SIGMOID 1       /* MiniMax / GLM: minimax/language.py:280-283 */
+#define CACHALOT_ORDER_ASCENDING 0     /* argsort(sel)[-k:]: router_mlx.py:197-202    */
+#define CACHALOT_ORDER_RANK 1          /* argpartition(-sel): minimax/gpu_select.py:81-106 */
+
+/* Byte layout of one expert record inside an HBM slot pool.  A slot's record
+ * starts at pool + slot * record_bytes; tensor t sits at offset[t].
+ * Tensor order: w1.weight, w1.scale(s), w1.biases, w2.weight, w2.scale(s),
+ * w2.biases, w3.weight, w3.scale(s), w3.biases (biases unused for FP4).
+ * Mirrors SlabSlotPool's fixed per-tensor record offsets
+ * (src/cachalot/cache/slots.py:185-216). */
+typedef struct cachalot_expert_layout {
+  int64_t record_bytes;
+  int64_t offset[9];
+} cachalot_expert_layout;
+
+/* Library identity and last error (thread-local). */
+int cachalot_version(void);
+const char* cachalot_last_error(void);
+
+/* Seeded synthetic fill of `n` elements (kinds 0..4: uint32 words, E8M0 bytes,
+ * bf16 uniform p0 + p1*t, bf16 normal sigma=p0, fp32 normal sigma=p0), element i
+ * from counter `start + i`.  Test/bench data only -- the reference has no
+ * counterpart (it loads checkpoints, storage/reader.py). */
+int cachalot_fill_synthetic(void* dst, int64_t n, int64_t start, uint64_t key, int kind,
+                            double p0, double p1, int64_t row_total, int64_t row_valid,
+                            cachalot_stream_t stream);
+
+/* Router: logits = W x / gate_temp (fixed fp32 order), scores = score_fn(logits),
+ * selection = scores + bias (bias_vl where image_mask[t] != 0), top-k with the
+ * chosen order and tie rule, weights = scores[idx] normalised (norm != 0 and
+ * k > 1) and scaled by route_scale.
+ *   x [T, D] bf16, W [E, D] bf16, bias/bias_vl [E] fp32, image_mask [T] u8 or NULL
+ *   idx [T, k] int32, w [T, k] fp32, scores [T, E] fp32.
+ * Replaces route_topk / route_topk_fused / route_topk_rows / route_topk_batch
+ * (src/cachalot/model/router_mlx.py:16-211, router_fused_metal.py:111-148,
+ * moe_prefill_batched.py:128-178) and the sigmoid route tail
+ * (minimax/gpu_select.py:80-133). */
+int cachalot_router_topk(const uint16_t* x, const uint16_t* W, const float* bias,
+                         const float* bias_vl, const uint8_t* image_mask,
+                         int T, int D, int E, int k, int score_fn, float gate_temp,
+                         float route_scale, int norm, int order,
+                         int32_t* idx, float* w, float* scores, cachalot_stream_t stream);
+
+/* Decode, one token, top-k routed experts on a 2-bit affine bank
+ * (MLX layout: weight [N, Kp/16] u32, scales/biases [N, Kp/group] bf16):
+ *   g = bf16(W1 x), u = bf16(W3 x), h = bf16(silu(min(g,L)) * clip(u,-L,L) * w_e),
+ *   y_e = bf16(W2 h), routed = sum_e y_e (route order, fp32),
+ *   out = bf16(routed + addend).
+ * Experts are addressed on the device: slot = slot_table[idx[e]], record at
+ * pool + slot * layout.record_bytes; a negative slot contributes zero rows.
+ *   x [D] bf16; idx [k] int32; w [k] fp32; slot_table [E] int32;
+ *   addend [D] bf16 or NULL; routed [D] fp32 or NULL; out [D] bf16 or NULL.
+ * Replaces affine_routed_experts / topk_core / the traced MoE block
+ * (src/cachalot/model/expert_affine.py:117-206, moe_layer_metal.py:93-130). */
+size_t cachalot_moe_decode_q2_workspace_bytes(int D, int F, int k);
+int cachalot_moe_decode_q2(const uint16_t* x, const uint8_t* pool,
+                           const cachalot_expert_layout* layout /* host */,
+                           const int32_t* slot_table, const int32_t* idx, const float* w,
+                           int D, int F, int E, int k, int group, float swiglu_limit,
+                           const uint16_t* addend, float* routed, uint16_t* out,
+                           void* workspace, size_t workspace_bytes, cachalot_stream_t stream);
+
+/* Decode, one token, top-k routed experts on an FP4 E2M1 / E8M0-block-32 bank:
+ *   g = W1 x, u = W3 x (fp32), h = silu(min(g,L)) * clip(u,-L,L) * w_e (fp32),
+ *   routed = sum_e W2_e h_e (fp32, route order); out = bf16(routed + addend).
+ * Same addressing and optional outputs as cachalot_moe_decode_q2.
+ * Replaces fused_routed_experts (src/cachalot/model/moe_fused_metal.py:189-233)
+ * and the unfused loop (moe_metal.py:8-37, expert_metal.py:9-64). */
+size_t cachalot_moe_decode_fp4_workspace_bytes(int D, int F, int k);
+int cachalot_moe_decode_fp4(const uint16_t* x, const uint8_t* pool,
+                            const cachalot_expert_layout* layout /* host */,
+                            const int32_t* slot_table, const int32_t* idx, const float* w,
+                            int D, int F, int E, int k, float swiglu_limit,
+                            const uint16_t* addend, float* routed, uint16_t* out,
+                            void* workspace, size_t workspace_bytes, cachalot_stream_t stream);
+
+/* Dense dequantisation (bit-exact weight checks and debugging).
+ * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32
+ *   (replaces dequantize_fp4_weight / dequantize_fp4_dense,
+ *    src/cachalot/model/fp4.py:67-109, fp4_dequant_metal.py:43-69);
+ *   as_bf16 != 0 converts through the bf16 path the GEMV/GEMM kernels use.
+ * 2-bit: w [N, row_words] u32, scales/biases [N, groups] bf16 -> out [N, K] fp32,
+ *   value fl(fl(s*q)+b) (replaces mx.dequantize on the affine views,
+ *   src/cachalot/model/expert_affine.py:26-51). */
+int cachalot_dequant_fp4(const uint8_t* packed, const uint8_t* scales, int N, int K, int as_bf16,
+                         float* out, cachalot_stream_t stream);
+int cachalot_dequant_q2(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                        int N, int K, int row_words, int groups, int group, float* out,
+                        cachalot_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CACHALOT_AMD_H */

@@ -1,0 +1,70 @@
+"""MLX affine 2-bit g128 layout and group formula, restated.
+
+* packing: 16 codes per uint32, least-significant field first
+  (``benchmarks/quant_affine.py:11-16,60-66``; layout pinned by the reference's
+  own ``tests/test_quant_affine.py:45-51`` against ``mx.quantize``);
+* dequantised value ``w = scale * q + bias`` per ``group``-element group along K
+  (``benchmarks/quant_affine.py:11-15``), scales/biases stored bf16
+  (``benchmarks/build_affine_bank.py:76,165-174``);
+* ``quantized_matmul(x, w, s, b, transpose=True)``: per group
+  ``s * sum(x_i q_i) + b * sum(x_i)`` with fp32 accumulation
+  (MLX ``qdot``, shown at ``src/cachalot/minimax/codes_qmv.py:86-100``).
+
+K that is not a whole number of groups (d_ff = 2880 at g128) is stored padded
+to ``ceil(K/g)*g`` with zero codes; padded activation lanes are 0, so the last
+group's ``sum(x_i)`` runs over the real K only.
+
+``qmv`` here accumulates in float64 (the accuracy reference); MLX's own fp32
+summation order lives inside a third-party kernel and is not restated, so the
+GPU path is checked to a tolerance, not bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import bf16_bits_to_f32
+
+PER_WORD = 16
+
+
+def pack_2bit(q) -> np.ndarray:
+    """[..., K] codes 0..3 -> [..., K/16] uint32, low field first."""
+    q = np.asarray(q)
+    if q.shape[-1] % PER_WORD:
+        raise ValueError(f"K={q.shape[-1]} is not a multiple of {PER_WORD}")
+    f = q.astype(np.uint64).reshape(*q.shape[:-1], -1, PER_WORD)
+    shifts = (np.arange(PER_WORD, dtype=np.uint64) * np.uint64(2))
+    return np.bitwise_or.reduce(f << shifts, axis=-1).astype(np.uint32)
+
+
+def unpack_2bit(w, k: int | None = None) -> np.ndarray:
+    """[..., W] uint32 -> [..., k] uint8 codes (k defaults to 16 * W)."""
+    w = np.asarray(w, dtype=np.uint32)
+    shifts = (np.arange(PER_WORD, dtype=np.uint32) * np.uint32(2))
+    q = ((w[..., None] >> shifts) & np.uint32(3)).astype(np.uint8)
+    q = q.reshape(*w.shape[:-1], -1)
+    return q if k is None else q[..., :k]
+
+
+def dequantize_affine(w, scales_bits, biases_bits, *, k: int, group: int = 128) -> np.ndarray:
+    """[N, K] fp32 with the declared rounding ``fl(fl(s * q) + b)`` (s, b exact from bf16)."""
+    q = unpack_2bit(w, k).astype(np.float32)
+    s = np.repeat(bf16_bits_to_f32(scales_bits), group, axis=-1)[..., :k]
+    b = np.repeat(bf16_bits_to_f32(biases_bits), group, axis=-1)[..., :k]
+    return (s * q) + b
+
+
+def dequantize_affine64(w, scales_bits, biases_bits, *, k: int, group: int = 128) -> np.ndarray:
+    q = unpack_2bit(w, k).astype(np.float64)
+    s = np.repeat(bf16_bits_to_f32(scales_bits).astype(np.float64), group, axis=-1)[..., :k]
+    b = np.repeat(bf16_bits_to_f32(biases_bits).astype(np.float64), group, axis=-1)[..., :k]
+    return s * q + b
+
+
+def qmv64(x, w, scales_bits, biases_bits, *, k: int, group: int = 128) -> np.ndarray:
+    """x [M, K] (bf16-exact values) -> float64 [M, N] = sum_g s_g*sum(x q) + b_g*sum(x).
+
+    s*q+b is exact in float64 for bf16 s, b and q in 0..3, so this equals
+    x @ dequant(W)^T evaluated in float64."""
+    x = np.asarray(x, dtype=np.float64)
+    return x @ dequantize_affine64(w, scales_bits, biases_bits, k=k, group=group).T

@@ -1,0 +1,58 @@
+"""Shared helpers for the GPU parity tests: synthetic banks in HBM and their
+oracle twins on the host."""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import synth as osynth
+from oracle.affine2 import qmv64
+from oracle.fp4 import dequantize_fp4_weight
+
+SEED = 20260917
+
+
+def make_store(fmt, *, n_layers=1, n_experts=384, keys=None, seed=SEED, n_slots=None, loader=False):
+    """A ResidentExpertStore with `keys` (default: every expert) preloaded from the synthetic generator."""
+    import torch
+
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+
+    syn = SyntheticLoader(fmt, seed)
+    store = ResidentExpertStore(fmt=fmt, n_slots=n_slots or n_layers * n_experts, n_layers=n_layers,
+                                n_experts=n_experts, device="cuda:0", loader=syn if loader else None)
+    if keys is None:
+        keys = [(la, e) for la in range(n_layers) for e in range(n_experts)]
+    store.preload(keys, syn.fill_key)
+    store.track_slots()
+    torch.cuda.synchronize()
+    return store
+
+
+def oracle_tensors(fmt, layer, expert, seed=SEED):
+    if fmt.kind == "fp4":
+        specs = osynth.fp4_tensor_specs(fmt.d_model, fmt.d_ff)
+    else:
+        specs = osynth.q2_tensor_specs(fmt.d_model, fmt.d_ff, fmt.group_size)
+    return osynth.expert_tensors(seed, layer, expert, specs)
+
+
+def q2_mats(fmt, tensors):
+    """(mm1, mm3, mm2): float64 products with W1^T, W3^T, W2^T of one 2-bit expert."""
+    g = fmt.group_size
+
+    def mm(proj, k):
+        w, s, b = tensors[f"{proj}.weight"], tensors[f"{proj}.scales"], tensors[f"{proj}.biases"]
+        return lambda x: qmv64(x, w, s, b, k=k, group=g)
+
+    return mm("w1", fmt.d_model), mm("w3", fmt.d_model), mm("w2", fmt.d_ff)
+
+
+def fp4_dense(tensors):
+    return tuple(dequantize_fp4_weight(tensors[f"{p}.weight"], tensors[f"{p}.scale"]) for p in ("w1", "w3", "w2"))
+
+
+def rel_err(got, want) -> float:
+    """max |got - want| / max |want|: the relative error the parity bar is stated in."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))

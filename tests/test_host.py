@@ -1,0 +1,129 @@
+"""Host-side checks that need no GPU: bank formats, record layout, the C-ABI
+library's exports, argument validation, and the synthetic-data definitions
+shared by the GPU generator and the oracle."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_expert_bytes_match_reference_counts():
+    from cachalot_amd.storage.index import affine_format, fp4_format
+
+    q2 = affine_format(4096, 2880)
+    assert q2.algorithmic_bytes == 9_953_280            # build_affine_bank.py:12-15
+    assert q2.expert_bytes == 10_027_008                # w2 padded to 23 groups
+    assert q2.shapes["w2.weight"] == (4096, 184) and q2.shapes["w2.scales"] == (4096, 23)
+    assert q2.shapes["w1.weight"] == (2880, 256) and q2.shapes["w1.scales"] == (2880, 32)
+    fp4 = fp4_format(4096, 2880)
+    assert fp4.expert_bytes == fp4.algorithmic_bytes == 18_800_640   # text_decode_runtime.py:347
+    # the reference-true DeepSeek shape is group-aligned: no padding at all
+    ds = affine_format(5120, 2304)
+    assert ds.expert_bytes == ds.algorithmic_bytes == 9_953_280
+
+
+def test_kernel_order_and_layout_offsets():
+    from cachalot_amd.storage.index import KERNEL_ORDER, affine_format, fp4_format, kernel_tensor_name
+
+    assert KERNEL_ORDER[0] == "w1.weight" and KERNEL_ORDER[4] == "w2.scales" and KERNEL_ORDER[8] == "w3.biases"
+    fmt = fp4_format(64, 64)
+    assert kernel_tensor_name(fmt, "w2.scales") == "w2.scale" and kernel_tensor_name(fmt, "w1.biases") is None
+    q2 = affine_format(4096, 2880)
+    # offsets the pool would use: page-aligned, in tensor order
+    pos, offs = 0, {}
+    for n in q2.tensor_names:
+        offs[n] = pos
+        pos += -(-q2.tensor_bytes(n) // 4096) * 4096
+    assert all(o % 4096 == 0 for o in offs.values())
+    assert pos == 10_027_008   # every tensor is already a whole number of pages
+
+
+def _header_functions():
+    text = (ROOT / "include/cachalot_amd.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|size_t)\s+(cachalot_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from cachalot_amd import _lib
+
+    declared = _header_functions()
+    assert declared and set(declared) == set(_lib.exported_symbols())
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared:
+        assert hasattr(handle, name), name
+
+
+def test_library_validates_without_a_gpu():
+    """Argument checks run on the host before any HIP call."""
+    from cachalot_amd import _lib
+
+    L = _lib.lib()
+    assert L.cachalot_version() == 1
+    rc = L.cachalot_router_topk(1, 1, 1, None, None, 0, 4096, 384, 6, 0, 1.0, 1.5, 1, 0, 1, 1, 1, None)
+    assert rc == _lib.EINVAL and "at least one token" in _lib.last_error()
+    rc = L.cachalot_router_topk(1, 1, 1, None, None, 1, 4096, 384, 400, 0, 1.0, 1.5, 1, 0, 1, 1, 1, None)
+    assert rc == _lib.EINVAL and "topk" in _lib.last_error()
+    rc = L.cachalot_router_topk(1, 1, 1, 1, None, 1, 4096, 384, 6, 0, 1.0, 1.5, 1, 0, 1, 1, 1, None)
+    assert rc == _lib.EINVAL and "together" in _lib.last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+    lay = _lib.ExpertLayout()
+    lay.record_bytes = 4096
+    rc = L.cachalot_moe_decode_q2(1, 1, ctypes.byref(lay), 1, 1, 1, 4096, 2880, 384, 9, 128, 10.0, None, 1, None,
+                                  1, 1 << 20, None)
+    assert rc == _lib.EINVAL and "k=9" in _lib.last_error()
+    need = L.cachalot_moe_decode_q2_workspace_bytes(4096, 2880, 6)
+    assert need == 6 * 2880 * 2
+    rc = L.cachalot_moe_decode_q2(1, 1, ctypes.byref(lay), 1, 1, 1, 4096, 2880, 384, 6, 128, 10.0, None, 1, None,
+                                  1, need - 1, None)
+    assert rc == _lib.ESPACE
+    with pytest.raises(MemoryError):
+        _lib.check(rc)
+    assert L.cachalot_dequant_fp4(1, 1, 4, 48, 0, 1, None) == _lib.EINVAL
+
+
+def test_synth_keys_and_specs_agree_with_oracle():
+    from cachalot_amd import synth
+    from cachalot_amd.storage.index import affine_format, fp4_format
+    from oracle import synth as osynth
+
+    for args in [(0, 0, 0, 0), (20260917, 39, 383, 8), (1, 2, 1 << 20, 5), (2**63 + 5, 7, 11, 3)]:
+        assert synth.stream_key(*args) == osynth.stream_key(*args)
+    assert synth.TENSOR_IDS == osynth.TENSOR_IDS
+    assert synth.IRWIN_HALL_STD == osynth.IRWIN_HALL_STD
+    # the product's tensor specs equal the oracle's (name, kind, params, padding)
+    for fmt, ospecs in ((affine_format(4096, 2880), osynth.q2_tensor_specs(4096, 2880)),
+                        (fp4_format(4096, 2880), osynth.fp4_tensor_specs(4096, 2880))):
+        prod = {s[0]: s[1:] for s in synth.tensor_specs(fmt)}
+        for name, shape, dtype, kind, p0, p1, rt, rv in ospecs:
+            assert prod[name] == (kind, p0, p1, rt, rv), name
+            assert fmt.shapes[name] == shape
+
+
+def test_oracle_synth_distributions():
+    from oracle import synth as osynth
+    from oracle.bf16 import bf16_bits_to_f32
+
+    x = bf16_bits_to_f32(osynth.activations(1, 0, 8, 4096))
+    assert abs(float(x.mean())) < 0.02 and abs(float(x.std()) - 1.0) < 0.02 and np.abs(x).max() < 3.47
+    ex = osynth.expert_tensors(3, 1, 2, osynth.q2_tensor_specs(4096, 2880))
+    s = bf16_bits_to_f32(ex["w1.scales"])
+    assert s.min() >= 0.0049 and s.max() <= 0.0502
+    assert np.all(ex["w2.weight"][:, 180:] == 0) and np.any(ex["w2.weight"][:, :180] != 0)
+    f = osynth.expert_tensors(3, 1, 2, osynth.fp4_tensor_specs(4096, 2880))
+    assert f["w1.scale"].min() == 119 and f["w1.scale"].max() == 127
+
+
+def test_zipf_bias_is_a_permutation_of_ranks():
+    from cachalot_amd.synth import zipf_bias
+
+    b = zipf_bias(384, seed=5)
+    ranks = sorted(b, reverse=True)
+    assert ranks[0] == pytest.approx(0.5) and ranks[-1] == pytest.approx(0.5 * 384 ** -1.1)
+    assert zipf_bias(384, seed=5) == b and zipf_bias(384, seed=6) != b

@@ -1,0 +1,124 @@
+"""Pins for the oracle's codecs: FP4 E2M1/E8M0, the MLX 2-bit affine layout, bf16.
+
+Each check comes from a source independent of the oracle's own code: the
+E2M1 bit-field definition (OCP Microscaling spec), hand-worked bytes and
+words, and torch's own bf16 conversion.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.affine2 import dequantize_affine, dequantize_affine64, pack_2bit, qmv64, unpack_2bit
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
+from oracle.fp4 import FP4_E2M1_TABLE, decode_e8m0, dequantize_fp4_weight, unpack_fp4_e2m1
+
+
+def e2m1_from_bits(code: int) -> float:
+    s, e, m = code >> 3, (code >> 1) & 3, code & 1
+    mag = m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1.0 + m / 2.0)
+    return -mag if s else mag
+
+
+def test_fp4_table_matches_e2m1_bitfield():
+    for code in range(16):
+        assert FP4_E2M1_TABLE[code] == e2m1_from_bits(code), code
+
+
+def test_e8m0_known_values():
+    got = decode_e8m0(np.array([127, 119, 128, 0, 254], np.uint8))
+    assert got.tolist() == [1.0, 2.0 ** -8, 2.0, 2.0 ** -127, 2.0 ** 127]
+
+
+def test_unpack_low_nibble_first():
+    got = unpack_fp4_e2m1(np.array([[0x21, 0xF9, 0x7A]], np.uint8))
+    # 0x21: low 1 -> 0.5, high 2 -> 1.0; 0xF9: low 9 -> -0.5, high 15 -> -6; 0x7A: low 10 -> -1, high 7 -> 6
+    assert got.tolist() == [[0.5, 1.0, -0.5, -6.0, -1.0, 6.0]]
+
+
+def test_dequantize_fp4_block_scales_and_errors():
+    packed = np.full((2, 32), 0x75, np.uint8)          # low 5 -> 3.0, high 7 -> 6.0
+    scales = np.array([[126, 127], [120, 130]], np.uint8)
+    w = dequantize_fp4_weight(packed, scales)
+    assert w.shape == (2, 64)
+    assert w[0, :32].tolist() == [1.5, 3.0] * 16 and w[0, 32:].tolist() == [3.0, 6.0] * 16
+    assert w[1, 0] == 3.0 * 2.0 ** -7 and w[1, 63] == 6.0 * 8.0
+    with pytest.raises(ValueError):
+        dequantize_fp4_weight(packed, scales[:, :1])
+    with pytest.raises(ValueError):
+        dequantize_fp4_weight(np.zeros((1, 8), np.uint8), np.zeros((1, 1), np.uint8))
+
+
+def test_pack_2bit_known_words():
+    q = np.zeros(16, np.uint8)
+    q[0] = 1
+    assert pack_2bit(q).tolist() == [1]
+    q = np.zeros(16, np.uint8)
+    q[15] = 3
+    assert pack_2bit(q).tolist() == [3 << 30]
+    q = np.array([0, 1, 2, 3] * 4, np.uint8)
+    # fields 2i hold q_i: 0b11100100 repeated per byte
+    assert pack_2bit(q).tolist() == [0xE4E4E4E4]
+    with pytest.raises(ValueError):
+        pack_2bit(np.zeros(10, np.uint8))
+
+
+def test_unpack_2bit_roundtrip():
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 4, size=(5, 64), dtype=np.uint8)
+    assert np.array_equal(unpack_2bit(pack_2bit(q)), q)
+    assert np.array_equal(unpack_2bit(pack_2bit(q), 40), q[:, :40])
+
+
+def test_dequantize_affine_elementwise():
+    rng = np.random.default_rng(4)
+    q = rng.integers(0, 4, size=(3, 48), dtype=np.uint8)
+    s = f32_to_bf16_bits(rng.uniform(0.005, 0.05, size=(3, 3)).astype(np.float32))
+    b = f32_to_bf16_bits(rng.normal(0, 0.02, size=(3, 3)).astype(np.float32))
+    w = pack_2bit(q)
+    got = dequantize_affine(w, s, b, k=40, group=16)
+    sf, bf = bf16_bits_to_f32(s), bf16_bits_to_f32(b)
+    for n in range(3):
+        for k in range(40):
+            want = np.float32(np.float32(sf[n, k // 16] * np.float32(q[n, k])) + bf[n, k // 16])
+            assert got[n, k] == want
+    # the float64 form equals the exact value of s*q+b
+    got64 = dequantize_affine64(w, s, b, k=40, group=16)
+    assert got64[1, 17] == float(sf[1, 1]) * int(q[1, 17]) + float(bf[1, 1])
+
+
+def test_qmv64_group_formula_with_partial_last_group():
+    """sum_g s_g * sum(x q) + b_g * sum(x) over a K that ends mid-group."""
+    rng = np.random.default_rng(5)
+    n, k, group = 4, 40, 16
+    q = rng.integers(0, 4, size=(n, 48), dtype=np.uint8)
+    q[:, k:] = 0
+    s = f32_to_bf16_bits(rng.uniform(0.005, 0.05, size=(n, 3)).astype(np.float32))
+    b = f32_to_bf16_bits(rng.normal(0, 0.02, size=(n, 3)).astype(np.float32))
+    x = round_bf16(rng.normal(size=(2, k)).astype(np.float32))
+    got = qmv64(x, pack_2bit(q), s, b, k=k, group=group)
+    sf, bf = bf16_bits_to_f32(s).astype(float), bf16_bits_to_f32(b).astype(float)
+    for m in range(2):
+        for r in range(n):
+            total = 0.0
+            for g in range(3):
+                lo, hi = g * group, min(k, (g + 1) * group)
+                xq = sum(float(x[m, i]) * int(q[r, i]) for i in range(lo, hi))
+                xs = sum(float(x[m, i]) for i in range(lo, hi))
+                total += sf[r, g] * xq + bf[r, g] * xs
+            assert abs(got[m, r] - total) <= 1e-12 * max(1.0, abs(total))
+
+
+def test_round_bf16_matches_torch():
+    rng = np.random.default_rng(6)
+    vals = np.concatenate([
+        rng.normal(size=20000).astype(np.float32),
+        (rng.normal(size=2000) * 1e-30).astype(np.float32),
+        # exact ties: mantissa ends in 0x8000
+        (np.arange(1, 2001, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38], np.float32),
+    ])
+    want = torch.from_numpy(vals).to(torch.bfloat16).float().numpy()
+    got = round_bf16(vals)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
