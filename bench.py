@@ -105,7 +105,7 @@ def main() -> int:
 
     from cachalot_amd import _lib, synth
     from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
-    from cachalot_amd.moe_decode import decode_experts
+    from cachalot_amd.moe_decode import moe_layer_decode
     from cachalot_amd.router import route_topk_fused
     from cachalot_amd.storage.index import affine_format
 
@@ -129,9 +129,8 @@ def main() -> int:
 
     def step(x, s):
         w, b = gates[s % L]
-        route = route_topk_fused(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
-        _, out = decode_experts(x, pool, table[s % L], route.indices, route.weights, swiglu_limit=10.0,
-                                addend=x, want_routed=False)
+        _, out, _ = moe_layer_decode(x, w, b, pool, table[s % L], topk=K, route_scale=1.0, score_fn="sigmoid",
+                                     swiglu_limit=10.0, addend=x)
         return out
 
     # The chain is captured in a HIP graph of G steps (G a multiple of L) and
@@ -190,7 +189,7 @@ def main() -> int:
     reps = max(1, args.steps // n_routes)
     routed_buf = torch.empty(D, dtype=torch.float32, device=dev)
     ws_bytes = _lib.lib().cachalot_moe_decode_q2_workspace_bytes(D, F, K)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     layout = pool.layout()
     stream = _lib.stream_handle(dev)
     Lh = _lib.lib()

@@ -65,6 +65,14 @@ _SIGNATURES = {
     "cachalot_moe_decode_fp4": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
                                         c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_moe_layer_decode_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_float,
+                                             c_int, c_int, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_int,
+                                             c_int, c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_moe_layer_decode_fp4": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_float,
+                                              c_int, c_int, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_int,
+                                              c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                              c_void_p, c_void_p, c_size_t, c_void_p]),
     "cachalot_dequant_fp4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "cachalot_dequant_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                     c_void_p]),

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "common.h"
+#include "topk.h"
 
 namespace cachalot {
 namespace decode {
@@ -39,29 +40,110 @@ __device__ __forceinline__ int expert_slot(const int32_t* slot_table, const int3
 
 __device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
-// After wave_transpose_sum<R_DN * KMAX>: value r*KMAX + e sits in lanes [4(r*KMAX+e), +4).
-// Sums the k expert values of each row in route order (bf16-rounded per expert
-// when BF16_PER_EXPERT), adds the addend and writes the requested outputs.
-template <bool BF16_PER_EXPERT>
-__device__ __forceinline__ void finish_rows(const float red, int lane, int row0, int D, int k,
-                                            const uint16_t* __restrict__ addend, float* __restrict__ routed,
-                                            uint16_t* __restrict__ out) {
-  static_assert(R_DN * KMAX == 16, "lane mapping assumes 16 reduced values");
-  float v[KMAX];
-#pragma unroll
-  for (int e = 0; e < KMAX; ++e) v[e] = __shfl(red, (lane & ~31) + 4 * e, 64);
-  if ((lane & 31) == 0) {
-    const int n = row0 + (lane >> 5);
-    if (n < D) {
-      float acc = 0.0f;
-      for (int e = 0; e < k; ++e) acc = acc + (BF16_PER_EXPERT ? round_bf16(v[e]) : v[e]);
-      if (routed) routed[n] = acc;
-      if (out) {
-        const float t = addend ? acc + bf16_to_f32(addend[n]) : acc;
-        out[n] = f32_to_bf16(t);
+struct RouteArgs {            // fused top-k inputs (FUSE_TOPK)
+  const float* scores;
+  const float* bias;
+  int E;
+  int order;
+  int norm;
+  float route_scale;
+  int32_t* idx_out;
+  float* w_out;
+};
+
+// Workgroup prologue shared by the gate/up kernels of both banks: the k
+// experts' slots and router weights into LDS; with FUSE the top-k itself.
+template <bool FUSE>
+__device__ __forceinline__ void expert_prologue(const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx,
+                                                const float* __restrict__ wts, int E, int k, const RouteArgs& ra,
+                                                int* s_slot, float* s_w, float4* sel4, int* top_i, float* top_v,
+                                                int32_t* ws_slots, float* ws_w) {
+  if constexpr (FUSE) {
+    const int E4 = (ra.E + 3) / 4;
+    load_selection(sel4, ra.E, E4, ra.scores, ra.bias);
+    __syncthreads();
+    block_topk_rank(sel4, ra.E, E4, k, ra.order, ra.scores, top_i, top_v);
+    __syncthreads();
+    if (threadIdx.x == 0) normalise_weights(top_v, k, ra.route_scale, ra.norm, s_w);
+    if (threadIdx.x < k) {
+      const int ex = top_i[threadIdx.x];
+      s_slot[threadIdx.x] = slot_table[ex];
+      if (blockIdx.x == 0 && ra.idx_out) ra.idx_out[threadIdx.x] = ex;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && threadIdx.x < k) {
+      if (ra.w_out) ra.w_out[threadIdx.x] = s_w[threadIdx.x];
+      ws_slots[threadIdx.x] = s_slot[threadIdx.x];
+      ws_w[threadIdx.x] = s_w[threadIdx.x];
+    }
+  } else {
+    if (threadIdx.x < k) {
+      const int ex = idx[threadIdx.x];
+      const int slot = (ex >= 0 && ex < E) ? slot_table[ex] : -1;
+      s_slot[threadIdx.x] = slot;
+      s_w[threadIdx.x] = wts[threadIdx.x];
+      if (blockIdx.x == 0) {
+        ws_slots[threadIdx.x] = slot;
+        ws_w[threadIdx.x] = wts[threadIdx.x];
       }
     }
+    __syncthreads();
   }
+}
+
+// Workspace layout of one decode call: [hidden][per-expert row values][row-block
+// counters][k slots][k weights], each region 256-byte aligned.  The counter
+// region must be zero before the first call; every call leaves it zero.
+struct WsOffsets {
+  size_t hidden, ybuf, counters, slots, weights, total;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+inline WsOffsets ws_offsets(int D, int F, int k, size_t hidden_bytes) {
+  (void)F;
+  WsOffsets o;
+  o.hidden = 0;
+  o.ybuf = align256(hidden_bytes);
+  o.counters = o.ybuf + align256((size_t)k * D * sizeof(float));
+  o.slots = o.counters + align256((size_t)((D + R_DN - 1) / R_DN) * sizeof(uint32_t));
+  o.weights = o.slots + align256(KMAX * sizeof(int32_t));
+  o.total = o.weights + align256(KMAX * sizeof(float));
+  return o;
+}
+
+// After wave_transpose_sum<R_DN>: row r's total sits in lanes [32r, 32r+32).
+// Stores this expert's row values, then the last of the k waves of row block
+// rb (device-scope counter) sums the k values in route order (bf16-rounded per
+// expert when BF16_PER_EXPERT), adds the addend, writes the outputs and resets
+// the counter for the next call.
+template <bool BF16_PER_EXPERT>
+__device__ __forceinline__ void combine_rows(float red, int lane, int e, int rb, int row0, int D, int k,
+                                             float* __restrict__ ybuf, uint32_t* __restrict__ counters,
+                                             const uint16_t* __restrict__ addend, float* __restrict__ routed,
+                                             uint16_t* __restrict__ out) {
+  static_assert(R_DN == 2, "lane mapping assumes two rows per wave");
+  const float y = BF16_PER_EXPERT ? round_bf16(red) : red;
+  const int n_own = row0 + (lane >> 5);
+  if ((lane & 31) == 0 && n_own < D) ybuf[(size_t)e * D + n_own] = y;
+  __threadfence();
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(&counters[rb], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  old = __shfl(old, 0, 64);
+  if (old != (uint32_t)(k - 1)) return;
+  __threadfence();
+  if (lane < R_DN && row0 + lane < D) {
+    const int n = row0 + lane;
+    float acc = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      const uint32_t bits = __hip_atomic_load(reinterpret_cast<uint32_t*>(ybuf + (size_t)j * D + n),
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      acc = acc + __uint_as_float(bits);
+    }
+    if (routed) routed[n] = acc;
+    if (out) out[n] = f32_to_bf16(addend ? acc + bf16_to_f32(addend[n]) : acc);
+  }
+  if (lane == 0) __hip_atomic_store(&counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace decode

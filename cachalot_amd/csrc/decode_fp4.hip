@@ -6,22 +6,26 @@
 // W2_e h_e in fp32 with experts in route order (:160-178).  No bf16 rounding
 // point anywhere on this path.
 //
-//   fp4_gate_up_kernel  one wave = R rows of one expert; lane l owns 64 codes
-//                       (two E8M0 blocks, 32 bytes) of the row, so K = 4096 is a
-//                       2 KiB coalesced wave load per matrix.  Nibbles become
-//                       bf16 pairs (value * 2^e, exact) in the gfx950 converter
-//                       and meet the bf16 activation pairs in v_dot2c_f32_bf16.
-//   fp4_down_kernel     one wave = R rows of W2 for all k experts; lane l owns
+//   fp4_gate_up_kernel  one wave = R rows of one expert (same prologue and
+//                       load-everything-first structure as the 2-bit kernel);
+//                       lane l owns 64 codes (two E8M0 blocks, 32 bytes) of the
+//                       row, so K = 4096 is a 2 KiB coalesced wave load per
+//                       matrix.  Nibbles become bf16 pairs (value * 2^e, exact)
+//                       in the gfx950 converter and meet the bf16 activation
+//                       pairs in v_dot2c_f32_bf16.
+//   fp4_down_kernel     one wave = R rows of W2 for one expert; lane l owns
 //                       words l + 64 i of the row (8 codes each); the fp32 hidden
 //                       vector stays fp32 (converter to f32 pairs, fp32 FMA).
+//                       Per-expert row values are combined in route order by the
+//                       last of the k waves of a row block.
 #include "decode_common.h"
+#include "router_launch.h"
 
 namespace cachalot {
 namespace {
 
 using namespace decode;
 constexpr int R_GU = 4;
-constexpr int MAXC = 2;   // 64-code chunks per lane, gate/up (D <= 8192)
 constexpr int MAXW = 6;   // 8-code words per lane, down (F <= 3072)
 
 __device__ __forceinline__ float fp4_word_dot_bf16(uint32_t w, float scale, const uint32_t* xp, float acc) {
@@ -32,17 +36,56 @@ __device__ __forceinline__ float fp4_word_dot_bf16(uint32_t w, float scale, cons
   return acc;
 }
 
+// 8 uint32 words of one 64-code chunk (two scale blocks) dotted with 32 bf16 pairs of x.
+__device__ __forceinline__ float fp4_chunk_dot(uint4 a, uint4 b, float s0, float s1, const uint32_t* xw) {
+  float acc = 0.0f;
+  acc = fp4_word_dot_bf16(a.x, s0, xw + 0, acc);
+  acc = fp4_word_dot_bf16(a.y, s0, xw + 4, acc);
+  acc = fp4_word_dot_bf16(a.z, s0, xw + 8, acc);
+  acc = fp4_word_dot_bf16(a.w, s0, xw + 12, acc);
+  acc = fp4_word_dot_bf16(b.x, s1, xw + 16, acc);
+  acc = fp4_word_dot_bf16(b.y, s1, xw + 20, acc);
+  acc = fp4_word_dot_bf16(b.z, s1, xw + 24, acc);
+  acc = fp4_word_dot_bf16(b.w, s1, xw + 28, acc);
+  return acc;
+}
+
+template <int C, bool FUSE>
 __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L,
     const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx, const float* __restrict__ wts,
-    int D, int F, int E, float limit, float* __restrict__ hidden) {
+    RouteArgs ra, int D, int F, int E, int k, float limit, float* __restrict__ hidden,
+    int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
+  extern __shared__ float4 lds4[];
+  __shared__ int s_slot[KMAX];
+  __shared__ float s_w[KMAX];
+  __shared__ int top_i[KMAX];
+  __shared__ float top_v[KMAX];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int e = blockIdx.y;
-  const int row0 = (blockIdx.x * WAVES + wave) * R_GU;
-  if (row0 >= F) return;
+  const int NC = D / 64;
+  const int SB = D / 32;
+
+  uint32_t xw[C][32];
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = min(lane + 64 * i, NC - 1);
+    const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)c * 64);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint4 v = xp[q];
+      xw[i][4 * q] = v.x; xw[i][4 * q + 1] = v.y; xw[i][4 * q + 2] = v.z; xw[i][4 * q + 3] = v.w;
+    }
+  }
+
+  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, lds4, top_i, top_v, ws_slots, ws_w);
+
+  const int RB = (F + R_GU - 1) / R_GU;
+  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (item >= k * RB) return;
+  const int e = item / RB;
+  const int row0 = (item % RB) * R_GU;
   float* hout = hidden + (size_t)e * F;
-  const int slot = expert_slot(slot_table, idx, e, E);
+  const int slot = s_slot[e];
   if (slot < 0) {
     if (lane < R_GU && row0 + lane < F) hout[row0 + lane] = 0.0f;
     return;
@@ -52,55 +95,35 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
   const uint8_t* s1 = base + L.off[1];
   const uint4* w3 = reinterpret_cast<const uint4*>(base + L.off[6]);
   const uint8_t* s3 = base + L.off[7];
-  const int NC = D / 64;        // 64-code chunks per row (two uint4 each)
-  const int SB = D / 32;        // scale blocks per row
 
-  uint32_t xw[MAXC][32];
+  uint4 ga[R_GU][C], gb[R_GU][C], ua[R_GU][C], ub[R_GU][C];
+  uint8_t sg0[R_GU][C], sg1[R_GU][C], su0[R_GU][C], su1[R_GU][C];
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)min(c, NC - 1) * 64);
+  for (int r = 0; r < R_GU; ++r) {
+    const int n = min(row0 + r, F - 1);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 v = c < NC ? xp[q] : make_uint4(0, 0, 0, 0);
-      xw[i][4 * q] = v.x; xw[i][4 * q + 1] = v.y; xw[i][4 * q + 2] = v.z; xw[i][4 * q + 3] = v.w;
+    for (int i = 0; i < C; ++i) {
+      const int c = min(lane + 64 * i, NC - 1);
+      ga[r][i] = w1[((size_t)n * NC + c) * 2];
+      gb[r][i] = w1[((size_t)n * NC + c) * 2 + 1];
+      ua[r][i] = w3[((size_t)n * NC + c) * 2];
+      ub[r][i] = w3[((size_t)n * NC + c) * 2 + 1];
+      sg0[r][i] = s1[(size_t)n * SB + 2 * c];
+      sg1[r][i] = s1[(size_t)n * SB + 2 * c + 1];
+      su0[r][i] = s3[(size_t)n * SB + 2 * c];
+      su1[r][i] = s3[(size_t)n * SB + 2 * c + 1];
     }
   }
 
   float part[2 * R_GU];
 #pragma unroll
   for (int r = 0; r < R_GU; ++r) {
-    const int n = min(row0 + r, F - 1);
     float pg = 0.0f, pu = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXC; ++i) {
-      const int c = lane + 64 * i;
-      if (c < NC) {
-        const uint4 g0 = w1[((size_t)n * NC + c) * 2];
-        const uint4 g1 = w1[((size_t)n * NC + c) * 2 + 1];
-        const uint4 u0 = w3[((size_t)n * NC + c) * 2];
-        const uint4 u1 = w3[((size_t)n * NC + c) * 2 + 1];
-        const float sg0 = e8m0_to_f32(s1[(size_t)n * SB + 2 * c]);
-        const float sg1 = e8m0_to_f32(s1[(size_t)n * SB + 2 * c + 1]);
-        const float su0 = e8m0_to_f32(s3[(size_t)n * SB + 2 * c]);
-        const float su1 = e8m0_to_f32(s3[(size_t)n * SB + 2 * c + 1]);
-        pg = fp4_word_dot_bf16(g0.x, sg0, &xw[i][0], pg);
-        pu = fp4_word_dot_bf16(u0.x, su0, &xw[i][0], pu);
-        pg = fp4_word_dot_bf16(g0.y, sg0, &xw[i][4], pg);
-        pu = fp4_word_dot_bf16(u0.y, su0, &xw[i][4], pu);
-        pg = fp4_word_dot_bf16(g0.z, sg0, &xw[i][8], pg);
-        pu = fp4_word_dot_bf16(u0.z, su0, &xw[i][8], pu);
-        pg = fp4_word_dot_bf16(g0.w, sg0, &xw[i][12], pg);
-        pu = fp4_word_dot_bf16(u0.w, su0, &xw[i][12], pu);
-        pg = fp4_word_dot_bf16(g1.x, sg1, &xw[i][16], pg);
-        pu = fp4_word_dot_bf16(u1.x, su1, &xw[i][16], pu);
-        pg = fp4_word_dot_bf16(g1.y, sg1, &xw[i][20], pg);
-        pu = fp4_word_dot_bf16(u1.y, su1, &xw[i][20], pu);
-        pg = fp4_word_dot_bf16(g1.z, sg1, &xw[i][24], pg);
-        pu = fp4_word_dot_bf16(u1.z, su1, &xw[i][24], pu);
-        pg = fp4_word_dot_bf16(g1.w, sg1, &xw[i][28], pg);
-        pu = fp4_word_dot_bf16(u1.w, su1, &xw[i][28], pu);
-      }
+    for (int i = 0; i < C; ++i) {
+      const float valid = (lane + 64 * i < NC) ? 1.0f : 0.0f;
+      pg = pg + valid * fp4_chunk_dot(ga[r][i], gb[r][i], e8m0_to_f32(sg0[r][i]), e8m0_to_f32(sg1[r][i]), xw[i]);
+      pu = pu + valid * fp4_chunk_dot(ua[r][i], ub[r][i], e8m0_to_f32(su0[r][i]), e8m0_to_f32(su1[r][i]), xw[i]);
     }
     part[2 * r] = pg;
     part[2 * r + 1] = pu;
@@ -115,82 +138,145 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
         u = fminf(fmaxf(u, -limit), limit);
         g = fminf(g, limit);
       }
-      hout[n] = (silu_f32(g) * u) * wts[e];
+      hout[n] = (silu_f32(g) * u) * s_w[e];
     }
   }
 }
 
 __global__ void __launch_bounds__(64 * WAVES) fp4_down_kernel(
-    const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ slot_table,
-    const int32_t* __restrict__ idx, int D, int F, int E, int k, const float* __restrict__ hidden,
+    const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
+    const float* __restrict__ hidden, float* __restrict__ ybuf, uint32_t* __restrict__ counters,
     const uint16_t* __restrict__ addend, float* __restrict__ routed, uint16_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * WAVES + wave) * R_DN;
-  if (row0 >= D) return;
+  const int RB = (D + R_DN - 1) / R_DN;
+  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (item >= k * RB) return;
+  const int e = item / RB;
+  const int rb = item % RB;
+  const int row0 = rb * R_DN;
   const int Kw = F / 8;     // 32-bit words per row
   const int SB = F / 32;    // scale blocks per row
-  float part[R_DN * KMAX];
+  const int slot = ws_slots[e];
+  float rowv[R_DN];
 #pragma unroll
-  for (int i = 0; i < R_DN * KMAX; ++i) part[i] = 0.0f;
-
-#pragma unroll 1
-  for (int e = 0; e < k; ++e) {
-    const int slot = expert_slot(slot_table, idx, e, E);
-    if (slot < 0) continue;
+  for (int r = 0; r < R_DN; ++r) rowv[r] = 0.0f;
+  if (slot >= 0) {
     const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
     const uint32_t* w2 = reinterpret_cast<const uint32_t*>(base + L.off[3]);
     const uint8_t* s2 = base + L.off[4];
     const float4* he = reinterpret_cast<const float4*>(hidden + (size_t)e * F);
-    float h[MAXW][8];
+    uint32_t wv[R_DN][MAXW];
+    uint8_t sv[R_DN][MAXW];
+    float4 ha[MAXW], hb[MAXW];
 #pragma unroll
     for (int i = 0; i < MAXW; ++i) {
-      const int j = lane + 64 * i;
-      const float4 a = j < Kw ? he[2 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 b = j < Kw ? he[2 * j + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
-      h[i][0] = a.x; h[i][1] = a.y; h[i][2] = a.z; h[i][3] = a.w;
-      h[i][4] = b.x; h[i][5] = b.y; h[i][6] = b.z; h[i][7] = b.w;
+      const int j = min(lane + 64 * i, Kw - 1);
+      ha[i] = he[2 * j];
+      hb[i] = he[2 * j + 1];
     }
 #pragma unroll
     for (int r = 0; r < R_DN; ++r) {
       const int n = min(row0 + r, D - 1);
+#pragma unroll
+      for (int i = 0; i < MAXW; ++i) {
+        const int j = min(lane + 64 * i, Kw - 1);
+        wv[r][i] = w2[(size_t)n * Kw + j];
+        sv[r][i] = s2[(size_t)n * SB + (j >> 2)];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R_DN; ++r) {
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < MAXW; ++i) {
-        const int j = lane + 64 * i;
-        if (j < Kw) {
-          const uint32_t wv = w2[(size_t)n * Kw + j];
-          const float sc = e8m0_to_f32(s2[(size_t)n * SB + (j >> 2)]);
-          const float2_t p0 = fp4x2_to_f32x2<0>(wv, sc);
-          const float2_t p1 = fp4x2_to_f32x2<1>(wv, sc);
-          const float2_t p2 = fp4x2_to_f32x2<2>(wv, sc);
-          const float2_t p3 = fp4x2_to_f32x2<3>(wv, sc);
-          acc = __builtin_fmaf(p0[0], h[i][0], acc);
-          acc = __builtin_fmaf(p0[1], h[i][1], acc);
-          acc = __builtin_fmaf(p1[0], h[i][2], acc);
-          acc = __builtin_fmaf(p1[1], h[i][3], acc);
-          acc = __builtin_fmaf(p2[0], h[i][4], acc);
-          acc = __builtin_fmaf(p2[1], h[i][5], acc);
-          acc = __builtin_fmaf(p3[0], h[i][6], acc);
-          acc = __builtin_fmaf(p3[1], h[i][7], acc);
+        if (lane + 64 * i < Kw) {
+          const float sc = e8m0_to_f32(sv[r][i]);
+          const float2_t p0 = fp4x2_to_f32x2<0>(wv[r][i], sc);
+          const float2_t p1 = fp4x2_to_f32x2<1>(wv[r][i], sc);
+          const float2_t p2 = fp4x2_to_f32x2<2>(wv[r][i], sc);
+          const float2_t p3 = fp4x2_to_f32x2<3>(wv[r][i], sc);
+          acc = __builtin_fmaf(p0[0], ha[i].x, acc);
+          acc = __builtin_fmaf(p0[1], ha[i].y, acc);
+          acc = __builtin_fmaf(p1[0], ha[i].z, acc);
+          acc = __builtin_fmaf(p1[1], ha[i].w, acc);
+          acc = __builtin_fmaf(p2[0], hb[i].x, acc);
+          acc = __builtin_fmaf(p2[1], hb[i].y, acc);
+          acc = __builtin_fmaf(p3[0], hb[i].z, acc);
+          acc = __builtin_fmaf(p3[1], hb[i].w, acc);
         }
       }
-#pragma unroll
-      for (int ee = 0; ee < KMAX; ++ee)
-        if (ee == e) part[r * KMAX + ee] = acc;
+      rowv[r] = acc;
     }
   }
-  const float red = wave_transpose_sum<R_DN * KMAX>(part, lane);
-  finish_rows<false>(red, lane, row0, D, k, addend, routed, out);
+  const float red = wave_transpose_sum<R_DN>(rowv, lane);
+  combine_rows<false>(red, lane, e, rb, row0, D, k, ybuf, counters, addend, routed, out);
 }
 
 }  // namespace
+
+size_t fp4_workspace_bytes(int D, int F, int k) {
+  return ws_offsets(D, F, k, (size_t)k * F * sizeof(float)).total;
+}
+
+int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
+                      const int32_t* slot_table, const int32_t* idx, const float* w, const RouteArgs* ra, int D,
+                      int F, int E, int k, float swiglu_limit, const uint16_t* addend, float* routed, uint16_t* out,
+                      void* workspace, size_t workspace_bytes, hipStream_t s) {
+  CACHALOT_REQUIRE(pool && layout && slot_table && x, "moe_decode_fp4: null pointer");
+  CACHALOT_REQUIRE(routed || out, "moe_decode_fp4: no output requested");
+  CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_fp4: k=%d outside 1..%d", k, KMAX);
+  CACHALOT_REQUIRE(E >= 1 && E <= 1024, "moe_decode_fp4: E=%d outside 1..1024", E);
+  CACHALOT_REQUIRE(D % 64 == 0 && D >= 64 && D <= 8192, "moe_decode_fp4: D=%d must be a multiple of 64 and <= 8192",
+                   D);
+  CACHALOT_REQUIRE(F % 32 == 0 && F >= 32 && F <= 8 * 64 * MAXW,
+                   "moe_decode_fp4: F=%d must be a multiple of 32 and <= %d", F, 8 * 64 * MAXW);
+  const WsOffsets wo = ws_offsets(D, F, k, (size_t)k * F * sizeof(float));
+  if (workspace == nullptr || workspace_bytes < wo.total)
+    return fail(CACHALOT_ESPACE, "moe_decode_fp4: workspace %zu < %zu bytes", workspace_bytes, wo.total);
+  Layout L;
+  static const int used[6] = {0, 1, 3, 4, 6, 7};
+  int rc = make_layout(layout, 6, used, L, "moe_decode_fp4");
+  if (rc) return rc;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* hidden = reinterpret_cast<float*>(ws + wo.hidden);
+  float* ybuf = reinterpret_cast<float*>(ws + wo.ybuf);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(ws + wo.counters);
+  int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
+  float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
+  RouteArgs none{};
+  const RouteArgs& r = ra ? *ra : none;
+  const int items = k * ((F + R_GU - 1) / R_GU);
+  const int blocks = (items + WAVES - 1) / WAVES;
+  const size_t lds = ra ? (size_t)((ra->E + 3) / 4) * sizeof(float4) : 0;
+  const bool c1 = D <= 4096;
+  if (ra) {
+    if (c1)
+      hipLaunchKernelGGL((fp4_gate_up_kernel<1, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L,
+                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
+    else
+      hipLaunchKernelGGL((fp4_gate_up_kernel<2, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L,
+                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
+  } else {
+    if (c1)
+      hipLaunchKernelGGL((fp4_gate_up_kernel<1, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L,
+                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
+    else
+      hipLaunchKernelGGL((fp4_gate_up_kernel<2, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L,
+                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
+  }
+  rc = check_launch("fp4_gate_up_kernel");
+  if (rc) return rc;
+  const int items2 = k * ((D + R_DN - 1) / R_DN);
+  hipLaunchKernelGGL(fp4_down_kernel, dim3((items2 + WAVES - 1) / WAVES), dim3(64 * WAVES), 0, s, pool, L, ws_slots,
+                     D, F, k, hidden, ybuf, counters, addend, routed, out);
+  return check_launch("fp4_down_kernel");
+}
+
 }  // namespace cachalot
 
 extern "C" size_t cachalot_moe_decode_fp4_workspace_bytes(int D, int F, int k) {
-  (void)D;
-  if (F <= 0 || k <= 0) return 0;
-  return (size_t)k * (size_t)F * sizeof(float);
+  if (D <= 0 || F <= 0 || k <= 0 || k > cachalot::decode::KMAX) return 0;
+  return cachalot::fp4_workspace_bytes(D, F, k);
 }
 
 extern "C" int cachalot_moe_decode_fp4(const uint16_t* x, const uint8_t* pool,
@@ -199,31 +285,31 @@ extern "C" int cachalot_moe_decode_fp4(const uint16_t* x, const uint8_t* pool,
                                        float swiglu_limit, const uint16_t* addend, float* routed, uint16_t* out,
                                        void* workspace, size_t workspace_bytes, cachalot_stream_t stream) {
   using namespace cachalot;
-  using namespace cachalot::decode;
-  CACHALOT_REQUIRE(x && pool && layout && slot_table && idx && w, "moe_decode_fp4: null pointer");
-  CACHALOT_REQUIRE(routed || out, "moe_decode_fp4: no output requested");
-  CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_fp4: k=%d outside 1..%d", k, KMAX);
-  CACHALOT_REQUIRE(E >= 1, "moe_decode_fp4: E=%d", E);
-  CACHALOT_REQUIRE(D % 64 == 0 && D >= 64 && D <= 64 * 64 * MAXC,
-                   "moe_decode_fp4: D=%d must be a multiple of 64 and <= %d", D, 64 * 64 * MAXC);
-  CACHALOT_REQUIRE(F % 32 == 0 && F >= 32 && F <= 8 * 64 * MAXW,
-                   "moe_decode_fp4: F=%d must be a multiple of 32 and <= %d", F, 8 * 64 * MAXW);
-  const size_t need = cachalot_moe_decode_fp4_workspace_bytes(D, F, k);
-  if (workspace_bytes < need || workspace == nullptr)
-    return fail(CACHALOT_ESPACE, "moe_decode_fp4: workspace %zu < %zu bytes", workspace_bytes, need);
-  Layout L;
-  static const int used[6] = {0, 1, 3, 4, 6, 7};
-  int rc = make_layout(layout, 6, used, L, "moe_decode_fp4");
-  if (rc) return rc;
+  CACHALOT_REQUIRE(idx && w, "moe_decode_fp4: null pointer");
+  return launch_fp4_decode(x, pool, layout, slot_table, idx, w, nullptr, D, F, E, k, swiglu_limit, addend, routed,
+                           out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                             int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                             int order, const uint8_t* pool, const cachalot_expert_layout* layout,
+                                             const int32_t* slot_table, int D, int F, float swiglu_limit,
+                                             const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
+                                             float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                             cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(gate_weight && gate_bias && scores, "moe_layer_decode_fp4: null router pointer");
+  CACHALOT_REQUIRE(D % 128 == 0, "moe_layer_decode_fp4: D=%d must be a multiple of 128", D);
+  CACHALOT_REQUIRE(score_fn == CACHALOT_SCORE_SQRT_SOFTPLUS || score_fn == CACHALOT_SCORE_SIGMOID,
+                   "moe_layer_decode_fp4: unknown score function %d", score_fn);
+  CACHALOT_REQUIRE(order == CACHALOT_ORDER_ASCENDING || order == CACHALOT_ORDER_RANK,
+                   "moe_layer_decode_fp4: unknown order %d", order);
+  CACHALOT_REQUIRE(gate_temp != 0.0f, "moe_layer_decode_fp4: gate_temp must be non-zero");
+  CACHALOT_REQUIRE(k >= 1 && k <= E && E <= 1024, "moe_layer_decode_fp4: invalid topk=%d for %d experts", k, E);
   hipStream_t s = (hipStream_t)stream;
-  float* hidden = static_cast<float*>(workspace);
-  dim3 g1((F + R_GU * WAVES - 1) / (R_GU * WAVES), k);
-  hipLaunchKernelGGL(fp4_gate_up_kernel, g1, dim3(64 * WAVES), 0, s, x, pool, L, slot_table, idx, w, D, F, E,
-                     swiglu_limit, hidden);
-  rc = check_launch("fp4_gate_up_kernel");
+  int rc = launch_router_scores(x, gate_weight, 1, D, E, gate_temp, score_fn, scores, s);
   if (rc) return rc;
-  dim3 g2((D + R_DN * WAVES - 1) / (R_DN * WAVES));
-  hipLaunchKernelGGL(fp4_down_kernel, g2, dim3(64 * WAVES), 0, s, pool, L, slot_table, idx, D, F, E, k, hidden,
-                     addend, routed, out);
-  return check_launch("fp4_down_kernel");
+  RouteArgs ra{scores, gate_bias, E, order, norm, route_scale, idx_out, w_out};
+  return launch_fp4_decode(x, pool, layout, slot_table, nullptr, nullptr, &ra, D, F, E, k, swiglu_limit, addend,
+                           routed, out, workspace, workspace_bytes, s);
 }

@@ -5,31 +5,38 @@
 // 93-130 (the traced block), mx.quantized_matmul's group formula
 // s * sum(x q) + b * sum(x) (MLX qdot, as copied at minimax/codes_qmv.py:86-100).
 //
-// Two launches per token-layer:
-//   q2_gate_up_kernel  one wave = R rows of one expert; each lane owns one
-//                      64-code uint4 chunk of the row (K = 4096 -> the whole row
-//                      in one coalesced 1 KiB wave load per matrix).  Codes are
-//                      spread into FP4 nibbles (q in 0..3 is the E2M1 code of
-//                      q/2) and turned into bf16 pairs by the gfx950 converter,
-//                      then dotted with pre-paired bf16 activations
-//                      (v_dot2c_f32_bf16, exact products, fp32 accumulation).
-//                      Epilogue: bf16(g), bf16(u), clamp, bf16(silu(g)*u*w_e),
-//                      written into the workspace in the pair order the down
-//                      kernel consumes.
-//   q2_down_kernel     one wave = R rows of W2 for all k experts; lane l owns
-//                      words l, l+64, l+128 of the row (K = 2880 -> 180 words);
-//                      per (row, expert) partials are reduced with one
-//                      transposed wave reduction, rounded to bf16 per expert
-//                      and summed in route order, + addend, -> fp32 / bf16.
+//   q2_gate_up_kernel  one wave = R_GU rows of one expert.  Prologue per
+//                      workgroup: (optionally) the top-k of the router scores,
+//                      then the k slot lookups, into LDS.  Every weight,
+//                      scale and bias load of the wave is issued before any
+//                      arithmetic, with clamped addresses instead of branches,
+//                      so a wave costs one memory round trip.  Lane l owns one
+//                      64-code uint4 chunk per row (K = 4096: the whole row is
+//                      one coalesced 1 KiB wave load per matrix).  Codes are
+//                      spread into FP4 nibbles (code q in 0..3 is the E2M1
+//                      encoding of q/2), converted to bf16 pairs by the gfx950
+//                      converter with scale 2, and dotted with pre-paired bf16
+//                      activations (v_dot2c_f32_bf16: exact products, fp32 sums).
+//                      Epilogue: bf16(g), bf16(u), clamp,
+//                      h = bf16(silu(g) * u * w_e), written in the pair order
+//                      the down kernel consumes.
+//   q2_down_kernel     one wave = R_DN rows of W2 for one expert; lane l owns
+//                      words l, l+64, l+128 of the row (K = 2880 -> 180 words).
+//                      The row value is rounded to bf16 (the reference's
+//                      per-expert cast) and stored per expert; the last of the
+//                      k waves of a row block (a device-scope counter) sums the
+//                      k values in route order, adds the addend and writes the
+//                      outputs, then resets the counter.
 #include "decode_common.h"
+#include "router_launch.h"
+#include "topk.h"
 
 namespace cachalot {
 namespace {
 
 using namespace decode;
 constexpr int R_GU = 4;     // rows per wave, gate/up
-constexpr int MAXC = 2;     // max 64-code chunks per lane in gate/up (D <= 8192)
-constexpr int MAXW = 3;     // max words per lane in down (F <= 3072)
+constexpr int MAXW = 3;     // words per lane in down (F <= 3072)
 
 // Pair layout of a 16-value word: E_b = (v[4b], v[4b+2]), O_b = (v[4b+1], v[4b+3]);
 // memory order E_0..E_3, O_0..O_3.  Position of value i (0..15) in uint16 units:
@@ -53,8 +60,7 @@ __device__ __forceinline__ float q2_word_dot(uint32_t w, const uint32_t* xe, con
   return acc;
 }
 
-// Build E/O pairs from 4 natural-order words holding (v0,v1),(v2,v3),(v4,v5),(v6,v7)
-// -> E = (v0,v2),(v4,v6); O = (v1,v3),(v5,v7).
+// (v0,v1),(v2,v3) -> E = (v0,v2), O = (v1,v3)
 __device__ __forceinline__ void make_pairs(uint32_t a, uint32_t b, uint32_t& e, uint32_t& o) {
   e = (a & 0xffffu) | (b << 16);
   o = (a >> 16) | (b & 0xffff0000u);
@@ -62,28 +68,46 @@ __device__ __forceinline__ void make_pairs(uint32_t a, uint32_t b, uint32_t& e, 
 
 constexpr uint32_t BF16_ONES = 0x3f803f80u;
 
-
+// grid.x = ceil(k * ceil(F / R_GU) / WAVES); C = 64-code chunks per lane (D <= 4096 * C)
+template <int C, bool FUSE>
 __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L,
     const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx, const float* __restrict__ wts,
-    int D, int F, int E, int group, float limit, uint16_t* __restrict__ hp) {
+    RouteArgs ra, int D, int F, int E, int k, int group, float limit, uint16_t* __restrict__ hp,
+    int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
+  extern __shared__ float4 lds4[];
+  __shared__ int s_slot[KMAX];
+  __shared__ float s_w[KMAX];
+  __shared__ int top_i[KMAX];
+  __shared__ float top_v[KMAX];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int e = blockIdx.y;
-  const int row0 = (blockIdx.x * WAVES + wave) * R_GU;
+  const int NC = D / 64;
+
+  // activation chunk loads first: they do not depend on the routing
+  uint4 xa[C][8];
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const int c = min(lane + 64 * i, NC - 1);
+    const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)c * 64);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) xa[i][q] = xp[q];
+  }
+
+  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, lds4, top_i, top_v, ws_slots, ws_w);
+
+  const int RB = (F + R_GU - 1) / R_GU;
+  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (item >= k * RB) return;
+  const int e = item / RB;
+  const int row0 = (item % RB) * R_GU;
   const int Fw = F / 16;
   uint16_t* hout = hp + (size_t)e * Fw * 16;
-  if (row0 >= F) return;
-  const int slot = expert_slot(slot_table, idx, e, E);
+  const int slot = s_slot[e];
   if (slot < 0) {
-    if (lane < R_GU && row0 + lane < F) {
-      const int n = row0 + lane;
-      hout[(n >> 4) * 16 + pair_pos(n & 15)] = 0;
-    }
+    if (lane < R_GU && row0 + lane < F) hout[((row0 + lane) >> 4) * 16 + pair_pos((row0 + lane) & 15)] = 0;
     return;
   }
   const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
-  const int words = D / 16;   // row stride (D is a whole number of groups)
   const int G = D / group;
   const uint4* w1 = reinterpret_cast<const uint4*>(base + L.off[0]);
   const uint16_t* s1 = reinterpret_cast<const uint16_t*>(base + L.off[1]);
@@ -91,69 +115,68 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
   const uint4* w3 = reinterpret_cast<const uint4*>(base + L.off[6]);
   const uint16_t* s3 = reinterpret_cast<const uint16_t*>(base + L.off[7]);
   const uint16_t* b3 = reinterpret_cast<const uint16_t*>(base + L.off[8]);
-  const int NC = D / 64;
 
-  // activation pairs and sums for this lane's chunks
-  uint32_t xe[MAXC][4][4], xo[MAXC][4][4];
-  float xs[MAXC];
+  // every weight / scale / bias load of this wave, issued together
+  uint4 vg[R_GU][C], vu[R_GU][C];
+  uint16_t sg[R_GU][C], bg[R_GU][C], su[R_GU][C], bu[R_GU][C];
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    const int c = lane + 64 * i;
-    xs[i] = 0.0f;
-    if (c < NC) {
-      const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)c * 64);
+  for (int r = 0; r < R_GU; ++r) {
+    const int n = min(row0 + r, F - 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {  // word j covers x[16j .. 16j+16)
-        const uint4 a = xp[2 * j];
-        const uint4 b = xp[2 * j + 1];
-        make_pairs(a.x, a.y, xe[i][j][0], xo[i][j][0]);
-        make_pairs(a.z, a.w, xe[i][j][1], xo[i][j][1]);
-        make_pairs(b.x, b.y, xe[i][j][2], xo[i][j][2]);
-        make_pairs(b.z, b.w, xe[i][j][3], xo[i][j][3]);
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          s = dot2_bf16(xe[i][j][q], BF16_ONES, s);
-          s = dot2_bf16(xo[i][j][q], BF16_ONES, s);
-        }
-        xs[i] = xs[i] + s;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) xe[i][j][q] = xo[i][j][q] = 0u;
+    for (int i = 0; i < C; ++i) {
+      const int c = min(lane + 64 * i, NC - 1);
+      const int g = (c * 64) / group;
+      vg[r][i] = w1[(size_t)n * NC + c];
+      vu[r][i] = w3[(size_t)n * NC + c];
+      sg[r][i] = s1[(size_t)n * G + g];
+      bg[r][i] = b1[(size_t)n * G + g];
+      su[r][i] = s3[(size_t)n * G + g];
+      bu[r][i] = b3[(size_t)n * G + g];
     }
+  }
+
+  // activation pairs and per-chunk sums
+  uint32_t xe[C][4][4], xo[C][4][4];
+  float xs[C];
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    const bool valid = lane + 64 * i < NC;
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 a = xa[i][2 * j];
+      const uint4 b = xa[i][2 * j + 1];
+      make_pairs(a.x, a.y, xe[i][j][0], xo[i][j][0]);
+      make_pairs(a.z, a.w, xe[i][j][1], xo[i][j][1]);
+      make_pairs(b.x, b.y, xe[i][j][2], xo[i][j][2]);
+      make_pairs(b.z, b.w, xe[i][j][3], xo[i][j][3]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!valid) xe[i][j][q] = xo[i][j][q] = 0u;
+        sum = dot2_bf16(xe[i][j][q], BF16_ONES, sum);
+        sum = dot2_bf16(xo[i][j][q], BF16_ONES, sum);
+      }
+    }
+    xs[i] = sum;
   }
 
   float part[2 * R_GU];
 #pragma unroll
   for (int r = 0; r < R_GU; ++r) {
-    const int n = min(row0 + r, F - 1);
     float pg = 0.0f, pu = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXC; ++i) {
-      const int c = lane + 64 * i;
-      if (c < NC) {
-        const uint4 vg = w1[(size_t)n * (words / 4) + c];
-        const uint4 vu = w3[(size_t)n * (words / 4) + c];
-        const int g = (c * 64) / group;
-        const float sg = bf16_to_f32(s1[(size_t)n * G + g]);
-        const float bg = bf16_to_f32(b1[(size_t)n * G + g]);
-        const float su = bf16_to_f32(s3[(size_t)n * G + g]);
-        const float bu = bf16_to_f32(b3[(size_t)n * G + g]);
-        float dg = 0.0f, du = 0.0f;
-        dg = q2_word_dot(vg.x, xe[i][0], xo[i][0], dg);
-        du = q2_word_dot(vu.x, xe[i][0], xo[i][0], du);
-        dg = q2_word_dot(vg.y, xe[i][1], xo[i][1], dg);
-        du = q2_word_dot(vu.y, xe[i][1], xo[i][1], du);
-        dg = q2_word_dot(vg.z, xe[i][2], xo[i][2], dg);
-        du = q2_word_dot(vu.z, xe[i][2], xo[i][2], du);
-        dg = q2_word_dot(vg.w, xe[i][3], xo[i][3], dg);
-        du = q2_word_dot(vu.w, xe[i][3], xo[i][3], du);
-        pg = pg + (sg * dg + bg * xs[i]);
-        pu = pu + (su * du + bu * xs[i]);
-      }
+    for (int i = 0; i < C; ++i) {
+      float dg = 0.0f, du = 0.0f;
+      dg = q2_word_dot(vg[r][i].x, xe[i][0], xo[i][0], dg);
+      du = q2_word_dot(vu[r][i].x, xe[i][0], xo[i][0], du);
+      dg = q2_word_dot(vg[r][i].y, xe[i][1], xo[i][1], dg);
+      du = q2_word_dot(vu[r][i].y, xe[i][1], xo[i][1], du);
+      dg = q2_word_dot(vg[r][i].z, xe[i][2], xo[i][2], dg);
+      du = q2_word_dot(vu[r][i].z, xe[i][2], xo[i][2], du);
+      dg = q2_word_dot(vg[r][i].w, xe[i][3], xo[i][3], dg);
+      du = q2_word_dot(vu[r][i].w, xe[i][3], xo[i][3], du);
+      pg = pg + (bf16_to_f32(sg[r][i]) * dg + bf16_to_f32(bg[r][i]) * xs[i]);
+      pu = pu + (bf16_to_f32(su[r][i]) * du + bf16_to_f32(bu[r][i]) * xs[i]);
     }
     part[2 * r] = pg;
     part[2 * r + 1] = pu;
@@ -162,8 +185,7 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
   const float red = wave_transpose_sum<2 * R_GU>(part, lane);
   const float up = __shfl(red, lane + 8, 64);
   if ((lane & 15) == 0) {
-    const int r = lane >> 4;
-    const int n = row0 + r;
+    const int n = row0 + (lane >> 4);
     if (n < F) {
       float g = round_bf16(red);
       float u = round_bf16(up);
@@ -171,92 +193,157 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
         u = fminf(fmaxf(u, -limit), limit);
         g = fminf(g, limit);
       }
-      const float h = (silu_f32(g) * u) * wts[e];
+      const float h = (silu_f32(g) * u) * s_w[e];
       hout[(n >> 4) * 16 + pair_pos(n & 15)] = f32_to_bf16(h);
     }
   }
 }
 
+// grid.x = ceil(k * ceil(D / R_DN) / WAVES)
 __global__ void __launch_bounds__(64 * WAVES) q2_down_kernel(
-    const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ slot_table,
-    const int32_t* __restrict__ idx, int D, int F, int E, int k, int group, const uint16_t* __restrict__ hp,
+    const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
+    int group, const uint16_t* __restrict__ hp, float* __restrict__ ybuf, uint32_t* __restrict__ counters,
     const uint16_t* __restrict__ addend, float* __restrict__ routed, uint16_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * WAVES + wave) * R_DN;
-  if (row0 >= D) return;
+  const int RB = (D + R_DN - 1) / R_DN;
+  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (item >= k * RB) return;
+  const int e = item / RB;
+  const int rb = item % RB;
+  const int row0 = rb * R_DN;
   const int Kw = F / 16;                   // valid words per row
-  const int G = (F + group - 1) / group;   // groups per row (last may be partial)
+  const int G = (F + group - 1) / group;   // groups per row (the last may be partial)
   const int stride = G * group / 16;       // stored words per row
-  float part[R_DN * KMAX];
-#pragma unroll
-  for (int i = 0; i < R_DN * KMAX; ++i) part[i] = 0.0f;
+  const int slot = ws_slots[e];
 
-#pragma unroll 1
-  for (int e = 0; e < k; ++e) {
-    const int slot = expert_slot(slot_table, idx, e, E);
-    if (slot < 0) continue;
+  float rowv[R_DN];
+#pragma unroll
+  for (int r = 0; r < R_DN; ++r) rowv[r] = 0.0f;
+  if (slot >= 0) {
     const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
     const uint32_t* w2 = reinterpret_cast<const uint32_t*>(base + L.off[3]);
     const uint16_t* s2 = reinterpret_cast<const uint16_t*>(base + L.off[4]);
     const uint16_t* b2 = reinterpret_cast<const uint16_t*>(base + L.off[5]);
     const uint4* hpe = reinterpret_cast<const uint4*>(hp + (size_t)e * Kw * 16);
-    uint32_t he[MAXW][4], ho[MAXW][4];
-    float hs[MAXW];
+    uint32_t wv[R_DN][MAXW];
+    uint16_t sv[R_DN][MAXW], bv[R_DN][MAXW];
+    uint4 ha[MAXW], hb[MAXW];
 #pragma unroll
     for (int i = 0; i < MAXW; ++i) {
-      const int j = lane + 64 * i;
-      hs[i] = 0.0f;
-      if (j < Kw) {
-        const uint4 a = hpe[2 * j];
-        const uint4 b = hpe[2 * j + 1];
-        he[i][0] = a.x; he[i][1] = a.y; he[i][2] = a.z; he[i][3] = a.w;
-        ho[i][0] = b.x; ho[i][1] = b.y; ho[i][2] = b.z; ho[i][3] = b.w;
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          s = dot2_bf16(he[i][q], BF16_ONES, s);
-          s = dot2_bf16(ho[i][q], BF16_ONES, s);
-        }
-        hs[i] = s;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) he[i][q] = ho[i][q] = 0u;
-      }
+      const int j = min(lane + 64 * i, Kw - 1);
+      ha[i] = hpe[2 * j];
+      hb[i] = hpe[2 * j + 1];
     }
 #pragma unroll
     for (int r = 0; r < R_DN; ++r) {
       const int n = min(row0 + r, D - 1);
+#pragma unroll
+      for (int i = 0; i < MAXW; ++i) {
+        const int j = min(lane + 64 * i, Kw - 1);
+        const int g = (j * 16) / group;
+        wv[r][i] = w2[(size_t)n * stride + j];
+        sv[r][i] = s2[(size_t)n * G + g];
+        bv[r][i] = b2[(size_t)n * G + g];
+      }
+    }
+    uint32_t he[MAXW][4], ho[MAXW][4];
+    float hs[MAXW];
+#pragma unroll
+    for (int i = 0; i < MAXW; ++i) {
+      const bool valid = lane + 64 * i < Kw;
+      he[i][0] = valid ? ha[i].x : 0u; he[i][1] = valid ? ha[i].y : 0u;
+      he[i][2] = valid ? ha[i].z : 0u; he[i][3] = valid ? ha[i].w : 0u;
+      ho[i][0] = valid ? hb[i].x : 0u; ho[i][1] = valid ? hb[i].y : 0u;
+      ho[i][2] = valid ? hb[i].z : 0u; ho[i][3] = valid ? hb[i].w : 0u;
+      float s = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        s = dot2_bf16(he[i][q], BF16_ONES, s);
+        s = dot2_bf16(ho[i][q], BF16_ONES, s);
+      }
+      hs[i] = s;
+    }
+#pragma unroll
+    for (int r = 0; r < R_DN; ++r) {
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < MAXW; ++i) {
-        const int j = lane + 64 * i;
-        if (j < Kw) {
-          const uint32_t wv = w2[(size_t)n * stride + j];
-          const int g = (j * 16) / group;
-          const float s = bf16_to_f32(s2[(size_t)n * G + g]);
-          const float b = bf16_to_f32(b2[(size_t)n * G + g]);
-          const float d = q2_word_dot(wv, he[i], ho[i], 0.0f);
-          acc = acc + (s * d + b * hs[i]);
-        }
+        const float d = q2_word_dot(wv[r][i], he[i], ho[i], 0.0f);
+        acc = acc + (bf16_to_f32(sv[r][i]) * d + bf16_to_f32(bv[r][i]) * hs[i]);
       }
-      // e < KMAX is guaranteed by the host
-#pragma unroll
-      for (int ee = 0; ee < KMAX; ++ee)
-        if (ee == e) part[r * KMAX + ee] = acc;
+      rowv[r] = acc;
     }
   }
-  const float red = wave_transpose_sum<R_DN * KMAX>(part, lane);
-  finish_rows<true>(red, lane, row0, D, k, addend, routed, out);
+  const float red = wave_transpose_sum<R_DN>(rowv, lane);
+  combine_rows<true>(red, lane, e, rb, row0, D, k, ybuf, counters, addend, routed, out);
 }
 
 }  // namespace
+
+size_t q2_workspace_bytes(int D, int F, int k) {
+  return ws_offsets(D, F, k, (size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t)).total;
+}
+
+int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
+                     const int32_t* slot_table, const int32_t* idx, const float* w, const RouteArgs* ra, int D,
+                     int F, int E, int k, int group, float swiglu_limit, const uint16_t* addend, float* routed,
+                     uint16_t* out, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  CACHALOT_REQUIRE(pool && layout && slot_table && x, "moe_decode_q2: null pointer");
+  CACHALOT_REQUIRE(routed || out, "moe_decode_q2: no output requested");
+  CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_q2: k=%d outside 1..%d", k, KMAX);
+  CACHALOT_REQUIRE(E >= 1 && E <= 1024, "moe_decode_q2: E=%d outside 1..1024", E);
+  CACHALOT_REQUIRE(group == 64 || group == 128, "moe_decode_q2: group_size %d (64 or 128)", group);
+  CACHALOT_REQUIRE(D % group == 0 && D >= 64 && D <= 8192,
+                   "moe_decode_q2: D=%d must be a multiple of group %d and <= 8192", D, group);
+  CACHALOT_REQUIRE(F % 16 == 0 && F >= 16 && F <= 16 * 64 * MAXW,
+                   "moe_decode_q2: F=%d must be a multiple of 16 and <= %d", F, 16 * 64 * MAXW);
+  const WsOffsets wo = ws_offsets(D, F, k, (size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t));
+  if (workspace == nullptr || workspace_bytes < wo.total)
+    return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, wo.total);
+  Layout L;
+  static const int used[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
+  int rc = make_layout(layout, 9, used, L, "moe_decode_q2");
+  if (rc) return rc;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* hp = reinterpret_cast<uint16_t*>(ws + wo.hidden);
+  float* ybuf = reinterpret_cast<float*>(ws + wo.ybuf);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(ws + wo.counters);
+  int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
+  float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
+  RouteArgs none{};
+  const RouteArgs& r = ra ? *ra : none;
+  const int items = k * ((F + R_GU - 1) / R_GU);
+  const int blocks = (items + WAVES - 1) / WAVES;
+  const size_t lds = ra ? (size_t)((ra->E + 3) / 4) * sizeof(float4) : 0;
+  const bool c1 = D <= 4096;
+  if (ra) {
+    if (c1)
+      hipLaunchKernelGGL((q2_gate_up_kernel<1, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L, slot_table,
+                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
+    else
+      hipLaunchKernelGGL((q2_gate_up_kernel<2, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L, slot_table,
+                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
+  } else {
+    if (c1)
+      hipLaunchKernelGGL((q2_gate_up_kernel<1, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L, slot_table,
+                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
+    else
+      hipLaunchKernelGGL((q2_gate_up_kernel<2, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L, slot_table,
+                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
+  }
+  rc = check_launch("q2_gate_up_kernel");
+  if (rc) return rc;
+  const int items2 = k * ((D + R_DN - 1) / R_DN);
+  hipLaunchKernelGGL(q2_down_kernel, dim3((items2 + WAVES - 1) / WAVES), dim3(64 * WAVES), 0, s, pool, L, ws_slots, D,
+                     F, k, group, hp, ybuf, counters, addend, routed, out);
+  return check_launch("q2_down_kernel");
+}
+
 }  // namespace cachalot
 
 extern "C" size_t cachalot_moe_decode_q2_workspace_bytes(int D, int F, int k) {
-  (void)D;
-  if (F <= 0 || k <= 0) return 0;
-  return (size_t)k * (size_t)((F + 15) / 16) * 16 * sizeof(uint16_t);
+  if (D <= 0 || F <= 0 || k <= 0 || k > cachalot::decode::KMAX) return 0;
+  return cachalot::q2_workspace_bytes(D, F, k);
 }
 
 extern "C" int cachalot_moe_decode_q2(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
@@ -265,31 +352,31 @@ extern "C" int cachalot_moe_decode_q2(const uint16_t* x, const uint8_t* pool, co
                                       float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
                                       cachalot_stream_t stream) {
   using namespace cachalot;
-  CACHALOT_REQUIRE(x && pool && layout && slot_table && idx && w, "moe_decode_q2: null pointer");
-  CACHALOT_REQUIRE(routed || out, "moe_decode_q2: no output requested");
-  CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_q2: k=%d outside 1..%d", k, KMAX);
-  CACHALOT_REQUIRE(E >= 1, "moe_decode_q2: E=%d", E);
-  CACHALOT_REQUIRE(group == 64 || group == 128, "moe_decode_q2: group_size %d (64 or 128)", group);
-  CACHALOT_REQUIRE(D % group == 0 && D >= 64 && D <= 64 * 64 * MAXC,
-                   "moe_decode_q2: D=%d must be a multiple of group %d and <= %d", D, group, 64 * 64 * MAXC);
-  CACHALOT_REQUIRE(F % 16 == 0 && F >= 16 && F <= 16 * 64 * MAXW,
-                   "moe_decode_q2: F=%d must be a multiple of 16 and <= %d", F, 16 * 64 * MAXW);
-  const size_t need = cachalot_moe_decode_q2_workspace_bytes(D, F, k);
-  if (workspace_bytes < need || workspace == nullptr)
-    return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, need);
-  Layout L;
-  static const int used[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
-  int rc = make_layout(layout, 9, used, L, "moe_decode_q2");
-  if (rc) return rc;
+  CACHALOT_REQUIRE(idx && w, "moe_decode_q2: null pointer");
+  return launch_q2_decode(x, pool, layout, slot_table, idx, w, nullptr, D, F, E, k, group, swiglu_limit, addend,
+                          routed, out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                            int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                            int order, const uint8_t* pool, const cachalot_expert_layout* layout,
+                                            const int32_t* slot_table, int D, int F, int group, float swiglu_limit,
+                                            const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
+                                            float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                            cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(gate_weight && gate_bias && scores, "moe_layer_decode_q2: null router pointer");
+  CACHALOT_REQUIRE(D % 128 == 0, "moe_layer_decode_q2: D=%d must be a multiple of 128", D);
+  CACHALOT_REQUIRE(score_fn == CACHALOT_SCORE_SQRT_SOFTPLUS || score_fn == CACHALOT_SCORE_SIGMOID,
+                   "moe_layer_decode_q2: unknown score function %d", score_fn);
+  CACHALOT_REQUIRE(order == CACHALOT_ORDER_ASCENDING || order == CACHALOT_ORDER_RANK,
+                   "moe_layer_decode_q2: unknown order %d", order);
+  CACHALOT_REQUIRE(gate_temp != 0.0f, "moe_layer_decode_q2: gate_temp must be non-zero");
+  CACHALOT_REQUIRE(k >= 1 && k <= E && E <= 1024, "moe_layer_decode_q2: invalid topk=%d for %d experts", k, E);
   hipStream_t s = (hipStream_t)stream;
-  uint16_t* hp = static_cast<uint16_t*>(workspace);
-  dim3 g1((F + R_GU * WAVES - 1) / (R_GU * WAVES), k);
-  hipLaunchKernelGGL(q2_gate_up_kernel, g1, dim3(64 * WAVES), 0, s, x, pool, L, slot_table, idx, w, D, F, E, group,
-                     swiglu_limit, hp);
-  rc = check_launch("q2_gate_up_kernel");
+  int rc = launch_router_scores(x, gate_weight, 1, D, E, gate_temp, score_fn, scores, s);
   if (rc) return rc;
-  dim3 g2((D + R_DN * WAVES - 1) / (R_DN * WAVES));
-  hipLaunchKernelGGL(q2_down_kernel, g2, dim3(64 * WAVES), 0, s, pool, L, slot_table, idx, D, F, E, k, group, hp,
-                     addend, routed, out);
-  return check_launch("q2_down_kernel");
+  RouteArgs ra{scores, gate_bias, E, order, norm, route_scale, idx_out, w_out};
+  return launch_q2_decode(x, pool, layout, slot_table, nullptr, nullptr, &ra, D, F, E, k, group, swiglu_limit,
+                          addend, routed, out, workspace, workspace_bytes, s);
 }

@@ -19,13 +19,13 @@
 //                         are loaded once per wave and reused for TT tokens.
 //   router_topk_kernel    one workgroup per token; thread e computes the rank of
 //                         expert e among all E by counting the experts that beat it.
-#include "common.h"
+#include "router_launch.h"
+#include "topk.h"
 
 namespace cachalot {
 namespace {
 
-constexpr int CHUNKS = 16;
-constexpr int TT = 4;  // tokens per wave pass
+constexpr int CHUNKS = 64;  // one chunk per lane of a wave64
 
 constexpr double INV_LN2 = 1.4426950408889634;
 constexpr double LN2_HI = 6.93147180369123816490e-01;
@@ -72,115 +72,118 @@ __device__ float score_of(float z32, int fn) {
   return sqrtf((float)sp);
 }
 
-// grid.x = ceil(E / (4 * waves)), grid.y = ceil(T / TT); block = 64 * waves
+// One wave per expert row (lane l owns chunk l of D/64 elements), TT tokens per
+// wave, 4 waves per workgroup.  NV = uint4 loads per lane per row (D = 512 * NV);
+// NV = 0 is the generic path (D a multiple of 128, u32 loads).
+template <int TT, int NV>
 __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ W, int T, int D,
                                                             int E, float gate_temp, int fn,
                                                             float* __restrict__ scores) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
-  const int row = (blockIdx.x * waves + wave) * 4 + (lane >> 4);
-  const int chunk = lane & 15;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= E) return;
   const int t0 = blockIdx.y * TT;
-  const int ch = D / CHUNKS;  // multiple of 8 (checked on the host)
-  const bool row_ok = row < E;
-  const uint4* wp = reinterpret_cast<const uint4*>(W + (size_t)(row_ok ? row : 0) * D + (size_t)chunk * ch);
+  const int ch = D / CHUNKS;
+  const uint16_t* wrow = W + (size_t)row * D + (size_t)lane * ch;
+  const uint16_t* xrow[TT];
+#pragma unroll
+  for (int j = 0; j < TT; ++j) xrow[j] = x + (size_t)min(t0 + j, T - 1) * D + (size_t)lane * ch;
   float acc[TT];
 #pragma unroll
   for (int j = 0; j < TT; ++j) acc[j] = 0.0f;
-  const uint4* xp[TT];
+  if constexpr (NV > 0) {
+    uint4 wv[NV];
 #pragma unroll
-  for (int j = 0; j < TT; ++j) {
-    const int t = min(t0 + j, T - 1);
-    xp[j] = reinterpret_cast<const uint4*>(x + (size_t)t * D + (size_t)chunk * ch);
-  }
-  for (int v = 0; v < ch / 8; ++v) {
-    const uint4 wv = wp[v];
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    for (int v = 0; v < NV; ++v) wv[v] = reinterpret_cast<const uint4*>(wrow)[v];
 #pragma unroll
     for (int j = 0; j < TT; ++j) {
-      const uint4 xv = xp[j][v];
-      const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+      uint4 xv[NV];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[j] = acc[j] + __uint_as_float(xx[q] << 16) * __uint_as_float(ww[q] << 16);
-        acc[j] = acc[j] + __uint_as_float(xx[q] & 0xffff0000u) * __uint_as_float(ww[q] & 0xffff0000u);
+      for (int v = 0; v < NV; ++v) xv[v] = reinterpret_cast<const uint4*>(xrow[j])[v];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const uint32_t ww[4] = {wv[v].x, wv[v].y, wv[v].z, wv[v].w};
+        const uint32_t xx[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[j] = acc[j] + __uint_as_float(xx[q] << 16) * __uint_as_float(ww[q] << 16);
+          acc[j] = acc[j] + __uint_as_float(xx[q] & 0xffff0000u) * __uint_as_float(ww[q] & 0xffff0000u);
+        }
+      }
+    }
+  } else {
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(wrow);
+    for (int v = 0; v < ch / 2; ++v) {
+      const uint32_t ww = wp[v];
+#pragma unroll
+      for (int j = 0; j < TT; ++j) {
+        const uint32_t xx = reinterpret_cast<const uint32_t*>(xrow[j])[v];
+        acc[j] = acc[j] + __uint_as_float(xx << 16) * __uint_as_float(ww << 16);
+        acc[j] = acc[j] + __uint_as_float(xx & 0xffff0000u) * __uint_as_float(ww & 0xffff0000u);
       }
     }
   }
 #pragma unroll
   for (int j = 0; j < TT; ++j) {
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) acc[j] = acc[j] + __shfl_xor(acc[j], m, 64);
+    for (int m = 32; m >= 1; m >>= 1) acc[j] = acc[j] + __shfl_xor(acc[j], m, 64);
   }
-  if (chunk == 0 && row_ok) {
+  if (lane < TT) {
+    // lane j finishes token j (all lanes hold every total after the butterfly)
+    float v = acc[0];
 #pragma unroll
-    for (int j = 0; j < TT; ++j) {
-      const int t = t0 + j;
-      if (t < T) scores[(size_t)t * E + row] = score_of(acc[j] / gate_temp, fn);
-    }
+    for (int j = 1; j < TT; ++j)
+      if (lane == j) v = acc[j];
+    const int t = t0 + lane;
+    if (t < T) scores[(size_t)t * E + row] = score_of(v / gate_temp, fn);
   }
 }
 
-// One workgroup (>= E threads, multiple of 64) per token.  Dynamic LDS holds
-// the E selection values followed by the k winners' scores.
+// One workgroup per token; LDS: ceil(E/4) float4 selection values, then k winners.
 __global__ void __launch_bounds__(1024) router_topk_kernel(const float* __restrict__ scores,
                                                            const float* __restrict__ bias,
                                                            const float* __restrict__ bias_vl,
                                                            const uint8_t* __restrict__ image_mask, int E,
                                                            int k, float route_scale, int norm, int order,
                                                            int32_t* __restrict__ idx, float* __restrict__ w) {
-  extern __shared__ float lds[];
-  float* sel = lds;
-  float* top = lds + E;
+  extern __shared__ float4 lds4[];
+  const int E4 = (E + 3) / 4;
+  float4* sel4 = lds4;
+  int* top_i = reinterpret_cast<int*>(lds4 + E4);
+  float* top_v = reinterpret_cast<float*>(top_i + k);
   const int t = blockIdx.x;
-  const int e = threadIdx.x;
   const float* s = scores + (size_t)t * E;
   const float* b = (image_mask != nullptr && image_mask[t] != 0) ? bias_vl : bias;
-  if (e < E) {
-    float v = s[e] + b[e];
-    if (v != v) v = -INFINITY;  // NaN never wins
-    sel[e] = v;
-  }
+  load_selection(sel4, E, E4, s, b);
   __syncthreads();
-  if (e < E) {
-    const float me = sel[e];
-    int rank = 0;
-    if (order == CACHALOT_ORDER_ASCENDING) {
-      // stable argsort(sel)[-k:]: a tie goes to the larger index
-      for (int j = 0; j < E; ++j) {
-        const float o = sel[j];
-        rank += (o > me || (o == me && j > e)) ? 1 : 0;
-      }
-    } else {
-      // argpartition(-sel): a tie goes to the lower index
-      for (int j = 0; j < E; ++j) {
-        const float o = sel[j];
-        rank += (o > me || (o == me && j < e)) ? 1 : 0;
-      }
-    }
-    if (rank < k) {
-      const int pos = order == CACHALOT_ORDER_ASCENDING ? k - 1 - rank : rank;
-      idx[(size_t)t * k + pos] = e;
-      top[pos] = s[e];
-    }
-  }
+  block_topk_rank(sel4, E, E4, k, order, s, top_i, top_v);
   __syncthreads();
-  if (e == 0) {
-    float* wt = w + (size_t)t * k;
-    if (norm && k > 1) {
-      float total = 0.0f;
-      for (int j = 0; j < k; ++j) total = total + top[j];
-      const float denom = total + 1e-20f;
-      for (int j = 0; j < k; ++j) wt[j] = (top[j] / denom) * route_scale;
-    } else {
-      for (int j = 0; j < k; ++j) wt[j] = top[j] * route_scale;
-    }
-  }
+  if (threadIdx.x < k) idx[(size_t)t * k + threadIdx.x] = top_i[threadIdx.x];
+  if (threadIdx.x == 0) normalise_weights(top_v, k, route_scale, norm, w + (size_t)t * k);
 }
 
 }  // namespace
+
+template <int TT>
+static void launch_scores_tt(const uint16_t* x, const uint16_t* W, int T, int D, int E, float temp, int fn,
+                             float* scores, hipStream_t s) {
+  dim3 grid((E + 3) / 4, (T + TT - 1) / TT);
+  switch (D) {
+    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
+    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
+    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
+    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
+  }
+}
+
+int launch_router_scores(const uint16_t* x, const uint16_t* W, int T, int D, int E, float gate_temp, int fn,
+                         float* scores, hipStream_t s) {
+  if (T >= 4) launch_scores_tt<4>(x, W, T, D, E, gate_temp, fn, scores, s);
+  else launch_scores_tt<1>(x, W, T, D, E, gate_temp, fn, scores, s);
+  return check_launch("router_scores_kernel");
+}
+
 }  // namespace cachalot
 
 extern "C" int cachalot_router_topk(const uint16_t* x, const uint16_t* W, const float* bias,
@@ -202,14 +205,11 @@ extern "C" int cachalot_router_topk(const uint16_t* x, const uint16_t* W, const 
   CACHALOT_REQUIRE((image_mask == nullptr) == (bias_vl == nullptr),
                    "router: bias_vl and image_mask must be supplied together, or neither");
   hipStream_t s = (hipStream_t)stream;
-  const int waves = 4;
-  dim3 g1((E + 4 * waves - 1) / (4 * waves), (T + TT - 1) / TT);
-  hipLaunchKernelGGL(router_scores_kernel, g1, dim3(64 * waves), 0, s, x, W, T, D, E, gate_temp, score_fn,
-                     scores);
-  int rc = check_launch("router_scores_kernel");
+  int rc = launch_router_scores(x, W, T, D, E, gate_temp, score_fn, scores, s);
   if (rc) return rc;
-  const int threads = ((E + 63) / 64) * 64;
-  hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(threads), (E + k) * sizeof(float), s, scores, bias, bias_vl,
-                     image_mask, E, k, route_scale, norm, order, idx, w);
+  const int threads = min(1024, ((E + 63) / 64) * 64);
+  const size_t lds = (size_t)((E + 3) / 4) * sizeof(float4) + (size_t)k * (sizeof(int) + sizeof(float));
+  hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(threads), lds, s, scores, bias, bias_vl, image_mask, E, k,
+                     route_scale, norm, order, idx, w);
   return check_launch("router_topk_kernel");
 }

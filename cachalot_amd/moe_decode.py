@@ -15,7 +15,25 @@ import torch
 
 from . import _lib
 from .cache.slots import HBMSlotPool
+from .router import RouterResult
 from .storage.index import ExpertFormat
+
+_WORKSPACES: dict[tuple, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A zero-filled decode workspace cached per (device, stream).
+
+    The kernels keep row-block counters in it and leave them at zero, so it is
+    zeroed once, at allocation.  Calls on one stream are ordered and may share
+    it; a HIP-graph capture must be preceded by an eager call of the same shape
+    so that the workspace exists before capture."""
+    key = (device.index, _lib.stream_handle(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor, idx: torch.Tensor,
@@ -53,7 +71,7 @@ def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor,
     e = int(slot_table.numel())
     if fmt.kind == "affine":
         nbytes = L.cachalot_moe_decode_q2_workspace_bytes(d, f, k)
-        ws = torch.empty((max(1, nbytes),), dtype=torch.uint8, device=dev)
+        ws = workspace(dev, nbytes)
         rc = L.cachalot_moe_decode_q2(x.data_ptr(), pool.storage.data_ptr(), layout, slot_table.data_ptr(),
                                       idx.data_ptr(), weights.data_ptr(), d, f, e, k, fmt.group_size,
                                       float(swiglu_limit), _lib.ptr(addend), _lib.ptr(routed), _lib.ptr(out),
@@ -61,7 +79,7 @@ def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor,
         _lib.check(rc, "moe_decode_q2")
     elif fmt.kind == "fp4":
         nbytes = L.cachalot_moe_decode_fp4_workspace_bytes(d, f, k)
-        ws = torch.empty((max(1, nbytes),), dtype=torch.uint8, device=dev)
+        ws = workspace(dev, nbytes)
         rc = L.cachalot_moe_decode_fp4(x.data_ptr(), pool.storage.data_ptr(), layout, slot_table.data_ptr(),
                                        idx.data_ptr(), weights.data_ptr(), d, f, e, k, float(swiglu_limit),
                                        _lib.ptr(addend), _lib.ptr(routed), _lib.ptr(out), ws.data_ptr(), nbytes,
@@ -70,6 +88,62 @@ def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor,
     else:
         raise ValueError(f"unknown expert format {fmt.kind!r}")
     return routed, out
+
+
+def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torch.Tensor, pool: HBMSlotPool,
+                     slot_table: torch.Tensor, *, topk: int = 6, gate_temp: float = 1.0, route_scale: float = 1.5,
+                     norm_topk_prob: bool = True, score_fn: str = "sqrt_softplus", order: str = "ascending",
+                     swiglu_limit: float = 10.0, addend: torch.Tensor | None = None, want_routed: bool = False,
+                     want_out: bool = True):
+    """One token through one MoE layer with routing on the device (three launches).
+
+    Returns (routed fp32 [D] or None, out bf16 [D] or None, RouterResult)."""
+    fmt: ExpertFormat = pool.format
+    d, f = fmt.d_model, fmt.d_ff
+    if x.ndim != 1 or x.shape[0] != d:
+        raise ValueError(f"x must be 1D with {d} elements, got {tuple(x.shape)}")
+    if x.dtype != torch.bfloat16 or gate_weight.dtype != torch.bfloat16:
+        raise TypeError("decode expects bf16 activations and a bf16 gate weight")
+    n_experts = gate_weight.shape[0]
+    if tuple(gate_weight.shape) != (n_experts, d) or tuple(gate_bias.shape) != (n_experts,):
+        raise ValueError(f"gate weight {tuple(gate_weight.shape)} / bias {tuple(gate_bias.shape)} do not match D={d}")
+    if slot_table.numel() != n_experts:
+        raise ValueError(f"slot table has {slot_table.numel()} entries for {n_experts} experts")
+    if not 1 <= topk <= min(n_experts, 8):
+        raise ValueError(f"Invalid topk={topk} for {n_experts} experts")
+    if score_fn not in _lib.SCORE_FNS or order not in _lib.ORDERS:
+        raise ValueError(f"unknown score_fn / order {score_fn!r} / {order!r}")
+    _lib.require_cuda(x, gate_weight, gate_bias, slot_table, addend)
+    dev = x.device
+    gate_bias = gate_bias.to(torch.float32).contiguous()
+    slot_table = slot_table.to(torch.int32).contiguous()
+    if addend is not None and (addend.dtype != torch.bfloat16 or addend.shape != x.shape):
+        raise ValueError("addend must be a bf16 vector shaped like x")
+    idx = torch.empty((topk,), dtype=torch.int32, device=dev)
+    w = torch.empty((topk,), dtype=torch.float32, device=dev)
+    scores = torch.empty((n_experts,), dtype=torch.float32, device=dev)
+    routed = torch.empty((d,), dtype=torch.float32, device=dev) if want_routed else None
+    out = torch.empty((d,), dtype=torch.bfloat16, device=dev) if want_out else None
+    L = _lib.lib()
+    args_route = (x.contiguous().data_ptr(), gate_weight.contiguous().data_ptr(), gate_bias.data_ptr(), n_experts,
+                  topk, _lib.SCORE_FNS[score_fn], float(gate_temp), float(route_scale),
+                  1 if norm_topk_prob else 0, _lib.ORDERS[order], pool.storage.data_ptr(), pool.layout(),
+                  slot_table.data_ptr(), d, f)
+    tail = (_lib.ptr(addend), idx.data_ptr(), w.data_ptr(), scores.data_ptr(), _lib.ptr(routed), _lib.ptr(out))
+    stream = _lib.stream_handle(dev)
+    if fmt.kind == "affine":
+        nbytes = L.cachalot_moe_decode_q2_workspace_bytes(d, f, topk)
+        ws = workspace(dev, nbytes)
+        rc = L.cachalot_moe_layer_decode_q2(*args_route, fmt.group_size, float(swiglu_limit), *tail, ws.data_ptr(),
+                                            nbytes, stream)
+    elif fmt.kind == "fp4":
+        nbytes = L.cachalot_moe_decode_fp4_workspace_bytes(d, f, topk)
+        ws = workspace(dev, nbytes)
+        rc = L.cachalot_moe_layer_decode_fp4(*args_route, float(swiglu_limit), *tail, ws.data_ptr(), nbytes, stream)
+    else:
+        raise ValueError(f"unknown expert format {fmt.kind!r}")
+    _lib.check(rc, "moe_layer_decode")
+    return routed, out, RouterResult(indices=idx, weights=w, scores=scores)
 
 
 def _experts_table(experts):

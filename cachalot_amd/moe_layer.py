@@ -9,8 +9,8 @@ reads the ids on the host, asks the store for the experts and launches the
 expert kernels (``moe_layer_metal.py:220-300``).  Here the whole bank is
 resident in HBM and the store's (layer, expert) -> slot table lives on the
 device, so the router's ids go straight into the expert kernels: three
-launches (router scores, top-k, gate/up) plus the down/combine launch, no host
-synchronisation.  When a layer is not fully resident the host path is taken:
+launches (router scores; top-k + slot lookup + gate/up; down + route-order
+combine), no host synchronisation.  When a layer is not fully resident the host path is taken:
 one synchronisation, ``get_many`` (which loads misses), then the same kernels.
 
 The FP8 shared expert the reference adds into the combine
@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from .cache.resident_store import ResidentExpertStore
-from .moe_decode import decode_experts
+from .moe_decode import decode_experts, moe_layer_decode
 from .router import RouterResult, route_topk, route_topk_fused
 from .storage.index import ExpertEntry
 
@@ -56,10 +56,17 @@ def moe_layer_forward(
     if any(t is not None for t in (shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3,
                                    shared_w3_scales)):
         raise NotImplementedError("the FP8 shared expert is not part of this build yet")
+    pool = expert_store.pool
+    if expert_store.layer_fully_resident(layer_id) and x.dtype == torch.bfloat16 and topk <= 8:
+        # routing, slot lookup and experts on the device, no host round trip
+        _, out, route = moe_layer_decode(x, gate_weight, gate_bias, pool, expert_store.layer_table(layer_id),
+                                         topk=topk, gate_temp=gate_temp, route_scale=route_scale,
+                                         norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order,
+                                         swiglu_limit=swiglu_limit, addend=addend)
+        return out, route
     router = route_topk_fused if norm_topk_prob else route_topk
     route = router(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp, route_scale=route_scale,
                    norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order)
-    pool = expert_store.pool
     if not expert_store.layer_fully_resident(layer_id):
         # host-addressed path: one sync for the ids, then load what is missing
         ids = route.indices.tolist()

@@ -8,7 +8,9 @@
  *   - all work is stream-ordered on `stream` (a hipStream_t; NULL = default
  *     stream) and asynchronous; nothing allocates device memory -- scratch
  *     space comes in through `workspace` (size from the *_workspace_bytes
- *     query);
+ *     query).  A decode workspace must be zero-filled once before its first
+ *     use (it holds row-block counters that every call leaves at zero); calls
+ *     that share one workspace must not overlap (same stream, or ordered);
  *   - return 0 on success or a negative CACHALOT_E* code; the message is in
  *     cachalot_last_error() (thread-local).  The Python layer maps EINVAL to
  *     ValueError, ENOTFOUND to KeyError, EHIP to RuntimeError, the exception
@@ -56,8 +58,9 @@ typedef struct cachalot_expert_layout {
 int cachalot_version(void);
 const char* cachalot_last_error(void);
 
-/* Seeded synthetic fill of `n` elements (kinds 0..4: uint32 words, E8M0 bytes,
- * bf16 uniform p0 + p1*t, bf16 normal sigma=p0, fp32 normal sigma=p0), element i
+/* Seeded synthetic fill of `n` elements (kinds 0..4: uint32 words, E8M0 bytes
+ * uniform in [p0, p1], bf16 uniform p0 + p1*t, bf16 / fp32 Irwin-Hall normal
+ * scaled by p1 = sigma / sqrt((65536^2 - 1) / 3)), element i
  * from counter `start + i`.  Test/bench data only -- the reference has no
  * counterpart (it loads checkpoints, storage/reader.py). */
 int cachalot_fill_synthetic(void* dst, int64_t n, int64_t start, uint64_t key, int kind,
@@ -112,6 +115,31 @@ int cachalot_moe_decode_fp4(const uint16_t* x, const uint8_t* pool,
                             int D, int F, int E, int k, float swiglu_limit,
                             const uint16_t* addend, float* routed, uint16_t* out,
                             void* workspace, size_t workspace_bytes, cachalot_stream_t stream);
+
+/* Whole decode MoE layer for one token, routing on the device: router scores
+ * (as cachalot_router_topk with T = 1, bias only), top-k, slot lookup, gate/up,
+ * down and route-order combine in three launches, no host synchronisation.
+ *   gate_weight [E, D] bf16, gate_bias [E] fp32; idx_out [k] int32, w_out [k]
+ *   fp32 (either may be NULL), scores [E] fp32 (required: it is the hand-off
+ *   between the first two launches).  Other arguments as cachalot_moe_decode_*.
+ * Replaces moe_layer_forward's routed part for a fully resident bank
+ * (src/cachalot/model/moe_layer_metal.py:133-405): the reference's host sync
+ * for store addressing (:220-300) becomes a device-side slot-table lookup,
+ * the pattern of minimax/gpu_select.py:1-30. */
+int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                 int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                 int order, const uint8_t* pool, const cachalot_expert_layout* layout /* host */,
+                                 const int32_t* slot_table, int D, int F, int group, float swiglu_limit,
+                                 const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
+                                 float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                 cachalot_stream_t stream);
+int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                  int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                  int order, const uint8_t* pool, const cachalot_expert_layout* layout /* host */,
+                                  const int32_t* slot_table, int D, int F, float swiglu_limit,
+                                  const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
+                                  float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                  cachalot_stream_t stream);
 
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32

@@ -21,10 +21,10 @@ Reference semantics (``src/cachalot/model/router_mlx.py:29-37``)::
 The reference leaves the fp32 summation order of the logit dot product to MLX.
 This build fixes one so ids are reproducible bit for bit on any device:
 
-* D is split into 16 contiguous chunks; each chunk is summed sequentially in
-  fp32 from 0 (bf16 x bf16 products are exact in fp32);
-* the 16 partials are combined by the butterfly ``p[i] + p[i ^ s]`` for
-  s = 8, 4, 2, 1 (a pairwise tree on bit-reversed leaves);
+* D is split into 64 contiguous chunks (one per lane of a wave64); each chunk
+  is summed sequentially in fp32 from 0 (bf16 x bf16 products are exact in fp32);
+* the 64 partials are combined by the butterfly ``p[i] + p[i ^ s]`` for
+  s = 32, 16, 8, 4, 2, 1 (a pairwise tree on bit-reversed leaves);
 * ``logit = tree / gate_temp`` in fp32.
 
 Score functions are evaluated with IEEE basic operations only, so that the
@@ -49,7 +49,7 @@ SCORE_SQRT_SOFTPLUS = 0
 SCORE_SIGMOID = 1
 ORDER_ASCENDING = 0
 ORDER_RANK = 1
-N_CHUNKS = 16
+N_CHUNKS = 64
 
 INV_LN2 = 1.4426950408889634
 LN2_HI = 6.93147180369123816490e-01
@@ -93,7 +93,7 @@ def score_fn(z32: np.ndarray, kind: int) -> np.ndarray:
     raise ValueError(f"unknown score function {kind}")
 
 
-def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: int = 64) -> np.ndarray:
+def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: int = 16) -> np.ndarray:
     """x [T, D], w [E, D] (bf16-exact fp32 values) -> fp32 [T, E] in the fixed order."""
     x32 = np.asarray(x32, dtype=np.float32)
     w32 = np.asarray(w32, dtype=np.float32)
@@ -111,7 +111,7 @@ def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: i
         acc = np.zeros((xs.shape[0], e, N_CHUNKS), dtype=np.float32)
         for j in range(ch):
             acc += xs[:, None, :, j] * wr[None, :, :, j]
-        for s in (8, 4, 2, 1):
+        for s in (32, 16, 8, 4, 2, 1):
             acc = acc + acc[..., lane ^ s]
         out[t0:t0 + block] = acc[..., 0]
     return out / np.float32(gate_temp)

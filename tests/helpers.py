@@ -56,3 +56,19 @@ def rel_err(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def bf16_ulp(v) -> np.ndarray:
+    """Spacing of bf16 numbers at |v| (8 significant bits)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def bf16_out_ok(got_bf16, want_total_f32, tol: float) -> bool:
+    """A bf16 output against the oracle's fp32 value before the cast: the bar plus
+    the cast's own half-ulp rounding, per element."""
+    got = np.asarray(got_bf16, np.float64)
+    want = np.asarray(want_total_f32, np.float64)
+    bound = tol * np.abs(want).max() + 0.5 * bf16_ulp(want)
+    return bool(np.all(np.abs(got - want) <= bound))
