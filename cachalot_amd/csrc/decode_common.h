@@ -91,11 +91,15 @@ __device__ __forceinline__ void expert_prologue(const int32_t* __restrict__ slot
   }
 }
 
-// Workspace layout of one decode call: [hidden][per-expert row values][row-block
-// counters][k slots][k weights], each region 256-byte aligned.  The counter
-// region must be zero before the first call; every call leaves it zero.
+// Workspace layout of one decode call: [row-block counters][k slots][k weights]
+// [hidden][per-expert row values], each region 256-byte aligned.  The counter
+// region comes first and has a fixed size (enough for D <= MAX_D), so every
+// call -- whatever its D, F, k or bank kind -- finds its counters at the same
+// place.  It must be zero before the first call; every call leaves it zero.
+constexpr int MAX_D = 8192;
+
 struct WsOffsets {
-  size_t hidden, ybuf, counters, slots, weights, total;
+  size_t counters, slots, weights, hidden, ybuf, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -103,12 +107,12 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 inline WsOffsets ws_offsets(int D, int F, int k, size_t hidden_bytes) {
   (void)F;
   WsOffsets o;
-  o.hidden = 0;
-  o.ybuf = align256(hidden_bytes);
-  o.counters = o.ybuf + align256((size_t)k * D * sizeof(float));
-  o.slots = o.counters + align256((size_t)((D + R_DN - 1) / R_DN) * sizeof(uint32_t));
+  o.counters = 0;
+  o.slots = align256((size_t)(MAX_D / R_DN) * sizeof(uint32_t));
   o.weights = o.slots + align256(KMAX * sizeof(int32_t));
-  o.total = o.weights + align256(KMAX * sizeof(float));
+  o.hidden = o.weights + align256(KMAX * sizeof(float));
+  o.ybuf = o.hidden + align256(hidden_bytes);
+  o.total = o.ybuf + align256((size_t)k * D * sizeof(float));
   return o;
 }
 
