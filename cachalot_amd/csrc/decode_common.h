@@ -8,7 +8,7 @@ namespace cachalot {
 namespace decode {
 
 constexpr int WAVES = 4;    // waves per workgroup
-constexpr int R_DN = 2;     // W2 rows per wave in the down kernels
+constexpr int R_DN = 4;     // W2 rows per workgroup in the down kernels (one wave per expert)
 constexpr int KMAX = 8;     // max experts per token
 
 struct Layout {
@@ -56,14 +56,10 @@ struct RouteArgs {            // fused top-k inputs (FUSE_TOPK)
 template <bool FUSE>
 __device__ __forceinline__ void expert_prologue(const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx,
                                                 const float* __restrict__ wts, int E, int k, const RouteArgs& ra,
-                                                int* s_slot, float* s_w, float4* sel4, int* top_i, float* top_v,
-                                                int32_t* ws_slots, float* ws_w) {
+                                                int* s_slot, float* s_w, int* top_i, float* top_v, float* lds_v,
+                                                int* lds_i, int32_t* ws_slots, float* ws_w) {
   if constexpr (FUSE) {
-    const int E4 = (ra.E + 3) / 4;
-    load_selection(sel4, ra.E, E4, ra.scores, ra.bias);
-    __syncthreads();
-    block_topk_rank(sel4, ra.E, E4, k, ra.order, ra.scores, top_i, top_v);
-    __syncthreads();
+    block_topk_rounds<4>(ra.scores, ra.bias, ra.E, k, ra.order, top_i, top_v, lds_v, lds_i);
     if (threadIdx.x == 0) normalise_weights(top_v, k, ra.route_scale, ra.norm, s_w);
     if (threadIdx.x < k) {
       const int ex = top_i[threadIdx.x];
@@ -91,63 +87,43 @@ __device__ __forceinline__ void expert_prologue(const int32_t* __restrict__ slot
   }
 }
 
-// Workspace layout of one decode call: [row-block counters][k slots][k weights]
-// [hidden][per-expert row values], each region 256-byte aligned.  The counter
-// region comes first and has a fixed size (enough for D <= MAX_D), so every
-// call -- whatever its D, F, k or bank kind -- finds its counters at the same
-// place.  It must be zero before the first call; every call leaves it zero.
-constexpr int MAX_D = 8192;
-
+// Workspace layout of one decode call: [k slots][k weights][hidden], each
+// region 256-byte aligned.  Scratch only: nothing in it survives a call.
 struct WsOffsets {
-  size_t counters, slots, weights, hidden, ybuf, total;
+  size_t slots, weights, hidden, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-inline WsOffsets ws_offsets(int D, int F, int k, size_t hidden_bytes) {
-  (void)F;
+inline WsOffsets ws_offsets(size_t hidden_bytes) {
   WsOffsets o;
-  o.counters = 0;
-  o.slots = align256((size_t)(MAX_D / R_DN) * sizeof(uint32_t));
-  o.weights = o.slots + align256(KMAX * sizeof(int32_t));
+  o.slots = 0;
+  o.weights = align256(KMAX * sizeof(int32_t));
   o.hidden = o.weights + align256(KMAX * sizeof(float));
-  o.ybuf = o.hidden + align256(hidden_bytes);
-  o.total = o.ybuf + align256((size_t)k * D * sizeof(float));
+  o.total = o.hidden + align256(hidden_bytes);
   return o;
 }
 
-// After wave_transpose_sum<R_DN>: row r's total sits in lanes [32r, 32r+32).
-// Stores this expert's row values, then the last of the k waves of row block
-// rb (device-scope counter) sums the k values in route order (bf16-rounded per
-// expert when BF16_PER_EXPERT), adds the addend, writes the outputs and resets
-// the counter for the next call.
+// Row r's total sits in lanes [16r, 16r+16) after wave_transpose_sum<R_DN>.
+// Each of the k waves of the workgroup (wave e = expert e) leaves its row values
+// in LDS; after the barrier the first R_DN threads sum the k values of their row
+// in route order (each bf16-rounded when BF16_PER_EXPERT), add the addend and
+// write the outputs.
 template <bool BF16_PER_EXPERT>
-__device__ __forceinline__ void combine_rows(float red, int lane, int e, int rb, int row0, int D, int k,
-                                             float* __restrict__ ybuf, uint32_t* __restrict__ counters,
-                                             const uint16_t* __restrict__ addend, float* __restrict__ routed,
-                                             uint16_t* __restrict__ out) {
-  static_assert(R_DN == 2, "lane mapping assumes two rows per wave");
-  const float y = BF16_PER_EXPERT ? round_bf16(red) : red;
-  const int n_own = row0 + (lane >> 5);
-  if ((lane & 31) == 0 && n_own < D) ybuf[(size_t)e * D + n_own] = y;
-  __threadfence();
-  uint32_t old = 0;
-  if (lane == 0) old = __hip_atomic_fetch_add(&counters[rb], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  old = __shfl(old, 0, 64);
-  if (old != (uint32_t)(k - 1)) return;
-  __threadfence();
-  if (lane < R_DN && row0 + lane < D) {
-    const int n = row0 + lane;
+__device__ __forceinline__ void combine_rows(float red, int lane, int e, int row0, int D, int k,
+                                             float (*vals)[R_DN], const uint16_t* __restrict__ addend,
+                                             float* __restrict__ routed, uint16_t* __restrict__ out) {
+  static_assert(R_DN == 4, "lane mapping assumes four rows per workgroup");
+  if ((lane & 15) == 0) vals[e][lane >> 4] = BF16_PER_EXPERT ? round_bf16(red) : red;
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < R_DN && row0 + t < D) {
+    const int n = row0 + t;
     float acc = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      const uint32_t bits = __hip_atomic_load(reinterpret_cast<uint32_t*>(ybuf + (size_t)j * D + n),
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      acc = acc + __uint_as_float(bits);
-    }
+    for (int j = 0; j < k; ++j) acc = acc + vals[j][t];
     if (routed) routed[n] = acc;
     if (out) out[n] = f32_to_bf16(addend ? acc + bf16_to_f32(addend[n]) : acc);
   }
-  if (lane == 0) __hip_atomic_store(&counters[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace decode

@@ -13,11 +13,11 @@
 //                       matrix.  Nibbles become bf16 pairs (value * 2^e, exact)
 //                       in the gfx950 converter and meet the bf16 activation
 //                       pairs in v_dot2c_f32_bf16.
-//   fp4_down_kernel     one wave = R rows of W2 for one expert; lane l owns
-//                       words l + 64 i of the row (8 codes each); the fp32 hidden
-//                       vector stays fp32 (converter to f32 pairs, fp32 FMA).
-//                       Per-expert row values are combined in route order by the
-//                       last of the k waves of a row block.
+//   fp4_down_kernel     one workgroup = R rows of W2, k waves (wave e = expert
+//                       e); lane l owns words l + 64 i of the row (8 codes each);
+//                       the fp32 hidden vector stays fp32 (converter to f32
+//                       pairs, fp32 FMA); per-expert row values meet in LDS and
+//                       are summed in route order.
 #include "decode_common.h"
 #include "router_launch.h"
 
@@ -56,11 +56,12 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
     const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx, const float* __restrict__ wts,
     RouteArgs ra, int D, int F, int E, int k, float limit, float* __restrict__ hidden,
     int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
-  extern __shared__ float4 lds4[];
   __shared__ int s_slot[KMAX];
   __shared__ float s_w[KMAX];
   __shared__ int top_i[KMAX];
   __shared__ float top_v[KMAX];
+  __shared__ float lds_v[16];
+  __shared__ int lds_i[16];
   const int lane = threadIdx.x & 63;
   const int NC = D / 64;
   const int SB = D / 32;
@@ -77,7 +78,7 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
     }
   }
 
-  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, lds4, top_i, top_v, ws_slots, ws_w);
+  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, top_i, top_v, lds_v, lds_i, ws_slots, ws_w);
 
   const int RB = (F + R_GU - 1) / R_GU;
   const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
@@ -114,6 +115,8 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
       su1[r][i] = s3[(size_t)n * SB + 2 * c + 1];
     }
   }
+  // keep every load above this point in flight before any arithmetic
+  __builtin_amdgcn_sched_barrier(0);
 
   float part[2 * R_GU];
 #pragma unroll
@@ -143,17 +146,15 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
   }
 }
 
-__global__ void __launch_bounds__(64 * WAVES) fp4_down_kernel(
+// grid.x = ceil(D / R_DN); one workgroup = k waves, wave e = expert e
+__global__ void __launch_bounds__(64 * KMAX) fp4_down_kernel(
     const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
-    const float* __restrict__ hidden, float* __restrict__ ybuf, uint32_t* __restrict__ counters,
-    const uint16_t* __restrict__ addend, float* __restrict__ routed, uint16_t* __restrict__ out) {
+    const float* __restrict__ hidden, const uint16_t* __restrict__ addend, float* __restrict__ routed,
+    uint16_t* __restrict__ out) {
+  __shared__ float vals[KMAX][R_DN];
   const int lane = threadIdx.x & 63;
-  const int RB = (D + R_DN - 1) / R_DN;
-  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  if (item >= k * RB) return;
-  const int e = item / RB;
-  const int rb = item % RB;
-  const int row0 = rb * R_DN;
+  const int e = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * R_DN;
   const int Kw = F / 8;     // 32-bit words per row
   const int SB = F / 32;    // scale blocks per row
   const int slot = ws_slots[e];
@@ -184,38 +185,41 @@ __global__ void __launch_bounds__(64 * WAVES) fp4_down_kernel(
         sv[r][i] = s2[(size_t)n * SB + (j >> 2)];
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < R_DN; ++r) {
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < MAXW; ++i) {
-        if (lane + 64 * i < Kw) {
-          const float sc = e8m0_to_f32(sv[r][i]);
-          const float2_t p0 = fp4x2_to_f32x2<0>(wv[r][i], sc);
-          const float2_t p1 = fp4x2_to_f32x2<1>(wv[r][i], sc);
-          const float2_t p2 = fp4x2_to_f32x2<2>(wv[r][i], sc);
-          const float2_t p3 = fp4x2_to_f32x2<3>(wv[r][i], sc);
-          acc = __builtin_fmaf(p0[0], ha[i].x, acc);
-          acc = __builtin_fmaf(p0[1], ha[i].y, acc);
-          acc = __builtin_fmaf(p1[0], ha[i].z, acc);
-          acc = __builtin_fmaf(p1[1], ha[i].w, acc);
-          acc = __builtin_fmaf(p2[0], hb[i].x, acc);
-          acc = __builtin_fmaf(p2[1], hb[i].y, acc);
-          acc = __builtin_fmaf(p3[0], hb[i].z, acc);
-          acc = __builtin_fmaf(p3[1], hb[i].w, acc);
-        }
+        const float valid = (lane + 64 * i < Kw) ? 1.0f : 0.0f;
+        const float sc = e8m0_to_f32(sv[r][i]);
+        const float2_t p0 = fp4x2_to_f32x2<0>(wv[r][i], sc);
+        const float2_t p1 = fp4x2_to_f32x2<1>(wv[r][i], sc);
+        const float2_t p2 = fp4x2_to_f32x2<2>(wv[r][i], sc);
+        const float2_t p3 = fp4x2_to_f32x2<3>(wv[r][i], sc);
+        float d = 0.0f;
+        d = __builtin_fmaf(p0[0], ha[i].x, d);
+        d = __builtin_fmaf(p0[1], ha[i].y, d);
+        d = __builtin_fmaf(p1[0], ha[i].z, d);
+        d = __builtin_fmaf(p1[1], ha[i].w, d);
+        d = __builtin_fmaf(p2[0], hb[i].x, d);
+        d = __builtin_fmaf(p2[1], hb[i].y, d);
+        d = __builtin_fmaf(p3[0], hb[i].z, d);
+        d = __builtin_fmaf(p3[1], hb[i].w, d);
+        acc = __builtin_fmaf(valid, d, acc);
       }
       rowv[r] = acc;
     }
   }
   const float red = wave_transpose_sum<R_DN>(rowv, lane);
-  combine_rows<false>(red, lane, e, rb, row0, D, k, ybuf, counters, addend, routed, out);
+  combine_rows<false>(red, lane, e, row0, D, k, vals, addend, routed, out);
 }
 
 }  // namespace
 
 size_t fp4_workspace_bytes(int D, int F, int k) {
-  return ws_offsets(D, F, k, (size_t)k * F * sizeof(float)).total;
+  (void)D;
+  return ws_offsets((size_t)k * F * sizeof(float)).total;
 }
 
 int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
@@ -230,7 +234,7 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
                    D);
   CACHALOT_REQUIRE(F % 32 == 0 && F >= 32 && F <= 8 * 64 * MAXW,
                    "moe_decode_fp4: F=%d must be a multiple of 32 and <= %d", F, 8 * 64 * MAXW);
-  const WsOffsets wo = ws_offsets(D, F, k, (size_t)k * F * sizeof(float));
+  const WsOffsets wo = ws_offsets((size_t)k * F * sizeof(float));
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "moe_decode_fp4: workspace %zu < %zu bytes", workspace_bytes, wo.total);
   Layout L;
@@ -239,15 +243,13 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   if (rc) return rc;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   float* hidden = reinterpret_cast<float*>(ws + wo.hidden);
-  float* ybuf = reinterpret_cast<float*>(ws + wo.ybuf);
-  uint32_t* counters = reinterpret_cast<uint32_t*>(ws + wo.counters);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
   RouteArgs none{};
   const RouteArgs& r = ra ? *ra : none;
   const int items = k * ((F + R_GU - 1) / R_GU);
   const int blocks = (items + WAVES - 1) / WAVES;
-  const size_t lds = ra ? (size_t)((ra->E + 3) / 4) * sizeof(float4) : 0;
+  const size_t lds = 0;
   const bool c1 = D <= 4096;
   if (ra) {
     if (c1)
@@ -266,9 +268,8 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   }
   rc = check_launch("fp4_gate_up_kernel");
   if (rc) return rc;
-  const int items2 = k * ((D + R_DN - 1) / R_DN);
-  hipLaunchKernelGGL(fp4_down_kernel, dim3((items2 + WAVES - 1) / WAVES), dim3(64 * WAVES), 0, s, pool, L, ws_slots,
-                     D, F, k, hidden, ybuf, counters, addend, routed, out);
+  hipLaunchKernelGGL(fp4_down_kernel, dim3((D + R_DN - 1) / R_DN), dim3(64 * k), 0, s, pool, L, ws_slots, D, F, k,
+                     hidden, addend, routed, out);
   return check_launch("fp4_down_kernel");
 }
 

@@ -20,13 +20,11 @@
 //                      Epilogue: bf16(g), bf16(u), clamp,
 //                      h = bf16(silu(g) * u * w_e), written in the pair order
 //                      the down kernel consumes.
-//   q2_down_kernel     one wave = R_DN rows of W2 for one expert; lane l owns
-//                      words l, l+64, l+128 of the row (K = 2880 -> 180 words).
-//                      The row value is rounded to bf16 (the reference's
-//                      per-expert cast) and stored per expert; the last of the
-//                      k waves of a row block (a device-scope counter) sums the
-//                      k values in route order, adds the addend and writes the
-//                      outputs, then resets the counter.
+//   q2_down_kernel     one workgroup = R_DN rows of W2, k waves (wave e = expert
+//                      e); lane l owns words l, l+64, l+128 of the row (K = 2880
+//                      -> 180 words).  Each row value is rounded to bf16 (the
+//                      reference's per-expert cast), handed over in LDS and
+//                      summed in route order, + addend, -> fp32 / bf16.
 #include "decode_common.h"
 #include "router_launch.h"
 #include "topk.h"
@@ -75,11 +73,12 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
     const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx, const float* __restrict__ wts,
     RouteArgs ra, int D, int F, int E, int k, int group, float limit, uint16_t* __restrict__ hp,
     int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
-  extern __shared__ float4 lds4[];
   __shared__ int s_slot[KMAX];
   __shared__ float s_w[KMAX];
   __shared__ int top_i[KMAX];
   __shared__ float top_v[KMAX];
+  __shared__ float lds_v[16];
+  __shared__ int lds_i[16];
   const int lane = threadIdx.x & 63;
   const int NC = D / 64;
 
@@ -93,7 +92,7 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
     for (int q = 0; q < 8; ++q) xa[i][q] = xp[q];
   }
 
-  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, lds4, top_i, top_v, ws_slots, ws_w);
+  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, top_i, top_v, lds_v, lds_i, ws_slots, ws_w);
 
   const int RB = (F + R_GU - 1) / R_GU;
   const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
@@ -134,6 +133,8 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
       bu[r][i] = b3[(size_t)n * G + g];
     }
   }
+  // keep every load above this point in flight before any arithmetic
+  __builtin_amdgcn_sched_barrier(0);
 
   // activation pairs and per-chunk sums
   uint32_t xe[C][4][4], xo[C][4][4];
@@ -199,18 +200,15 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
   }
 }
 
-// grid.x = ceil(k * ceil(D / R_DN) / WAVES)
-__global__ void __launch_bounds__(64 * WAVES) q2_down_kernel(
+// grid.x = ceil(D / R_DN); one workgroup = k waves, wave e = expert e
+__global__ void __launch_bounds__(64 * KMAX) q2_down_kernel(
     const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
-    int group, const uint16_t* __restrict__ hp, float* __restrict__ ybuf, uint32_t* __restrict__ counters,
-    const uint16_t* __restrict__ addend, float* __restrict__ routed, uint16_t* __restrict__ out) {
+    int group, const uint16_t* __restrict__ hp, const uint16_t* __restrict__ addend, float* __restrict__ routed,
+    uint16_t* __restrict__ out) {
+  __shared__ float vals[KMAX][R_DN];
   const int lane = threadIdx.x & 63;
-  const int RB = (D + R_DN - 1) / R_DN;
-  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  if (item >= k * RB) return;
-  const int e = item / RB;
-  const int rb = item % RB;
-  const int row0 = rb * R_DN;
+  const int e = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * R_DN;
   const int Kw = F / 16;                   // valid words per row
   const int G = (F + group - 1) / group;   // groups per row (the last may be partial)
   const int stride = G * group / 16;       // stored words per row
@@ -246,6 +244,7 @@ __global__ void __launch_bounds__(64 * WAVES) q2_down_kernel(
         bv[r][i] = b2[(size_t)n * G + g];
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t he[MAXW][4], ho[MAXW][4];
     float hs[MAXW];
 #pragma unroll
@@ -275,13 +274,14 @@ __global__ void __launch_bounds__(64 * WAVES) q2_down_kernel(
     }
   }
   const float red = wave_transpose_sum<R_DN>(rowv, lane);
-  combine_rows<true>(red, lane, e, rb, row0, D, k, ybuf, counters, addend, routed, out);
+  combine_rows<true>(red, lane, e, row0, D, k, vals, addend, routed, out);
 }
 
 }  // namespace
 
 size_t q2_workspace_bytes(int D, int F, int k) {
-  return ws_offsets(D, F, k, (size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t)).total;
+  (void)D;
+  return ws_offsets((size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t)).total;
 }
 
 int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
@@ -297,7 +297,7 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
                    "moe_decode_q2: D=%d must be a multiple of group %d and <= 8192", D, group);
   CACHALOT_REQUIRE(F % 16 == 0 && F >= 16 && F <= 16 * 64 * MAXW,
                    "moe_decode_q2: F=%d must be a multiple of 16 and <= %d", F, 16 * 64 * MAXW);
-  const WsOffsets wo = ws_offsets(D, F, k, (size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t));
+  const WsOffsets wo = ws_offsets((size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t));
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, wo.total);
   Layout L;
@@ -306,15 +306,13 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   if (rc) return rc;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint16_t* hp = reinterpret_cast<uint16_t*>(ws + wo.hidden);
-  float* ybuf = reinterpret_cast<float*>(ws + wo.ybuf);
-  uint32_t* counters = reinterpret_cast<uint32_t*>(ws + wo.counters);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
   RouteArgs none{};
   const RouteArgs& r = ra ? *ra : none;
   const int items = k * ((F + R_GU - 1) / R_GU);
   const int blocks = (items + WAVES - 1) / WAVES;
-  const size_t lds = ra ? (size_t)((ra->E + 3) / 4) * sizeof(float4) : 0;
+  const size_t lds = 0;
   const bool c1 = D <= 4096;
   if (ra) {
     if (c1)
@@ -333,9 +331,8 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   }
   rc = check_launch("q2_gate_up_kernel");
   if (rc) return rc;
-  const int items2 = k * ((D + R_DN - 1) / R_DN);
-  hipLaunchKernelGGL(q2_down_kernel, dim3((items2 + WAVES - 1) / WAVES), dim3(64 * WAVES), 0, s, pool, L, ws_slots, D,
-                     F, k, group, hp, ybuf, counters, addend, routed, out);
+  hipLaunchKernelGGL(q2_down_kernel, dim3((D + R_DN - 1) / R_DN), dim3(64 * k), 0, s, pool, L, ws_slots, D, F, k,
+                     group, hp, addend, routed, out);
   return check_launch("q2_down_kernel");
 }
 

@@ -17,8 +17,8 @@
 // Kernels
 //   router_scores_kernel  one wave = 4 expert rows x up to TT tokens; W row chunks
 //                         are loaded once per wave and reused for TT tokens.
-//   router_topk_kernel    one workgroup per token; thread e computes the rank of
-//                         expert e among all E by counting the experts that beat it.
+//   router_topk_kernel    one workgroup per token; k rounds of a block-wide argmax
+//                         under the order's total order (value, then index).
 #include "router_launch.h"
 #include "topk.h"
 
@@ -140,26 +140,22 @@ __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __re
   }
 }
 
-// One workgroup per token; LDS: ceil(E/4) float4 selection values, then k winners.
-__global__ void __launch_bounds__(1024) router_topk_kernel(const float* __restrict__ scores,
-                                                           const float* __restrict__ bias,
-                                                           const float* __restrict__ bias_vl,
-                                                           const uint8_t* __restrict__ image_mask, int E,
-                                                           int k, float route_scale, int norm, int order,
-                                                           int32_t* __restrict__ idx, float* __restrict__ w) {
-  extern __shared__ float4 lds4[];
-  const int E4 = (E + 3) / 4;
-  float4* sel4 = lds4;
-  int* top_i = reinterpret_cast<int*>(lds4 + E4);
-  float* top_v = reinterpret_cast<float*>(top_i + k);
+// One 256-thread workgroup per token: k rounds of a block-wide argmax.
+__global__ void __launch_bounds__(256) router_topk_kernel(const float* __restrict__ scores,
+                                                          const float* __restrict__ bias,
+                                                          const float* __restrict__ bias_vl,
+                                                          const uint8_t* __restrict__ image_mask, int E, int k,
+                                                          float route_scale, int norm, int order,
+                                                          int32_t* __restrict__ idx, float* __restrict__ w) {
+  __shared__ int top_i[1024];
+  __shared__ float top_v[1024];
+  __shared__ float lds_v[16];
+  __shared__ int lds_i[16];
   const int t = blockIdx.x;
   const float* s = scores + (size_t)t * E;
   const float* b = (image_mask != nullptr && image_mask[t] != 0) ? bias_vl : bias;
-  load_selection(sel4, E, E4, s, b);
-  __syncthreads();
-  block_topk_rank(sel4, E, E4, k, order, s, top_i, top_v);
-  __syncthreads();
-  if (threadIdx.x < k) idx[(size_t)t * k + threadIdx.x] = top_i[threadIdx.x];
+  block_topk_rounds<4>(s, b, E, k, order, top_i, top_v, lds_v, lds_i);
+  for (int j = threadIdx.x; j < k; j += blockDim.x) idx[(size_t)t * k + j] = top_i[j];
   if (threadIdx.x == 0) normalise_weights(top_v, k, route_scale, norm, w + (size_t)t * k);
 }
 
@@ -207,9 +203,7 @@ extern "C" int cachalot_router_topk(const uint16_t* x, const uint16_t* W, const 
   hipStream_t s = (hipStream_t)stream;
   int rc = launch_router_scores(x, W, T, D, E, gate_temp, score_fn, scores, s);
   if (rc) return rc;
-  const int threads = min(1024, ((E + 63) / 64) * 64);
-  const size_t lds = (size_t)((E + 3) / 4) * sizeof(float4) + (size_t)k * (sizeof(int) + sizeof(float));
-  hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(threads), lds, s, scores, bias, bias_vl, image_mask, E, k,
+  hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(256), 0, s, scores, bias, bias_vl, image_mask, E, k,
                      route_scale, norm, order, idx, w);
   return check_launch("router_topk_kernel");
 }

@@ -50,6 +50,82 @@ __device__ __forceinline__ void block_topk_rank(const float4* __restrict__ sel4,
   }
 }
 
+// a beats b under the order's total order; an index < 0 marks "no candidate".
+__device__ __forceinline__ bool topk_better(float a, int ai, float b, int bi, int order) {
+  if (ai < 0) return false;
+  if (bi < 0) return true;
+  if (a != b) return a > b;
+  return order == CACHALOT_ORDER_ASCENDING ? ai > bi : ai < bi;
+}
+
+// k rounds of a block-wide argmax (O(E) work per round): each thread keeps up
+// to EPT candidates, a wave butterfly finds the wave's best, LDS holds one
+// entry per wave, every thread derives the same block winner, the owner marks
+// it taken.  Round r yields rank r.  Requires E <= EPT * blockDim.x and
+// blockDim.x a multiple of 64 (<= 1024).  lds_v / lds_i: LDS [16].
+template <int EPT>
+__device__ __forceinline__ void block_topk_rounds(const float* __restrict__ scores, const float* __restrict__ bias,
+                                                  int E, int k, int order, int* top_i, float* top_v, float* lds_v,
+                                                  int* lds_i) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int nwaves = blockDim.x >> 6;
+  float v[EPT];
+  int id[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid + j * blockDim.x;
+    id[j] = -1;
+    v[j] = -INFINITY;
+    if (e < E) {
+      float s = scores[e] + bias[e];
+      if (s != s) s = -INFINITY;  // NaN never wins
+      v[j] = s;
+      id[j] = e;
+    }
+  }
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int bi = -1;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+      if (topk_better(v[j], id[j], bv, bi, order)) {
+        bv = v[j];
+        bi = id[j];
+      }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      const float ov = __shfl_xor(bv, m, 64);
+      const int oi = __shfl_xor(bi, m, 64);
+      if (topk_better(ov, oi, bv, bi, order)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      lds_v[tid >> 6] = bv;
+      lds_i[tid >> 6] = bi;
+    }
+    __syncthreads();
+    float wv = lds_v[0];
+    int wi = lds_i[0];
+    for (int w = 1; w < nwaves; ++w)
+      if (topk_better(lds_v[w], lds_i[w], wv, wi, order)) {
+        wv = lds_v[w];
+        wi = lds_i[w];
+      }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+      if (id[j] == wi) id[j] = -1;
+    if (tid == 0) {
+      const int pos = order == CACHALOT_ORDER_ASCENDING ? k - 1 - r : r;
+      top_i[pos] = wi;
+      top_v[pos] = scores[wi];
+    }
+    __syncthreads();
+  }
+}
+
 // Fill sel4 from scores + bias (NaN -> -inf, padding -inf).
 __device__ __forceinline__ void load_selection(float4* sel4, int E, int E4, const float* __restrict__ scores,
                                                const float* __restrict__ bias) {

@@ -22,17 +22,16 @@ _WORKSPACES: dict[tuple, torch.Tensor] = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A zero-filled decode workspace cached per device.
+    """The decode scratch workspace, cached per device (grown on demand).
 
-    The kernels keep row-block counters in it and leave them at zero, so it is
-    zeroed once, at allocation.  Decode calls on one device share it and must
-    therefore be ordered (one stream, or streams that wait on each other); a
-    HIP-graph capture must be preceded by an eager call of the same shape so
-    that the workspace exists before capture."""
+    Decode calls on one device share it and must therefore be ordered (one
+    stream, or streams that wait on each other); a HIP-graph capture must be
+    preceded by an eager call of the same shape so that the workspace exists
+    before capture."""
     key = (device.index,)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

@@ -8,9 +8,8 @@
  *   - all work is stream-ordered on `stream` (a hipStream_t; NULL = default
  *     stream) and asynchronous; nothing allocates device memory -- scratch
  *     space comes in through `workspace` (size from the *_workspace_bytes
- *     query).  A decode workspace must be zero-filled once before its first
- *     use (it holds row-block counters that every call leaves at zero); calls
- *     that share one workspace must not overlap (same stream, or ordered);
+ *     query; scratch only, nothing survives a call); calls that share one
+ *     workspace must not overlap (same stream, or ordered);
  *   - return 0 on success or a negative CACHALOT_E* code; the message is in
  *     cachalot_last_error() (thread-local).  The Python layer maps EINVAL to
  *     ValueError, ENOTFOUND to KeyError, EHIP to RuntimeError, the exception
