@@ -71,43 +71,121 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t raw) {
 }
 
 // ------------------------------------------------------- wave reductions ---
+// Lane exchanges without the LDS crossbar: DPP for partners inside a row of 16
+// lanes, the gfx950 permlane swaps across rows.  xorN(v) returns the value of
+// lane (lane ^ N); mirror8 returns lane (lane ^ 7) within each group of 8.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t xor1_u32(uint32_t v) { return dpp_u32<0xB1>(v); }    // quad_perm [1,0,3,2]
+__device__ __forceinline__ uint32_t xor2_u32(uint32_t v) { return dpp_u32<0x4E>(v); }    // quad_perm [2,3,0,1]
+__device__ __forceinline__ uint32_t mirror8_u32(uint32_t v) { return dpp_u32<0x141>(v); } // row_half_mirror
+__device__ __forceinline__ uint32_t mirror16_u32(uint32_t v) { return dpp_u32<0x140>(v); } // row_mirror
+__device__ __forceinline__ uint32_t xor8_u32(uint32_t v) { return dpp_u32<0x128>(v); }   // row_ror:8
+__device__ __forceinline__ uint32_t xor4_u32(uint32_t v) { return (uint32_t)__shfl_xor((int)v, 4, 64); }
+__device__ __forceinline__ uint32_t xor16_u32(uint32_t v) {
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (__lane_id() & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t xor32_u32(uint32_t v) {
+  auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (__lane_id() & 32) ? r[0] : r[1];
+}
+template <int M>
+__device__ __forceinline__ uint32_t xor_u32(uint32_t v) {
+  if constexpr (M == 1) return xor1_u32(v);
+  else if constexpr (M == 2) return xor2_u32(v);
+  else if constexpr (M == 4) return xor4_u32(v);
+  else if constexpr (M == 8) return xor8_u32(v);
+  else if constexpr (M == 16) return xor16_u32(v);
+  else return xor32_u32(v);
+}
+template <int M>
+__device__ __forceinline__ float xor_f(float v) {
+  return __uint_as_float(xor_u32<M>(__float_as_uint(v)));
+}
+
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
-// Full wave64 sum (every lane gets the total).
+// Full wave64 sum, every lane ends with the same value.  Partners: 1, 2 (exact
+// xor), then the mirror of the other half of 8 and of 16 (after the earlier
+// steps those lanes hold the same value as the xor-4 / xor-8 partner), then 16
+// and 32.  Bit-identical to the xor butterfly 1, 2, 4, 8, 16, 32.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f(v, m);
+  v = v + __uint_as_float(xor1_u32(__float_as_uint(v)));
+  v = v + __uint_as_float(xor2_u32(__float_as_uint(v)));
+  v = v + __uint_as_float(mirror8_u32(__float_as_uint(v)));
+  v = v + __uint_as_float(mirror16_u32(__float_as_uint(v)));
+  v = v + xor_f<16>(v);
+  v = v + xor_f<32>(v);
   return v;
 }
 
-// Transposed reduction of N (power of two, <= 64) per-lane values:
-// afterwards lane L holds, in v[0], the wave-wide sum of value index
-// (L >> (6 - log2 N)) -- i.e. value i ends in lanes [i*64/N, (i+1)*64/N).
+// Sum over the 16 lanes of each row (xor 1, 2, then mirrors), bit-identical to
+// the xor butterfly 1, 2, 4, 8.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + __uint_as_float(xor1_u32(__float_as_uint(v)));
+  v = v + __uint_as_float(xor2_u32(__float_as_uint(v)));
+  v = v + __uint_as_float(mirror8_u32(__float_as_uint(v)));
+  v = v + __uint_as_float(mirror16_u32(__float_as_uint(v)));
+  return v;
+}
+
+// Butterfly 32, 16, 8, 4, 2, 1 as the router contract states it (a + partner).
+__device__ __forceinline__ float wave_sum_xor_desc(float v) {
+  v = v + xor_f<32>(v);
+  v = v + xor_f<16>(v);
+  v = v + xor_f<8>(v);
+  v = v + xor_f<4>(v);
+  v = v + xor_f<2>(v);
+  v = v + xor_f<1>(v);
+  return v;
+}
+
+// Transposed reduction of N (power of two, <= 8) per-lane values: afterwards
+// every lane of [i*64/N, (i+1)*64/N) holds the wave-wide sum of value i.
+// The transposing steps use exact xor partners 32, 16, 8; the rest is a row sum.
 template <int N>
 __device__ __forceinline__ float wave_transpose_sum(float (&v)[N], int lane) {
-  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
-  int n = N;
-  int bit = 32;
-#pragma unroll
-  for (int step = 0; (1 << step) < N; ++step) {
-    const int half = n >> 1;
-    const bool hi = (lane & bit) != 0;
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8, "N must be 1, 2, 4 or 8");
+  if constexpr (N >= 2) {
+    const bool hi = (lane & 32) != 0;
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
-      if (i < half) {
-        float keep = hi ? v[i + half] : v[i];
-        float send = hi ? v[i] : v[i + half];
-        v[i] = keep + shfl_xor_f(send, bit);
-      }
+      const float keep = hi ? v[i + N / 2] : v[i];
+      const float send = hi ? v[i] : v[i + N / 2];
+      v[i] = keep + xor_f<32>(send);
     }
-    n = half;
-    bit >>= 1;
+  }
+  if constexpr (N >= 4) {
+    const bool hi = (lane & 16) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const float keep = hi ? v[i + N / 4] : v[i];
+      const float send = hi ? v[i] : v[i + N / 4];
+      v[i] = keep + xor_f<16>(send);
+    }
+  }
+  if constexpr (N >= 8) {
+    const bool hi = (lane & 8) != 0;
+    const float keep = hi ? v[1] : v[0];
+    const float send = hi ? v[0] : v[1];
+    v[0] = keep + xor_f<8>(send);
   }
   float r = v[0];
-  for (; bit >= 1; bit >>= 1) r += shfl_xor_f(r, bit);
-  return r;
+  if constexpr (N == 1) return wave_sum(r);
+  if constexpr (N == 2) {  // lanes of a 32-half: sum over bits 4..0
+    r = row16_sum(r);
+    return r + xor_f<16>(r);
+  }
+  if constexpr (N == 4) return row16_sum(r);
+  // N == 8: sum over bits 2..0 (groups of 8)
+  r = r + __uint_as_float(xor1_u32(__float_as_uint(r)));
+  r = r + __uint_as_float(xor2_u32(__float_as_uint(r)));
+  return r + __uint_as_float(mirror8_u32(__float_as_uint(r)));
 }
 
 }  // namespace cachalot

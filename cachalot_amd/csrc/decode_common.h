@@ -59,7 +59,11 @@ __device__ __forceinline__ void expert_prologue(const int32_t* __restrict__ slot
                                                 int* s_slot, float* s_w, int* top_i, float* top_v, float* lds_v,
                                                 int* lds_i, int32_t* ws_slots, float* ws_w) {
   if constexpr (FUSE) {
-    block_topk_rounds<4>(ra.scores, ra.bias, ra.E, k, ra.order, top_i, top_v, lds_v, lds_i);
+    if (threadIdx.x < 64) {
+      if (ra.E <= 384) wave_topk<6>(ra.scores, ra.bias, ra.E, k, ra.order, top_i, top_v);
+      else wave_topk<16>(ra.scores, ra.bias, ra.E, k, ra.order, top_i, top_v);
+    }
+    __syncthreads();
     if (threadIdx.x == 0) normalise_weights(top_v, k, ra.route_scale, ra.norm, s_w);
     if (threadIdx.x < k) {
       const int ex = top_i[threadIdx.x];

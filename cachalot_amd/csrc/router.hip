@@ -5,9 +5,10 @@
 // 280-292 and minimax/gpu_select.py:80-115 (sigmoid, rank order).
 //
 // Arithmetic contract (fixed so ids are reproducible bit for bit):
-//   * D is cut into 16 contiguous chunks of D/16; 16 lanes own one chunk each
-//     and add their bf16*bf16 products (exact in fp32) sequentially in fp32;
-//   * the 16 partials are combined by an xor butterfly (8, 4, 2, 1);
+//   * D is cut into 64 contiguous chunks of D/64; lane l owns chunk l and adds
+//     its bf16*bf16 products (exact in fp32) sequentially in fp32;
+//   * the 64 partials are combined by the xor butterfly 1, 2, 4, 8, 16, 32
+//     (pairwise summation over the chunks in natural order);
 //   * logit = sum / gate_temp (fp32);
 //   * score functions use only IEEE basic operations (Cody-Waite exp with
 //     a degree-13 Taylor polynomial, an atanh series for log1p), so a host
@@ -17,7 +18,7 @@
 // Kernels
 //   router_scores_kernel  one wave = 4 expert rows x up to TT tokens; W row chunks
 //                         are loaded once per wave and reused for TT tokens.
-//   router_topk_kernel    one workgroup per token; k rounds of a block-wide argmax
+//   router_topk_kernel    one wave per token; k rounds of a wave-wide argmax
 //                         under the order's total order (value, then index).
 #include "router_launch.h"
 #include "topk.h"
@@ -125,10 +126,7 @@ __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __re
     }
   }
 #pragma unroll
-  for (int j = 0; j < TT; ++j) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) acc[j] = acc[j] + __shfl_xor(acc[j], m, 64);
-  }
+  for (int j = 0; j < TT; ++j) acc[j] = wave_sum(acc[j]);
   if (lane < TT) {
     // lane j finishes token j (all lanes hold every total after the butterfly)
     float v = acc[0];
@@ -140,22 +138,22 @@ __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __re
   }
 }
 
-// One 256-thread workgroup per token: k rounds of a block-wide argmax.
-__global__ void __launch_bounds__(256) router_topk_kernel(const float* __restrict__ scores,
-                                                          const float* __restrict__ bias,
-                                                          const float* __restrict__ bias_vl,
-                                                          const uint8_t* __restrict__ image_mask, int E, int k,
-                                                          float route_scale, int norm, int order,
-                                                          int32_t* __restrict__ idx, float* __restrict__ w) {
+// One wave per token: k rounds of a wave-wide argmax (EPT = ceil(E / 64) candidates per lane).
+template <int EPT>
+__global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict__ scores,
+                                                         const float* __restrict__ bias,
+                                                         const float* __restrict__ bias_vl,
+                                                         const uint8_t* __restrict__ image_mask, int E, int k,
+                                                         float route_scale, int norm, int order,
+                                                         int32_t* __restrict__ idx, float* __restrict__ w) {
   __shared__ int top_i[1024];
   __shared__ float top_v[1024];
-  __shared__ float lds_v[16];
-  __shared__ int lds_i[16];
   const int t = blockIdx.x;
   const float* s = scores + (size_t)t * E;
   const float* b = (image_mask != nullptr && image_mask[t] != 0) ? bias_vl : bias;
-  block_topk_rounds<4>(s, b, E, k, order, top_i, top_v, lds_v, lds_i);
-  for (int j = threadIdx.x; j < k; j += blockDim.x) idx[(size_t)t * k + j] = top_i[j];
+  wave_topk<EPT>(s, b, E, k, order, top_i, top_v);
+  __syncthreads();
+  for (int j = threadIdx.x; j < k; j += 64) idx[(size_t)t * k + j] = top_i[j];
   if (threadIdx.x == 0) normalise_weights(top_v, k, route_scale, norm, w + (size_t)t * k);
 }
 
@@ -203,7 +201,11 @@ extern "C" int cachalot_router_topk(const uint16_t* x, const uint16_t* W, const 
   hipStream_t s = (hipStream_t)stream;
   int rc = launch_router_scores(x, W, T, D, E, gate_temp, score_fn, scores, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(256), 0, s, scores, bias, bias_vl, image_mask, E, k,
-                     route_scale, norm, order, idx, w);
+  if (E <= 384)
+    hipLaunchKernelGGL((router_topk_kernel<6>), dim3(T), dim3(64), 0, s, scores, bias, bias_vl, image_mask, E, k,
+                       route_scale, norm, order, idx, w);
+  else
+    hipLaunchKernelGGL((router_topk_kernel<16>), dim3(T), dim3(64), 0, s, scores, bias, bias_vl, image_mask, E, k,
+                       route_scale, norm, order, idx, w);
   return check_launch("router_topk_kernel");
 }

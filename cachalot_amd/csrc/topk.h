@@ -58,23 +58,39 @@ __device__ __forceinline__ bool topk_better(float a, int ai, float b, int bi, in
   return order == CACHALOT_ORDER_ASCENDING ? ai > bi : ai < bi;
 }
 
-// k rounds of a block-wide argmax (O(E) work per round): each thread keeps up
-// to EPT candidates, a wave butterfly finds the wave's best, LDS holds one
-// entry per wave, every thread derives the same block winner, the owner marks
-// it taken.  Round r yields rank r.  Requires E <= EPT * blockDim.x and
-// blockDim.x a multiple of 64 (<= 1024).  lds_v / lds_i: LDS [16].
+template <int M>
+__device__ __forceinline__ void topk_exchange_step(float& bv, int& bi, int order) {
+  float ov;
+  int oi;
+  if constexpr (M == 7) {
+    ov = __uint_as_float(mirror8_u32(__float_as_uint(bv)));
+    oi = (int)mirror8_u32((uint32_t)bi);
+  } else if constexpr (M == 15) {
+    ov = __uint_as_float(mirror16_u32(__float_as_uint(bv)));
+    oi = (int)mirror16_u32((uint32_t)bi);
+  } else {
+    ov = xor_f<M>(bv);
+    oi = (int)xor_u32<M>((uint32_t)bi);
+  }
+  if (topk_better(ov, oi, bv, bi, order)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+// Top-k by one wave: k rounds of a wave-wide argmax under the order's total
+// order (a max-reduction, so the exchange pattern does not change the result),
+// the winner's owner marks it taken.  Round r yields rank r.  Lane 0 writes
+// top_i / top_v (LDS or global).  Requires E <= 64 * EPT.
 template <int EPT>
-__device__ __forceinline__ void block_topk_rounds(const float* __restrict__ scores, const float* __restrict__ bias,
-                                                  int E, int k, int order, int* top_i, float* top_v, float* lds_v,
-                                                  int* lds_i) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int nwaves = blockDim.x >> 6;
+__device__ __forceinline__ void wave_topk(const float* __restrict__ scores, const float* __restrict__ bias, int E,
+                                          int k, int order, int* top_i, float* top_v) {
+  const int lane = threadIdx.x & 63;
   float v[EPT];
   int id[EPT];
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int e = tid + j * blockDim.x;
+    const int e = lane + 64 * j;
     id[j] = -1;
     v[j] = -INFINITY;
     if (e < E) {
@@ -93,36 +109,20 @@ __device__ __forceinline__ void block_topk_rounds(const float* __restrict__ scor
         bv = v[j];
         bi = id[j];
       }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ov = __shfl_xor(bv, m, 64);
-      const int oi = __shfl_xor(bi, m, 64);
-      if (topk_better(ov, oi, bv, bi, order)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (lane == 0) {
-      lds_v[tid >> 6] = bv;
-      lds_i[tid >> 6] = bi;
-    }
-    __syncthreads();
-    float wv = lds_v[0];
-    int wi = lds_i[0];
-    for (int w = 1; w < nwaves; ++w)
-      if (topk_better(lds_v[w], lds_i[w], wv, wi, order)) {
-        wv = lds_v[w];
-        wi = lds_i[w];
-      }
+    topk_exchange_step<1>(bv, bi, order);
+    topk_exchange_step<2>(bv, bi, order);
+    topk_exchange_step<7>(bv, bi, order);
+    topk_exchange_step<15>(bv, bi, order);
+    topk_exchange_step<16>(bv, bi, order);
+    topk_exchange_step<32>(bv, bi, order);
 #pragma unroll
     for (int j = 0; j < EPT; ++j)
-      if (id[j] == wi) id[j] = -1;
-    if (tid == 0) {
+      if (id[j] == bi) id[j] = -1;
+    if (lane == 0) {
       const int pos = order == CACHALOT_ORDER_ASCENDING ? k - 1 - r : r;
-      top_i[pos] = wi;
-      top_v[pos] = scores[wi];
+      top_i[pos] = bi;
+      top_v[pos] = scores[bi];
     }
-    __syncthreads();
   }
 }
 

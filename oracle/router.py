@@ -24,7 +24,7 @@ This build fixes one so ids are reproducible bit for bit on any device:
 * D is split into 64 contiguous chunks (one per lane of a wave64); each chunk
   is summed sequentially in fp32 from 0 (bf16 x bf16 products are exact in fp32);
 * the 64 partials are combined by the butterfly ``p[i] + p[i ^ s]`` for
-  s = 32, 16, 8, 4, 2, 1 (a pairwise tree on bit-reversed leaves);
+  s = 1, 2, 4, 8, 16, 32 (pairwise summation over the chunks in natural order);
 * ``logit = tree / gate_temp`` in fp32.
 
 Score functions are evaluated with IEEE basic operations only, so that the
@@ -111,7 +111,7 @@ def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: i
         acc = np.zeros((xs.shape[0], e, N_CHUNKS), dtype=np.float32)
         for j in range(ch):
             acc += xs[:, None, :, j] * wr[None, :, :, j]
-        for s in (32, 16, 8, 4, 2, 1):
+        for s in (1, 2, 4, 8, 16, 32):
             acc = acc + acc[..., lane ^ s]
         out[t0:t0 + block] = acc[..., 0]
     return out / np.float32(gate_temp)

@@ -2,8 +2,8 @@
 
 Independent checks: the score functions against Python's libm in float64
 (within one fp32 ulp of the correctly rounded value), the logit reduction
-against ``math.fsum`` and against an explicit pairwise tree on bit-reversed
-chunk order (the identity the GPU's xor butterfly relies on), top-k against a
+against ``math.fsum`` and against an explicit pairwise tree over the chunks in
+natural order (the identity the GPU's xor butterfly relies on), top-k against a
 brute-force sort with the stated tie rules, and the reference's invariants
 (bias affects selection only; weights sum to route_scale).
 """
@@ -58,16 +58,15 @@ def test_score_fn_within_two_ulp(kind):
     assert _ulp_diff32(got, want.astype(np.float32)).max() <= 2
 
 
-def _tree_bitreversed(p):
-    """Pairwise tree over 64 partials taken in bit-reversed chunk order."""
-    order = [int(f"{i:06b}"[::-1], 2) for i in range(64)]
-    level = [p[i] for i in order]
+def _tree_pairwise(p):
+    """Pairwise tree over the 64 partials in natural chunk order."""
+    level = list(p)
     while len(level) > 1:
         level = [np.float32(level[i] + level[i + 1]) for i in range(0, len(level), 2)]
     return level[0]
 
 
-def test_logits_fixed_order_is_sequential_chunks_then_bitreversed_tree():
+def test_logits_fixed_order_is_sequential_chunks_then_pairwise_tree():
     rng = np.random.default_rng(2)
     d, e = 512, 5
     x = round_bf16(rng.normal(size=(2, d)).astype(np.float32))
@@ -82,7 +81,7 @@ def test_logits_fixed_order_is_sequential_chunks_then_bitreversed_tree():
                 for j in range(ch):
                     acc = np.float32(acc + np.float32(x[t, c * ch + j] * w[r, c * ch + j]))
                 parts.append(acc)
-            assert got[t, r] == _tree_bitreversed(parts)
+            assert got[t, r] == _tree_pairwise(parts)
             exact = math.fsum(float(x[t, i]) * float(w[r, i]) for i in range(d))
             assert abs(got[t, r] - exact) <= 1e-5 * max(1.0, abs(exact))
 
