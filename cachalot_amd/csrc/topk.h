@@ -52,10 +52,8 @@ __device__ __forceinline__ void block_topk_rank(const float4* __restrict__ sel4,
 
 // a beats b under the order's total order; an index < 0 marks "no candidate".
 __device__ __forceinline__ bool topk_better(float a, int ai, float b, int bi, int order) {
-  if (ai < 0) return false;
-  if (bi < 0) return true;
-  if (a != b) return a > b;
-  return order == CACHALOT_ORDER_ASCENDING ? ai > bi : ai < bi;
+  const bool idx_wins = order == CACHALOT_ORDER_ASCENDING ? ai > bi : ai < bi;
+  return (ai >= 0) & ((bi < 0) | (a > b) | ((a == b) & idx_wins));
 }
 
 template <int M>
@@ -72,10 +70,9 @@ __device__ __forceinline__ void topk_exchange_step(float& bv, int& bi, int order
     ov = xor_f<M>(bv);
     oi = (int)xor_u32<M>((uint32_t)bi);
   }
-  if (topk_better(ov, oi, bv, bi, order)) {
-    bv = ov;
-    bi = oi;
-  }
+  const bool take = topk_better(ov, oi, bv, bi, order);
+  bv = take ? ov : bv;
+  bi = take ? oi : bi;
 }
 
 // Top-k by one wave: k rounds of a wave-wide argmax under the order's total
@@ -88,27 +85,31 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ scores, cons
   const int lane = threadIdx.x & 63;
   float v[EPT];
   int id[EPT];
+  // unconditional (clamped) loads, so all of them are in flight together
+  float sv[EPT], bv0[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = min(lane + 64 * j, E - 1);
+    sv[j] = scores[e];
+    bv0[j] = bias[e];
+  }
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
     const int e = lane + 64 * j;
-    id[j] = -1;
-    v[j] = -INFINITY;
-    if (e < E) {
-      float s = scores[e] + bias[e];
-      if (s != s) s = -INFINITY;  // NaN never wins
-      v[j] = s;
-      id[j] = e;
-    }
+    float s = sv[j] + bv0[j];
+    if (s != s) s = -INFINITY;  // NaN never wins
+    v[j] = s;
+    id[j] = e < E ? e : -1;
   }
   for (int r = 0; r < k; ++r) {
     float bv = -INFINITY;
     int bi = -1;
 #pragma unroll
-    for (int j = 0; j < EPT; ++j)
-      if (topk_better(v[j], id[j], bv, bi, order)) {
-        bv = v[j];
-        bi = id[j];
-      }
+    for (int j = 0; j < EPT; ++j) {
+      const bool take = topk_better(v[j], id[j], bv, bi, order);
+      bv = take ? v[j] : bv;
+      bi = take ? id[j] : bi;
+    }
     topk_exchange_step<1>(bv, bi, order);
     topk_exchange_step<2>(bv, bi, order);
     topk_exchange_step<7>(bv, bi, order);
@@ -116,14 +117,14 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ scores, cons
     topk_exchange_step<16>(bv, bi, order);
     topk_exchange_step<32>(bv, bi, order);
 #pragma unroll
-    for (int j = 0; j < EPT; ++j)
-      if (id[j] == bi) id[j] = -1;
+    for (int j = 0; j < EPT; ++j) id[j] = id[j] == bi ? -1 : id[j];
     if (lane == 0) {
       const int pos = order == CACHALOT_ORDER_ASCENDING ? k - 1 - r : r;
       top_i[pos] = bi;
-      top_v[pos] = scores[bi];
     }
   }
+  // the raw scores of the winners (the weights are taken from scores, not selection values)
+  for (int j = lane; j < k; j += 64) top_v[j] = scores[top_i[j]];
 }
 
 // Fill sel4 from scores + bias (NaN -> -inf, padding -inf).

@@ -67,15 +67,20 @@ def swiglu_rows(x, mm1, mm3, mm2, weights, limit: float = 10.0) -> np.ndarray:
     return round_bf16(mm2(h).astype(np.float32))
 
 
-def affine_decode(x, mats, weights, limit: float = 10.0, addend=None):
+def affine_decode(x, mats, weights, limit: float = 10.0, addend=None, *, terms: bool = False):
     """x [D] bf16-exact; mats: per expert (mm1, mm3, mm2) as in ``swiglu_rows``.
 
-    -> (routed fp32 [D], out fp32 [D] holding bf16(routed + addend))."""
+    -> (routed fp32 [D], out fp32 [D] holding bf16(routed + addend)), plus the
+    per-expert outputs y_e (bf16-exact fp32 [k, D]) when ``terms``."""
     x = np.asarray(x, dtype=np.float64)[None, :]
     routed = None
+    ys = []
     for (mm1, mm3, mm2), w in zip(mats, weights, strict=True):
         y = swiglu_rows(x, mm1, mm3, mm2, np.asarray([w], np.float32), limit)[0]
+        ys.append(y)
         routed = (np.float32(0.0) + y) if routed is None else (routed + y)
     routed = routed.astype(np.float32)
     total = routed if addend is None else routed + np.asarray(addend, np.float32)
+    if terms:
+        return routed, round_bf16(total), np.stack(ys)
     return routed, round_bf16(total)

@@ -72,3 +72,14 @@ def bf16_out_ok(got_bf16, want_total_f32, tol: float) -> bool:
     want = np.asarray(want_total_f32, np.float64)
     bound = tol * np.abs(want).max() + 0.5 * bf16_ulp(want)
     return bool(np.all(np.abs(got - want) <= bound))
+
+
+def bf16_terms_ok(got, want, terms, tol: float) -> bool:
+    """Outputs that sum per-expert bf16 casts (the 2-bit path rounds every expert's
+    y_e to bf16, ``expert_affine.py:81,149-151``): the bar plus one bf16 ulp per
+    expert term, since a different fp32 summation order may move a y_e across a
+    rounding boundary."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    slack = np.sum(bf16_ulp(np.asarray(terms, np.float64)), axis=0)
+    return bool(np.all(np.abs(got - want) <= tol * np.abs(want).max() + slack))
