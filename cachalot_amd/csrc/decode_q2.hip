@@ -20,11 +20,12 @@
 //                      Epilogue: bf16(g), bf16(u), clamp,
 //                      h = bf16(silu(g) * u * w_e), written in the pair order
 //                      the down kernel consumes.
-//   q2_down_kernel     one workgroup = R_DN rows of W2, k waves (wave e = expert
-//                      e); lane l owns words l, l+64, l+128 of the row (K = 2880
-//                      -> 180 words).  Each row value is rounded to bf16 (the
-//                      reference's per-expert cast), handed over in LDS and
-//                      summed in route order, + addend, -> fp32 / bf16.
+//   q2_down_kernel     one workgroup = RD rows of W2, k waves (wave e = expert
+//                      e); lane l owns the 64-code chunk l of a row (one
+//                      quantisation group: a 16-byte load, one scale, one bias;
+//                      K = 2880 -> 45 chunks).  Each row value is rounded to
+//                      bf16 (the reference's per-expert cast), handed over in
+//                      LDS and summed in route order, + addend, -> fp32 / bf16.
 #include "decode_common.h"
 #include "router_launch.h"
 #include "topk.h"
@@ -34,7 +35,9 @@ namespace {
 
 using namespace decode;
 constexpr int R_GU = 4;     // rows per wave, gate/up
-constexpr int MAXW = 3;     // words per lane in down (F <= 3072)
+#ifndef Q2_DOWN_ROWS
+#define Q2_DOWN_ROWS 8      // W2 rows per down workgroup
+#endif
 
 // Pair layout of a 16-value word: E_b = (v[4b], v[4b+2]), O_b = (v[4b+1], v[4b+3]);
 // memory order E_0..E_3, O_0..O_3.  Position of value i (0..15) in uint16 units:
@@ -200,81 +203,96 @@ __global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
   }
 }
 
-// grid.x = ceil(D / R_DN); one workgroup = k waves, wave e = expert e
+// grid.x = ceil(D / RD); one workgroup = k waves, wave e = expert e, RD rows.
+// Lane l owns the 64-code chunk l of a row (words 4l .. 4l+3, one quantisation
+// group): one 16-byte weight load, one scale and one bias per row; lanes past
+// the row's last chunk (K = 2880: 45 chunks) only take part in the reductions.
+// The expert's hidden pairs for the lane's chunk are loaded once and reused for
+// all RD rows.
+template <int RD>
 __global__ void __launch_bounds__(64 * KMAX) q2_down_kernel(
     const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
     int group, const uint16_t* __restrict__ hp, const uint16_t* __restrict__ addend, float* __restrict__ routed,
     uint16_t* __restrict__ out) {
-  __shared__ float vals[KMAX][R_DN];
+  __shared__ float vals[KMAX][RD];
   const int lane = threadIdx.x & 63;
   const int e = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * R_DN;
+  const int row0 = blockIdx.x * RD;
   const int Kw = F / 16;                   // valid words per row
+  const int NCH = (Kw + 3) / 4;            // 64-code chunks per row (the last may be partial)
   const int G = (F + group - 1) / group;   // groups per row (the last may be partial)
   const int stride = G * group / 16;       // stored words per row
+  const int c = min(lane, NCH - 1);
+  const bool active = lane < NCH;
+  const int g = (c * 64) / group;
   const int slot = ws_slots[e];
 
-  float rowv[R_DN];
+  float rowv[RD];
 #pragma unroll
-  for (int r = 0; r < R_DN; ++r) rowv[r] = 0.0f;
+  for (int r = 0; r < RD; ++r) rowv[r] = 0.0f;
   if (slot >= 0) {
     const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
     const uint32_t* w2 = reinterpret_cast<const uint32_t*>(base + L.off[3]);
     const uint16_t* s2 = reinterpret_cast<const uint16_t*>(base + L.off[4]);
     const uint16_t* b2 = reinterpret_cast<const uint16_t*>(base + L.off[5]);
     const uint4* hpe = reinterpret_cast<const uint4*>(hp + (size_t)e * Kw * 16);
-    uint32_t wv[R_DN][MAXW];
-    uint16_t sv[R_DN][MAXW], bv[R_DN][MAXW];
-    uint4 ha[MAXW], hb[MAXW];
+    uint4 hv[8];
 #pragma unroll
-    for (int i = 0; i < MAXW; ++i) {
-      const int j = min(lane + 64 * i, Kw - 1);
-      ha[i] = hpe[2 * j];
-      hb[i] = hpe[2 * j + 1];
+    for (int q = 0; q < 4; ++q) {
+      const int j = min(4 * c + q, Kw - 1);
+      hv[2 * q] = hpe[2 * j];
+      hv[2 * q + 1] = hpe[2 * j + 1];
     }
+    uint4 wv[RD];
+    uint16_t sv[RD], bv[RD];
 #pragma unroll
-    for (int r = 0; r < R_DN; ++r) {
+    for (int r = 0; r < RD; ++r) {
       const int n = min(row0 + r, D - 1);
-#pragma unroll
-      for (int i = 0; i < MAXW; ++i) {
-        const int j = min(lane + 64 * i, Kw - 1);
-        const int g = (j * 16) / group;
-        wv[r][i] = w2[(size_t)n * stride + j];
-        sv[r][i] = s2[(size_t)n * G + g];
-        bv[r][i] = b2[(size_t)n * G + g];
-      }
+      // the chunk's words: 4 whole words unless the row ends inside it (then the
+      // missing words are padding codes, multiplied by zeroed hidden pairs below)
+      wv[r] = *reinterpret_cast<const uint4*>(w2 + (size_t)n * stride + 4 * c);
+      sv[r] = s2[(size_t)n * G + g];
+      bv[r] = b2[(size_t)n * G + g];
     }
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t he[MAXW][4], ho[MAXW][4];
-    float hs[MAXW];
+    uint32_t he[4][4], ho[4][4];
+    float hs = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXW; ++i) {
-      const bool valid = lane + 64 * i < Kw;
-      he[i][0] = valid ? ha[i].x : 0u; he[i][1] = valid ? ha[i].y : 0u;
-      he[i][2] = valid ? ha[i].z : 0u; he[i][3] = valid ? ha[i].w : 0u;
-      ho[i][0] = valid ? hb[i].x : 0u; ho[i][1] = valid ? hb[i].y : 0u;
-      ho[i][2] = valid ? hb[i].z : 0u; ho[i][3] = valid ? hb[i].w : 0u;
-      float s = 0.0f;
+    for (int q = 0; q < 4; ++q) {
+      const bool valid = active && (4 * c + q < Kw);
+      he[q][0] = valid ? hv[2 * q].x : 0u; he[q][1] = valid ? hv[2 * q].y : 0u;
+      he[q][2] = valid ? hv[2 * q].z : 0u; he[q][3] = valid ? hv[2 * q].w : 0u;
+      ho[q][0] = valid ? hv[2 * q + 1].x : 0u; ho[q][1] = valid ? hv[2 * q + 1].y : 0u;
+      ho[q][2] = valid ? hv[2 * q + 1].z : 0u; ho[q][3] = valid ? hv[2 * q + 1].w : 0u;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        s = dot2_bf16(he[i][q], BF16_ONES, s);
-        s = dot2_bf16(ho[i][q], BF16_ONES, s);
+      for (int p = 0; p < 4; ++p) {
+        hs = dot2_bf16(he[q][p], BF16_ONES, hs);
+        hs = dot2_bf16(ho[q][p], BF16_ONES, hs);
       }
-      hs[i] = s;
     }
 #pragma unroll
-    for (int r = 0; r < R_DN; ++r) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < MAXW; ++i) {
-        const float d = q2_word_dot(wv[r][i], he[i], ho[i], 0.0f);
-        acc = acc + (bf16_to_f32(sv[r][i]) * d + bf16_to_f32(bv[r][i]) * hs[i]);
-      }
-      rowv[r] = acc;
+    for (int r = 0; r < RD; ++r) {
+      float d = 0.0f;
+      d = q2_word_dot(wv[r].x, he[0], ho[0], d);
+      d = q2_word_dot(wv[r].y, he[1], ho[1], d);
+      d = q2_word_dot(wv[r].z, he[2], ho[2], d);
+      d = q2_word_dot(wv[r].w, he[3], ho[3], d);
+      rowv[r] = bf16_to_f32(sv[r]) * d + bf16_to_f32(bv[r]) * hs;
     }
   }
-  const float red = wave_transpose_sum<R_DN>(rowv, lane);
-  combine_rows<true>(red, lane, e, row0, D, k, vals, addend, routed, out);
+  // row sums (row r ends in lanes [r * 64/RD, (r+1) * 64/RD)); the wave hands its
+  // expert's bf16-rounded rows to LDS
+  const float red = wave_transpose_sum<RD>(rowv, lane);
+  if ((lane & (64 / RD - 1)) == 0) vals[e][lane / (64 / RD)] = round_bf16(red);
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < RD && row0 + t < D) {
+    const int n = row0 + t;
+    float acc = 0.0f;
+    for (int j = 0; j < k; ++j) acc = acc + vals[j][t];
+    if (routed) routed[n] = acc;
+    if (out) out[n] = f32_to_bf16(addend ? acc + bf16_to_f32(addend[n]) : acc);
+  }
 }
 
 }  // namespace
@@ -295,8 +313,8 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   CACHALOT_REQUIRE(group == 64 || group == 128, "moe_decode_q2: group_size %d (64 or 128)", group);
   CACHALOT_REQUIRE(D % group == 0 && D >= 64 && D <= 8192,
                    "moe_decode_q2: D=%d must be a multiple of group %d and <= 8192", D, group);
-  CACHALOT_REQUIRE(F % 16 == 0 && F >= 16 && F <= 16 * 64 * MAXW,
-                   "moe_decode_q2: F=%d must be a multiple of 16 and <= %d", F, 16 * 64 * MAXW);
+  CACHALOT_REQUIRE(F % 16 == 0 && F >= 64 && F <= 4096, "moe_decode_q2: F=%d must be a multiple of 16 in 64..4096",
+                   F);
   const WsOffsets wo = ws_offsets((size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t));
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, wo.total);
@@ -331,8 +349,8 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   }
   rc = check_launch("q2_gate_up_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(q2_down_kernel, dim3((D + R_DN - 1) / R_DN), dim3(64 * k), 0, s, pool, L, ws_slots, D, F, k,
-                     group, hp, addend, routed, out);
+  hipLaunchKernelGGL((q2_down_kernel<Q2_DOWN_ROWS>), dim3((D + Q2_DOWN_ROWS - 1) / Q2_DOWN_ROWS), dim3(64 * k), 0, s,
+                     pool, L, ws_slots, D, F, k, group, hp, addend, routed, out);
   return check_launch("q2_down_kernel");
 }
 
