@@ -1,4 +1,4 @@
-// Decode (one token) over an FP4 E2M1 / E8M0-block-32 expert bank.
+// Decode (one token) over an FP4 E2M1 / E8M0-block-32 expert bank, on the matrix cores.
 //
 // Reference: src/cachalot/model/moe_fused_metal.py:189-233 (fused_gate_up +
 // fused_down): x read as fp32, gate/up accumulated in fp32,
@@ -6,213 +6,208 @@
 // W2_e h_e in fp32 with experts in route order (:160-178).  No bf16 rounding
 // point anywhere on this path.
 //
-//   fp4_gate_up_kernel  one wave = R rows of one expert (same prologue and
-//                       load-everything-first structure as the 2-bit kernel);
-//                       lane l owns 64 codes (two E8M0 blocks, 32 bytes) of the
-//                       row, so K = 4096 is a 2 KiB coalesced wave load per
-//                       matrix.  Nibbles become bf16 pairs (value * 2^e, exact)
-//                       in the gfx950 converter and meet the bf16 activation
-//                       pairs in v_dot2c_f32_bf16.
-//   fp4_down_kernel     one workgroup = R rows of W2, k waves (wave e = expert
-//                       e); lane l owns words l + 64 i of the row (8 codes each);
-//                       the fp32 hidden vector stays fp32 (converter to f32
-//                       pairs, fp32 FMA); per-expert row values meet in LDS and
-//                       are summed in route order.
+// A "piece" is 32 codes of a row: 16 bytes of nibbles and one E8M0 scale.  The
+// converter turns a nibble word into 8 exact bf16 values (E2M1 x 2^e), which
+// meet bf16 activations in v_mfma_f32_16x16x32_bf16 (exact products, fp32 sums).
+//
+//   fp4_gate_up_kernel  one workgroup = one expert x one 16-row tile of W1 and
+//                       W3; four waves split K into quarters; lane group kg of
+//                       block b takes piece 4b + kg of the wave's quarter (one
+//                       load instruction covers whole 64-byte runs of a row).
+//                       Every A row carries x, so D[i][j] is the dot product of
+//                       weight row j for every i.  Epilogue in fp32:
+//                       h = silu(min(g, L)) * clip(u, +-L) * w_e.
+//   fp4_down_kernel     one workgroup = one 16-row tile of W2 for all k experts,
+//                       2k waves (expert, K half).  The fp32 hidden vectors are
+//                       staged in LDS as bf16 hi + lo parts (A rows 0 and 1:
+//                       h = hi + lo to 16 significant bits); expert row values
+//                       are summed in fp32 in route order.
 #include "decode_common.h"
+#include "mfma_tile.h"
 #include "router_launch.h"
 
 namespace cachalot {
 namespace {
 
 using namespace decode;
-constexpr int R_GU = 4;
-constexpr int MAXW = 6;   // 8-code words per lane, down (F <= 3072)
+using namespace tile;
 
-__device__ __forceinline__ float fp4_word_dot_bf16(uint32_t w, float scale, const uint32_t* xp, float acc) {
-  acc = dot2_bf16(fp4x2_to_bf16x2<0>(w, scale), xp[0], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<1>(w, scale), xp[1], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<2>(w, scale), xp[2], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<3>(w, scale), xp[3], acc);
-  return acc;
-}
+constexpr int GU_WAVES = 4;
+constexpr int DN_HALVES = 2;
+constexpr int PIECE = 32;                        // codes per piece (one E8M0 scale)
+constexpr int MAX_D = 8192;
+constexpr int MAX_KF = 24576;                    // k * F staged by the down kernel
+constexpr int ZERO_BYTES = 64;                   // 4 steps x 16 bytes
+constexpr int GU_ZERO = MAX_D * 2;
+constexpr int DN_ZERO = MAX_KF * 4;
 
-// 8 uint32 words of one 64-code chunk (two scale blocks) dotted with 32 bf16 pairs of x.
-__device__ __forceinline__ float fp4_chunk_dot(uint4 a, uint4 b, float s0, float s1, const uint32_t* xw) {
-  float acc = 0.0f;
-  acc = fp4_word_dot_bf16(a.x, s0, xw + 0, acc);
-  acc = fp4_word_dot_bf16(a.y, s0, xw + 4, acc);
-  acc = fp4_word_dot_bf16(a.z, s0, xw + 8, acc);
-  acc = fp4_word_dot_bf16(a.w, s0, xw + 12, acc);
-  acc = fp4_word_dot_bf16(b.x, s1, xw + 16, acc);
-  acc = fp4_word_dot_bf16(b.y, s1, xw + 20, acc);
-  acc = fp4_word_dot_bf16(b.z, s1, xw + 24, acc);
-  acc = fp4_word_dot_bf16(b.w, s1, xw + 28, acc);
-  return acc;
-}
-
-template <int C, bool FUSE>
-__global__ void __launch_bounds__(64 * WAVES) fp4_gate_up_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L,
-    const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx, const float* __restrict__ wts,
-    RouteArgs ra, int D, int F, int E, int k, float limit, float* __restrict__ hidden,
-    int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
-  __shared__ int s_slot[KMAX];
-  __shared__ float s_w[KMAX];
-  __shared__ int top_i[KMAX];
-  __shared__ float top_v[KMAX];
-  __shared__ float lds_v[16];
-  __shared__ int lds_i[16];
-  const int lane = threadIdx.x & 63;
-  const int NC = D / 64;
-  const int SB = D / 32;
-
-  uint32_t xw[C][32];
+template <int NB>
+__device__ __forceinline__ void lane_pieces(int first, int PW, int pieces, int kg, int (&pi)[NB], bool (&pv)[NB]) {
 #pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const int c = min(lane + 64 * i, NC - 1);
-    const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)c * 64);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 v = xp[q];
-      xw[i][4 * q] = v.x; xw[i][4 * q + 1] = v.y; xw[i][4 * q + 2] = v.z; xw[i][4 * q + 3] = v.w;
-    }
+  for (int b = 0; b < NB; ++b) {
+    const int within = 4 * b + kg;
+    const int P = first + within;
+    pv[b] = within < PW && P < pieces;
+    pi[b] = min(P, pieces - 1);
   }
+}
 
-  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, top_i, top_v, lds_v, lds_i, ws_slots, ws_w);
-
-  const int RB = (F + R_GU - 1) / R_GU;
-  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  if (item >= k * RB) return;
-  const int e = item / RB;
-  const int row0 = (item % RB) * R_GU;
-  float* hout = hidden + (size_t)e * F;
-  const int slot = s_slot[e];
+// grid.x = k * F / 16.  NB = ceil(ceil(D/32 / 4) / 4); XI = ceil(D / 4096).
+template <int NB, int XI>
+__global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L, ExpertSource src, int D, int F,
+    float limit, uint16_t* __restrict__ hidden, int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
+  __shared__ __align__(16) uint8_t xl[GU_ZERO + ZERO_BYTES];
+  __shared__ __align__(16) uint8_t sc[2 * 16 * (MAX_D / PIECE)];   // s1, s3 of the tile's rows
+  __shared__ float red[GU_WAVES][2][16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int PT = D / PIECE;
+  const int tiles = F / 16;
+  const int e = blockIdx.x / tiles;
+  const int tile = blockIdx.x - e * tiles;
+  const int row0 = tile * 16;
+  int slot;
+  float wexp;
+  resolve_expert(src, e, tile == 0, ws_slots, ws_w, slot, wexp);
+  uint16_t* hout = hidden + (size_t)e * F * 2;   // per expert: hi [F], lo [F] (bf16)
   if (slot < 0) {
-    if (lane < R_GU && row0 + lane < F) hout[row0 + lane] = 0.0f;
+    if (threadIdx.x < 16) hout[row0 + threadIdx.x] = hout[F + row0 + threadIdx.x] = 0;
     return;
   }
   const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
-  const uint4* w1 = reinterpret_cast<const uint4*>(base + L.off[0]);
-  const uint8_t* s1 = base + L.off[1];
-  const uint4* w3 = reinterpret_cast<const uint4*>(base + L.off[6]);
-  const uint8_t* s3 = base + L.off[7];
+  const int j = lane & 15, kg = lane >> 4;
+  const int row = row0 + j;
+  const int PW = (PT + GU_WAVES - 1) / GU_WAVES;
+  int pi[NB];
+  bool pv[NB];
+  lane_pieces<NB>(wave * PW, PW, PT, kg, pi, pv);
 
-  uint4 ga[R_GU][C], gb[R_GU][C], ua[R_GU][C], ub[R_GU][C];
-  uint8_t sg0[R_GU][C], sg1[R_GU][C], su0[R_GU][C], su1[R_GU][C];
+  uint4 wg[NB], wu[NB];
+  {
+    const uint4* r1 = reinterpret_cast<const uint4*>(base + L.off[0]) + (size_t)row * PT;
+    const uint4* r3 = reinterpret_cast<const uint4*>(base + L.off[6]) + (size_t)row * PT;
 #pragma unroll
-  for (int r = 0; r < R_GU; ++r) {
-    const int n = min(row0 + r, F - 1);
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-      const int c = min(lane + 64 * i, NC - 1);
-      ga[r][i] = w1[((size_t)n * NC + c) * 2];
-      gb[r][i] = w1[((size_t)n * NC + c) * 2 + 1];
-      ua[r][i] = w3[((size_t)n * NC + c) * 2];
-      ub[r][i] = w3[((size_t)n * NC + c) * 2 + 1];
-      sg0[r][i] = s1[(size_t)n * SB + 2 * c];
-      sg1[r][i] = s1[(size_t)n * SB + 2 * c + 1];
-      su0[r][i] = s3[(size_t)n * SB + 2 * c];
-      su1[r][i] = s3[(size_t)n * SB + 2 * c + 1];
+    for (int b = 0; b < NB; ++b) {
+      wg[b] = r1[pi[b]];
+      wu[b] = r3[pi[b]];
     }
   }
-  // keep every load above this point in flight before any arithmetic
-  __builtin_amdgcn_sched_barrier(0);
+  // the tile's scales (two runs of 16 rows x PT bytes) and the activations into LDS
+  dma_to_lds(base + L.off[1] + (int64_t)row0 * PT, sc, 16 * PT, wave, GU_WAVES, lane);
+  dma_to_lds(base + L.off[7] + (int64_t)row0 * PT, sc + 16 * PT, 16 * PT, (wave + 2) & 3, GU_WAVES, lane);
+  dma_to_lds(x, xl, D * 2, wave, GU_WAVES, lane);
+  if (threadIdx.x < ZERO_BYTES / 16) reinterpret_cast<uint4*>(xl + GU_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+  wait_vmem();
+  __syncthreads();
 
-  float part[2 * R_GU];
+  f32x4_t cg = {0.0f, 0.0f, 0.0f, 0.0f}, cu = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int r = 0; r < R_GU; ++r) {
-    float pg = 0.0f, pu = 0.0f;
+  for (int b = 0; b < NB; ++b) {
+    const uint32_t aoff = pv[b] ? (uint32_t)pi[b] * (PIECE * 2) : (uint32_t)GU_ZERO;
+    const float sg = e8m0_to_f32(sc[j * PT + pi[b]]);
+    const float su = e8m0_to_f32(sc[(16 + j) * PT + pi[b]]);
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-      const float valid = (lane + 64 * i < NC) ? 1.0f : 0.0f;
-      pg = pg + valid * fp4_chunk_dot(ga[r][i], gb[r][i], e8m0_to_f32(sg0[r][i]), e8m0_to_f32(sg1[r][i]), xw[i]);
-      pu = pu + valid * fp4_chunk_dot(ua[r][i], ub[r][i], e8m0_to_f32(su0[r][i]), e8m0_to_f32(su1[r][i]), xw[i]);
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8_t a = lds_a(xl, aoff + 16 * s);
+      cg = mfma(a, fp4_codes_to_b(word_of(wg[b], s), sg), cg);
+      cu = mfma(a, fp4_codes_to_b(word_of(wu[b], s), su), cu);
     }
-    part[2 * r] = pg;
-    part[2 * r + 1] = pu;
   }
-  const float red = wave_transpose_sum<2 * R_GU>(part, lane);
-  const float up = __shfl(red, lane + 8, 64);
-  if ((lane & 15) == 0) {
-    const int n = row0 + (lane >> 4);
-    if (n < F) {
-      float g = red, u = up;
-      if (limit > 0.0f) {
-        u = fminf(fmaxf(u, -limit), limit);
-        g = fminf(g, limit);
-      }
-      hout[n] = (silu_f32(g) * u) * s_w[e];
+  if (lane < 16) {
+    red[wave][0][lane] = cg[0];
+    red[wave][1][lane] = cu[0];
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    float g = 0.0f, u = 0.0f;
+#pragma unroll
+    for (int w = 0; w < GU_WAVES; ++w) {
+      g = g + red[w][0][t];
+      u = u + red[w][1][t];
     }
+    if (limit > 0.0f) {
+      u = fminf(fmaxf(u, -limit), limit);
+      g = fminf(g, limit);
+    }
+    const float h = (silu_f32(g) * u) * wexp;
+    const uint16_t hi = f32_to_bf16(h);
+    hout[row0 + t] = hi;                                         // bf16 hi part
+    hout[F + row0 + t] = f32_to_bf16(h - bf16_to_f32(hi));      // bf16 lo part
   }
 }
 
-// grid.x = ceil(D / R_DN); one workgroup = k waves, wave e = expert e
-__global__ void __launch_bounds__(64 * KMAX) fp4_down_kernel(
+// grid.x = D / 16; block = 64 * k * DN_HALVES.  NB = ceil(ceil(F/32 / 2) / 4).
+template <int NB>
+__global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
     const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
-    const float* __restrict__ hidden, const uint16_t* __restrict__ addend, float* __restrict__ routed,
+    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ addend, float* __restrict__ routed,
     uint16_t* __restrict__ out) {
-  __shared__ float vals[KMAX][R_DN];
+  __shared__ __align__(16) uint8_t hl[DN_ZERO + ZERO_BYTES];   // per expert: hi [F] bf16, lo [F] bf16
+  __shared__ __align__(16) uint8_t sc[MAX_KF / 2];              // per expert: s2 of the tile's rows
+  __shared__ float vals[KMAX][DN_HALVES][16];
   const int lane = threadIdx.x & 63;
-  const int e = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * R_DN;
-  const int Kw = F / 8;     // 32-bit words per row
-  const int SB = F / 32;    // scale blocks per row
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int PK = F / PIECE;
+  const int e = wave / DN_HALVES;
+  const int half = wave - e * DN_HALVES;
+  const int row0 = blockIdx.x * 16;
+  const int j = lane & 15, kg = lane >> 4;
   const int slot = ws_slots[e];
-  float rowv[R_DN];
-#pragma unroll
-  for (int r = 0; r < R_DN; ++r) rowv[r] = 0.0f;
+  const int PW = (PK + DN_HALVES - 1) / DN_HALVES;
+  int pi[NB];
+  bool pv[NB];
+  lane_pieces<NB>(half * PW, PW, PK, kg, pi, pv);
+
+  uint4 wd[NB];
   if (slot >= 0) {
-    const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
-    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(base + L.off[3]);
-    const uint8_t* s2 = base + L.off[4];
-    const float4* he = reinterpret_cast<const float4*>(hidden + (size_t)e * F);
-    uint32_t wv[R_DN][MAXW];
-    uint8_t sv[R_DN][MAXW];
-    float4 ha[MAXW], hb[MAXW];
+    const uint4* r2 =
+        reinterpret_cast<const uint4*>(pool + (int64_t)slot * L.record_bytes + L.off[3]) + (size_t)(row0 + j) * PK;
 #pragma unroll
-    for (int i = 0; i < MAXW; ++i) {
-      const int j = min(lane + 64 * i, Kw - 1);
-      ha[i] = he[2 * j];
-      hb[i] = he[2 * j + 1];
-    }
+    for (int b = 0; b < NB; ++b) wd[b] = r2[pi[b]];
+  }
+  // hidden hi / lo parts and, per expert, the tile's scales (16 rows x PK bytes) into LDS
+  dma_to_lds(hidden, hl, k * F * 4, wave, nwaves, lane);
+  for (int r = wave; r < k; r += nwaves) {
+    const int ps = max(ws_slots[r], 0);   // a missing expert's rows are never used
+    dma_to_lds(pool + (int64_t)ps * L.record_bytes + L.off[4] + (int64_t)row0 * PK, sc + r * 16 * PK, 16 * PK, 0, 1,
+               lane);
+  }
+  if (threadIdx.x < ZERO_BYTES / 16) reinterpret_cast<uint4*>(hl + DN_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+  wait_vmem();
+  __syncthreads();
+
+  f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (slot >= 0) {
+    const uint32_t part = j == 0 ? 0u : (uint32_t)F * 2;   // A row 0: hi, row 1: lo, others: zero
+    const uint8_t* scale_rows = sc + (size_t)e * 16 * PK;
 #pragma unroll
-    for (int r = 0; r < R_DN; ++r) {
-      const int n = min(row0 + r, D - 1);
+    for (int b = 0; b < NB; ++b) {
+      const uint32_t aoff =
+          (pv[b] && j < 2) ? (uint32_t)e * F * 4 + part + (uint32_t)pi[b] * (PIECE * 2) : (uint32_t)DN_ZERO;
+      const float sd = e8m0_to_f32(scale_rows[j * PK + pi[b]]);
 #pragma unroll
-      for (int i = 0; i < MAXW; ++i) {
-        const int j = min(lane + 64 * i, Kw - 1);
-        wv[r][i] = w2[(size_t)n * Kw + j];
-        sv[r][i] = s2[(size_t)n * SB + (j >> 2)];
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < R_DN; ++r) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int i = 0; i < MAXW; ++i) {
-        const float valid = (lane + 64 * i < Kw) ? 1.0f : 0.0f;
-        const float sc = e8m0_to_f32(sv[r][i]);
-        const float2_t p0 = fp4x2_to_f32x2<0>(wv[r][i], sc);
-        const float2_t p1 = fp4x2_to_f32x2<1>(wv[r][i], sc);
-        const float2_t p2 = fp4x2_to_f32x2<2>(wv[r][i], sc);
-        const float2_t p3 = fp4x2_to_f32x2<3>(wv[r][i], sc);
-        float d = 0.0f;
-        d = __builtin_fmaf(p0[0], ha[i].x, d);
-        d = __builtin_fmaf(p0[1], ha[i].y, d);
-        d = __builtin_fmaf(p1[0], ha[i].z, d);
-        d = __builtin_fmaf(p1[1], ha[i].w, d);
-        d = __builtin_fmaf(p2[0], hb[i].x, d);
-        d = __builtin_fmaf(p2[1], hb[i].y, d);
-        d = __builtin_fmaf(p3[0], hb[i].z, d);
-        d = __builtin_fmaf(p3[1], hb[i].w, d);
-        acc = __builtin_fmaf(valid, d, acc);
-      }
-      rowv[r] = acc;
+      for (int s = 0; s < 4; ++s) c = mfma(lds_a(hl, aoff + 16 * s), fp4_codes_to_b(word_of(wd[b], s), sd), c);
     }
   }
-  const float red = wave_transpose_sum<R_DN>(rowv, lane);
-  combine_rows<false>(red, lane, e, row0, D, k, vals, addend, routed, out);
+  // D[0][j] (hi) and D[1][j] (lo) sit in lane j, registers 0 and 1
+  if (lane < 16) vals[e][half][lane] = c[0] + c[1];
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    const int n = row0 + t;
+    float total = 0.0f;
+    for (int x = 0; x < k; ++x) {
+      float y = 0.0f;
+#pragma unroll
+      for (int h = 0; h < DN_HALVES; ++h) y = y + vals[x][h][t];
+      total = total + y;
+    }
+    if (routed) routed[n] = total;
+    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(addend[n]) : total);
+  }
 }
 
 }  // namespace
@@ -223,17 +218,19 @@ size_t fp4_workspace_bytes(int D, int F, int k) {
 }
 
 int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
-                      const int32_t* slot_table, const int32_t* idx, const float* w, const RouteArgs* ra, int D,
-                      int F, int E, int k, float swiglu_limit, const uint16_t* addend, float* routed, uint16_t* out,
-                      void* workspace, size_t workspace_bytes, hipStream_t s) {
-  CACHALOT_REQUIRE(pool && layout && slot_table && x, "moe_decode_fp4: null pointer");
+                      ExpertSource src, const RouterCall* router, int D, int F, int k, float swiglu_limit,
+                      const uint16_t* addend, float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                      hipStream_t s) {
+  CACHALOT_REQUIRE(pool && layout && src.slot_table && x, "moe_decode_fp4: null pointer");
   CACHALOT_REQUIRE(routed || out, "moe_decode_fp4: no output requested");
   CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_fp4: k=%d outside 1..%d", k, KMAX);
-  CACHALOT_REQUIRE(E >= 1 && E <= 1024, "moe_decode_fp4: E=%d outside 1..1024", E);
-  CACHALOT_REQUIRE(D % 64 == 0 && D >= 64 && D <= 8192, "moe_decode_fp4: D=%d must be a multiple of 64 and <= 8192",
-                   D);
-  CACHALOT_REQUIRE(F % 32 == 0 && F >= 32 && F <= 8 * 64 * MAXW,
-                   "moe_decode_fp4: F=%d must be a multiple of 32 and <= %d", F, 8 * 64 * MAXW);
+  CACHALOT_REQUIRE(src.E >= 1 && src.E <= 1024, "moe_decode_fp4: E=%d outside 1..1024", src.E);
+  CACHALOT_REQUIRE(D % 128 == 0 && D >= 128 && D <= MAX_D, "moe_decode_fp4: D=%d must be a multiple of 128 in 128..%d",
+                   D, MAX_D);
+  CACHALOT_REQUIRE(F % 32 == 0 && F >= 64 && F <= 4096, "moe_decode_fp4: F=%d must be a multiple of 32 in 64..4096",
+                   F);
+  CACHALOT_REQUIRE(k * F <= MAX_KF, "moe_decode_fp4: k*F=%d exceeds the %d hidden values staged per workgroup",
+                   k * F, MAX_KF);
   const WsOffsets wo = ws_offsets((size_t)k * F * sizeof(float));
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "moe_decode_fp4: workspace %zu < %zu bytes", workspace_bytes, wo.total);
@@ -242,34 +239,52 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   int rc = make_layout(layout, 6, used, L, "moe_decode_fp4");
   if (rc) return rc;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  float* hidden = reinterpret_cast<float*>(ws + wo.hidden);
+  uint16_t* hidden = reinterpret_cast<uint16_t*>(ws + wo.hidden);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
-  RouteArgs none{};
-  const RouteArgs& r = ra ? *ra : none;
-  const int items = k * ((F + R_GU - 1) / R_GU);
-  const int blocks = (items + WAVES - 1) / WAVES;
-  const size_t lds = 0;
-  const bool c1 = D <= 4096;
-  if (ra) {
-    if (c1)
-      hipLaunchKernelGGL((fp4_gate_up_kernel<1, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L,
-                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
-    else
-      hipLaunchKernelGGL((fp4_gate_up_kernel<2, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L,
-                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
-  } else {
-    if (c1)
-      hipLaunchKernelGGL((fp4_gate_up_kernel<1, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L,
-                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
-    else
-      hipLaunchKernelGGL((fp4_gate_up_kernel<2, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L,
-                         slot_table, idx, w, r, D, F, E, k, swiglu_limit, hidden, ws_slots, ws_w);
+  if (router) {
+    RouteTail tail = router->tail;
+    tail.ws_slots = ws_slots;
+    tail.ws_w = ws_w;
+    tail.counter = reinterpret_cast<unsigned int*>(ws + wo.counter);
+    rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
+                              router->scores, s, &tail);
+    if (rc) return rc;
+    src.idx = nullptr;
+    src.w = nullptr;
   }
+  const int PT = D / PIECE;
+  const int nb_gu = ((PT + GU_WAVES - 1) / GU_WAVES + 3) / 4;
+  const int xi = (D / 16 + 255) / 256;
+  const dim3 grid_gu(k * (F / 16)), block_gu(64 * GU_WAVES);
+#define CACHALOT_GU(NBV, XIV)                                                                                   \
+  hipLaunchKernelGGL((fp4_gate_up_kernel<NBV, XIV>), grid_gu, block_gu, 0, s, x, pool, L, src, D, F, swiglu_limit, \
+                     hidden, ws_slots, ws_w)
+  // the smallest instantiated NB >= nb_gu (extra blocks are masked)
+  if (xi == 1) {
+    if (nb_gu <= 1) CACHALOT_GU(1, 1);
+    else if (nb_gu <= 2) CACHALOT_GU(2, 1);
+    else if (nb_gu <= 4) CACHALOT_GU(4, 1);
+    else if (nb_gu <= 6) CACHALOT_GU(6, 1);
+    else CACHALOT_GU(8, 1);
+  } else {
+    if (nb_gu <= 12) CACHALOT_GU(12, 2);
+    else CACHALOT_GU(16, 2);
+  }
+#undef CACHALOT_GU
   rc = check_launch("fp4_gate_up_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(fp4_down_kernel, dim3((D + R_DN - 1) / R_DN), dim3(64 * k), 0, s, pool, L, ws_slots, D, F, k,
-                     hidden, addend, routed, out);
+  const int PK = F / PIECE;
+  const int nb_dn = ((PK + DN_HALVES - 1) / DN_HALVES + 3) / 4;
+  const dim3 grid_dn(D / 16), block_dn(64 * k * DN_HALVES);
+#define CACHALOT_DN(NBV)                                                                                    \
+  hipLaunchKernelGGL((fp4_down_kernel<NBV>), grid_dn, block_dn, 0, s, pool, L, ws_slots, D, F, k, hidden, addend, \
+                     routed, out)
+  if (nb_dn <= 4) CACHALOT_DN(4);
+  else if (nb_dn <= 8) CACHALOT_DN(8);
+  else if (nb_dn <= 12) CACHALOT_DN(12);
+  else CACHALOT_DN(16);
+#undef CACHALOT_DN
   return check_launch("fp4_down_kernel");
 }
 
@@ -287,8 +302,9 @@ extern "C" int cachalot_moe_decode_fp4(const uint16_t* x, const uint8_t* pool,
                                        void* workspace, size_t workspace_bytes, cachalot_stream_t stream) {
   using namespace cachalot;
   CACHALOT_REQUIRE(idx && w, "moe_decode_fp4: null pointer");
-  return launch_fp4_decode(x, pool, layout, slot_table, idx, w, nullptr, D, F, E, k, swiglu_limit, addend, routed,
-                           out, workspace, workspace_bytes, (hipStream_t)stream);
+  decode::ExpertSource src{slot_table, idx, w, E};
+  return launch_fp4_decode(x, pool, layout, src, nullptr, D, F, k, swiglu_limit, addend, routed, out, workspace,
+                           workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
@@ -307,10 +323,10 @@ extern "C" int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* 
                    "moe_layer_decode_fp4: unknown order %d", order);
   CACHALOT_REQUIRE(gate_temp != 0.0f, "moe_layer_decode_fp4: gate_temp must be non-zero");
   CACHALOT_REQUIRE(k >= 1 && k <= E && E <= 1024, "moe_layer_decode_fp4: invalid topk=%d for %d experts", k, E);
-  hipStream_t s = (hipStream_t)stream;
-  int rc = launch_router_scores(x, gate_weight, 1, D, E, gate_temp, score_fn, scores, s);
-  if (rc) return rc;
-  RouteArgs ra{scores, gate_bias, E, order, norm, route_scale, idx_out, w_out};
-  return launch_fp4_decode(x, pool, layout, slot_table, nullptr, nullptr, &ra, D, F, E, k, swiglu_limit, addend,
-                           routed, out, workspace, workspace_bytes, s);
+  decode::ExpertSource src{slot_table, nullptr, nullptr, E};
+  RouterCall rt{gate_weight, score_fn, gate_temp, scores, {}};
+  rt.tail = decode::RouteTail{gate_bias, slot_table, idx_out, w_out, nullptr, nullptr, nullptr, E, k, order, norm,
+                              route_scale};
+  return launch_fp4_decode(x, pool, layout, src, &rt, D, F, k, swiglu_limit, addend, routed, out, workspace,
+                           workspace_bytes, (hipStream_t)stream);
 }

@@ -1,297 +1,321 @@
-// Decode (one token) over a 2-bit affine g128 expert bank.
+// Decode (one token) over a 2-bit affine g128 expert bank, on the matrix cores.
 //
 // Reference: src/cachalot/model/expert_affine.py:65-81 (rounding points),
 // :117-152 (topk_core: experts summed in route order), moe_layer_metal.py:
 // 93-130 (the traced block), mx.quantized_matmul's group formula
 // s * sum(x q) + b * sum(x) (MLX qdot, as copied at minimax/codes_qmv.py:86-100).
 //
-//   q2_gate_up_kernel  one wave = R_GU rows of one expert.  Prologue per
-//                      workgroup: (optionally) the top-k of the router scores,
-//                      then the k slot lookups, into LDS.  Every weight,
-//                      scale and bias load of the wave is issued before any
-//                      arithmetic, with clamped addresses instead of branches,
-//                      so a wave costs one memory round trip.  Lane l owns one
-//                      64-code uint4 chunk per row (K = 4096: the whole row is
-//                      one coalesced 1 KiB wave load per matrix).  Codes are
-//                      spread into FP4 nibbles (code q in 0..3 is the E2M1
-//                      encoding of q/2), converted to bf16 pairs by the gfx950
-//                      converter with scale 2, and dotted with pre-paired bf16
-//                      activations (v_dot2c_f32_bf16: exact products, fp32 sums).
-//                      Epilogue: bf16(g), bf16(u), clamp,
-//                      h = bf16(silu(g) * u * w_e), written in the pair order
-//                      the down kernel consumes.
-//   q2_down_kernel     one workgroup = RD rows of W2, k waves (wave e = expert
-//                      e); lane l owns the 64-code chunk l of a row (one
-//                      quantisation group: a 16-byte load, one scale, one bias;
-//                      K = 2880 -> 45 chunks).  Each row value is rounded to
-//                      bf16 (the reference's per-expert cast), handed over in
-//                      LDS and summed in route order, + addend, -> fp32 / bf16.
+//   q2_gate_up_kernel  one workgroup = one expert x one 16-row tile of W1 and
+//                      W3; its four waves split K into quarters.  Every load is
+//                      issued before any arithmetic: the lane's codes (lane
+//                      group kg of block b takes group 4b + kg of the wave's
+//                      quarter, so one load instruction covers whole 128-byte
+//                      lines), the tile's scales and biases (one 16-byte load
+//                      per thread, staged in LDS) and the token's activations
+//                      (staged in LDS in MFMA order with their group sums).
+//                      Then 16 v_mfma_f32_16x16x32_bf16 steps per group and
+//                      matrix, gate and up sharing each A read; the group
+//                      formula is applied per group.  Quarters meet in LDS;
+//                      epilogue bf16(g), bf16(u), clamp, h = bf16(silu(g) * u *
+//                      w_e), stored group-major in MFMA order.
+//   q2_down_kernel     one workgroup = one 16-row tile of W2 for all k experts:
+//                      2k waves, wave = (expert, K half).  The k hidden vectors
+//                      and the tile's scales are staged in LDS; each expert's row
+//                      value is rounded to bf16 (the reference's per-expert
+//                      cast) and the experts are summed in route order,
+//                      + addend, -> fp32 / bf16.
 #include "decode_common.h"
+#include "mfma_tile.h"
 #include "router_launch.h"
-#include "topk.h"
 
 namespace cachalot {
 namespace {
 
 using namespace decode;
-constexpr int R_GU = 4;     // rows per wave, gate/up
-#ifndef Q2_DOWN_ROWS
-#define Q2_DOWN_ROWS 8      // W2 rows per down workgroup
-#endif
+using namespace tile;
 
-// Pair layout of a 16-value word: E_b = (v[4b], v[4b+2]), O_b = (v[4b+1], v[4b+3]);
-// memory order E_0..E_3, O_0..O_3.  Position of value i (0..15) in uint16 units:
-__device__ __forceinline__ int pair_pos(int i) {
-  const int b = i >> 2, r = i & 3;
-  return ((r & 1) ? 8 : 0) + 2 * b + (r >> 1);
-}
+constexpr int GU_WAVES = 4;             // K quarters per gate/up workgroup
+constexpr int DN_HALVES = 2;            // K halves per expert in the down workgroup
+constexpr int MAX_D_GROUPS = 64;        // D <= 8192
+constexpr int MAX_F_GROUPS = 32;        // F <= 4096
+constexpr int GU_LDS_ZERO = MAX_D_GROUPS * LDS_GROUP_BYTES;
+constexpr int DN_LDS_ZERO = KMAX * MAX_F_GROUPS * LDS_GROUP_BYTES;
 
-// sum_i x_i * q_i over the 16 codes of word w, x pre-paired (xe = E pairs, xo = O pairs).
-__device__ __forceinline__ float q2_word_dot(uint32_t w, const uint32_t* xe, const uint32_t* xo, float acc) {
-  const uint32_t ev = w & 0x33333333u;
-  const uint32_t od = (w >> 2) & 0x33333333u;
-  acc = dot2_bf16(fp4x2_to_bf16x2<0>(ev, 2.0f), xe[0], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<0>(od, 2.0f), xo[0], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<1>(ev, 2.0f), xe[1], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<1>(od, 2.0f), xo[1], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<2>(ev, 2.0f), xe[2], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<2>(od, 2.0f), xo[2], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<3>(ev, 2.0f), xe[3], acc);
-  acc = dot2_bf16(fp4x2_to_bf16x2<3>(od, 2.0f), xo[3], acc);
-  return acc;
-}
+// Hidden vector of one expert in the workspace: ceil(F / 128) groups, each 128 bf16
+// in MFMA order padded to LDS_GROUP_BYTES -- the layout the down kernel stages
+// into LDS as is.  Elements from F up to the group boundary are zero.
+__host__ __device__ inline int hidden_stride(int F) { return (F + GROUP - 1) / GROUP * (LDS_GROUP_BYTES / 2); }
+__device__ __forceinline__ int hidden_index(int n) { return (n >> 7) * (LDS_GROUP_BYTES / 2) + mfma_index(n & 127); }
 
-// (v0,v1),(v2,v3) -> E = (v0,v2), O = (v1,v3)
-__device__ __forceinline__ void make_pairs(uint32_t a, uint32_t b, uint32_t& e, uint32_t& o) {
-  e = (a & 0xffffu) | (b << 16);
-  o = (a >> 16) | (b & 0xffff0000u);
-}
-
-constexpr uint32_t BF16_ONES = 0x3f803f80u;
-
-// grid.x = ceil(k * ceil(F / R_GU) / WAVES); C = 64-code chunks per lane (D <= 4096 * C)
-template <int C, bool FUSE>
-__global__ void __launch_bounds__(64 * WAVES) q2_gate_up_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L,
-    const int32_t* __restrict__ slot_table, const int32_t* __restrict__ idx, const float* __restrict__ wts,
-    RouteArgs ra, int D, int F, int E, int k, int group, float limit, uint16_t* __restrict__ hp,
-    int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
-  __shared__ int s_slot[KMAX];
-  __shared__ float s_w[KMAX];
-  __shared__ int top_i[KMAX];
-  __shared__ float top_v[KMAX];
-  __shared__ float lds_v[16];
-  __shared__ int lds_i[16];
-  const int lane = threadIdx.x & 63;
-  const int NC = D / 64;
-
-  // activation chunk loads first: they do not depend on the routing
-  uint4 xa[C][8];
+// 16 MFMA steps over one 128-code group and two matrices sharing A.
+__device__ __forceinline__ void group_steps2(const uint8_t* lds, uint32_t aoff, const uint4 (&wa)[2],
+                                             const uint4 (&wb)[2], f32x4_t& ca, f32x4_t& cb) {
+  ca = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  cb = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const int c = min(lane + 64 * i, NC - 1);
-    const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)c * 64);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) xa[i][q] = xp[q];
+  for (int s = 0; s < 16; ++s) {
+    const bf16x8_t a = lds_a(lds, aoff + 16 * s);
+    const uint32_t w0 = word_of(wa[s >> 3], (s >> 1) & 3);
+    const uint32_t w1 = word_of(wb[s >> 3], (s >> 1) & 3);
+    if (s & 1) {
+      ca = mfma(a, q2_codes_to_b<1>(w0), ca);
+      cb = mfma(a, q2_codes_to_b<1>(w1), cb);
+    } else {
+      ca = mfma(a, q2_codes_to_b<0>(w0), ca);
+      cb = mfma(a, q2_codes_to_b<0>(w1), cb);
+    }
   }
+}
 
-  expert_prologue<FUSE>(slot_table, idx, wts, E, k, ra, s_slot, s_w, top_i, top_v, lds_v, lds_i, ws_slots, ws_w);
+__device__ __forceinline__ f32x4_t group_steps1(const uint8_t* lds, uint32_t aoff, const uint4 (&wa)[2]) {
+  f32x4_t ca = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const bf16x8_t a = lds_a(lds, aoff + 16 * s);
+    const uint32_t w0 = word_of(wa[s >> 3], (s >> 1) & 3);
+    if (s & 1) ca = mfma(a, q2_codes_to_b<1>(w0), ca);
+    else ca = mfma(a, q2_codes_to_b<0>(w0), ca);
+  }
+  return ca;
+}
 
-  const int RB = (F + R_GU - 1) / R_GU;
-  const int item = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  if (item >= k * RB) return;
-  const int e = item / RB;
-  const int row0 = (item % RB) * R_GU;
-  const int Fw = F / 16;
-  uint16_t* hout = hp + (size_t)e * Fw * 16;
-  const int slot = s_slot[e];
-  if (slot < 0) {
-    if (lane < R_GU && row0 + lane < F) hout[((row0 + lane) >> 4) * 16 + pair_pos((row0 + lane) & 15)] = 0;
+// Lane group kg of block b of a wave owning groups [first, first + GW) takes
+// group first + 4b + kg (valid when 4b + kg < GW and below `groups`).
+template <int NB>
+__device__ __forceinline__ void lane_groups(int first, int GW, int groups, int kg, int (&gi)[NB], bool (&gv)[NB]) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int within = 4 * b + kg;
+    const int G = first + within;
+    gv[b] = within < GW && G < groups;
+    gi[b] = min(G, groups - 1);
+  }
+}
+
+// grid.x = k * F / 16.  NB = ceil(ceil(D/128 / 4) / 4) groups per lane group;
+// XI = ceil(D / 4096) activation items (and scale pieces) per thread.
+template <int NB, int XI>
+__global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L, ExpertSource src, int D, int F,
+    float limit, uint16_t* __restrict__ hp, int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
+  __shared__ __align__(16) uint8_t xm[GU_LDS_ZERO + LDS_ZERO_BYTES];
+  __shared__ __align__(16) uint16_t sc[4 * 16 * MAX_D_GROUPS];   // s1, b1, s3, b3 of the tile's rows
+  __shared__ float xs[MAX_D_GROUPS];
+  __shared__ float red[GU_WAVES][2][16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int GT = D / GROUP;
+  const int tiles = F / 16;
+  const int e = blockIdx.x / tiles;
+  const int tile = blockIdx.x - e * tiles;
+  const int row0 = tile * 16;
+  int slot;
+  float wexp;
+  resolve_expert(src, e, tile == 0, ws_slots, ws_w, slot, wexp);
+  uint16_t* hout = hp + (size_t)e * hidden_stride(F);
+  const int tail = (F + GROUP - 1) / GROUP * GROUP - F;
+  if (tile == 0 && (int)threadIdx.x < tail) hout[hidden_index(F + threadIdx.x)] = 0;
+  if (slot < 0) {   // the expert has no slot: its hidden rows are zero
+    if (threadIdx.x < 16) hout[hidden_index(row0 + threadIdx.x)] = 0;
     return;
   }
   const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
-  const int G = D / group;
-  const uint4* w1 = reinterpret_cast<const uint4*>(base + L.off[0]);
-  const uint16_t* s1 = reinterpret_cast<const uint16_t*>(base + L.off[1]);
-  const uint16_t* b1 = reinterpret_cast<const uint16_t*>(base + L.off[2]);
-  const uint4* w3 = reinterpret_cast<const uint4*>(base + L.off[6]);
-  const uint16_t* s3 = reinterpret_cast<const uint16_t*>(base + L.off[7]);
-  const uint16_t* b3 = reinterpret_cast<const uint16_t*>(base + L.off[8]);
+  const int j = lane & 15, kg = lane >> 4;
+  const int row = row0 + j;
+  int gi[NB];
+  bool gv[NB];
+  const int GW = (GT + GU_WAVES - 1) / GU_WAVES;
+  lane_groups<NB>(wave * GW, GW, GT, kg, gi, gv);
 
-  // every weight / scale / bias load of this wave, issued together
-  uint4 vg[R_GU][C], vu[R_GU][C];
-  uint16_t sg[R_GU][C], bg[R_GU][C], su[R_GU][C], bu[R_GU][C];
+  // 1. the lane's codes (both matrices)
+  uint4 wg[NB][2], wu[NB][2];
+  {
+    const uint4* r1 = reinterpret_cast<const uint4*>(base + L.off[0]) + (size_t)row * GT * 2;
+    const uint4* r3 = reinterpret_cast<const uint4*>(base + L.off[6]) + (size_t)row * GT * 2;
 #pragma unroll
-  for (int r = 0; r < R_GU; ++r) {
-    const int n = min(row0 + r, F - 1);
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-      const int c = min(lane + 64 * i, NC - 1);
-      const int g = (c * 64) / group;
-      vg[r][i] = w1[(size_t)n * NC + c];
-      vu[r][i] = w3[(size_t)n * NC + c];
-      sg[r][i] = s1[(size_t)n * G + g];
-      bg[r][i] = b1[(size_t)n * G + g];
-      su[r][i] = s3[(size_t)n * G + g];
-      bu[r][i] = b3[(size_t)n * G + g];
+    for (int b = 0; b < NB; ++b) {
+      wg[b][0] = r1[2 * gi[b]];
+      wg[b][1] = r1[2 * gi[b] + 1];
+      wu[b][0] = r3[2 * gi[b]];
+      wu[b][1] = r3[2 * gi[b] + 1];
     }
   }
-  // keep every load above this point in flight before any arithmetic
+  // 2. the tile's scales and biases (4 tensors x 16 rows x GT bf16, each a contiguous run) into LDS
+  {
+    const int run = 32 * GT;
+    const int64_t toff[4] = {L.off[1], L.off[2], L.off[7], L.off[8]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      dma_to_lds(base + toff[q] + (int64_t)row0 * GT * 2, reinterpret_cast<uint8_t*>(sc) + q * run, run,
+                 (wave + q) & 3, GU_WAVES, lane);
+  }
+  // 3. the activations: 16 values per item
+  uint4 xa[XI][2];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int t = min((int)threadIdx.x + 256 * i, D / 16 - 1);
+    const uint4* p = reinterpret_cast<const uint4*>(x + (size_t)t * 16);
+    xa[i][0] = p[0];
+    xa[i][1] = p[1];
+  }
   __builtin_amdgcn_sched_barrier(0);
 
-  // activation pairs and per-chunk sums
-  uint32_t xe[C][4][4], xo[C][4][4];
-  float xs[C];
 #pragma unroll
-  for (int i = 0; i < C; ++i) {
-    const bool valid = lane + 64 * i < NC;
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 a = xa[i][2 * j];
-      const uint4 b = xa[i][2 * j + 1];
-      make_pairs(a.x, a.y, xe[i][j][0], xo[i][j][0]);
-      make_pairs(a.z, a.w, xe[i][j][1], xo[i][j][1]);
-      make_pairs(b.x, b.y, xe[i][j][2], xo[i][j][2]);
-      make_pairs(b.z, b.w, xe[i][j][3], xo[i][j][3]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (!valid) xe[i][j][q] = xo[i][j][q] = 0u;
-        sum = dot2_bf16(xe[i][j][q], BF16_ONES, sum);
-        sum = dot2_bf16(xo[i][j][q], BF16_ONES, sum);
-      }
+  for (int i = 0; i < XI; ++i) {
+    const int t = threadIdx.x + 256 * i;
+    uint4 lo, hi;
+    pairs_mfma(xa[i][0].x, xa[i][0].y, lo.x, lo.y);
+    pairs_mfma(xa[i][0].z, xa[i][0].w, lo.z, lo.w);
+    pairs_mfma(xa[i][1].x, xa[i][1].y, hi.x, hi.y);
+    pairs_mfma(xa[i][1].z, xa[i][1].w, hi.z, hi.w);
+    const float sum = sum8_lanes(sum_bf16x8(lo) + sum_bf16x8(hi));
+    if (t < D / 16) {
+      uint4* d = reinterpret_cast<uint4*>(xm + (t >> 3) * LDS_GROUP_BYTES + (t & 7) * 32);
+      d[0] = lo;
+      d[1] = hi;
+      if ((t & 7) == 0) xs[t >> 3] = sum;
     }
-    xs[i] = sum;
   }
+  if (threadIdx.x < LDS_ZERO_BYTES / 16)
+    reinterpret_cast<uint4*>(xm + GU_LDS_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+  wait_vmem();
+  __syncthreads();
 
-  float part[2 * R_GU];
+  const uint16_t* s1 = sc;
+  const uint16_t* b1 = sc + 16 * GT;
+  const uint16_t* s3 = sc + 32 * GT;
+  const uint16_t* b3 = sc + 48 * GT;
+  float accg = 0.0f, accu = 0.0f;
 #pragma unroll
-  for (int r = 0; r < R_GU; ++r) {
-    float pg = 0.0f, pu = 0.0f;
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-      float dg = 0.0f, du = 0.0f;
-      dg = q2_word_dot(vg[r][i].x, xe[i][0], xo[i][0], dg);
-      du = q2_word_dot(vu[r][i].x, xe[i][0], xo[i][0], du);
-      dg = q2_word_dot(vg[r][i].y, xe[i][1], xo[i][1], dg);
-      du = q2_word_dot(vu[r][i].y, xe[i][1], xo[i][1], du);
-      dg = q2_word_dot(vg[r][i].z, xe[i][2], xo[i][2], dg);
-      du = q2_word_dot(vu[r][i].z, xe[i][2], xo[i][2], du);
-      dg = q2_word_dot(vg[r][i].w, xe[i][3], xo[i][3], dg);
-      du = q2_word_dot(vu[r][i].w, xe[i][3], xo[i][3], du);
-      pg = pg + (bf16_to_f32(sg[r][i]) * dg + bf16_to_f32(bg[r][i]) * xs[i]);
-      pu = pu + (bf16_to_f32(su[r][i]) * du + bf16_to_f32(bu[r][i]) * xs[i]);
-    }
-    part[2 * r] = pg;
-    part[2 * r + 1] = pu;
+  for (int b = 0; b < NB; ++b) {
+    const uint32_t aoff = (gv[b] && j == 4 * kg) ? (uint32_t)gi[b] * LDS_GROUP_BYTES : (uint32_t)GU_LDS_ZERO;
+    f32x4_t cg, cu;
+    group_steps2(xm, aoff, wg[b], wu[b], cg, cu);
+    const float gs = gv[b] ? xs[gi[b]] : 0.0f;
+    const int si = j * GT + gi[b];
+    accg = accg + (bf16_to_f32(s1[si]) * cg[0] + bf16_to_f32(b1[si]) * gs);
+    accu = accu + (bf16_to_f32(s3[si]) * cu[0] + bf16_to_f32(b3[si]) * gs);
   }
-  // value 2r+v ends in lanes [8(2r+v), 8(2r+v)+8)
-  const float red = wave_transpose_sum<2 * R_GU>(part, lane);
-  const float up = __shfl(red, lane + 8, 64);
-  if ((lane & 15) == 0) {
-    const int n = row0 + (lane >> 4);
-    if (n < F) {
-      float g = round_bf16(red);
-      float u = round_bf16(up);
-      if (limit > 0.0f) {
-        u = fminf(fmaxf(u, -limit), limit);
-        g = fminf(g, limit);
-      }
-      const float h = (silu_f32(g) * u) * s_w[e];
-      hout[(n >> 4) * 16 + pair_pos(n & 15)] = f32_to_bf16(h);
+  accg = sum_lane_groups(accg);
+  accu = sum_lane_groups(accu);
+  if (lane < 16) {
+    red[wave][0][lane] = accg;
+    red[wave][1][lane] = accu;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    float g = 0.0f, u = 0.0f;
+#pragma unroll
+    for (int w = 0; w < GU_WAVES; ++w) {
+      g = g + red[w][0][t];
+      u = u + red[w][1][t];
     }
+    g = round_bf16(g);
+    u = round_bf16(u);
+    if (limit > 0.0f) {
+      u = fminf(fmaxf(u, -limit), limit);
+      g = fminf(g, limit);
+    }
+    const float h = (silu_f32(g) * u) * wexp;
+    hout[hidden_index(row0 + t)] = f32_to_bf16(h);
   }
 }
 
-// grid.x = ceil(D / RD); one workgroup = k waves, wave e = expert e, RD rows.
-// Lane l owns the 64-code chunk l of a row (words 4l .. 4l+3, one quantisation
-// group): one 16-byte weight load, one scale and one bias per row; lanes past
-// the row's last chunk (K = 2880: 45 chunks) only take part in the reductions.
-// The expert's hidden pairs for the lane's chunk are loaded once and reused for
-// all RD rows.
-template <int RD>
-__global__ void __launch_bounds__(64 * KMAX) q2_down_kernel(
+// grid.x = D / 16; block = 64 * k * DN_HALVES threads.  NB = ceil(GK / 8) with
+// GK = ceil(F / 128) groups per lane group.
+template <int NB>
+__global__ void __launch_bounds__(64 * KMAX * DN_HALVES) q2_down_kernel(
     const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
-    int group, const uint16_t* __restrict__ hp, const uint16_t* __restrict__ addend, float* __restrict__ routed,
+    const uint16_t* __restrict__ hp, const uint16_t* __restrict__ addend, float* __restrict__ routed,
     uint16_t* __restrict__ out) {
-  __shared__ float vals[KMAX][RD];
+  __shared__ __align__(16) uint8_t hm[DN_LDS_ZERO + LDS_ZERO_BYTES];
+  __shared__ __align__(16) uint16_t sc[KMAX * 2 * 16 * MAX_F_GROUPS];   // per expert: s2, b2 of the tile's rows
+  __shared__ float hsum[KMAX * MAX_F_GROUPS];
+  __shared__ float vals[KMAX][DN_HALVES][16];
   const int lane = threadIdx.x & 63;
-  const int e = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * RD;
-  const int Kw = F / 16;                   // valid words per row
-  const int NCH = (Kw + 3) / 4;            // 64-code chunks per row (the last may be partial)
-  const int G = (F + group - 1) / group;   // groups per row (the last may be partial)
-  const int stride = G * group / 16;       // stored words per row
-  const int c = min(lane, NCH - 1);
-  const bool active = lane < NCH;
-  const int g = (c * 64) / group;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int GK = (F + GROUP - 1) / GROUP;   // groups per W2 row (the last may be partial)
+  const int e = wave / DN_HALVES;
+  const int half = wave - e * DN_HALVES;
+  const int row0 = blockIdx.x * 16;
+  const int j = lane & 15, kg = lane >> 4;
   const int slot = ws_slots[e];
+  const int GW = (GK + DN_HALVES - 1) / DN_HALVES;
+  int gi[NB];
+  bool gv[NB];
+  lane_groups<NB>(half * GW, GW, GK, kg, gi, gv);
 
-  float rowv[RD];
-#pragma unroll
-  for (int r = 0; r < RD; ++r) rowv[r] = 0.0f;
+  // 1. the lane's codes
+  uint4 wd[NB][2];
   if (slot >= 0) {
-    const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
-    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(base + L.off[3]);
-    const uint16_t* s2 = reinterpret_cast<const uint16_t*>(base + L.off[4]);
-    const uint16_t* b2 = reinterpret_cast<const uint16_t*>(base + L.off[5]);
-    const uint4* hpe = reinterpret_cast<const uint4*>(hp + (size_t)e * Kw * 16);
-    uint4 hv[8];
+    const uint4* r2 =
+        reinterpret_cast<const uint4*>(pool + (int64_t)slot * L.record_bytes + L.off[3]) + (size_t)(row0 + j) * GK * 2;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int j = min(4 * c + q, Kw - 1);
-      hv[2 * q] = hpe[2 * j];
-      hv[2 * q + 1] = hpe[2 * j + 1];
-    }
-    uint4 wv[RD];
-    uint16_t sv[RD], bv[RD];
-#pragma unroll
-    for (int r = 0; r < RD; ++r) {
-      const int n = min(row0 + r, D - 1);
-      // the chunk's words: 4 whole words unless the row ends inside it (then the
-      // missing words are padding codes, multiplied by zeroed hidden pairs below)
-      wv[r] = *reinterpret_cast<const uint4*>(w2 + (size_t)n * stride + 4 * c);
-      sv[r] = s2[(size_t)n * G + g];
-      bv[r] = b2[(size_t)n * G + g];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t he[4][4], ho[4][4];
-    float hs = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const bool valid = active && (4 * c + q < Kw);
-      he[q][0] = valid ? hv[2 * q].x : 0u; he[q][1] = valid ? hv[2 * q].y : 0u;
-      he[q][2] = valid ? hv[2 * q].z : 0u; he[q][3] = valid ? hv[2 * q].w : 0u;
-      ho[q][0] = valid ? hv[2 * q + 1].x : 0u; ho[q][1] = valid ? hv[2 * q + 1].y : 0u;
-      ho[q][2] = valid ? hv[2 * q + 1].z : 0u; ho[q][3] = valid ? hv[2 * q + 1].w : 0u;
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        hs = dot2_bf16(he[q][p], BF16_ONES, hs);
-        hs = dot2_bf16(ho[q][p], BF16_ONES, hs);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < RD; ++r) {
-      float d = 0.0f;
-      d = q2_word_dot(wv[r].x, he[0], ho[0], d);
-      d = q2_word_dot(wv[r].y, he[1], ho[1], d);
-      d = q2_word_dot(wv[r].z, he[2], ho[2], d);
-      d = q2_word_dot(wv[r].w, he[3], ho[3], d);
-      rowv[r] = bf16_to_f32(sv[r]) * d + bf16_to_f32(bv[r]) * hs;
+    for (int b = 0; b < NB; ++b) {
+      wd[b][0] = r2[2 * gi[b]];
+      wd[b][1] = r2[2 * gi[b] + 1];
     }
   }
-  // row sums (row r ends in lanes [r * 64/RD, (r+1) * 64/RD)); the wave hands its
-  // expert's bf16-rounded rows to LDS
-  const float red = wave_transpose_sum<RD>(rowv, lane);
-  if ((lane & (64 / RD - 1)) == 0) vals[e][lane / (64 / RD)] = round_bf16(red);
+  // 2. the hidden vectors (already in LDS layout) and, per expert, the tile's
+  //    scales and biases (two contiguous runs of 16 rows x GK bf16) into LDS
+  dma_to_lds(hp, hm, k * GK * LDS_GROUP_BYTES, wave, nwaves, lane);
+  {
+    const int run = 32 * GK;
+    for (int r = wave; r < 2 * k; r += nwaves) {
+      const int re = r >> 1;
+      const int ps = max(ws_slots[re], 0);   // a missing expert's rows are never used
+      dma_to_lds(pool + (int64_t)ps * L.record_bytes + ((r & 1) ? L.off[5] : L.off[4]) + (int64_t)row0 * GK * 2,
+                 reinterpret_cast<uint8_t*>(sc) + r * run, run, 0, 1, lane);
+    }
+  }
+  if (threadIdx.x < LDS_ZERO_BYTES / 16)
+    reinterpret_cast<uint4*>(hm + DN_LDS_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+  wait_vmem();
   __syncthreads();
-  const int t = threadIdx.x;
-  if (t < RD && row0 + t < D) {
+  // group sums of the hidden vectors: 16 chunks of 8 values per group
+  {
+    const int chunks = k * GK * 16;
+    for (int c0 = 0; c0 < chunks; c0 += blockDim.x) {
+      const int c = c0 + threadIdx.x;
+      const int cc = min(c, chunks - 1);
+      const uint4 v = *reinterpret_cast<const uint4*>(hm + (cc >> 4) * LDS_GROUP_BYTES + (cc & 15) * 16);
+      const float sum = row16_sum(sum_bf16x8(v));
+      if (c < chunks && (c & 15) == 0) hsum[c >> 4] = sum;
+    }
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  if (slot >= 0) {
+    const uint16_t* s2 = sc + e * 32 * GK;
+    const uint16_t* b2 = s2 + 16 * GK;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const uint32_t aoff =
+          (gv[b] && j == 4 * kg) ? (uint32_t)(e * GK + gi[b]) * LDS_GROUP_BYTES : (uint32_t)DN_LDS_ZERO;
+      const f32x4_t c = group_steps1(hm, aoff, wd[b]);
+      const float gs = gv[b] ? hsum[e * GK + gi[b]] : 0.0f;
+      const int si = j * GK + gi[b];
+      acc = acc + (bf16_to_f32(s2[si]) * c[0] + bf16_to_f32(b2[si]) * gs);
+    }
+  }
+  acc = sum_lane_groups(acc);
+  if (lane < 16) vals[e][half][lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
     const int n = row0 + t;
-    float acc = 0.0f;
-    for (int j = 0; j < k; ++j) acc = acc + vals[j][t];
-    if (routed) routed[n] = acc;
-    if (out) out[n] = f32_to_bf16(addend ? acc + bf16_to_f32(addend[n]) : acc);
+    float total = 0.0f;
+    for (int x = 0; x < k; ++x) {
+      float y = 0.0f;
+#pragma unroll
+      for (int h = 0; h < DN_HALVES; ++h) y = y + vals[x][h][t];
+      total = total + round_bf16(y);
+    }
+    if (routed) routed[n] = total;
+    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(addend[n]) : total);
   }
 }
 
@@ -299,23 +323,26 @@ __global__ void __launch_bounds__(64 * KMAX) q2_down_kernel(
 
 size_t q2_workspace_bytes(int D, int F, int k) {
   (void)D;
-  return ws_offsets((size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t)).total;
+  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total;
 }
 
+// Validates, then launches [router + top-k tail], gate/up and down on stream s.
+// With `router` the experts come from the router tail, else from src.idx / src.w.
+
 int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
-                     const int32_t* slot_table, const int32_t* idx, const float* w, const RouteArgs* ra, int D,
-                     int F, int E, int k, int group, float swiglu_limit, const uint16_t* addend, float* routed,
-                     uint16_t* out, void* workspace, size_t workspace_bytes, hipStream_t s) {
-  CACHALOT_REQUIRE(pool && layout && slot_table && x, "moe_decode_q2: null pointer");
+                     ExpertSource src, const RouterCall* router, int D, int F, int k, int group, float swiglu_limit,
+                     const uint16_t* addend, float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                     hipStream_t s) {
+  CACHALOT_REQUIRE(pool && layout && src.slot_table && x, "moe_decode_q2: null pointer");
   CACHALOT_REQUIRE(routed || out, "moe_decode_q2: no output requested");
   CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_q2: k=%d outside 1..%d", k, KMAX);
-  CACHALOT_REQUIRE(E >= 1 && E <= 1024, "moe_decode_q2: E=%d outside 1..1024", E);
-  CACHALOT_REQUIRE(group == 64 || group == 128, "moe_decode_q2: group_size %d (64 or 128)", group);
-  CACHALOT_REQUIRE(D % group == 0 && D >= 64 && D <= 8192,
-                   "moe_decode_q2: D=%d must be a multiple of group %d and <= 8192", D, group);
-  CACHALOT_REQUIRE(F % 16 == 0 && F >= 64 && F <= 4096, "moe_decode_q2: F=%d must be a multiple of 16 in 64..4096",
-                   F);
-  const WsOffsets wo = ws_offsets((size_t)k * ((F + 15) / 16) * 16 * sizeof(uint16_t));
+  CACHALOT_REQUIRE(src.E >= 1 && src.E <= 1024, "moe_decode_q2: E=%d outside 1..1024", src.E);
+  CACHALOT_REQUIRE(group == GROUP, "moe_decode_q2: group_size %d (the bank format uses 128)", group);
+  CACHALOT_REQUIRE(D % GROUP == 0 && D >= GROUP && D <= GROUP * MAX_D_GROUPS,
+                   "moe_decode_q2: D=%d must be a multiple of 128 in 128..8192", D);
+  CACHALOT_REQUIRE(F % 16 == 0 && F >= 64 && F <= GROUP * MAX_F_GROUPS,
+                   "moe_decode_q2: F=%d must be a multiple of 16 in 64..4096", F);
+  const WsOffsets wo = ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t));
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, wo.total);
   Layout L;
@@ -326,31 +353,51 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   uint16_t* hp = reinterpret_cast<uint16_t*>(ws + wo.hidden);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
-  RouteArgs none{};
-  const RouteArgs& r = ra ? *ra : none;
-  const int items = k * ((F + R_GU - 1) / R_GU);
-  const int blocks = (items + WAVES - 1) / WAVES;
-  const size_t lds = 0;
-  const bool c1 = D <= 4096;
-  if (ra) {
-    if (c1)
-      hipLaunchKernelGGL((q2_gate_up_kernel<1, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L, slot_table,
-                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
-    else
-      hipLaunchKernelGGL((q2_gate_up_kernel<2, true>), dim3(blocks), dim3(64 * WAVES), lds, s, x, pool, L, slot_table,
-                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
-  } else {
-    if (c1)
-      hipLaunchKernelGGL((q2_gate_up_kernel<1, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L, slot_table,
-                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
-    else
-      hipLaunchKernelGGL((q2_gate_up_kernel<2, false>), dim3(blocks), dim3(64 * WAVES), 0, s, x, pool, L, slot_table,
-                         idx, w, r, D, F, E, k, group, swiglu_limit, hp, ws_slots, ws_w);
+  if (router) {
+    RouteTail tail = router->tail;
+    tail.ws_slots = ws_slots;
+    tail.ws_w = ws_w;
+    tail.counter = reinterpret_cast<unsigned int*>(ws + wo.counter);
+    rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
+                              router->scores, s, &tail);
+    if (rc) return rc;
+    src.idx = nullptr;
+    src.w = nullptr;
   }
+  const int GT = D / GROUP;
+  const int nb_gu = ((GT + GU_WAVES - 1) / GU_WAVES + 3) / 4;
+  const int xi = (D / 16 + 255) / 256;
+  const dim3 grid_gu(k * (F / 16)), block_gu(64 * GU_WAVES);
+#define CACHALOT_GU(NBV, XIV)                                                                                  \
+  hipLaunchKernelGGL((q2_gate_up_kernel<NBV, XIV>), grid_gu, block_gu, 0, s, x, pool, L, src, D, F, swiglu_limit, \
+                     hp, ws_slots, ws_w)
+  if (xi == 1) {
+    switch (nb_gu) {
+      case 1: CACHALOT_GU(1, 1); break;
+      default: CACHALOT_GU(2, 1); break;
+    }
+  } else {
+    switch (nb_gu) {
+      case 3: CACHALOT_GU(3, 2); break;
+      default: CACHALOT_GU(4, 2); break;
+    }
+  }
+#undef CACHALOT_GU
   rc = check_launch("q2_gate_up_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL((q2_down_kernel<Q2_DOWN_ROWS>), dim3((D + Q2_DOWN_ROWS - 1) / Q2_DOWN_ROWS), dim3(64 * k), 0, s,
-                     pool, L, ws_slots, D, F, k, group, hp, addend, routed, out);
+  const int GK = (F + GROUP - 1) / GROUP;
+  const int nb_dn = (GK + 7) / 8;
+  const dim3 grid_dn(D / 16), block_dn(64 * k * DN_HALVES);
+#define CACHALOT_DN(NBV)                                                                                   \
+  hipLaunchKernelGGL((q2_down_kernel<NBV>), grid_dn, block_dn, 0, s, pool, L, ws_slots, D, F, k, hp, addend, \
+                     routed, out)
+  switch (nb_dn) {
+    case 1: CACHALOT_DN(1); break;
+    case 2: CACHALOT_DN(2); break;
+    case 3: CACHALOT_DN(3); break;
+    default: CACHALOT_DN(4); break;
+  }
+#undef CACHALOT_DN
   return check_launch("q2_down_kernel");
 }
 
@@ -368,8 +415,9 @@ extern "C" int cachalot_moe_decode_q2(const uint16_t* x, const uint8_t* pool, co
                                       cachalot_stream_t stream) {
   using namespace cachalot;
   CACHALOT_REQUIRE(idx && w, "moe_decode_q2: null pointer");
-  return launch_q2_decode(x, pool, layout, slot_table, idx, w, nullptr, D, F, E, k, group, swiglu_limit, addend,
-                          routed, out, workspace, workspace_bytes, (hipStream_t)stream);
+  decode::ExpertSource src{slot_table, idx, w, E};
+  return launch_q2_decode(x, pool, layout, src, nullptr, D, F, k, group, swiglu_limit, addend, routed, out,
+                          workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
@@ -388,10 +436,10 @@ extern "C" int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* g
                    "moe_layer_decode_q2: unknown order %d", order);
   CACHALOT_REQUIRE(gate_temp != 0.0f, "moe_layer_decode_q2: gate_temp must be non-zero");
   CACHALOT_REQUIRE(k >= 1 && k <= E && E <= 1024, "moe_layer_decode_q2: invalid topk=%d for %d experts", k, E);
-  hipStream_t s = (hipStream_t)stream;
-  int rc = launch_router_scores(x, gate_weight, 1, D, E, gate_temp, score_fn, scores, s);
-  if (rc) return rc;
-  RouteArgs ra{scores, gate_bias, E, order, norm, route_scale, idx_out, w_out};
-  return launch_q2_decode(x, pool, layout, slot_table, nullptr, nullptr, &ra, D, F, E, k, group, swiglu_limit,
-                          addend, routed, out, workspace, workspace_bytes, s);
+  decode::ExpertSource src{slot_table, nullptr, nullptr, E};
+  RouterCall rt{gate_weight, score_fn, gate_temp, scores, {}};
+  rt.tail = decode::RouteTail{gate_bias, slot_table, idx_out, w_out, nullptr, nullptr, nullptr, E, k, order, norm,
+                              route_scale};
+  return launch_q2_decode(x, pool, layout, src, &rt, D, F, k, group, swiglu_limit, addend, routed, out, workspace,
+                          workspace_bytes, (hipStream_t)stream);
 }

@@ -73,17 +73,13 @@ __device__ float score_of(float z32, int fn) {
   return sqrtf((float)sp);
 }
 
-// One wave per expert row (lane l owns chunk l of D/64 elements), TT tokens per
-// wave, 4 waves per workgroup.  NV = uint4 loads per lane per row (D = 512 * NV);
-// NV = 0 is the generic path (D a multiple of 128, u32 loads).
+// Score of one expert row: lane l owns chunk l of D/64 elements, TT tokens.
+// NV = uint4 loads per lane per row (D = 512 * NV); NV = 0 is the generic path
+// (D a multiple of 128, u32 loads).
 template <int TT, int NV>
-__global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ W, int T, int D,
-                                                            int E, float gate_temp, int fn,
-                                                            float* __restrict__ scores) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= E) return;
+__device__ __forceinline__ void router_row(const uint16_t* __restrict__ x, const uint16_t* __restrict__ W, int T,
+                                           int D, int E, float gate_temp, int fn, float* __restrict__ scores,
+                                           int row, int lane) {
   const int t0 = blockIdx.y * TT;
   const int ch = D / CHUNKS;
   const uint16_t* wrow = W + (size_t)row * D + (size_t)lane * ch;
@@ -138,6 +134,50 @@ __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __re
   }
 }
 
+// Top-k tail for one token: every workgroup counts itself finished; the last one
+// selects the experts (one wave), normalises the weights, resolves the slots and
+// returns the counter to zero.  The release/acquire fences order the other
+// workgroups' score stores before the selection's loads.
+__device__ __forceinline__ void route_tail(const float* __restrict__ scores, const decode::RouteTail& tail) {
+  __shared__ int last;
+  __shared__ int top_i[decode::KMAX];
+  __shared__ float top_v[decode::KMAX];
+  __shared__ float w[decode::KMAX];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const unsigned done = atomicAdd(tail.counter, 1u);
+    last = done == gridDim.x * gridDim.y - 1;
+  }
+  __syncthreads();
+  if (!last || threadIdx.x >= 64) return;
+  __threadfence();
+  if (tail.E <= 384) wave_topk<6>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v);
+  else wave_topk<16>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v);
+  if (threadIdx.x == 0) normalise_weights(top_v, tail.k, tail.route_scale, tail.norm, w);
+  if (threadIdx.x < tail.k) {
+    const int ex = top_i[threadIdx.x];
+    tail.ws_slots[threadIdx.x] = tail.slot_table[ex];
+    tail.ws_w[threadIdx.x] = w[threadIdx.x];
+    if (tail.idx_out) tail.idx_out[threadIdx.x] = ex;
+    if (tail.w_out) tail.w_out[threadIdx.x] = w[threadIdx.x];
+  }
+  if (threadIdx.x == 0) *tail.counter = 0u;
+}
+
+// One wave per expert row (lane l owns chunk l of D/64 elements), TT tokens per
+// wave, 4 waves per workgroup; optionally the top-k tail (one token).
+template <int TT, int NV>
+__global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ W, int T, int D,
+                                                            int E, float gate_temp, int fn,
+                                                            float* __restrict__ scores, decode::RouteTail tail) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row < E) router_row<TT, NV>(x, W, T, D, E, gate_temp, fn, scores, row, lane);
+  if (tail.counter != nullptr) route_tail(scores, tail);
+}
+
 // One wave per token: k rounds of a wave-wide argmax (EPT = ceil(E / 64) candidates per lane).
 template <int EPT>
 __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict__ scores,
@@ -161,20 +201,21 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict
 
 template <int TT>
 static void launch_scores_tt(const uint16_t* x, const uint16_t* W, int T, int D, int E, float temp, int fn,
-                             float* scores, hipStream_t s) {
+                             float* scores, hipStream_t s, const decode::RouteTail& tail) {
   dim3 grid((E + 3) / 4, (T + TT - 1) / TT);
   switch (D) {
-    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
-    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
-    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
-    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores); break;
+    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
+    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
+    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
+    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
   }
 }
 
 int launch_router_scores(const uint16_t* x, const uint16_t* W, int T, int D, int E, float gate_temp, int fn,
-                         float* scores, hipStream_t s) {
-  if (T >= 4) launch_scores_tt<4>(x, W, T, D, E, gate_temp, fn, scores, s);
-  else launch_scores_tt<1>(x, W, T, D, E, gate_temp, fn, scores, s);
+                         float* scores, hipStream_t s, const decode::RouteTail* tail) {
+  decode::RouteTail none{};
+  if (T >= 4) launch_scores_tt<4>(x, W, T, D, E, gate_temp, fn, scores, s, none);
+  else launch_scores_tt<1>(x, W, T, D, E, gate_temp, fn, scores, s, tail && T == 1 ? *tail : none);
   return check_launch("router_scores_kernel");
 }
 

@@ -27,11 +27,13 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     Decode calls on one device share it and must therefore be ordered (one
     stream, or streams that wait on each other); a HIP-graph capture must be
     preceded by an eager call of the same shape so that the workspace exists
-    before capture."""
+    before capture.  A new workspace is zero-filled: the fused layer calls keep
+    a completion counter in its first bytes that must start at zero (every call
+    leaves it zero)."""
     key = (device.index,)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 

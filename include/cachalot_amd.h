@@ -8,8 +8,10 @@
  *   - all work is stream-ordered on `stream` (a hipStream_t; NULL = default
  *     stream) and asynchronous; nothing allocates device memory -- scratch
  *     space comes in through `workspace` (size from the *_workspace_bytes
- *     query; scratch only, nothing survives a call); calls that share one
- *     workspace must not overlap (same stream, or ordered);
+ *     query); a workspace must be zero-filled once before its first use (its
+ *     first 256 bytes hold a completion counter that every call leaves at
+ *     zero; the rest is scratch and nothing in it survives a call); calls
+ *     that share one workspace must not overlap (same stream, or ordered);
  *   - return 0 on success or a negative CACHALOT_E* code; the message is in
  *     cachalot_last_error() (thread-local).  The Python layer maps EINVAL to
  *     ValueError, ENOTFOUND to KeyError, EHIP to RuntimeError, the exception
