@@ -24,6 +24,10 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per decode launch pair (gate/up + down) at config 1, from two rocprofv3
+# counter passes (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
+# plain 1 GiB device copy (read x 2.0, write x 1.0); summary under profiles/.
+PAIR_TRAFFIC_BYTES = 61_162_400
 METRIC = "MoE-layer decode tok/s + expert-byte HBM GB/s (B=1); prefill grouped-GEMM TFLOPS"
 
 
@@ -36,6 +40,10 @@ def parse():
     ap.add_argument("--seed", type=int, default=20260917)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget for the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager-only", action="store_true",
+                    help="profiling aid: run --steps eager chained steps (no graphs, no JSON) and exit")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
     return ap.parse_args()
 
 
@@ -103,6 +111,15 @@ def main() -> int:
         return 2
     import torch
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 3 x 1 GiB")
+        return 0
+
     from cachalot_amd import _lib, synth
     from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
     from cachalot_amd.moe_decode import moe_layer_decode
@@ -132,6 +149,14 @@ def main() -> int:
         _, out, _ = moe_layer_decode(x, w, b, pool, table[s % L], topk=K, route_scale=1.0, score_fn="sigmoid",
                                      swiglu_limit=10.0, addend=x)
         return out
+
+    if args.eager_only:
+        xe = x0
+        for s in range(args.steps):
+            xe = step(xe, s)
+        torch.cuda.synchronize()
+        log(f"{args.steps} eager steps done")
+        return 0
 
     # The chain is captured in a HIP graph of G steps (G a multiple of L) and
     # replayed, so host launch overhead stays out of the GPU timeline.
@@ -253,7 +278,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": PAIR_TRAFFIC_BYTES,
             "us_per_launch": round(us_kernel, 3),
             "algorithmic_bytes_per_launch": alg_bytes,
         },

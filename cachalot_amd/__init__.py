@@ -6,6 +6,7 @@ mirror the reference's call sites:
 
 * routing: ``route_topk``, ``route_topk_fused``, ``route_topk_batch``, ``route_topk_rows``
 * decode:  ``moe_layer_forward``, ``fused_routed_experts``, ``affine_routed_experts``
+* prefill / batched decode: ``moe_prefill_grouped``, ``grouped_experts``
 * store:   ``ResidentExpertStore`` over an ``HBMSlotPool``; formats in ``storage.index``
 """
 from __future__ import annotations
@@ -14,7 +15,7 @@ __version__ = "0.1.0"
 
 __all__ = [
     "RouterResult", "route_topk", "route_topk_fused", "route_topk_batch", "route_topk_rows",
-    "moe_layer_forward", "fused_routed_experts", "affine_routed_experts", "affine_expert_forward",
+    "moe_layer_forward", "moe_prefill_grouped", "grouped_experts", "fused_routed_experts", "affine_routed_experts", "affine_expert_forward",
     "ResidentExpertStore", "HBMSlotPool", "ExpertFormat", "FP4_FORMAT", "affine_format", "fp4_format",
 ]
 
@@ -26,6 +27,9 @@ def __getattr__(name):  # lazy: importing the package does not load torch or the
     if name in ("fused_routed_experts", "affine_routed_experts", "affine_expert_forward"):
         from . import moe_decode
         return getattr(moe_decode, name)
+    if name in ("moe_prefill_grouped", "grouped_experts"):
+        from . import moe_prefill
+        return getattr(moe_prefill, name)
     if name == "moe_layer_forward":
         from .moe_layer import moe_layer_forward
         return moe_layer_forward

@@ -73,6 +73,16 @@ _SIGNATURES = {
                                               c_int, c_int, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_int,
                                               c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                               c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_permute": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                 c_void_p]),
+    "cachalot_grouped_experts_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "cachalot_grouped_experts_q2": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                            c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_grouped_experts_fp4": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                             c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_unpermute_combine": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "cachalot_dequant_fp4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "cachalot_dequant_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
                                     c_void_p]),

@@ -32,6 +32,40 @@ inline int make_layout(const cachalot_expert_layout* layout, int n_tensors, cons
 
 __device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
+// Completion counters at the head of a decode workspace.  All are zero between
+// calls: the router tail and the last down workgroup return them to zero.
+struct Counters {
+  unsigned int route_done;     // router workgroups finished (router tail)
+  unsigned int gate_up_done;   // gate/up workgroups whose hidden rows are published
+  unsigned int down_done;      // down workgroups finished
+  unsigned int timeouts;       // waits that gave up (never expected; results then invalid)
+};
+
+// Upper bound on the polls of one wait (each poll sleeps ~64 clocks): a wait
+// that has not seen its count by then gives up, so every wave always exits.
+constexpr unsigned int SPIN_LIMIT = 1u << 22;
+
+// Polls *c (agent-coherent loads) until it reaches `target`; false on timeout.
+__device__ __forceinline__ bool wait_count(unsigned int* c, unsigned int target, unsigned int* timeouts) {
+  for (unsigned int polls = 0; __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++polls) {
+    if (polls >= SPIN_LIMIT) {
+      atomicAdd(timeouts, 1u);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
+}
+
+// Agent-coherent 32-bit store (written through to the point every XCD reads from).
+__device__ __forceinline__ void store_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void reset_counter(unsigned int* c) {
+  __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Top-k tail of the router kernel (one token): the last workgroup to finish
 // selects the experts, normalises their weights and resolves their slots.
 struct RouteTail {
@@ -46,10 +80,10 @@ struct RouteTail {
   float route_scale;
 };
 
-// Workspace layout of one decode call: [counter][k slots][k weights][hidden],
-// each region 256-byte aligned.  The counter must be zero before the first call
-// on a workspace (a zero-filled allocation); every call leaves it zero.  The
-// rest is scratch: nothing in it survives a call.
+// Workspace layout of one decode call: [counters][k slots][k weights][hidden],
+// each region 256-byte aligned.  The counters must be zero before the first
+// call on a workspace (a zero-filled allocation); every call leaves them zero.
+// The rest is scratch: nothing in it survives a call.
 struct WsOffsets {
   size_t counter, slots, weights, hidden, total;
 };
@@ -66,9 +100,8 @@ inline WsOffsets ws_offsets(size_t hidden_bytes) {
   return o;
 }
 
-// Where a gate/up workgroup finds its expert: given ids (idx != null: the slot
-// comes from slot_table, and the tile-0 workgroup of each expert records slot and
-// weight for the down kernel) or the router tail's ws_slots / ws_w.
+// Where the expert kernels find routed expert e: given ids (idx != null: the
+// slot comes from slot_table) or the router tail's ws_slots / ws_w.
 struct ExpertSource {
   const int32_t* slot_table;
   const int32_t* idx;
@@ -76,20 +109,16 @@ struct ExpertSource {
   int E;
 };
 
-__device__ __forceinline__ void resolve_expert(const ExpertSource& src, int e, bool first_tile, int32_t* ws_slots,
-                                               float* ws_w, int& slot, float& weight) {
+__device__ __forceinline__ int expert_slot(const ExpertSource& src, const int32_t* ws_slots, int e) {
   if (src.idx) {
     const int ex = src.idx[e];
-    slot = (ex >= 0 && ex < src.E) ? src.slot_table[ex] : -1;
-    weight = src.w[e];
-    if (first_tile && threadIdx.x == 0) {
-      ws_slots[e] = slot;
-      ws_w[e] = weight;
-    }
-  } else {
-    slot = ws_slots[e];
-    weight = ws_w[e];
+    return (ex >= 0 && ex < src.E) ? src.slot_table[ex] : -1;
   }
+  return ws_slots[e];
+}
+
+__device__ __forceinline__ float expert_weight(const ExpertSource& src, const float* ws_w, int e) {
+  return src.idx ? src.w[e] : ws_w[e];
 }
 
 }  // namespace decode

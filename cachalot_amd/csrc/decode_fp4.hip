@@ -56,7 +56,8 @@ __device__ __forceinline__ void lane_pieces(int first, int PW, int pieces, int k
 template <int NB, int XI>
 __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L, ExpertSource src, int D, int F,
-    float limit, uint16_t* __restrict__ hidden, int32_t* __restrict__ ws_slots, float* __restrict__ ws_w) {
+    float limit, uint16_t* __restrict__ hidden, const int32_t* __restrict__ ws_slots,
+    const float* __restrict__ ws_w) {
   __shared__ __align__(16) uint8_t xl[GU_ZERO + ZERO_BYTES];
   __shared__ __align__(16) uint8_t sc[2 * 16 * (MAX_D / PIECE)];   // s1, s3 of the tile's rows
   __shared__ float red[GU_WAVES][2][16];
@@ -67,9 +68,8 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   const int e = blockIdx.x / tiles;
   const int tile = blockIdx.x - e * tiles;
   const int row0 = tile * 16;
-  int slot;
-  float wexp;
-  resolve_expert(src, e, tile == 0, ws_slots, ws_w, slot, wexp);
+  const int slot = expert_slot(src, ws_slots, e);
+  const float wexp = expert_weight(src, ws_w, e);
   uint16_t* hout = hidden + (size_t)e * F * 2;   // per expert: hi [F], lo [F] (bf16)
   if (slot < 0) {
     if (threadIdx.x < 16) hout[row0 + threadIdx.x] = hout[F + row0 + threadIdx.x] = 0;
@@ -141,8 +141,8 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
 // grid.x = D / 16; block = 64 * k * DN_HALVES.  NB = ceil(ceil(F/32 / 2) / 4).
 template <int NB>
 __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
-    const uint8_t* __restrict__ pool, Layout L, const int32_t* __restrict__ ws_slots, int D, int F, int k,
-    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ addend, float* __restrict__ routed,
+    const uint8_t* __restrict__ pool, Layout L, ExpertSource src, const int32_t* __restrict__ ws_slots, int D, int F,
+    int k, const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ addend, float* __restrict__ routed,
     uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint8_t hl[DN_ZERO + ZERO_BYTES];   // per expert: hi [F] bf16, lo [F] bf16
   __shared__ __align__(16) uint8_t sc[MAX_KF / 2];              // per expert: s2 of the tile's rows
@@ -155,7 +155,7 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   const int half = wave - e * DN_HALVES;
   const int row0 = blockIdx.x * 16;
   const int j = lane & 15, kg = lane >> 4;
-  const int slot = ws_slots[e];
+  const int slot = expert_slot(src, ws_slots, e);
   const int PW = (PK + DN_HALVES - 1) / DN_HALVES;
   int pi[NB];
   bool pv[NB];
@@ -171,7 +171,7 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   // hidden hi / lo parts and, per expert, the tile's scales (16 rows x PK bytes) into LDS
   dma_to_lds(hidden, hl, k * F * 4, wave, nwaves, lane);
   for (int r = wave; r < k; r += nwaves) {
-    const int ps = max(ws_slots[r], 0);   // a missing expert's rows are never used
+    const int ps = max(expert_slot(src, ws_slots, r), 0);   // a missing expert's rows are never used
     dma_to_lds(pool + (int64_t)ps * L.record_bytes + L.off[4] + (int64_t)row0 * PK, sc + r * 16 * PK, 16 * PK, 0, 1,
                lane);
   }
@@ -246,7 +246,7 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
     RouteTail tail = router->tail;
     tail.ws_slots = ws_slots;
     tail.ws_w = ws_w;
-    tail.counter = reinterpret_cast<unsigned int*>(ws + wo.counter);
+    tail.counter = &reinterpret_cast<Counters*>(ws + wo.counter)->route_done;
     rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
                               router->scores, s, &tail);
     if (rc) return rc;
@@ -278,7 +278,7 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   const int nb_dn = ((PK + DN_HALVES - 1) / DN_HALVES + 3) / 4;
   const dim3 grid_dn(D / 16), block_dn(64 * k * DN_HALVES);
 #define CACHALOT_DN(NBV)                                                                                    \
-  hipLaunchKernelGGL((fp4_down_kernel<NBV>), grid_dn, block_dn, 0, s, pool, L, ws_slots, D, F, k, hidden, addend, \
+  hipLaunchKernelGGL((fp4_down_kernel<NBV>), grid_dn, block_dn, 0, s, pool, L, src, ws_slots, D, F, k, hidden, addend, \
                      routed, out)
   if (nb_dn <= 4) CACHALOT_DN(4);
   else if (nb_dn <= 8) CACHALOT_DN(8);

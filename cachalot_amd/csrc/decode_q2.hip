@@ -109,9 +109,12 @@ __global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
   const int e = blockIdx.x / tiles;
   const int tile = blockIdx.x - e * tiles;
   const int row0 = tile * 16;
-  int slot;
-  float wexp;
-  resolve_expert(src, e, tile == 0, ws_slots, ws_w, slot, wexp);
+  const int slot = expert_slot(src, ws_slots, e);
+  const float wexp = expert_weight(src, ws_w, e);
+  if (src.idx && tile == 0 && threadIdx.x == 0) {   // the down kernel reads the slots from the workspace
+    ws_slots[e] = slot;
+    ws_w[e] = wexp;
+  }
   uint16_t* hout = hp + (size_t)e * hidden_stride(F);
   const int tail = (F + GROUP - 1) / GROUP * GROUP - F;
   if (tile == 0 && (int)threadIdx.x < tail) hout[hidden_index(F + threadIdx.x)] = 0;
@@ -357,7 +360,7 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
     RouteTail tail = router->tail;
     tail.ws_slots = ws_slots;
     tail.ws_w = ws_w;
-    tail.counter = reinterpret_cast<unsigned int*>(ws + wo.counter);
+    tail.counter = &reinterpret_cast<Counters*>(ws + wo.counter)->route_done;
     rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
                               router->scores, s, &tail);
     if (rc) return rc;

@@ -1,0 +1,587 @@
+// Expert-major (grouped) MoE for many tokens: prefill chunks and batched decode.
+//
+// Reference: src/cachalot/model/moe_prefill_grouped.py -- dispatch :199-245
+// (assignments per expert, tokens ascending, route slot kept), per-expert
+// forward :420-467 (affine_expert_forward_batched, expert_affine.py:84-99;
+// routed_expert_forward_sgmm / _batched, fp4_sgmm_metal.py:318-333,
+// moe_prefill_batched.py:31-61), combine :526-545 (slot 0 + ... + slot k-1 in
+// fp32, then the dtype cast).  Rounding points of every path: g = bf16(x W1),
+// u = bf16(x W3), h = bf16(silu(min(g, L)) * clip(u, +-L) * w), y = bf16(h W2).
+//
+//   permute_count_kernel / permute_scatter_kernel
+//       rows grouped by expert (ascending), tokens ascending inside an expert:
+//       offsets [E+1], row_token, row_slot, row_w.  The scatter runs one
+//       workgroup per expert over all T*k routes with ballot compaction, so
+//       the order is the reference's by construction.
+//   tile_list_kernel   (expert, first row) of every MT-row tile.
+//   grouped_gate_up_kernel<KIND, MT>
+//       one workgroup = one M tile (MT rows of one expert, gathered from x by
+//       row_token) x 64 rows of W1 and W3; wave w owns 16 weight rows; K in
+//       chunks of 128 (one 2-bit group, four FP4 blocks) with the A chunk
+//       double-buffered in LDS and the next chunk's codes prefetched in
+//       registers.  v_mfma_f32_16x16x32_bf16 with A = activations, B = codes
+//       converted to bf16 (2-bit: integer codes, group formula applied per
+//       chunk as s * C + b * sum(x); FP4: E2M1 x 2^e, exact).  Epilogue writes
+//       h = bf16(silu(min(bf16 g, L)) * clip(bf16 u) * w) row-major [rows, F].
+//   grouped_down_kernel<KIND, MT>
+//       same tiling over W2 with A = h rows; y = bf16(h W2) goes straight to
+//       its (token, route slot) place: y [T, k, D] bf16.
+//   combine_kernel     out[t] = bf16(0 + y[t,0] + ... + y[t,k-1] (+ addend)).
+#include "decode_common.h"
+#include "mfma_tile.h"
+
+#include <algorithm>
+
+namespace cachalot {
+namespace {
+
+using namespace decode;
+using namespace tile;
+
+constexpr int KIND_Q2 = 0;
+constexpr int KIND_FP4 = 1;
+constexpr int NT = 64;                 // weight rows per workgroup (4 waves x 16)
+constexpr int KC = 128;                // K chunk
+constexpr int A_ROW_BYTES = 272;       // one staged A row: 128 bf16 + 16 bytes padding
+constexpr int MAX_GROUPS = 64;         // K <= 8192
+constexpr int PERMUTE_THREADS = 1024;
+
+// ------------------------------------------------------------------ permute ---
+// offsets[e] = rows before expert e (E+1 entries).
+__global__ void __launch_bounds__(PERMUTE_THREADS) permute_count_kernel(const int32_t* __restrict__ idx, int n, int E,
+                                                                        int32_t* __restrict__ offsets) {
+  __shared__ int cnt[1024 + 1];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int e = idx[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {   // E <= 1024: a serial scan is short
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = cnt[e];
+      offsets[e] = run;
+      run += c;
+    }
+    offsets[E] = run;
+  }
+}
+
+// One workgroup per expert e: walk the routes in order, keep those that chose e.
+__global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __restrict__ idx,
+                                                              const float* __restrict__ w, int n, int k,
+                                                              const int32_t* __restrict__ offsets,
+                                                              int32_t* __restrict__ row_token,
+                                                              int32_t* __restrict__ row_slot,
+                                                              float* __restrict__ row_w) {
+  __shared__ int wave_count[4];
+  const int e = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int base = offsets[e];
+  if (offsets[e + 1] == base) return;
+  for (int i0 = 0; i0 < n; i0 += 256) {
+    const int i = i0 + threadIdx.x;
+    const bool hit = i < n && idx[i] == e;
+    const uint64_t mask = __ballot(hit);
+    if (lane == 0) wave_count[wave] = __popcll(mask);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      before += q < wave ? wave_count[q] : 0;
+      total += wave_count[q];
+    }
+    if (hit) {
+      const int pos = base + before + __popcll(mask & ((1ull << lane) - 1ull));
+      row_token[pos] = i / k;
+      row_slot[pos] = i - (i / k) * k;
+      row_w[pos] = w[i];
+    }
+    base += total;
+    __syncthreads();
+  }
+}
+
+// tiles[t] = (expert, first row of the tile); count in tiles_n[0].
+__global__ void __launch_bounds__(1024) tile_list_kernel(const int32_t* __restrict__ offsets, int E, int MT,
+                                                         int2* __restrict__ tiles, int32_t* __restrict__ tiles_n) {
+  __shared__ int first[1024 + 1];
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      first[e] = run;
+      run += (offsets[e + 1] - offsets[e] + MT - 1) / MT;
+    }
+    first[E] = run;
+    tiles_n[0] = run;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    for (int t = first[e]; t < first[e + 1]; ++t) tiles[t] = make_int2(e, offsets[e] + (t - first[e]) * MT);
+}
+
+// ------------------------------------------------------------ grouped GEMM ---
+struct GroupedArgs {
+  const uint16_t* a;            // A source rows (x [T, D] or h [rows, F]), bf16
+  int a_stride;                 // elements per A source row
+  const int32_t* a_gather;      // A source row of tile row r (row_token) or null (row r itself)
+  const uint8_t* pool;
+  Layout L;
+  const int32_t* slot_table;    // [E] slot of expert e (-1: not resident)
+  const int32_t* offsets;       // [E+1]
+  const int2* tiles;
+  const int32_t* tiles_n;
+  const int32_t* row_token;
+  const int32_t* row_slot;
+  const float* row_w;
+  int K, N, k;
+  float limit;
+  uint16_t* out;                // gate/up: h [rows, N]; down: y [T, k, N]
+};
+
+// LDS: A double buffer (MT rows x 272 B), per-row chunk sums (2-bit), then the
+// staged scales (2-bit: scales and biases of each matrix; FP4: E8M0 bytes).
+template <int MT>
+struct GroupedLds {
+  static constexpr int A = 2 * MT * A_ROW_BYTES;
+  static constexpr int SUMS = 2 * MT * 4;
+};
+inline size_t grouped_lds_bytes(int kind, int MT, int NM, int K) {
+  const int per_row = kind == KIND_Q2 ? (K + KC - 1) / KC : K / 32;
+  const size_t scales = kind == KIND_Q2 ? (size_t)2 * NM * NT * per_row * 2 : (size_t)NM * NT * per_row;
+  return (size_t)2 * MT * A_ROW_BYTES + (size_t)2 * MT * 4 + scales;
+}
+
+// Stage chunk c of the tile's A rows: MT rows x 128 values, 16 values per item
+// (8 items per row).  2-bit: each 8-value piece in MFMA order, plus the row's
+// chunk sum; FP4: natural order.  Rows past the tile's end and columns past K are
+// zero.
+template <int KIND, int MT>
+struct AStage {
+  static constexpr int ITEMS = (MT * 8 + 255) / 256;   // per thread (MT * 8 items in all)
+  uint4 v[ITEMS][2];
+
+  __device__ __forceinline__ void load(const GroupedArgs& g, int row0, int rows, int c) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int item = threadIdx.x + 256 * i;
+      const int r = item >> 3;
+      const int col = c * KC + (item & 7) * 16;
+      const bool live = item < MT * 8 && r < rows && col < g.K;
+      const int src_row = live ? (g.a_gather ? g.a_gather[row0 + r] : row0 + r) : 0;
+      const uint4* p = reinterpret_cast<const uint4*>(g.a + (size_t)src_row * g.a_stride + (live ? col : 0));
+      v[i][0] = p[0];
+      v[i][1] = p[1];
+      if (!live) v[i][0] = v[i][1] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  __device__ __forceinline__ void store(uint8_t* abuf, float* sums) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int item = threadIdx.x + 256 * i;
+      const int r = item >> 3;
+      uint4 lo = v[i][0], hi = v[i][1];
+      if constexpr (KIND == KIND_Q2) {
+        pairs_mfma(v[i][0].x, v[i][0].y, lo.x, lo.y);
+        pairs_mfma(v[i][0].z, v[i][0].w, lo.z, lo.w);
+        pairs_mfma(v[i][1].x, v[i][1].y, hi.x, hi.y);
+        pairs_mfma(v[i][1].z, v[i][1].w, hi.z, hi.w);
+        const float s = sum8_lanes(sum_bf16x8(lo) + sum_bf16x8(hi));
+        if (item < MT * 8 && (item & 7) == 0) sums[r] = s;
+      }
+      if (item < MT * 8) {
+        uint4* d = reinterpret_cast<uint4*>(abuf + r * A_ROW_BYTES + (item & 7) * 32);
+        d[0] = lo;
+        d[1] = hi;
+      }
+    }
+  }
+};
+
+// The lane's codes of chunk c for weight row `row` of one matrix.
+// 2-bit: lane group kg owns codes [32kg, 32kg+32) of the group = 8 bytes.
+// FP4: lane group kg owns block kg of the chunk = 16 bytes.
+template <int KIND>
+struct BChunk {
+  uint4 v;
+  __device__ __forceinline__ void load(const uint8_t* wrow, int c, int kg, int row_bytes) {
+    if constexpr (KIND == KIND_Q2) {
+      const int off = min(c * 32 + kg * 8, row_bytes - 8);
+      const uint2 t = *reinterpret_cast<const uint2*>(wrow + off);
+      v = make_uint4(t.x, t.y, 0, 0);
+    } else {
+      const int off = min(c * 64 + kg * 16, row_bytes - 16);
+      v = *reinterpret_cast<const uint4*>(wrow + off);
+    }
+  }
+  __device__ __forceinline__ bf16x8_t step(int s, float scale) const {
+    if constexpr (KIND == KIND_Q2) {
+      const uint32_t wd = (s >> 1) ? v.y : v.x;
+      return (s & 1) ? q2_codes_to_b<1>(wd) : q2_codes_to_b<0>(wd);
+    } else {
+      return fp4_codes_to_b(word_of(v, s), scale);
+    }
+  }
+};
+
+// Per-lane accumulation of one K chunk for NM matrices over MT/16 token blocks:
+// each step converts the lane's codes once per matrix and feeds every token block.
+template <int KIND, int MT, int NM>
+__device__ __forceinline__ void chunk_mma(const uint8_t* abuf, const float* sums, const BChunk<KIND> (&b)[NM],
+                                          const float (&scale)[NM], const float (&bias)[NM], int lane,
+                                          f32x4_t (&acc)[NM][MT / 16]) {
+  const int i = lane & 15, kg = lane >> 4;
+  f32x4_t c[NM][MT / 16];
+  if constexpr (KIND == KIND_Q2) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int tb = 0; tb < MT / 16; ++tb) c[m][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    bf16x8_t bv[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) bv[m] = b[m].step(s, scale[m]);
+#pragma unroll
+    for (int tb = 0; tb < MT / 16; ++tb) {
+      const bf16x8_t a = lds_a(abuf, (tb * 16 + i) * A_ROW_BYTES + kg * 64 + s * 16);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        if constexpr (KIND == KIND_Q2) c[m][tb] = mfma(a, bv[m], c[m][tb]);
+        else acc[m][tb] = mfma(a, bv[m], acc[m][tb]);
+      }
+    }
+  }
+  if constexpr (KIND == KIND_Q2) {
+    // D rows of this lane are tokens tb*16 + 4kg + r: the group formula per token
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int tb = 0; tb < MT / 16; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[m][tb][r] = acc[m][tb][r] + (scale[m] * c[m][tb][r] + bias[m] * sums[tb * 16 + 4 * kg + r]);
+  }
+}
+
+// Scale of (row j of the workgroup, chunk c) for tensor q: 2-bit bf16 scale/bias of
+// group c; FP4 E8M0 of block 4c + kg.
+template <int KIND>
+__device__ __forceinline__ float staged_scale(const uint8_t* sc, int q, int j, int c, int kg, int per_row) {
+  if constexpr (KIND == KIND_Q2) {
+    return bf16_to_f32(reinterpret_cast<const uint16_t*>(sc)[(q * NT + j) * per_row + c]);
+  } else {
+    // blocks past K (the last chunk of K = 2880) meet zero activations: any finite scale
+    return 4 * c + kg < per_row ? e8m0_to_f32(sc[(q * NT + j) * per_row + 4 * c + kg]) : 1.0f;
+  }
+}
+
+// Shared main loop of both grouped kernels.  NM = 2 (W1, W3) or 1 (W2); tq =
+// kernel tensor indices of the matrices (codes) in the record layout.
+template <int KIND, int MT, int NM>
+__device__ __forceinline__ bool grouped_main(const GroupedArgs& g, uint8_t* lds, const int (&tq)[NM], int& e,
+                                             int& row0, int& rows, f32x4_t (&acc)[NM][MT / 16]) {
+  using Lds = GroupedLds<MT>;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int kg = lane >> 4;
+  if ((int)blockIdx.x >= g.tiles_n[0]) return false;
+  const int2 tile = g.tiles[blockIdx.x];
+  e = tile.x;
+  row0 = tile.y;
+  rows = min(MT, g.offsets[e + 1] - row0);
+  const int n0 = blockIdx.y * NT;
+  const int slot = g.slot_table[e];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int tb = 0; tb < MT / 16; ++tb) acc[m][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (slot < 0) return true;   // not resident: zero rows
+
+  uint8_t* abuf[2] = {lds, lds + MT * A_ROW_BYTES};
+  float* sums[2] = {reinterpret_cast<float*>(lds + Lds::A), reinterpret_cast<float*>(lds + Lds::A) + MT};
+  uint8_t* sc = lds + Lds::A + Lds::SUMS;
+  const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
+  const int nchunks = (g.K + KC - 1) / KC;
+  // bytes per weight row and per scale row
+  const int groups = nchunks;                                   // 2-bit: stored groups per row
+  const int row_bytes = KIND == KIND_Q2 ? groups * 32 : g.K / 2;
+  const int per_row = KIND == KIND_Q2 ? groups : g.K / 32;      // scale entries per row
+  const int row = n0 + wave * 16 + (lane & 15);
+  const uint8_t* wrow[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) wrow[m] = base + g.L.off[tq[m]] + (int64_t)row * row_bytes;
+
+  // scales (and biases) of the 64 weight rows: contiguous runs, straight into LDS
+  {
+    const int run = NT * per_row * (KIND == KIND_Q2 ? 2 : 1);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      // 2-bit: slot 2m = scales, 2m+1 = biases; FP4: slot m = E8M0 bytes
+      const int q = KIND == KIND_Q2 ? 2 * m : m;
+      dma_to_lds(base + g.L.off[tq[m] + 1] + (int64_t)n0 * run / NT, sc + q * run, run, (wave + m) & 3, 4, lane);
+      if constexpr (KIND == KIND_Q2)
+        dma_to_lds(base + g.L.off[tq[m] + 2] + (int64_t)n0 * run / NT, sc + (q + 1) * run, run, (wave + m + 2) & 3,
+                   4, lane);
+    }
+  }
+  AStage<KIND, MT> as;
+  BChunk<KIND> bc[NM], bn[NM];
+  as.load(g, row0, rows, 0);
+#pragma unroll
+  for (int m = 0; m < NM; ++m) bc[m].load(wrow[m], 0, kg, row_bytes);
+  as.store(abuf[0], sums[0]);
+  wait_vmem();
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int cur = c & 1;
+    const bool more = c + 1 < nchunks;
+    if (more) {
+      as.load(g, row0, rows, c + 1);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) bn[m].load(wrow[m], c + 1, kg, row_bytes);
+    }
+    float scale[NM], bias[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      // 2-bit: tensor slots 2m (scales) and 2m+1 (biases); FP4: slot 2m (E8M0)
+      scale[m] = staged_scale<KIND>(sc, KIND == KIND_Q2 ? 2 * m : m, wave * 16 + (lane & 15), c, kg, per_row);
+      bias[m] = KIND == KIND_Q2 ? staged_scale<KIND>(sc, 2 * m + 1, wave * 16 + (lane & 15), c, kg, per_row) : 0.0f;
+    }
+    chunk_mma<KIND, MT, NM>(abuf[cur], sums[cur], bc, scale, bias, lane, acc);
+    if (more) {
+      as.store(abuf[cur ^ 1], sums[cur ^ 1]);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) bc[m] = bn[m];
+    }
+    __syncthreads();
+  }
+  return true;
+}
+
+template <int KIND, int MT>
+__global__ void __launch_bounds__(256) grouped_gate_up_kernel(GroupedArgs g) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  f32x4_t acc[2][MT / 16];
+  int e, row0, rows;
+  const int tq[2] = {0, 6};   // w1, w3
+  if (!grouped_main<KIND, MT, 2>(g, lds, tq, e, row0, rows, acc)) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n = blockIdx.y * NT + wave * 16 + (lane & 15);
+  const int kg = lane >> 4;
+#pragma unroll
+  for (int tb = 0; tb < MT / 16; ++tb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tr = tb * 16 + 4 * kg + r;
+      if (tr < rows) {
+        float gv = round_bf16(acc[0][tb][r]);
+        float uv = round_bf16(acc[1][tb][r]);
+        if (g.limit > 0.0f) {
+          uv = fminf(fmaxf(uv, -g.limit), g.limit);
+          gv = fminf(gv, g.limit);
+        }
+        const float h = (silu_f32(gv) * uv) * g.row_w[row0 + tr];
+        g.out[(size_t)(row0 + tr) * g.N + n] = f32_to_bf16(h);
+      }
+    }
+}
+
+template <int KIND, int MT>
+__global__ void __launch_bounds__(256) grouped_down_kernel(GroupedArgs g) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  f32x4_t acc[1][MT / 16];
+  int e, row0, rows;
+  const int tq[1] = {3};      // w2
+  if (!grouped_main<KIND, MT, 1>(g, lds, tq, e, row0, rows, acc)) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n = blockIdx.y * NT + wave * 16 + (lane & 15);
+  const int kg = lane >> 4;
+#pragma unroll
+  for (int tb = 0; tb < MT / 16; ++tb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tr = tb * 16 + 4 * kg + r;
+      if (tr < rows) {
+        const int rr = row0 + tr;
+        g.out[((size_t)g.row_token[rr] * g.k + g.row_slot[rr]) * g.N + n] = f32_to_bf16(acc[0][tb][r]);
+      }
+    }
+}
+
+// out[t, d] = bf16(0 + y[t,0,d] + ... + y[t,k-1,d] (+ addend[t,d])); routed likewise in fp32.
+__global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ y, const uint16_t* __restrict__ addend,
+                                                      int T, int k, int D, float* __restrict__ routed,
+                                                      uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // one pair of columns
+  const int64_t pairs = (int64_t)T * D / 2;
+  if (i >= pairs) return;
+  const int64_t t = (2 * i) / D;
+  const int d = (int)(2 * i - t * D);
+  float a0 = 0.0f, a1 = 0.0f;
+  for (int s = 0; s < k; ++s) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(y + ((size_t)t * k + s) * D + d);
+    a0 = a0 + bf16_to_f32((uint16_t)(v & 0xffff));
+    a1 = a1 + bf16_to_f32((uint16_t)(v >> 16));
+  }
+  if (routed) {
+    routed[t * D + d] = a0;
+    routed[t * D + d + 1] = a1;
+  }
+  if (out) {
+    float o0 = a0, o1 = a1;
+    if (addend) {
+      const uint32_t av = *reinterpret_cast<const uint32_t*>(addend + t * D + d);
+      o0 = o0 + bf16_to_f32((uint16_t)(av & 0xffff));
+      o1 = o1 + bf16_to_f32((uint16_t)(av >> 16));
+    }
+    *reinterpret_cast<uint32_t*>(out + t * D + d) = (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16);
+  }
+}
+
+// Workspace of a grouped call: [tiles_n][tiles][hidden rows x F bf16], 256-byte aligned regions.
+struct GroupedWs {
+  size_t tiles_n, tiles, hidden, total;
+  int max_tiles;
+};
+
+inline GroupedWs grouped_ws(int T, int k, int E, int F) {
+  GroupedWs w;
+  const int rows = T * k;
+  w.max_tiles = rows / 16 + std::min(E, rows) + 1;   // bound for MT >= 16
+  w.tiles_n = 0;
+  w.tiles = 256;
+  w.hidden = w.tiles + align256((size_t)w.max_tiles * sizeof(int2));
+  w.total = w.hidden + align256((size_t)rows * F * sizeof(uint16_t));
+  return w;
+}
+
+template <int KIND, int MT>
+int launch_grouped_mt(const GroupedArgs& gu, const GroupedArgs& dn, int max_tiles, size_t lds_gu, size_t lds_dn,
+                      hipStream_t s) {
+  auto kgu = grouped_gate_up_kernel<KIND, MT>;
+  auto kdn = grouped_down_kernel<KIND, MT>;
+  if (lds_gu > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds_gu) != hipSuccess)
+    return fail(CACHALOT_EHIP, "grouped experts: cannot grant %zu bytes of LDS", lds_gu);
+  if (lds_dn > 65536 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kdn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds_dn) != hipSuccess)
+    return fail(CACHALOT_EHIP, "grouped experts: cannot grant %zu bytes of LDS", lds_dn);
+  hipLaunchKernelGGL(kgu, dim3(max_tiles, gu.N / NT), dim3(256), lds_gu, s, gu);
+  int rc = check_launch("grouped_gate_up_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(kdn, dim3(max_tiles, dn.N / NT), dim3(256), lds_dn, s, dn);
+  return check_launch("grouped_down_kernel");
+}
+
+template <int KIND>
+int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
+                   const int32_t* slot_table, const int32_t* offsets, const int32_t* row_token,
+                   const int32_t* row_slot, const float* row_w, int T, int D, int F, int E, int k, float limit,
+                   uint16_t* y, void* workspace, size_t workspace_bytes, hipStream_t s, const char* who) {
+  CACHALOT_REQUIRE(x && pool && layout && slot_table && offsets && row_token && row_slot && row_w && y,
+                   "%s: null pointer", who);
+  CACHALOT_REQUIRE(T >= 1, "%s: x must contain at least one token (T=%d)", who, T);
+  CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "%s: k=%d outside 1..%d", who, k, KMAX);
+  CACHALOT_REQUIRE(E >= 1 && E <= 1024, "%s: E=%d outside 1..1024", who, E);
+  CACHALOT_REQUIRE(D % NT == 0 && D >= 128 && D <= KC * MAX_GROUPS,
+                   "%s: D=%d must be a multiple of 64 in 128..8192", who, D);
+  CACHALOT_REQUIRE(F % NT == 0 && F >= 64 && F <= KC * MAX_GROUPS, "%s: F=%d must be a multiple of 64 in 64..8192",
+                   who, F);
+  if (KIND == KIND_Q2) CACHALOT_REQUIRE(D % KC == 0, "%s: D=%d must be a multiple of the 128-code group", who, D);
+  const GroupedWs wo = grouped_ws(T, k, E, F);
+  if (workspace == nullptr || workspace_bytes < wo.total)
+    return fail(CACHALOT_ESPACE, "%s: workspace %zu < %zu bytes", who, workspace_bytes, wo.total);
+  Layout L;
+  static const int used_q2[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
+  static const int used_fp4[6] = {0, 1, 3, 4, 6, 7};
+  int rc = KIND == KIND_Q2 ? make_layout(layout, 9, used_q2, L, who) : make_layout(layout, 6, used_fp4, L, who);
+  if (rc) return rc;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  int32_t* tiles_n = reinterpret_cast<int32_t*>(ws + wo.tiles_n);
+  int2* tiles = reinterpret_cast<int2*>(ws + wo.tiles);
+  uint16_t* hidden = reinterpret_cast<uint16_t*>(ws + wo.hidden);
+  // tiles of 64 rows when experts see many tokens, 16 for batched decode
+  const int MT = T * k >= 4 * E ? 64 : 16;
+  hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, MT, tiles, tiles_n);
+  rc = check_launch("tile_list_kernel");
+  if (rc) return rc;
+  const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
+  GroupedArgs gu{x, D, row_token, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
+                 D, F, k, limit, hidden};
+  GroupedArgs dn{hidden, F, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
+                 F, D, k, limit, y};
+  const size_t lds_gu = grouped_lds_bytes(KIND, MT, 2, D), lds_dn = grouped_lds_bytes(KIND, MT, 1, F);
+  return MT == 64 ? launch_grouped_mt<KIND, 64>(gu, dn, max_tiles, lds_gu, lds_dn, s)
+                  : launch_grouped_mt<KIND, 16>(gu, dn, max_tiles, lds_gu, lds_dn, s);
+}
+
+}  // namespace
+}  // namespace cachalot
+
+extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k, int E, int32_t* offsets,
+                                int32_t* row_token, int32_t* row_slot, float* row_w, cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(idx && w && offsets && row_token && row_slot && row_w, "permute: null pointer");
+  CACHALOT_REQUIRE(T >= 1 && k >= 1 && (int64_t)T * k <= (1 << 30), "permute: T=%d k=%d", T, k);
+  CACHALOT_REQUIRE(E >= 1 && E <= 1024, "permute: E=%d outside 1..1024", E);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(permute_count_kernel, dim3(1), dim3(PERMUTE_THREADS), 0, s, idx, T * k, E, offsets);
+  int rc = check_launch("permute_count_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(E), dim3(256), 0, s, idx, w, T * k, k, offsets, row_token, row_slot,
+                     row_w);
+  return check_launch("permute_scatter_kernel");
+}
+
+extern "C" size_t cachalot_grouped_experts_workspace_bytes(int T, int k, int E, int D, int F) {
+  (void)D;
+  if (T <= 0 || k <= 0 || E <= 0 || F <= 0) return 0;
+  return cachalot::grouped_ws(T, k, E, F).total;
+}
+
+extern "C" int cachalot_grouped_experts_q2(const uint16_t* x, const uint8_t* pool,
+                                           const cachalot_expert_layout* layout, const int32_t* slot_table,
+                                           const int32_t* offsets, const int32_t* row_token, const int32_t* row_slot,
+                                           const float* row_w, int T, int D, int F, int E, int k, int group,
+                                           float swiglu_limit, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                           cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(group == KC, "grouped_experts_q2: group_size %d (the bank format uses 128)", group);
+  return launch_grouped<KIND_Q2>(x, pool, layout, slot_table, offsets, row_token, row_slot, row_w, T, D, F, E, k,
+                                 swiglu_limit, y, workspace, workspace_bytes, (hipStream_t)stream,
+                                 "grouped_experts_q2");
+}
+
+extern "C" int cachalot_grouped_experts_fp4(const uint16_t* x, const uint8_t* pool,
+                                            const cachalot_expert_layout* layout, const int32_t* slot_table,
+                                            const int32_t* offsets, const int32_t* row_token,
+                                            const int32_t* row_slot, const float* row_w, int T, int D, int F, int E,
+                                            int k, float swiglu_limit, uint16_t* y, void* workspace,
+                                            size_t workspace_bytes, cachalot_stream_t stream) {
+  using namespace cachalot;
+  return launch_grouped<KIND_FP4>(x, pool, layout, slot_table, offsets, row_token, row_slot, row_w, T, D, F, E, k,
+                                  swiglu_limit, y, workspace, workspace_bytes, (hipStream_t)stream,
+                                  "grouped_experts_fp4");
+}
+
+extern "C" int cachalot_unpermute_combine(const uint16_t* y, const uint16_t* addend, int T, int k, int D,
+                                          float* routed, uint16_t* out, cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(y, "unpermute_combine: null pointer");
+  CACHALOT_REQUIRE(routed || out, "unpermute_combine: no output requested");
+  CACHALOT_REQUIRE(T >= 1 && k >= 1 && D >= 2 && D % 2 == 0, "unpermute_combine: T=%d k=%d D=%d", T, k, D);
+  const int64_t pairs = (int64_t)T * D / 2;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, (hipStream_t)stream, y,
+                     addend, T, k, D, routed, out);
+  return check_launch("combine_kernel");
+}

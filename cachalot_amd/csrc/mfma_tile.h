@@ -120,13 +120,17 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
 // dst + 16 l), wave-cooperatively: wave w of nwaves copies the 1 KiB chunks w,
 // w + nwaves, ...  No registers are involved; the copy is complete once the
 // wave's vector-memory counter has drained (wait_vmem) and, for other waves'
-// chunks, after the following workgroup barrier.
+// chunks, after the following workgroup barrier.  COHERENT = 1 reads at agent
+// scope (sc1), for data other workgroups of the same launch published with
+// agent-coherent stores.
+template <int COHERENT = 0>
 __device__ __forceinline__ void dma_to_lds(const void* src, uint8_t* dst, int bytes, int wave, int nwaves,
                                            int lane) {
   for (int c = wave * 1024; c < bytes; c += nwaves * 1024) {
     const int off = c + lane * 16;
     if (off < bytes)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(src) + off, dst + c, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t*>(src) + off, dst + c, 16, 0,
+                                       COHERENT ? 16 : 0);
   }
 }
 

@@ -1,0 +1,173 @@
+"""Expert-major MoE for many tokens: prefill chunks and batched decode.
+
+Keeps the call-site signature of ``moe_prefill_grouped``
+(``src/cachalot/model/moe_prefill_grouped.py:74-103``) and its return value
+``(output [T, D] in x.dtype, RouterResult)``.
+
+Mechanism: route all tokens on the device, permute the T*k routes into rows
+grouped by expert (tokens ascending inside an expert, the order the
+reference's assignment loop produces, ``:199-225``), run every expert's SwiGLU
+over its rows as two grouped matrix-core launches (``y = bf16(W2 bf16(silu(
+bf16 g) * bf16 u * w))`` per row, the rounding points of
+``affine_expert_forward_batched`` / ``routed_expert_forward_sgmm``), and sum the
+route slots in decode order (``:526-545``).  The host reads nothing back when
+the layer is fully resident in HBM; otherwise one synchronisation fetches the
+routed expert ids so that ``get_many`` can load the misses first.
+
+The FP8 shared expert of the reference (``:532-545``) is not built yet:
+``shared_*`` must be None; ``addend`` ([T, D] bf16, optional) is added before
+the final cast instead.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .cache.resident_store import ResidentExpertStore
+from .cache.slots import HBMSlotPool
+from .router import RouterResult, route_topk_batch, route_topk_rows
+from .storage.index import ExpertEntry
+
+_WORKSPACES: dict[int, torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Scratch for grouped calls, cached per device (grown on demand); calls sharing it must be ordered."""
+    ws = _WORKSPACES.get(device.index)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[device.index] = ws
+    return ws
+
+
+def permute(indices: torch.Tensor, weights: torch.Tensor, n_experts: int):
+    """Routes [T, k] -> (offsets [E+1], row_token, row_slot, row_w) grouped by expert (device tensors)."""
+    if indices.ndim != 2 or tuple(weights.shape) != tuple(indices.shape):
+        raise ValueError(f"indices {tuple(indices.shape)} / weights {tuple(weights.shape)} must be [T, k]")
+    _lib.require_cuda(indices, weights)
+    t, k = indices.shape
+    dev = indices.device
+    indices = indices.to(torch.int32).contiguous()
+    weights = weights.to(torch.float32).contiguous()
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(t * k, dtype=torch.int32, device=dev)
+    row_slot = torch.empty(t * k, dtype=torch.int32, device=dev)
+    row_w = torch.empty(t * k, dtype=torch.float32, device=dev)
+    rc = _lib.lib().cachalot_permute(indices.data_ptr(), weights.data_ptr(), t, k, n_experts, offsets.data_ptr(),
+                                     row_token.data_ptr(), row_slot.data_ptr(), row_w.data_ptr(),
+                                     _lib.stream_handle(dev))
+    _lib.check(rc, "permute")
+    return offsets, row_token, row_slot, row_w
+
+
+def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, pool: HBMSlotPool,
+                    slot_table: torch.Tensor, *, swiglu_limit: float = 10.0, addend: torch.Tensor | None = None,
+                    want_routed: bool = False, want_out: bool = True):
+    """x [T, D] bf16, routes [T, k] -> (routed fp32 [T, D] or None, out bf16 [T, D] or None).
+
+    routed[t] = sum over route slots s (in order) of expert idx[t, s] applied to x[t]
+    with router weight w[t, s]; out = bf16(routed + addend)."""
+    fmt = pool.format
+    d, f = fmt.d_model, fmt.d_ff
+    if x.ndim != 2 or x.shape[1] != d:
+        raise ValueError(f"x must be [tokens, {d}], got {tuple(x.shape)}")
+    if x.shape[0] == 0:
+        raise ValueError("x must contain at least one token")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("grouped experts expect bf16 activations")
+    if indices.shape[0] != x.shape[0]:
+        raise ValueError(f"{indices.shape[0]} routes for {x.shape[0]} tokens")
+    if addend is not None and (addend.dtype != torch.bfloat16 or tuple(addend.shape) != tuple(x.shape)):
+        raise ValueError("addend must be bf16 shaped like x")
+    _lib.require_cuda(x, slot_table, addend)
+    t, k = indices.shape
+    n_experts = slot_table.numel()
+    dev = x.device
+    x = x.contiguous()
+    slot_table = slot_table.to(torch.int32).contiguous()
+    offsets, row_token, row_slot, row_w = permute(indices, weights, n_experts)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    y = torch.empty((t, k, d), dtype=torch.bfloat16, device=dev)
+    nbytes = L.cachalot_grouped_experts_workspace_bytes(t, k, n_experts, d, f)
+    ws = _workspace(dev, nbytes)
+    common = (x.data_ptr(), pool.storage.data_ptr(), pool.layout(), slot_table.data_ptr(), offsets.data_ptr(),
+              row_token.data_ptr(), row_slot.data_ptr(), row_w.data_ptr(), t, d, f, n_experts, k)
+    if fmt.kind == "affine":
+        rc = L.cachalot_grouped_experts_q2(*common, fmt.group_size, float(swiglu_limit), y.data_ptr(), ws.data_ptr(),
+                                           nbytes, stream)
+    elif fmt.kind == "fp4":
+        rc = L.cachalot_grouped_experts_fp4(*common, float(swiglu_limit), y.data_ptr(), ws.data_ptr(), nbytes, stream)
+    else:
+        raise ValueError(f"unknown expert format {fmt.kind!r}")
+    _lib.check(rc, "grouped_experts")
+    routed = torch.empty((t, d), dtype=torch.float32, device=dev) if want_routed else None
+    out = torch.empty((t, d), dtype=torch.bfloat16, device=dev) if want_out else None
+    rc = L.cachalot_unpermute_combine(y.data_ptr(), _lib.ptr(addend), t, k, d, _lib.ptr(routed), _lib.ptr(out), stream)
+    _lib.check(rc, "unpermute_combine")
+    return routed, out
+
+
+def moe_prefill_grouped(
+    x: torch.Tensor,
+    *,
+    layer_id: int,
+    gate_weight: torch.Tensor,
+    gate_bias: torch.Tensor,
+    expert_index: dict | None,
+    expert_store: ResidentExpertStore,
+    expert_prefetcher=None,
+    shared_w1=None,
+    shared_w1_scales=None,
+    shared_w2=None,
+    shared_w2_scales=None,
+    shared_w3=None,
+    shared_w3_scales=None,
+    topk: int = 6,
+    gate_temp: float = 1.0,
+    route_scale: float = 1.5,
+    norm_topk_prob: bool = True,
+    swiglu_limit: float = 10.0,
+    batched: bool = True,
+    gate_bias_vl: torch.Tensor | None = None,
+    image_mask: torch.Tensor | None = None,
+    score_fn: str = "sqrt_softplus",
+    order: str = "ascending",
+    addend: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, RouterResult]:
+    if x.ndim != 2:
+        raise ValueError(f"x must be 2D [tokens, hidden], got {tuple(x.shape)}")
+    if x.shape[0] == 0:
+        raise ValueError("x must contain at least one token")
+    if image_mask is not None and not batched:
+        raise NotImplementedError(
+            "per-token bias_vl selection is only wired for the batched (route_topk_rows) path; "
+            "batched=False has no image_mask support")
+    if any(t is not None for t in (shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3,
+                                   shared_w3_scales)):
+        raise NotImplementedError("the FP8 shared expert is not part of this build yet")
+    if batched:
+        indices, weights, scores = route_topk_rows(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp,
+                                                   route_scale=route_scale, norm_topk_prob=norm_topk_prob,
+                                                   bias_vl=gate_bias_vl, image_mask=image_mask, score_fn=score_fn,
+                                                   order=order)
+        route = RouterResult(indices=indices, weights=weights, scores=scores)
+    else:
+        route = route_topk_batch(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp,
+                                 route_scale=route_scale, norm_topk_prob=norm_topk_prob, score_fn=score_fn,
+                                 order=order)
+    if not expert_store.layer_fully_resident(layer_id):
+        # host-addressed: one sync for the routed ids, then load what is missing
+        ids = sorted({int(e) for e in route.indices.reshape(-1).tolist()})
+        entries = []
+        for e in ids:
+            key = (layer_id, e)
+            entry = expert_index.get(key) if expert_index is not None else ExpertEntry(*key)
+            if entry is None:
+                raise KeyError(f"Missing routed expert layer={layer_id}, expert={e}")
+            entries.append(entry)
+        expert_store.get_many(entries)
+    table = expert_store.layer_table(layer_id)
+    _, out = grouped_experts(x.to(torch.bfloat16), route.indices, route.weights, expert_store.pool, table,
+                             swiglu_limit=swiglu_limit, addend=addend)
+    return out.to(x.dtype), route

@@ -119,7 +119,8 @@ int cachalot_moe_decode_fp4(const uint16_t* x, const uint8_t* pool,
 
 /* Whole decode MoE layer for one token, routing on the device: router scores
  * (as cachalot_router_topk with T = 1, bias only), top-k, slot lookup, gate/up,
- * down and route-order combine in three launches, no host synchronisation.
+ * down and route-order combine in three launches (router with the top-k as
+ * its last workgroup's tail, gate/up, down), no host synchronisation.
  *   gate_weight [E, D] bf16, gate_bias [E] fp32; idx_out [k] int32, w_out [k]
  *   fp32 (either may be NULL), scores [E] fp32 (required: it is the hand-off
  *   between the first two launches).  Other arguments as cachalot_moe_decode_*.
@@ -141,6 +142,46 @@ int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight
                                   const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
                                   float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
                                   cachalot_stream_t stream);
+
+/* Many tokens (prefill chunk, batched decode), expert-major.
+ *
+ * cachalot_permute: routes idx/w [T, k] -> rows grouped by expert id
+ * (ascending), tokens ascending inside an expert: offsets [E+1] (rows of
+ * expert e are offsets[e] .. offsets[e+1]-1), row_token / row_slot / row_w
+ * [T*k].  Replaces the host-side assignment build of moe_prefill_grouped
+ * (src/cachalot/model/moe_prefill_grouped.py:199-225) and the per-expert
+ * x[token_idx] gather lists (:420-437).
+ *
+ * cachalot_grouped_experts_{q2,fp4}: for every expert with rows, the SwiGLU
+ * expert on its rows (x gathered by row_token): g = bf16(x W1), u = bf16(x W3),
+ * h = bf16(silu(min(g,L)) * clip(u,-L,L) * row_w), y = bf16(h W2), written to
+ * y[row_token, row_slot, :] ([T, k, D] bf16).  Experts whose slot_table entry
+ * is negative give zero rows.  Workspace from
+ * cachalot_grouped_experts_workspace_bytes (scratch, no state across calls).
+ * Replaces affine_expert_forward_batched (expert_affine.py:84-99),
+ * routed_expert_forward_sgmm (fp4_sgmm_metal.py:318-333) and
+ * routed_expert_forward_batched (moe_prefill_batched.py:31-61) called per
+ * expert from moe_prefill_grouped.py:420-467.
+ *
+ * cachalot_unpermute_combine: routed[t] = 0 + y[t,0] + ... + y[t,k-1] (fp32),
+ * out[t] = bf16(routed[t] + addend[t]) (addend NULL: no add).  Replaces the
+ * slot-buffer sum of moe_prefill_grouped.py:526-545. */
+int cachalot_permute(const int32_t* idx, const float* w, int T, int k, int E, int32_t* offsets,
+                     int32_t* row_token, int32_t* row_slot, float* row_w, cachalot_stream_t stream);
+size_t cachalot_grouped_experts_workspace_bytes(int T, int k, int E, int D, int F);
+int cachalot_grouped_experts_q2(const uint16_t* x, const uint8_t* pool,
+                                const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                const int32_t* offsets, const int32_t* row_token, const int32_t* row_slot,
+                                const float* row_w, int T, int D, int F, int E, int k, int group,
+                                float swiglu_limit, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                cachalot_stream_t stream);
+int cachalot_grouped_experts_fp4(const uint16_t* x, const uint8_t* pool,
+                                 const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                 const int32_t* offsets, const int32_t* row_token, const int32_t* row_slot,
+                                 const float* row_w, int T, int D, int F, int E, int k, float swiglu_limit,
+                                 uint16_t* y, void* workspace, size_t workspace_bytes, cachalot_stream_t stream);
+int cachalot_unpermute_combine(const uint16_t* y, const uint16_t* addend, int T, int k, int D, float* routed,
+                               uint16_t* out, cachalot_stream_t stream);
 
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32

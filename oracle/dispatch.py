@@ -40,7 +40,7 @@ def combine(y_rows, pos, addend=None):
     """y_rows [T*k, D] fp32, pos [T, k] -> (routed fp32 [T, D], out fp32 holding bf16 values)."""
     y_rows = np.asarray(y_rows, dtype=np.float32)
     pos = np.asarray(pos)
-    routed = y_rows[pos[:, 0]].copy()
+    routed = np.float32(0.0) + y_rows[pos[:, 0]]      # slot_buffer starts at zeros (:244-247)
     for s in range(1, pos.shape[1]):
         routed = routed + y_rows[pos[:, s]]
     total = routed if addend is None else routed + np.asarray(addend, np.float32)
