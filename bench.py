@@ -36,7 +36,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=4000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--layers", type=int, default=16, help="resident layers rotated through (MALL defeat)")
+    ap.add_argument("--layers", type=int, default=40,
+                    help="resident 2-bit layers the decode chain rotates through (40 = BASELINE config 4's stack)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config 2 / config 3 measurements")
     ap.add_argument("--seed", type=int, default=20260917)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget for the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -101,6 +103,107 @@ def cpu_baseline(seed: int, budget_s: float):
         "ms_per_token_layer": round(per * 1e3, 2),
         "expert_GBps": round(6 * fmt.algorithmic_bytes / per / 1e9, 4),
     }
+
+
+def batched_decode(args, store, gates, log_fn):
+    """B tokens per step routed together, grouped experts over the union."""
+    import torch
+
+    from cachalot_amd import synth
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.router import route_topk_rows
+
+    L = len(gates)
+    fmt = store.pool.format
+    out = {}
+    for B in (4, 16, 32):
+        S = 2 * L                                   # steps per graph: every layer twice
+        xs = [synth.activations(args.seed, 5000 + B * 1000 + s, B, fmt.d_model, store.pool.device) for s in range(S)]
+        routes = []
+
+        def run():
+            routes.clear()
+            for s in range(S):
+                w, b = gates[s % L]
+                idx, wt, _ = route_topk_rows(xs[s], w, b, topk=6, route_scale=1.0, score_fn="sigmoid")
+                routes.append(idx)
+                grouped_experts(xs[s], idx, wt, store.pool, store.layer_table(s % L), addend=xs[s])
+
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run()
+        g.replay()
+        torch.cuda.synchronize()
+        reps = 3
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(e) * 1e3 / (reps * S)
+        union = sum(len(set(r.reshape(-1).tolist())) for r in routes) / S
+        gbps = union * fmt.algorithmic_bytes / (us * 1e-6) / 1e9
+        out[f"B{B}"] = {"us_per_step": round(us, 2), "tok_per_s": round(B / (us * 1e-6), 1),
+                        "mean_union_experts": round(union, 1), "expert_GBps": round(gbps, 1),
+                        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+        log_fn(f"config 2 B={B}: {us:.1f} us/step, union {union:.1f} experts, {gbps:.0f} GB/s")
+    return out
+
+
+def prefill_config3(args, dev, log_fn):
+    """4096 tokens, FP4 bank, Zipf(1.1)-skewed router bias; one MoE layer."""
+    import torch
+
+    from cachalot_amd import synth
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.router import route_topk_rows
+    from cachalot_amd.storage.index import fp4_format
+
+    D, F, E, K, T = 4096, 2880, 384, 6, 4096
+    fmt = fp4_format(D, F)
+    loader = SyntheticLoader(fmt, args.seed + 3)
+    store = ResidentExpertStore(fmt=fmt, n_slots=E, n_layers=1, n_experts=E, device=dev)
+    store.preload([(0, e) for e in range(E)], loader.fill_key)
+    w, b = synth.router_weights(args.seed + 3, 0, E, D, dev)
+    b = b + torch.tensor(synth.zipf_bias(E, seed=args.seed), dtype=torch.float32, device=dev)
+    x = synth.activations(args.seed + 3, 0, T, D, dev)
+    table = store.layer_table(0)
+
+    def layer():
+        idx, wt, _ = route_topk_rows(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+        _, out = grouped_experts(x, idx, wt, store.pool, table)
+        return idx, out
+
+    idx, _ = layer()
+    torch.cuda.synchronize()
+    reps = 5
+    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        layer()
+    e.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(e) / reps
+    counts = torch.bincount(idx.reshape(-1).long(), minlength=E)
+    touched = int((counts > 0).sum())
+    flops = 2.0 * T * K * 3 * D * F
+    tflops = flops / (ms * 1e-3) / 1e12
+    wbytes = touched * fmt.algorithmic_bytes
+    res = {"ms_per_layer": round(ms, 3), "tflops": round(tflops, 1),
+           "frac_bf16_mfma_peak": round(tflops / 2500.0, 4), "frac_mxfp4_mfma_peak": round(tflops / 10100.0, 4),
+           "experts_touched": touched, "max_rows_per_expert": int(counts.max()),
+           "weight_GBps": round(wbytes / (ms * 1e-3) / 1e9, 1),
+           "note": "exact bf16-MFMA path (FP4 dequantised to bf16 in registers), routing + permute + "
+                   "grouped gate/up + down + combine, eager launches"}
+    log_fn(f"config 3 prefill: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s, {touched} experts touched, "
+           f"max {int(counts.max())} rows/expert")
+    del store
+    torch.cuda.empty_cache()
+    return res
 
 
 def main() -> int:
@@ -283,6 +386,13 @@ def main() -> int:
             "algorithmic_bytes_per_launch": alg_bytes,
         },
     }
+    result["stack40"] = {"layers": L, "us_per_layer_step": round(ms_per_step * 1e3, 2),
+                         "tok_per_s_full_stack": round(1e3 / (ms_per_step * L), 1),
+                         "note": "the chained decode above walks all resident layers in order: one token through "
+                                 f"the {L}-layer stack = {L} steps"}
+    if not args.no_extra:
+        result["config2_batched_decode"] = batched_decode(args, store, gates, log)
+        result["config3_prefill"] = prefill_config3(args, dev, log)
     if not args.no_cpu:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_seconds)
