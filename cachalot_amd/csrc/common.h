@@ -70,6 +70,18 @@ __device__ __forceinline__ float e8m0_to_f32(uint32_t raw) {
   return raw == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(raw << 23);
 }
 
+// ------------------------------------------------------------- barriers ---
+// Workgroup barrier that orders LDS only.  __syncthreads() is a workgroup
+// release/acquire fence on all memory, and since gfx9 counts loads and stores
+// in one counter that fence waits for every outstanding global load; kernels
+// that keep weight loads in flight across a barrier use this one instead and
+// wait for their own global traffic explicitly where another wave consumes it.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ------------------------------------------------------- wave reductions ---
 // Lane exchanges without the LDS crossbar: DPP for partners inside a row of 16
 // lanes, the gfx950 permlane swaps across rows.  xorN(v) returns the value of

@@ -80,12 +80,19 @@ struct RouteTail {
   float route_scale;
 };
 
-// Workspace layout of one decode call: [counters][k slots][k weights][hidden],
-// each region 256-byte aligned.  The counters must be zero before the first
-// call on a workspace (a zero-filled allocation); every call leaves them zero.
-// The rest is scratch: nothing in it survives a call.
+// Workspace layout of one decode call:
+//   [counters 256 B][grid-barrier block 4224 B][k slots][k weights][hidden]
+// each region 256-byte aligned, the first two at fixed offsets whatever k and F
+// are, so calls of different shapes on one workspace never overlap another's
+// counters.  The counters must be zero before the first call on a workspace (a
+// zero-filled allocation); every call leaves them zero.  The grid-barrier block
+// of the one-launch decode keeps a generation count instead (never reset).  The
+// rest is scratch: nothing in it survives a call.
+constexpr size_t WS_SYNC_OFF = 256;
+constexpr size_t WS_SYNC_BYTES = 4352;
+
 struct WsOffsets {
-  size_t counter, slots, weights, hidden, total;
+  size_t counter, sync, slots, weights, hidden, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -93,7 +100,8 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 inline WsOffsets ws_offsets(size_t hidden_bytes) {
   WsOffsets o;
   o.counter = 0;
-  o.slots = 256;
+  o.sync = WS_SYNC_OFF;
+  o.slots = WS_SYNC_OFF + WS_SYNC_BYTES;
   o.weights = o.slots + align256(KMAX * sizeof(int32_t));
   o.hidden = o.weights + align256(KMAX * sizeof(float));
   o.total = o.hidden + align256(hidden_bytes);

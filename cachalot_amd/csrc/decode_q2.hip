@@ -324,9 +324,18 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) q2_down_kernel(
 
 }  // namespace
 
+size_t q2_fused_region_bytes(int F, int k);
+int q2_fused_grid(int D, int F, int k);
+int launch_q2_decode_fused(int G, const uint16_t* x, const uint8_t* pool, const Layout& L, const ExpertSource& src,
+                           const int32_t* ws_slots, const float* ws_w, int D, int F, int k, float limit,
+                           const uint16_t* addend, float* routed, uint16_t* out, uint8_t* sync, uint8_t* hid,
+                           hipStream_t s);
+
+// [two-kernel layout (counters, grid-barrier block, slots, weights, hidden)]
+// [one-launch path: hidden plane blocks]
 size_t q2_workspace_bytes(int D, int F, int k) {
   (void)D;
-  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total;
+  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total + q2_fused_region_bytes(F, k);
 }
 
 // Validates, then launches [router + top-k tail], gate/up and down on stream s.
@@ -346,8 +355,9 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   CACHALOT_REQUIRE(F % 16 == 0 && F >= 64 && F <= GROUP * MAX_F_GROUPS,
                    "moe_decode_q2: F=%d must be a multiple of 16 in 64..4096", F);
   const WsOffsets wo = ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t));
-  if (workspace == nullptr || workspace_bytes < wo.total)
-    return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, wo.total);
+  const size_t need = wo.total + q2_fused_region_bytes(F, k);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, need);
   Layout L;
   static const int used[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
   int rc = make_layout(layout, 9, used, L, "moe_decode_q2");
@@ -367,6 +377,10 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
     src.idx = nullptr;
     src.w = nullptr;
   }
+  const int G = q2_fused_grid(D, F, k);
+  if (G > 0)
+    return launch_q2_decode_fused(G, x, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit, addend, routed, out,
+                                  ws + wo.sync, ws + wo.total, s);
   const int GT = D / GROUP;
   const int nb_gu = ((GT + GU_WAVES - 1) / GU_WAVES + 3) / 4;
   const int xi = (D / 16 + 255) / 256;

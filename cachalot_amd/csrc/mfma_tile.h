@@ -134,8 +134,24 @@ __device__ __forceinline__ void dma_to_lds(const void* src, uint8_t* dst, int by
   }
 }
 
+// One direct-to-LDS load of 16 bytes per lane (lane l writes lds + 16 l), issued as
+// inline asm so the compiler's wait-count tracking does not see it: that tracking
+// cannot tell which LDS reads depend on which such load and would otherwise wait for
+// every outstanding load before the first LDS read.  The caller guarantees
+// completion: a later wait for a register load issued after this one (loads
+// complete in issue order), or wait_vmem().  Clobbers m0.
+__device__ __forceinline__ void lds_load16_untracked(const void* src, void* lds) {
+  const uint32_t la = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(src) : "memory", "m0");
+}
+
 // Wait until every vector-memory load of this wave has landed (registers and LDS).
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// (The builtin, unlike inline asm, is visible to the compiler's wait-count tracking, so
+// it knows that LDS written by direct-to-LDS loads is complete after it.)
+__device__ __forceinline__ void wait_vmem() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // gfx9 encoding: vmcnt(0), expcnt and lgkmcnt unconstrained
+  asm volatile("" ::: "memory");
+}
 
 }  // namespace tile
 }  // namespace cachalot

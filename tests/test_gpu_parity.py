@@ -21,6 +21,14 @@ from oracle.bf16 import bf16_bits_to_f32
 from oracle.fp4 import dequantize_fp4_weight
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["two_kernel", "one_launch"])
+def q2_path(request, monkeypatch):
+    """The 2-bit decode runs as two kernels by default; the one-launch persistent
+    kernel is selected per call with CACHALOT_DECODE_FUSED=1.  Both are pinned."""
+    monkeypatch.setenv("CACHALOT_DECODE_FUSED", "1" if request.param == "one_launch" else "0")
+    return request.param
 TOL = 2e-3
 
 
@@ -236,7 +244,7 @@ def _assert_q2(routed, want, ys, what):
 
 
 @pytest.mark.parametrize("shape", [(4096, 2880), (5120, 2304)])
-def test_decode_q2_parity(cuda, shape):
+def test_decode_q2_parity(cuda, shape, q2_path):
     from cachalot_amd.storage.index import affine_format
 
     D, F = shape
@@ -261,7 +269,7 @@ def test_decode_q2_parity(cuda, shape):
         assert bf16_terms_ok(out, want_r + a, np.concatenate([ys, (want_r + a)[None]]), TOL), t
 
 
-def test_decode_q2_k_range_and_missing_slot(cuda):
+def test_decode_q2_k_range_and_missing_slot(cuda, q2_path):
     from cachalot_amd.storage.index import affine_format
 
     fmt = affine_format(4096, 2880)
@@ -300,7 +308,7 @@ def test_decode_fp4_parity(cuda):
     assert rel_err(routed, want) <= 1e-5     # no bf16 rounding point on this path: fp32-level agreement
 
 
-def test_moe_layer_forward_end_to_end(cuda):
+def test_moe_layer_forward_end_to_end(cuda, q2_path):
     """Router ids bit-exact and the layer output within the bar, through the reference-shaped entry."""
     from cachalot_amd import synth
     from cachalot_amd.moe_layer import moe_layer_forward
@@ -323,7 +331,7 @@ def test_moe_layer_forward_end_to_end(cuda):
 
 
 @pytest.mark.parametrize("kind", ["affine", "fp4"])
-def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind):
+def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind, q2_path):
     """Device-routed decode (scores -> top-k in the gate/up prologue -> down with the
     counter-based combine): ids bit-exact, outputs within the bar, and repeated calls
     on one workspace (counters reset by the kernels) give identical results."""
@@ -363,7 +371,7 @@ def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind):
         assert torch.equal(r, r0) and torch.equal(o, o0)
 
 
-def test_layer_decode_graph_replays_match_eager(cuda):
+def test_layer_decode_graph_replays_match_eager(cuda, q2_path):
     """A captured chain of decode steps replays identically, several times, with
     eager work and synchronisation between replays."""
     from cachalot_amd import synth
