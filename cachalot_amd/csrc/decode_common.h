@@ -109,12 +109,21 @@ inline WsOffsets ws_offsets(size_t hidden_bytes) {
 }
 
 // Where the expert kernels find routed expert e: given ids (idx != null: the
-// slot comes from slot_table) or the router tail's ws_slots / ws_w.
+// slot comes from slot_table), the router's scores (scores != null: the gate/up
+// kernels select the experts themselves, route_expert below) or the workspace's
+// ws_slots / ws_w (written by whoever selected the experts).
 struct ExpertSource {
   const int32_t* slot_table;
   const int32_t* idx;
   const float* w;
   int E;
+  // selection from scores (router half of a layer-decode call)
+  const float* scores;
+  const float* bias;
+  int k, order, norm;
+  float route_scale;
+  int32_t* idx_out;   // may be null
+  float* w_out;       // may be null
 };
 
 __device__ __forceinline__ int expert_slot(const ExpertSource& src, const int32_t* ws_slots, int e) {
@@ -127,6 +136,45 @@ __device__ __forceinline__ int expert_slot(const ExpertSource& src, const int32_
 
 __device__ __forceinline__ float expert_weight(const ExpertSource& src, const float* ws_w, int e) {
   return src.idx ? src.w[e] : ws_w[e];
+}
+
+// Slot of routed expert e, resolved by one whole wave.  With scores the wave
+// runs the selection itself (the router's top-k, the same steps as
+// router_topk_kernel), so no workgroup waits for another; lds_i / lds_v / lds_s
+// are this wave's own KMAX-entry LDS arrays.  Every gate/up workgroup selects
+// for itself and the results are identical.
+__device__ __forceinline__ int route_slot(const ExpertSource& src, const int32_t* ws_slots, int e, int* lds_i,
+                                          float* lds_v, int* lds_s) {
+  if (src.scores == nullptr) return expert_slot(src, ws_slots, e);
+  if (src.E <= 384) wave_topk<6>(src.scores, src.bias, src.E, src.k, src.order, lds_i, lds_v, src.slot_table, lds_s);
+  else wave_topk<16>(src.scores, src.bias, src.E, src.k, src.order, lds_i, lds_v, src.slot_table, lds_s);
+  return lds_s[e];
+}
+
+// Router weight of routed expert e (after route_slot; with scores, the
+// normalisation of the selected scores by lane 0 into lds_w).
+__device__ __forceinline__ float route_weight(const ExpertSource& src, const float* ws_w, int e, const float* lds_v,
+                                              float* lds_w) {
+  if (src.scores == nullptr) return expert_weight(src, ws_w, e);
+  if ((threadIdx.x & 63) == 0) normalise_weights(lds_v, src.k, src.route_scale, src.norm, lds_w);
+  return lds_w[e];
+}
+
+// Epilogue of a gate/up workgroup, lanes 0..15 of wave 0 (the wave whose LDS
+// arrays route_slot filled): the router weight of expert e, also stored for the
+// caller -- ws_w[e] by the expert's first tile, and the selection's ids and
+// weights by workgroup 0.
+__device__ __forceinline__ float route_finish(const ExpertSource& src, float* ws_w, int e, int tile,
+                                              const float* lds_v, float* lds_w, const int* lds_i) {
+  const float w = route_weight(src, ws_w, e, lds_v, lds_w);
+  const int lane = threadIdx.x & 63;
+  if (src.scores == nullptr) return w;
+  if (tile == 0 && lane == 0) ws_w[e] = w;
+  if (blockIdx.x == 0 && lane < src.k) {
+    if (src.idx_out) src.idx_out[lane] = lds_i[lane];
+    if (src.w_out) src.w_out[lane] = lds_w[lane];
+  }
+  return w;
 }
 
 }  // namespace decode

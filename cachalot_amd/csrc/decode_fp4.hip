@@ -56,8 +56,8 @@ __device__ __forceinline__ void lane_pieces(int first, int PW, int pieces, int k
 template <int NB, int XI>
 __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L, ExpertSource src, int D, int F,
-    float limit, uint16_t* __restrict__ hidden, const int32_t* __restrict__ ws_slots,
-    const float* __restrict__ ws_w) {
+    float limit, uint16_t* __restrict__ hidden, int32_t* __restrict__ ws_slots,
+    float* __restrict__ ws_w) {
   __shared__ __align__(16) uint8_t xl[GU_ZERO + ZERO_BYTES];
   __shared__ __align__(16) uint8_t sc[2 * 16 * (MAX_D / PIECE)];   // s1, s3 of the tile's rows
   __shared__ float red[GU_WAVES][2][16];
@@ -68,11 +68,17 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   const int e = blockIdx.x / tiles;
   const int tile = blockIdx.x - e * tiles;
   const int row0 = tile * 16;
-  const int slot = expert_slot(src, ws_slots, e);
-  const float wexp = expert_weight(src, ws_w, e);
+  __shared__ int top_i[GU_WAVES][KMAX];
+  __shared__ float top_v[GU_WAVES][KMAX], top_w[GU_WAVES][KMAX];
+  __shared__ int top_s[GU_WAVES][KMAX];
+  const int slot = route_slot(src, ws_slots, e, top_i[wave], top_v[wave], top_s[wave]);
+  if (src.scores && tile == 0 && threadIdx.x == 0) ws_slots[e] = slot;   // read by the down kernel
   uint16_t* hout = hidden + (size_t)e * F * 2;   // per expert: hi [F], lo [F] (bf16)
   if (slot < 0) {
-    if (threadIdx.x < 16) hout[row0 + threadIdx.x] = hout[F + row0 + threadIdx.x] = 0;
+    if (threadIdx.x < 16) {
+      hout[row0 + threadIdx.x] = hout[F + row0 + threadIdx.x] = 0;
+      route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
+    }
     return;
   }
   const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
@@ -120,6 +126,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   }
   __syncthreads();
   if (threadIdx.x < 16) {
+    const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
     const int t = threadIdx.x;
     float g = 0.0f, u = 0.0f;
 #pragma unroll
@@ -242,16 +249,11 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   uint16_t* hidden = reinterpret_cast<uint16_t*>(ws + wo.hidden);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
-  if (router) {
-    RouteTail tail = router->tail;
-    tail.ws_slots = ws_slots;
-    tail.ws_w = ws_w;
-    tail.counter = &reinterpret_cast<Counters*>(ws + wo.counter)->route_done;
+  if (router) {   // scores only; the gate/up workgroups select the experts
     rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
-                              router->scores, s, &tail);
+                              router->scores, s);
     if (rc) return rc;
-    src.idx = nullptr;
-    src.w = nullptr;
+    src = route_source(src, *router);
   }
   const int PT = D / PIECE;
   const int nb_gu = ((PT + GU_WAVES - 1) / GU_WAVES + 3) / 4;

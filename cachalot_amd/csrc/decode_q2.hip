@@ -109,17 +109,19 @@ __global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
   const int e = blockIdx.x / tiles;
   const int tile = blockIdx.x - e * tiles;
   const int row0 = tile * 16;
-  const int slot = expert_slot(src, ws_slots, e);
-  const float wexp = expert_weight(src, ws_w, e);
-  if (src.idx && tile == 0 && threadIdx.x == 0) {   // the down kernel reads the slots from the workspace
-    ws_slots[e] = slot;
-    ws_w[e] = wexp;
-  }
+  __shared__ int top_i[GU_WAVES][KMAX];
+  __shared__ float top_v[GU_WAVES][KMAX], top_w[GU_WAVES][KMAX];
+  __shared__ int top_s[GU_WAVES][KMAX];
+  const int slot = route_slot(src, ws_slots, e, top_i[wave], top_v[wave], top_s[wave]);
+  if ((src.idx || src.scores) && tile == 0 && threadIdx.x == 0) ws_slots[e] = slot;   // read by the down kernel
   uint16_t* hout = hp + (size_t)e * hidden_stride(F);
   const int tail = (F + GROUP - 1) / GROUP * GROUP - F;
   if (tile == 0 && (int)threadIdx.x < tail) hout[hidden_index(F + threadIdx.x)] = 0;
   if (slot < 0) {   // the expert has no slot: its hidden rows are zero
-    if (threadIdx.x < 16) hout[hidden_index(row0 + threadIdx.x)] = 0;
+    if (threadIdx.x < 16) {
+      hout[hidden_index(row0 + threadIdx.x)] = 0;
+      route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
+    }
     return;
   }
   const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
@@ -207,6 +209,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
   }
   __syncthreads();
   if (threadIdx.x < 16) {
+    const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
     const int t = threadIdx.x;
     float g = 0.0f, u = 0.0f;
 #pragma unroll
@@ -332,14 +335,27 @@ int launch_q2_decode_fused(int G, const uint16_t* x, const uint8_t* pool, const 
                            hipStream_t s);
 
 // [two-kernel layout (counters, grid-barrier block, slots, weights, hidden)]
-// [one-launch path: hidden plane blocks]
+// [matrix-core paths: hidden plane blocks][matrix-core two-kernel path: x plane blocks]
+static size_t xplanes_bytes(int D) { return align256((size_t)(D + 127) / 128 * 320); }
 size_t q2_workspace_bytes(int D, int F, int k) {
-  (void)D;
-  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total + q2_fused_region_bytes(F, k);
+  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total + q2_fused_region_bytes(F, k) +
+         xplanes_bytes(D);
 }
 
 // Validates, then launches [router + top-k tail], gate/up and down on stream s.
 // With `router` the experts come from the router tail, else from src.idx / src.w.
+
+bool q2mx_supported(int D, int F, int k);
+int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, const uint8_t* pool,
+                       const Layout& L, const ExpertSource& src, int32_t* ws_slots, float* ws_w, int D, int F,
+                       int k, float limit, const uint16_t* addend, float* routed, uint16_t* out, uint8_t* hid,
+                       hipStream_t s);
+
+// The bf16 kernels stay selectable (CACHALOT_DECODE_BF16=1) for comparison.
+static bool bf16_requested() {
+  const char* env = getenv("CACHALOT_DECODE_BF16");
+  return env && env[0] == '1';
+}
 
 int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
                      ExpertSource src, const RouterCall* router, int D, int F, int k, int group, float swiglu_limit,
@@ -355,7 +371,7 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   CACHALOT_REQUIRE(F % 16 == 0 && F >= 64 && F <= GROUP * MAX_F_GROUPS,
                    "moe_decode_q2: F=%d must be a multiple of 16 in 64..4096", F);
   const WsOffsets wo = ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t));
-  const size_t need = wo.total + q2_fused_region_bytes(F, k);
+  const size_t need = q2_workspace_bytes(D, F, k);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, need);
   Layout L;
@@ -366,7 +382,15 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   uint16_t* hp = reinterpret_cast<uint16_t*>(ws + wo.hidden);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
-  if (router) {
+  const int G = q2_fused_grid(D, F, k);
+  const bool mx = G == 0 && q2mx_supported(D, F, k) && !bf16_requested();
+  uint8_t* xplanes = ws + wo.total + q2_fused_region_bytes(F, k);
+  if (router && G == 0) {   // scores only; the gate/up workgroups select the experts
+    rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
+                              router->scores, s, nullptr, mx ? xplanes : nullptr);
+    if (rc) return rc;
+    src = route_source(src, *router);
+  } else if (router) {
     RouteTail tail = router->tail;
     tail.ws_slots = ws_slots;
     tail.ws_w = ws_w;
@@ -377,7 +401,9 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
     src.idx = nullptr;
     src.w = nullptr;
   }
-  const int G = q2_fused_grid(D, F, k);
+  if (mx)
+    return launch_q2mx_decode(x, router != nullptr, xplanes, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit,
+                              addend, routed, out, ws + wo.total, s);
   if (G > 0)
     return launch_q2_decode_fused(G, x, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit, addend, routed, out,
                                   ws + wo.sync, ws + wo.total, s);

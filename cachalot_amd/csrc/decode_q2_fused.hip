@@ -44,6 +44,15 @@ using mx::i32x8_t;
 using mx::PB_BYTES;
 using mx::PB_SCALE;
 using mx::PB_SUM;
+using mx::ARole;
+using mx::Chain;
+using mx::a_role;
+using mx::chain_init;
+using mx::chain_load;
+using mx::dot4;
+using mx::piece_sums;
+using mx::lds16;
+using mx::bf16_lo;
 
 constexpr int THREADS = 1024;
 constexpr int WAVES = THREADS / 64;
@@ -112,81 +121,6 @@ struct Lds {
   uint8_t dn_tdl[MAX_DN_ITEMS], dn_e[MAX_DN_ITEMS], dn_q2[MAX_DN_ITEMS];
   int16_t t_e[MAX_T], t_p[MAX_T];                     // tile -> expert, 16-row piece within the expert
 };
-
-__device__ __forceinline__ uint4 lds16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ __forceinline__ uint32_t lds32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
-
-// Per-lane roles in the group-separated layout (mx_tile.h): which half of the A
-// operand carries this lane's data (lo: bytes 0..15, hi: 16..31, or neither) and
-// whether it supplies its row's scale.
-struct ARole {
-  int kgR, halfR, planeR;
-  bool lo, hi, scale;
-};
-__device__ __forceinline__ ARole a_role(int lane) {
-  ARole r;
-  const int row = lane & 15, kgA = lane >> 4;
-  r.kgR = row >> 2;
-  r.halfR = (row >> 1) & 1;
-  r.planeR = row & 1;
-  const bool act = kgA == 2 * (r.kgR & 1) + r.halfR;
-  r.lo = act && r.kgR < 2;
-  r.hi = act && r.kgR >= 2;
-  r.scale = kgA == r.kgR;
-  return r;
-}
-
-// The A operands of one group-separated chain (four steps) in persistent
-// registers: a lane's role never changes, so only its data half is rewritten, by
-// one exec-masked block of four contiguous 16-byte LDS reads (the plane block keeps
-// a lane's four steps together); the other half, the other lanes' data and the
-// other lanes' scales (1.0: their blocks of the row hold zeros, so any finite scale
-// gives exact zeros) keep the values set once by chain_init.  The scale lanes read
-// one u32 holding their four step scales (byte c for step c).
-struct Chain {
-  i32x8_t a[4];
-  uint32_t sa;
-};
-__device__ __forceinline__ void chain_init(Chain& ch) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ch.a[c][i] = 0;
-  ch.sa = 0x7F7F7F7Fu;
-}
-__device__ __forceinline__ void chain_load(Chain& ch, const uint8_t* blk, const ARole& ro) {
-  const uint8_t* src = blk + (ro.halfR * 2 + ro.planeR) * 64;
-  if (ro.lo) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint4 d = lds16(src + 16 * c);
-      ch.a[c][0] = (int)d.x; ch.a[c][1] = (int)d.y; ch.a[c][2] = (int)d.z; ch.a[c][3] = (int)d.w;
-    }
-  }
-  if (ro.hi) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint4 d = lds16(src + 16 * c);
-      ch.a[c][4] = (int)d.x; ch.a[c][5] = (int)d.y; ch.a[c][6] = (int)d.z; ch.a[c][7] = (int)d.w;
-    }
-  }
-  if (ro.scale) ch.sa = lds32(blk + PB_SCALE + (ro.halfR * 2 + ro.planeR) * 4);
-}
-
-__device__ __forceinline__ float dot4(const f32x4_t& d) { return (d[0] + d[1]) + (d[2] + d[3]); }
-
-// Sum of the first `npieces` piece sums of a plane block (fixed order).
-__device__ __forceinline__ float piece_sums(const uint8_t* blk, int npieces) {
-  const float4 a = *reinterpret_cast<const float4*>(blk + PB_SUM);
-  const float4 b = *reinterpret_cast<const float4*>(blk + PB_SUM + 16);
-  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  float s = 0.0f;
-#pragma unroll
-  for (int p = 0; p < mx::PIECES; ++p) s = s + (p < npieces ? v[p] : 0.0f);
-  return s;
-}
-
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return bf16_to_f32((uint16_t)w); }
 
 template <int MAXGU, int MAXDN, int XP>
 __global__ void __launch_bounds__(THREADS) q2_decode_fused_kernel(FusedQ2 p) {
@@ -268,24 +202,7 @@ __global__ void __launch_bounds__(THREADS) q2_decode_fused_kernel(FusedQ2 p) {
 #pragma unroll
   for (int i = 0; i < XP; ++i) {
     const int t4 = tid + THREADS * i;
-    if (4 * t4 < D) {   // uniform per quad
-      const float v0 = bf16_to_f32((uint16_t)xr[i].x), v1 = bf16_to_f32((uint16_t)(xr[i].x >> 16));
-      const float v2 = bf16_to_f32((uint16_t)xr[i].y), v3 = bf16_to_f32((uint16_t)(xr[i].y >> 16));
-      const mx::PieceCode4 pc = mx::encode_piece4(v0, v1, v2, v3);
-      const int P = t4 >> 2, q4 = t4 & 3, pp = P & 7;
-      uint8_t* gb = s.planes + (P >> 3) * PB_BYTES;
-      uint8_t* hi = gb + mx::pb_data(pp, 0);
-      uint8_t* lo = gb + mx::pb_data(pp, 1);
-      *reinterpret_cast<uint16_t*>(hi + 2 * q4) = (uint16_t)pc.hi_a;
-      *reinterpret_cast<uint16_t*>(hi + 8 + 2 * q4) = (uint16_t)pc.hi_b;
-      *reinterpret_cast<uint16_t*>(lo + 2 * q4) = (uint16_t)pc.lo_a;
-      *reinterpret_cast<uint16_t*>(lo + 8 + 2 * q4) = (uint16_t)pc.lo_b;
-      if (q4 == 0) {
-        gb[mx::pb_scale(pp, 0)] = (uint8_t)pc.scales;
-        gb[mx::pb_scale(pp, 1)] = (uint8_t)(pc.scales >> 8);
-        *reinterpret_cast<float*>(gb + PB_SUM + 4 * pp) = pc.sum;
-      }
-    }
+    if (4 * t4 < D) mx::encode_x_quad(s.planes, t4, xr[i]);   // uniform per quad
   }
   lds_sync();
   PHASE(2);

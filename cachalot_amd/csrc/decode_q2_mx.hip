@@ -1,0 +1,390 @@
+// Decode (one token) over a 2-bit affine g128 bank in two launches on the
+// block-scaled fp8 x fp4 matrix cores (mx_tile.h): v_mfma_scale_f32_16x16x128
+// takes 16 weight rows x 128 codes per instruction, four times the weights of
+// a bf16 step, with the 2-bit codes used as fp4 operands unconverted.
+//
+// Reference semantics: src/cachalot/model/expert_affine.py:65-81 (bf16 g, u,
+// h, y_e rounding points), :117-152 (experts summed in route order from zero),
+// mx.quantized_matmul's group formula s * sum(x q) + b * sum(x) (as copied at
+// minimax/codes_qmv.py:86-100).
+//
+//   q2mx_gate_up_kernel  one 256-thread workgroup = one expert x one 16-row tile
+//     of W1 and W3.  One wave (blockIdx % 4, so the routing waves of the
+//     workgroups sharing a CU sit on different SIMDs) resolves the expert --
+//     with the router's scores it runs the top-k itself -- while the other
+//     three copy x's fp8 plane blocks (written once per token by the router
+//     kernel or x_planes_kernel) into LDS.  Items are (tile, quad of four
+//     128-code groups), quad q to wave q % 4; per item one direct-to-LDS copy of
+//     the four scale / bias chunks, then the codes, then four block-scaled MFMAs
+//     per matrix sharing the A operand.  Epilogue: bf16(g), bf16(u), clamp,
+//     h = bf16(silu(g) * u * w_e), stored as one fp8 plane piece of the
+//     expert's hidden plane blocks (16 rows = one piece).
+//   q2mx_down_kernel  one 768-thread workgroup = one 16-row tile of W2 for all k
+//     experts; items (expert, quad) dealt round-robin to 12 waves.  The k
+//     hidden plane blocks and the tile's scale / bias runs are copied into LDS;
+//     each expert's row value is rounded to bf16 and the experts are summed in
+//     route order, + addend.
+//
+// Summation orders (fixed, so results are reproducible): per item the four
+// (piece, plane) partial sums of a group, then the four groups of a quad
+// (lane-group butterfly), then the quads in order.
+#include "decode_common.h"
+#include "mfma_tile.h"
+#include "mx_tile.h"
+
+namespace cachalot {
+namespace {
+
+using namespace decode;
+using mx::a_role;
+using mx::ARole;
+using mx::bf16_lo;
+using mx::Chain;
+using mx::chain_init;
+using mx::chain_load;
+using mx::dot4;
+using mx::f32x4_t;
+using mx::i32x8_t;
+using mx::PB_BYTES;
+using mx::PB_SCALE;
+using mx::PB_SUM;
+using mx::piece_sums;
+
+constexpr int GU_THREADS = 256;
+constexpr int GU_WAVES = GU_THREADS / 64;
+constexpr int MAX_GT = 40;                     // D <= 5120
+constexpr int MAX_NQ = MAX_GT / 4;
+constexpr int MAX_GK = 24;                     // F <= 3072
+constexpr int MAX_NQ2 = MAX_GK / 4;
+constexpr int GU_MAXM = (MAX_NQ + GU_WAVES - 1) / GU_WAVES;   // items per wave
+constexpr int DN_THREADS = 768;
+constexpr int DN_WAVES = DN_THREADS / 64;
+
+struct GuLds {
+  uint8_t planes[MAX_GT * PB_BYTES];
+  uint8_t scl[GU_WAVES][GU_MAXM][1024];   // per wave and item: [s1, b1, s3, b3][16 rows] 16-byte chunks
+  float red[MAX_NQ][2][16];
+  int top_i[KMAX], top_s[KMAX];
+  float top_v[KMAX], top_w[KMAX];
+  int slot;
+};
+
+struct DnLds {
+  uint8_t planes[KMAX * MAX_GK * PB_BYTES];
+  uint16_t sc[KMAX][2][16 * MAX_GK];      // per expert: s2, b2 runs of the tile's rows
+  float red[KMAX][MAX_NQ2][16];
+  float y[KMAX][16];
+};
+
+// Copy `bytes` (a multiple of 16) into LDS with untracked direct-to-LDS loads
+// (tile::lds_load16_untracked): 1 KiB chunks c = part, part + parts, ...  The
+// caller waits (wait_vmem) before the data is read.
+__device__ __forceinline__ void copy_to_lds_untracked(const uint8_t* src, uint8_t* dst, int bytes, int part,
+                                                      int parts, int lane) {
+  for (int c = part * 1024; c < bytes; c += parts * 1024)
+    if (c + 16 * lane < bytes) tile::lds_load16_untracked(src + c + 16 * lane, dst + c);
+}
+
+// x (one token) as fp8 plane blocks, for calls whose experts are given (no router launch).
+__global__ void __launch_bounds__(256) x_planes_kernel(const uint16_t* __restrict__ x, int D,
+                                                       uint8_t* __restrict__ xplanes) {
+  const int t4 = blockIdx.x * 256 + threadIdx.x;
+  if (4 * t4 < D) mx::encode_x_quad(xplanes, t4, reinterpret_cast<const uint2*>(x)[t4]);   // whole quads
+}
+
+// grid.x = k * F / 16.  MAXM = ceil(D / 512 / 4) items per wave.
+template <int MAXM>
+__global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t* __restrict__ xplanes,
+                                                                  const uint8_t* __restrict__ pool, Layout L,
+                                                                  ExpertSource src, int D, int F, float limit,
+                                                                  uint8_t* __restrict__ hid,
+                                                                  int32_t* __restrict__ ws_slots,
+                                                                  float* __restrict__ ws_w) {
+  __shared__ __align__(16) GuLds s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kg = lane >> 4;
+  const int GT = D / 128, NQ = GT / 4;
+  const int GK = (F + 127) / 128, FT = F / 16;
+  const int e = blockIdx.x / FT;
+  const int tile = blockIdx.x - e * FT;
+  const int row0 = tile * 16;
+  const int rw = blockIdx.x & (GU_WAVES - 1);   // the routing wave
+
+  // ---- 0. routing wave: the expert's slot; the others: x's plane blocks into LDS
+  if (wave == rw) {
+    const int slot = route_slot(src, ws_slots, e, s.top_i, s.top_v, s.top_s);
+    if (lane == 0) {
+      s.slot = slot;
+      if ((src.idx || src.scores) && tile == 0) ws_slots[e] = slot;   // read by the down kernel
+    }
+  } else {
+    copy_to_lds_untracked(xplanes, s.planes, GT * PB_BYTES, wave < rw ? wave : wave - 1, GU_WAVES - 1, lane);
+    tile::wait_vmem();
+  }
+  lds_sync();
+  const int slot = s.slot;
+  const bool live = slot >= 0;
+
+  // ---- 1. loads: per item the scale / bias chunk copy (lane = tensor x row), then the codes
+  uint4 c1[MAXM][2], c3[MAXM][2];
+  int gsb[MAXM];   // byte of the item's first group inside its scale chunks
+  if (live) {
+    const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
+    const int t = lane >> 4, r = lane & 15;
+    const int64_t toff = t == 0 ? L.off[1] : t == 1 ? L.off[2] : t == 2 ? L.off[7] : L.off[8];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int q = min(wave + GU_WAVES * m, NQ - 1);
+      const int o = ((row0 + r) * GT + 4 * q) * 2;
+      tile::lds_load16_untracked(base + toff + (o & ~15), s.scl[wave][m]);
+      gsb[m] = (8 * q) & 15;
+      const int64_t off = (int64_t)(row0 + j) * (D / 4) + (4 * q + kg) * 32;
+      const uint4* r1 = reinterpret_cast<const uint4*>(base + L.off[0] + off);
+      const uint4* r3 = reinterpret_cast<const uint4*>(base + L.off[6] + off);
+      c1[m][0] = r1[0];
+      c1[m][1] = r1[1];
+      c3[m][0] = r3[0];
+      c3[m][1] = r3[1];
+    }
+  }
+
+  // ---- 2. items
+  const ARole ro = a_role(lane);
+  Chain ch;
+  chain_init(ch);
+#pragma unroll
+  for (int m = 0; m < MAXM; ++m) {
+    const int q = wave + GU_WAVES * m;
+    if (!live || q >= NQ) break;
+    // the item's last code load has landed, hence (loads complete in issue order) its
+    // earlier scale copy too; no LDS read of the scales may move above this point
+    asm volatile("" ::"v"(c3[m][1].w) : "memory");
+    f32x4_t a1 = mx::zero_acc(), a3 = mx::zero_acc();
+    chain_load(ch, s.planes + (4 * q + ro.kgR) * PB_BYTES, ro);
+    a1 = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c1[m][0].x, c1[m][0].y), a1, ch.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c3[m][0].x, c3[m][0].y), a3, ch.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c1[m][0].z, c1[m][0].w), a1, ch.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c3[m][0].z, c3[m][0].w), a3, ch.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c1[m][1].x, c1[m][1].y), a1, ch.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c3[m][1].x, c3[m][1].y), a3, ch.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c1[m][1].z, c1[m][1].w), a1, ch.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c3[m][1].z, c3[m][1].w), a3, ch.sa, mx::E8M0_TWO);
+    const float sx = piece_sums(s.planes + (4 * q + kg) * PB_BYTES, mx::PIECES);
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(s.scl[wave][m]) + (j * 16 + gsb[m] + 2 * kg) / 2;
+    const float v1 = bf16_to_f32(sc[0]) * dot4(a1) + bf16_to_f32(sc[128]) * sx;
+    const float v3 = bf16_to_f32(sc[256]) * dot4(a3) + bf16_to_f32(sc[384]) * sx;
+    const float r1 = tile::sum_lane_groups(v1);
+    const float r3 = tile::sum_lane_groups(v3);
+    if (lane < 16) {
+      s.red[q][0][lane] = r1;
+      s.red[q][1][lane] = r3;
+    }
+  }
+  lds_sync();
+
+  // ---- 3. epilogue (16 lanes of wave 0): h for the tile's rows as one plane piece
+  if (tid < 16) {
+    const float wexp = route_finish(src, ws_w, e, tile, s.top_v, s.top_w, s.top_i);
+    float hv = 0.0f;
+    if (live) {
+      float rg[MAX_NQ], ru[MAX_NQ];
+#pragma unroll
+      for (int q = 0; q < MAX_NQ; ++q) {
+        rg[q] = s.red[q][0][tid];
+        ru[q] = s.red[q][1][tid];
+      }
+      float g = 0.0f, u = 0.0f;
+#pragma unroll
+      for (int q = 0; q < MAX_NQ; ++q) {
+        if (q < NQ) {
+          g = g + rg[q];
+          u = u + ru[q];
+        }
+      }
+      g = round_bf16(g);
+      u = round_bf16(u);
+      if (limit > 0.0f) {
+        u = fminf(fmaxf(u, -limit), limit);
+        g = fminf(g, limit);
+      }
+      hv = round_bf16((silu_f32(g) * u) * wexp);
+    }
+    const mx::PieceCode pc = mx::encode_piece(hv);
+    const int pp = tile & 7;
+    uint8_t* blk = hid + ((int64_t)e * GK + (tile >> 3)) * PB_BYTES;
+    blk[mx::pb_data(pp, 0) + mx::piece_pos(tid)] = (uint8_t)pc.hi;
+    blk[mx::pb_data(pp, 1) + mx::piece_pos(tid)] = (uint8_t)pc.lo;
+    if (tid == 0) {
+      blk[mx::pb_scale(pp, 0)] = (uint8_t)pc.scales;
+      blk[mx::pb_scale(pp, 1)] = (uint8_t)(pc.scales >> 8);
+      *reinterpret_cast<float*>(blk + PB_SUM + 4 * pp) = pc.sum;
+    }
+    if (tile == FT - 1) {   // pieces of the last group past F: zeros (consumers read whole steps)
+      for (int z = pp + 1; z < mx::PIECES; ++z) {
+        blk[mx::pb_data(z, 0) + tid] = 0;
+        blk[mx::pb_data(z, 1) + tid] = 0;
+        if (tid == 0) {
+          blk[mx::pb_scale(z, 0)] = 127;
+          blk[mx::pb_scale(z, 1)] = 127;
+          *reinterpret_cast<float*>(blk + PB_SUM + 4 * z) = 0.0f;
+        }
+      }
+    }
+  }
+}
+
+// grid.x = D / 16.  MAXM = ceil(k * ceil(GK / 4) / 12) items per wave.
+template <int MAXM>
+__global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __restrict__ pool, Layout L,
+                                                               const int32_t* __restrict__ ws_slots, int D, int F,
+                                                               int k, const uint8_t* __restrict__ hid,
+                                                               const uint16_t* __restrict__ addend,
+                                                               float* __restrict__ routed,
+                                                               uint16_t* __restrict__ out) {
+  __shared__ __align__(16) DnLds s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kg = lane >> 4;
+  const int GK = (F + 127) / 128, NQ2 = (GK + 3) / 4, FT = F / 16;
+  const int row0 = blockIdx.x * 16;
+  const int n_items = k * NQ2;
+
+  // ---- 0. the slots (KMAX entries are allocated) -> the wave's W2 codes into
+  //         registers, then the tile's scale / bias runs and the hidden plane
+  //         blocks into LDS; one wait for all of it
+  int eslot[KMAX];
+#pragma unroll
+  for (int e = 0; e < KMAX; ++e) eslot[e] = ws_slots[e];
+  uint4 c2[MAXM][2];
+  int it_e[MAXM], it_q[MAXM];
+  bool on[MAXM];
+#pragma unroll
+  for (int m = 0; m < MAXM; ++m) {
+    const int it = wave + DN_WAVES * m;
+    const int itc = min(it, n_items - 1);
+    it_e[m] = itc / NQ2;
+    it_q[m] = itc - it_e[m] * NQ2;
+    int slot = eslot[0];
+#pragma unroll
+    for (int e = 1; e < KMAX; ++e) slot = e == it_e[m] ? eslot[e] : slot;
+    on[m] = it < n_items && slot >= 0;
+    const int g2 = min(4 * it_q[m] + kg, GK - 1);
+    const uint8_t* base = pool + (int64_t)max(slot, 0) * L.record_bytes;
+    const uint4* r2 = reinterpret_cast<const uint4*>(base + L.off[3] + (int64_t)(row0 + j) * (GK * 32) + g2 * 32);
+    c2[m][0] = r2[0];
+    c2[m][1] = r2[1];
+  }
+  {
+    const int run = 32 * GK;   // 16 rows x GK bf16
+#pragma unroll
+    for (int r0 = 0; r0 < 2 * KMAX; r0 += DN_WAVES) {
+      const int r = r0 + wave;
+      if (r < 2 * k) {
+        int ps = eslot[0];
+#pragma unroll
+        for (int e = 1; e < KMAX; ++e) ps = e == (r >> 1) ? eslot[e] : ps;
+        ps = max(ps, 0);   // a missing expert's rows are never used
+        copy_to_lds_untracked(pool + (int64_t)ps * L.record_bytes + ((r & 1) ? L.off[5] : L.off[4]) +
+                                  (int64_t)row0 * GK * 2,
+                              reinterpret_cast<uint8_t*>(s.sc[r >> 1][r & 1]), run, 0, 1, lane);
+      }
+    }
+  }
+  copy_to_lds_untracked(hid, s.planes, k * GK * PB_BYTES, wave, DN_WAVES, lane);
+  tile::wait_vmem();
+  lds_sync();
+
+  // ---- 1. items
+  const ARole ro = a_role(lane);
+  Chain ch;
+  chain_init(ch);
+#pragma unroll
+  for (int m = 0; m < MAXM; ++m) {
+    if (!on[m]) continue;
+    const int e = it_e[m], q2 = it_q[m];
+    const int g2 = 4 * q2 + kg;
+    const uint8_t* blkA = s.planes + (e * GK + min(4 * q2 + ro.kgR, GK - 1)) * PB_BYTES;
+    const float sh = g2 < GK ? piece_sums(s.planes + (e * GK + g2) * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
+    f32x4_t acc = mx::zero_acc();
+    chain_load(ch, blkA, ro);
+    acc = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c2[m][0].x, c2[m][0].y), acc, ch.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c2[m][0].z, c2[m][0].w), acc, ch.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c2[m][1].x, c2[m][1].y), acc, ch.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c2[m][1].z, c2[m][1].w), acc, ch.sa, mx::E8M0_TWO);
+    const int si = j * GK + min(g2, GK - 1);
+    float v = g2 < GK ? bf16_to_f32(s.sc[e][0][si]) * dot4(acc) + bf16_to_f32(s.sc[e][1][si]) * sh : 0.0f;
+    v = tile::sum_lane_groups(v);
+    if (lane < 16) s.red[e][q2][lane] = v;
+  }
+  lds_sync();
+
+  // ---- 2. per expert (16 lanes each): the row values rounded to bf16; then the
+  //         route-order sum of the tile's rows
+  if (tid < 16 * k) {
+    const int e = tid >> 4, r = tid & 15;
+    float part[MAX_NQ2];
+#pragma unroll
+    for (int q2 = 0; q2 < MAX_NQ2; ++q2) part[q2] = s.red[e][q2][r];
+    float y = 0.0f;
+#pragma unroll
+    for (int q2 = 0; q2 < MAX_NQ2; ++q2)
+      if (q2 < NQ2) y = y + part[q2];
+    int se = eslot[0];
+#pragma unroll
+    for (int x = 1; x < KMAX; ++x) se = x == e ? eslot[x] : se;
+    s.y[e][r] = se >= 0 ? round_bf16(y) : 0.0f;
+  }
+  lds_sync();
+  if (tid < 16) {
+    const int n = row0 + tid;
+    float total = 0.0f;
+    for (int e = 0; e < k; ++e) total = total + s.y[e][tid];
+    if (routed) routed[n] = total;
+    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(addend[n]) : total);
+  }
+}
+
+}  // namespace
+
+// The shapes the matrix-core path takes (the rest use the bf16 kernels).
+bool q2mx_supported(int D, int F, int k) {
+  return D % 1024 == 0 && D <= 128 * MAX_GT && F % 16 == 0 && F <= 128 * MAX_GK && k >= 1 && k <= KMAX;
+}
+
+// hid: k * ceil(F / 128) plane blocks; xplanes: D / 128 plane blocks, written by
+// the router kernel when planes_ready, else here.
+int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, const uint8_t* pool,
+                       const Layout& L, const ExpertSource& src, int32_t* ws_slots, float* ws_w, int D, int F,
+                       int k, float limit, const uint16_t* addend, float* routed, uint16_t* out, uint8_t* hid,
+                       hipStream_t s) {
+  if (!planes_ready) {
+    hipLaunchKernelGGL(x_planes_kernel, dim3((D / 4 + 255) / 256), dim3(256), 0, s, x, D, xplanes);
+    const int rc = check_launch("x_planes_kernel");
+    if (rc) return rc;
+  }
+  const int NQ = D / 512;
+  const int mg = (NQ + GU_WAVES - 1) / GU_WAVES;
+  const dim3 grid_gu(k * (F / 16));
+#define CACHALOT_GU(MV)                                                                                           \
+  hipLaunchKernelGGL((q2mx_gate_up_kernel<MV>), grid_gu, dim3(GU_THREADS), 0, s, xplanes, pool, L, src, D, F, limit, \
+                     hid, ws_slots, ws_w)
+  if (mg <= 2) CACHALOT_GU(2);
+  else CACHALOT_GU(3);
+#undef CACHALOT_GU
+  int rc = check_launch("q2mx_gate_up_kernel");
+  if (rc) return rc;
+  const int NQ2 = ((F + 127) / 128 + 3) / 4;
+  const int md = (k * NQ2 + DN_WAVES - 1) / DN_WAVES;
+#define CACHALOT_DN(MV)                                                                                          \
+  hipLaunchKernelGGL((q2mx_down_kernel<MV>), dim3(D / 16), dim3(DN_THREADS), 0, s, pool, L, ws_slots, D, F, k, hid, \
+                     addend, routed, out)
+  if (md <= 3) CACHALOT_DN(3);
+  else CACHALOT_DN(4);
+#undef CACHALOT_DN
+  return check_launch("q2mx_down_kernel");
+}
+
+}  // namespace cachalot

@@ -20,6 +20,7 @@
 //                         are loaded once per wave and reused for TT tokens.
 //   router_topk_kernel    one wave per token; k rounds of a wave-wide argmax
 //                         under the order's total order (value, then index).
+#include "mx_tile.h"
 #include "router_launch.h"
 #include "topk.h"
 
@@ -79,7 +80,7 @@ __device__ float score_of(float z32, int fn) {
 template <int TT, int NV>
 __device__ __forceinline__ void router_row(const uint16_t* __restrict__ x, const uint16_t* __restrict__ W, int T,
                                            int D, int E, float gate_temp, int fn, float* __restrict__ scores,
-                                           int row, int lane) {
+                                           int row, int lane, bool coherent) {
   const int t0 = blockIdx.y * TT;
   const int ch = D / CHUNKS;
   const uint16_t* wrow = W + (size_t)row * D + (size_t)lane * ch;
@@ -130,39 +131,47 @@ __device__ __forceinline__ void router_row(const uint16_t* __restrict__ x, const
     for (int j = 1; j < TT; ++j)
       if (lane == j) v = acc[j];
     const int t = t0 + lane;
-    if (t < T) scores[(size_t)t * E + row] = score_of(v / gate_temp, fn);
+    if (t < T) {
+      const float sc = score_of(v / gate_temp, fn);
+      // with the top-k tail, stored through to where every XCD reads (see route_tail)
+      if (coherent) __hip_atomic_store(&scores[(size_t)t * E + row], sc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else scores[(size_t)t * E + row] = sc;
+    }
   }
 }
 
 // Top-k tail for one token: every workgroup counts itself finished; the last one
 // selects the experts (one wave), normalises the weights, resolves the slots and
-// returns the counter to zero.  The release/acquire fences order the other
-// workgroups' score stores before the selection's loads.
+// returns the counter to zero.  Protocol: the scores are stored with agent-scope
+// (write-through) stores and each wave waits for its stores to complete before
+// the workgroup counts itself with a returning agent-scope add; the selecting
+// wave reads the scores with agent-scope loads.  (No release/acquire fences:
+// those write back / invalidate whole L2s.)
 __device__ __forceinline__ void route_tail(const float* __restrict__ scores, const decode::RouteTail& tail) {
   __shared__ int last;
-  __shared__ int top_i[decode::KMAX];
+  __shared__ int top_i[decode::KMAX], top_s[decode::KMAX];
   __shared__ float top_v[decode::KMAX];
   __shared__ float w[decode::KMAX];
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's score stores are complete
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
-    const unsigned done = atomicAdd(tail.counter, 1u);
+    const unsigned done = __hip_atomic_fetch_add(tail.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = done == gridDim.x * gridDim.y - 1;
   }
   __syncthreads();
   if (!last || threadIdx.x >= 64) return;
-  __threadfence();
-  if (tail.E <= 384) wave_topk<6>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v);
-  else wave_topk<16>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v);
+  if (tail.E <= 384)
+    wave_topk<6, true>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v, tail.slot_table, top_s);
+  else
+    wave_topk<16, true>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v, tail.slot_table, top_s);
   if (threadIdx.x == 0) normalise_weights(top_v, tail.k, tail.route_scale, tail.norm, w);
   if (threadIdx.x < tail.k) {
-    const int ex = top_i[threadIdx.x];
-    tail.ws_slots[threadIdx.x] = tail.slot_table[ex];
+    tail.ws_slots[threadIdx.x] = top_s[threadIdx.x];
     tail.ws_w[threadIdx.x] = w[threadIdx.x];
-    if (tail.idx_out) tail.idx_out[threadIdx.x] = ex;
+    if (tail.idx_out) tail.idx_out[threadIdx.x] = top_i[threadIdx.x];
     if (tail.w_out) tail.w_out[threadIdx.x] = w[threadIdx.x];
   }
-  if (threadIdx.x == 0) *tail.counter = 0u;
+  if (threadIdx.x == 0) __hip_atomic_store(tail.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One wave per expert row (lane l owns chunk l of D/64 elements), TT tokens per
@@ -171,10 +180,15 @@ template <int TT, int NV>
 __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ W, int T, int D,
                                                             int E, float gate_temp, int fn,
-                                                            float* __restrict__ scores, decode::RouteTail tail) {
+                                                            float* __restrict__ scores, decode::RouteTail tail,
+                                                            uint8_t* __restrict__ xplanes) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row < E) router_row<TT, NV>(x, W, T, D, E, gate_temp, fn, scores, row, lane);
+  if (xplanes != nullptr && blockIdx.y == 0) {   // token 0 as fp8 planes for the matrix-core decode
+    for (int t4 = blockIdx.x * 256 + (int)threadIdx.x; 4 * t4 < D; t4 += gridDim.x * 256)
+      mx::encode_x_quad(xplanes, t4, reinterpret_cast<const uint2*>(x)[t4]);   // whole quads of lanes
+  }
+  if (row < E) router_row<TT, NV>(x, W, T, D, E, gate_temp, fn, scores, row, lane, tail.counter != nullptr);
   if (tail.counter != nullptr) route_tail(scores, tail);
 }
 
@@ -201,21 +215,21 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict
 
 template <int TT>
 static void launch_scores_tt(const uint16_t* x, const uint16_t* W, int T, int D, int E, float temp, int fn,
-                             float* scores, hipStream_t s, const decode::RouteTail& tail) {
+                             float* scores, hipStream_t s, const decode::RouteTail& tail, uint8_t* xplanes) {
   dim3 grid((E + 3) / 4, (T + TT - 1) / TT);
   switch (D) {
-    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
-    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
-    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
-    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail); break;
+    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
   }
 }
 
 int launch_router_scores(const uint16_t* x, const uint16_t* W, int T, int D, int E, float gate_temp, int fn,
-                         float* scores, hipStream_t s, const decode::RouteTail* tail) {
+                         float* scores, hipStream_t s, const decode::RouteTail* tail, uint8_t* xplanes) {
   decode::RouteTail none{};
-  if (T >= 4) launch_scores_tt<4>(x, W, T, D, E, gate_temp, fn, scores, s, none);
-  else launch_scores_tt<1>(x, W, T, D, E, gate_temp, fn, scores, s, tail && T == 1 ? *tail : none);
+  if (T >= 4) launch_scores_tt<4>(x, W, T, D, E, gate_temp, fn, scores, s, none, nullptr);
+  else launch_scores_tt<1>(x, W, T, D, E, gate_temp, fn, scores, s, tail && T == 1 ? *tail : none, xplanes);
   return check_launch("router_scores_kernel");
 }
 
