@@ -235,6 +235,49 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
   }
 }
 
+// Down items m0 .. m0 + NI - 1 of a wave, interleaved.
+template <int NI, int MAXM>
+__device__ __forceinline__ void down_items(DnLds& s, const uint4 (&c2)[MAXM][2], const int (&it_e)[MAXM],
+                                           const int (&it_q)[MAXM], const bool (&on)[MAXM], int m0,
+                                           const ARole& ro, int GK, int FT, int j, int kg, int lane) {
+  Chain ch[NI];
+  f32x4_t acc[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int m = m0 + i;
+    chain_init(ch[i]);
+    chain_load(ch[i], s.planes + (it_e[m] * GK + min(4 * it_q[m] + ro.kgR, GK - 1)) * PB_BYTES, ro);
+    acc[i] = mx::zero_acc();
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    acc[i] = mx::mfma_fp8_fp4<0>(ch[i].a[0], mx::q2_spread(c2[m0 + i][0].x, c2[m0 + i][0].y), acc[i], ch[i].sa,
+                                 mx::E8M0_TWO);
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    acc[i] = mx::mfma_fp8_fp4<1>(ch[i].a[1], mx::q2_spread(c2[m0 + i][0].z, c2[m0 + i][0].w), acc[i], ch[i].sa,
+                                 mx::E8M0_TWO);
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    acc[i] = mx::mfma_fp8_fp4<2>(ch[i].a[2], mx::q2_spread(c2[m0 + i][1].x, c2[m0 + i][1].y), acc[i], ch[i].sa,
+                                 mx::E8M0_TWO);
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    acc[i] = mx::mfma_fp8_fp4<3>(ch[i].a[3], mx::q2_spread(c2[m0 + i][1].z, c2[m0 + i][1].w), acc[i], ch[i].sa,
+                                 mx::E8M0_TWO);
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int m = m0 + i;
+    const int e = it_e[m], q2 = it_q[m];
+    const int g2 = 4 * q2 + kg;
+    const float sh = g2 < GK ? piece_sums(s.planes + (e * GK + g2) * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
+    const int si = j * GK + min(g2, GK - 1);
+    float v = g2 < GK ? bf16_to_f32(s.sc[e][0][si]) * dot4(acc[i]) + bf16_to_f32(s.sc[e][1][si]) * sh : 0.0f;
+    v = tile::sum_lane_groups(v);
+    if (on[m] && lane < 16) s.red[e][q2][lane] = v;
+  }
+}
+
 // grid.x = D / 16.  MAXM = ceil(k * ceil(GK / 4) / 12) items per wave.
 template <int MAXM>
 __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __restrict__ pool, Layout L,
@@ -297,27 +340,16 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   tile::wait_vmem();
   lds_sync();
 
-  // ---- 1. items
+  // ---- 1. items, in interleaved groups (every item's A operands, then each MFMA step
+  //         for all items of the group: independent accumulators keep the matrix
+  //         pipeline busy), then the group formulas.  Items that are off compute on
+  //         valid (clamped) data and are discarded.
   const ARole ro = a_role(lane);
-  Chain ch;
-  chain_init(ch);
-#pragma unroll
-  for (int m = 0; m < MAXM; ++m) {
-    if (!on[m]) continue;
-    const int e = it_e[m], q2 = it_q[m];
-    const int g2 = 4 * q2 + kg;
-    const uint8_t* blkA = s.planes + (e * GK + min(4 * q2 + ro.kgR, GK - 1)) * PB_BYTES;
-    const float sh = g2 < GK ? piece_sums(s.planes + (e * GK + g2) * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
-    f32x4_t acc = mx::zero_acc();
-    chain_load(ch, blkA, ro);
-    acc = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c2[m][0].x, c2[m][0].y), acc, ch.sa, mx::E8M0_TWO);
-    acc = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c2[m][0].z, c2[m][0].w), acc, ch.sa, mx::E8M0_TWO);
-    acc = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c2[m][1].x, c2[m][1].y), acc, ch.sa, mx::E8M0_TWO);
-    acc = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c2[m][1].z, c2[m][1].w), acc, ch.sa, mx::E8M0_TWO);
-    const int si = j * GK + min(g2, GK - 1);
-    float v = g2 < GK ? bf16_to_f32(s.sc[e][0][si]) * dot4(acc) + bf16_to_f32(s.sc[e][1][si]) * sh : 0.0f;
-    v = tile::sum_lane_groups(v);
-    if (lane < 16) s.red[e][q2][lane] = v;
+  if constexpr (MAXM <= 3) {
+    down_items<MAXM>(s, c2, it_e, it_q, on, 0, ro, GK, FT, j, kg, lane);
+  } else {
+    down_items<2>(s, c2, it_e, it_q, on, 0, ro, GK, FT, j, kg, lane);
+    down_items<MAXM - 2>(s, c2, it_e, it_q, on, 2, ro, GK, FT, j, kg, lane);
   }
   lds_sync();
 

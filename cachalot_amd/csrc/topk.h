@@ -6,8 +6,8 @@
 // NaN never wins (it ranks as -inf) and -0 ties with +0, as float comparison
 // has it.  Each value becomes an order-preserving u32 key, so one round is a
 // u32 max over the lane's EPT keys, four DPP steps inside rows of 16 lanes and
-// four lane reads; the index rule is applied to the ballot of the lanes holding
-// the maximum (scalar bit scans), and the winner's owner clears its key.
+// four lane reads; the index rule is a second such max over the indices of the
+// holders of the maximum, and the winner's owner clears its key.
 #pragma once
 
 #include "common.h"
@@ -23,8 +23,8 @@ __device__ __forceinline__ uint32_t topk_key(float s) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Lane 0 writes top_i[pos] / top_v[pos] (winner index and its raw score), pos =
-// k-1-r (ascending order) or r (rank order) for round r, and, with a slot table,
+// Writes top_i[pos] / top_v[pos] (winner index and its raw score), pos = k-1-r
+// (ascending order) or r (rank order) for round r, and, with a slot table,
 // top_s[pos] = slot_table[winner] (the table is read with the scores, so the
 // slot costs no dependent load).  COHERENT: the scores are read with agent-scope
 // loads (written by other workgroups of the running kernel).  Requires
@@ -58,31 +58,48 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ scores, cons
     m = max(m, mirror16_u32(m));
     const uint32_t mu = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
                             max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
-    int win = -1;
+    // winner among the holders of the maximum: ascending order takes the largest
+    // index, rank order the smallest -- a second u32 max, over (index rank + 1)
+    // of the lane's holders (0: none)
+    uint32_t cj[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      const uint64_t b = __ballot(key[j] == mu);
-      if (b != 0) {
-        if (asc) win = 64 * j + 63 - __builtin_clzll(b);   // the largest index holding the maximum
-        else if (win < 0) win = 64 * j + __builtin_ctzll(b);
-      }
+    for (int j = 0; j < EPT; ++j) {   // independent selects, then a max tree (short dependency chain)
+      const uint32_t idx = (uint32_t)(lane + 64 * j);
+      cj[j] = key[j] == mu ? (asc ? idx + 1u : 65535u - idx) : 0u;
     }
+#pragma unroll
+    for (int w = 1; w < EPT; w *= 2)
+#pragma unroll
+      for (int j = 0; j + w < EPT; j += 2 * w) cj[j] = max(cj[j], cj[j + w]);
+    uint32_t c = cj[0];
+    c = max(c, xor1_u32(c));
+    c = max(c, xor2_u32(c));
+    c = max(c, mirror8_u32(c));
+    c = max(c, mirror16_u32(c));
+    const uint32_t cu = max(max((uint32_t)__builtin_amdgcn_readlane((int)c, 0), (uint32_t)__builtin_amdgcn_readlane((int)c, 16)),
+                            max((uint32_t)__builtin_amdgcn_readlane((int)c, 32), (uint32_t)__builtin_amdgcn_readlane((int)c, 48)));
+    const int win = asc ? (int)cu - 1 : 65535 - (int)cu;
     const int wl = win & 63, wj = win >> 6;
-    float sw = sv[0];
-#pragma unroll
-    for (int j = 1; j < EPT; ++j) sw = j == wj ? sv[j] : sw;
-    sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sw), wl));
-    int ss = st[0];
-#pragma unroll
-    for (int j = 1; j < EPT; ++j) ss = j == wj ? st[j] : ss;
-    ss = __builtin_amdgcn_readlane(ss, wl);
 #pragma unroll
     for (int j = 0; j < EPT; ++j) key[j] = (j == wj && lane == wl) ? 0u : key[j];
-    if (lane == 0) {
-      const int pos = asc ? k - 1 - r : r;
-      top_i[pos] = win;
-      top_v[pos] = sw;
-      if (top_s) top_s[pos] = ss;
+    if (lane == 0) top_i[asc ? k - 1 - r : r] = win;
+  }
+  // position p (lane p % 64): the raw score (and slot) of winner top_i[p], fetched from its owner lane
+  for (int p0 = 0; p0 < k; p0 += 64) {
+    const int p = p0 + lane;
+    const int wi = p < k ? top_i[p] : 0;
+    float sw = 0.0f;
+    int ss = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const float vj = __shfl(sv[j], wi & 63, 64);
+      const int tj = __shfl(st[j], wi & 63, 64);
+      sw = (wi >> 6) == j ? vj : sw;
+      ss = (wi >> 6) == j ? tj : ss;
+    }
+    if (p < k) {
+      top_v[p] = sw;
+      if (top_s) top_s[p] = ss;
     }
   }
 }
