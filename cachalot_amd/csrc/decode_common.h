@@ -163,14 +163,14 @@ __device__ __forceinline__ float route_weight(const ExpertSource& src, const flo
 // Epilogue of a gate/up workgroup, lanes 0..15 of wave 0 (the wave whose LDS
 // arrays route_slot filled): the router weight of expert e, also stored for the
 // caller -- ws_w[e] by the expert's first tile, and the selection's ids and
-// weights by workgroup 0.
+// weights by the publishing workgroup.
 __device__ __forceinline__ float route_finish(const ExpertSource& src, float* ws_w, int e, int tile,
-                                              const float* lds_v, float* lds_w, const int* lds_i) {
+                                              const float* lds_v, float* lds_w, const int* lds_i, bool publisher) {
   const float w = route_weight(src, ws_w, e, lds_v, lds_w);
   const int lane = threadIdx.x & 63;
   if (src.scores == nullptr) return w;
   if (tile == 0 && lane == 0) ws_w[e] = w;
-  if (blockIdx.x == 0 && lane < src.k) {
+  if (publisher && lane < src.k) {
     if (src.idx_out) src.idx_out[lane] = lds_i[lane];
     if (src.w_out) src.w_out[lane] = lds_w[lane];
   }

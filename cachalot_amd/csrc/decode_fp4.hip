@@ -77,7 +77,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   if (slot < 0) {
     if (threadIdx.x < 16) {
       hout[row0 + threadIdx.x] = hout[F + row0 + threadIdx.x] = 0;
-      route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
+      route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0], blockIdx.x == 0);
     }
     return;
   }
@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   }
   __syncthreads();
   if (threadIdx.x < 16) {
-    const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
+    const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0], blockIdx.x == 0);
     const int t = threadIdx.x;
     float g = 0.0f, u = 0.0f;
 #pragma unroll

@@ -120,7 +120,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
   if (slot < 0) {   // the expert has no slot: its hidden rows are zero
     if (threadIdx.x < 16) {
       hout[hidden_index(row0 + threadIdx.x)] = 0;
-      route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
+      route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0], blockIdx.x == 0);
     }
     return;
   }
@@ -209,7 +209,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
   }
   __syncthreads();
   if (threadIdx.x < 16) {
-    const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0]);
+    const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0], blockIdx.x == 0);
     const int t = threadIdx.x;
     float g = 0.0f, u = 0.0f;
 #pragma unroll

@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
 
   // ---- 3. epilogue (16 lanes of wave 0): h for the tile's rows as one plane piece
   if (tid < 16) {
-    const float wexp = route_finish(src, ws_w, e, tile, s.top_v, s.top_w, s.top_i);
+    const float wexp = route_finish(src, ws_w, e, tile, s.top_v, s.top_w, s.top_i, blockIdx.x == 0);
     float hv = 0.0f;
     if (live) {
       float rg[MAX_NQ], ru[MAX_NQ];

@@ -139,8 +139,8 @@ def test_route_bias_affects_selection_only_and_bias_vl():
 
 
 def test_hip_constants_match_oracle():
-    """The polynomial / reduction constants in router.hip are the oracle's doubles."""
-    src = (ROOT / "cachalot_amd/csrc/router.hip").read_text()
+    """The polynomial / reduction constants in router_math.h are the oracle's doubles."""
+    src = (ROOT / "cachalot_amd/csrc/router_math.h").read_text()
 
     def arr(name):
         body = re.search(name + r"\[\d+\] = \{([^}]*)\}", src).group(1)
