@@ -24,10 +24,10 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
-# HBM bytes per decode launch pair (gate/up + down) at config 1, from two rocprofv3
+# HBM bytes per decode (gate/up + down kernels) at config 1, from two rocprofv3
 # counter passes (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
 # plain 1 GiB device copy (read x 2.0, write x 1.0); summary under profiles/.
-PAIR_TRAFFIC_BYTES = 61_162_400
+PAIR_TRAFFIC_BYTES = 61_416_756
 METRIC = "MoE-layer decode tok/s + expert-byte HBM GB/s (B=1); prefill grouped-GEMM TFLOPS"
 
 
@@ -375,7 +375,7 @@ def main() -> int:
         "expert_GBps_step": round(alg_bytes / (ms_per_step * 1e-3) / 1e9, 1),
         "hbm_frac_step": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
         "roofline": {
-            "kernel": "q2_gate_up_kernel + q2_down_kernel (one decode launch pair)",
+            "kernel": "x_planes_kernel + q2mx_gate_up_kernel + q2mx_down_kernel (one decode call, experts given)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
