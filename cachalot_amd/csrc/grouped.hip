@@ -45,6 +45,7 @@ constexpr int KC = 128;                // K chunk
 constexpr int A_ROW_BYTES = 272;       // one staged A row: 128 bf16 + 16 bytes padding
 constexpr int MAX_GROUPS = 64;         // K <= 8192
 constexpr int PERMUTE_THREADS = 1024;
+constexpr int ZERO_WORDS = 16;         // 64 zero bytes at offset 128 of the workspace
 
 // ------------------------------------------------------------------ permute ---
 // offsets[e] = rows before expert e (E+1 entries).
@@ -107,8 +108,10 @@ __global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __r
 
 // tiles[t] = (expert, first row of the tile); count in tiles_n[0].
 __global__ void __launch_bounds__(1024) tile_list_kernel(const int32_t* __restrict__ offsets, int E, int MT,
-                                                         int2* __restrict__ tiles, int32_t* __restrict__ tiles_n) {
+                                                         int2* __restrict__ tiles, int32_t* __restrict__ tiles_n,
+                                                         uint32_t* __restrict__ zeros) {
   __shared__ int first[1024 + 1];
+  if (threadIdx.x < ZERO_WORDS) zeros[threadIdx.x] = 0u;   // source of the zero A columns past K
   if (threadIdx.x == 0) {
     int run = 0;
     for (int e = 0; e < E; ++e) {
@@ -416,6 +419,192 @@ __global__ void __launch_bounds__(256) grouped_down_kernel(GroupedArgs g) {
     }
 }
 
+// -------------------------------------------------- FP4 grouped GEMM, large tiles ---
+// One 512-thread workgroup = one M tile (128 rows of one expert) x 256 weight rows of
+// each matrix (W1 and W3 for gate/up, W2 for down); wave w owns weight rows
+// [32w, 32w + 32) as two 16-row fragments and all eight 16-row token fragments.
+// The A tile is read once per 256 weight rows (the 64-row tiles read it once per 64)
+// and each expert's weights once per 128 of its rows.
+// K runs in chunks of 128 through a three-stage LDS ring filled by untracked
+// direct-to-LDS loads (one 16-byte slot per lane, gathered rows, rows swizzled by
+// XOR so the MFMA reads hit distinct bank groups); each wave's codes and E8M0 scales
+// are prefetched two chunks ahead in registers.  Same arithmetic as the 64-row
+// kernels: B = E2M1 x 2^e converted exactly to bf16, v_mfma_f32_16x16x32_bf16, fp32.
+constexpr int G2_THREADS = 512;
+constexpr int G2_WAVES = G2_THREADS / 64;
+constexpr int G2_MT = 128;                 // token rows per workgroup (8 fragments)
+constexpr int G2_TB = G2_MT / 16;
+constexpr int G2_NT = 32 * G2_WAVES;       // 256 weight rows per matrix
+constexpr int G2_STAGES = 3;
+constexpr int G2_ABYTES = G2_MT * 256;     // one A chunk: 128 rows x 128 bf16
+constexpr int G2_ASLICES = G2_ABYTES / 1024 / G2_WAVES;   // 1 KiB direct-to-LDS slices per wave and chunk
+
+// Wait until the load that produced v has landed (the compiler's own wait; loads
+// complete in issue order, so everything this wave issued before it has too), then
+// an LDS-only workgroup barrier.
+__device__ __forceinline__ void lds_sync_after(uint32_t v) {
+  asm volatile("" ::"v"(v) : "memory");
+  lds_sync();
+}
+
+// Byte offset of (row r, 16-byte column slot k16) in a staged A chunk.
+__device__ __forceinline__ uint32_t g2_aoff(int r, int k16) { return (uint32_t)(r * 256 + ((k16 ^ (r & 15)) << 4)); }
+
+template <int NM>
+struct G2Chunk {
+  uint4 codes[NM][2];
+  uint32_t sc[NM][2];
+};
+
+template <int NM>
+__device__ __forceinline__ void g2_issue(const GroupedArgs& g, uint8_t* stage, const uint8_t* (&arow)[G2_ASLICES],
+                                         const int (&ak16)[G2_ASLICES], const uint8_t* zeros,
+                                         const uint8_t* (&wrow)[NM][2],
+                                         const uint8_t* (&srow)[NM][2], int c, int kg, int wave, int lane,
+                                         int row_bytes, int blocks, G2Chunk<NM>& out) {
+  // A: this wave's 1 KiB slices of the chunk (slot = 64 * (G2_ASLICES wave + q) + lane)
+#pragma unroll
+  for (int q = 0; q < G2_ASLICES; ++q) {
+    const int kcol = c * 128 + ak16[q] * 8;
+    const uint8_t* src = kcol < g.K ? arow[q] + c * 256 + ak16[q] * 16 : zeros;
+    tile::lds_load16_untracked(src, stage + (G2_ASLICES * wave + q) * 1024);
+  }
+  // B: the lane's 32 codes (block kg of the chunk) and their E8M0 scale, per matrix and fragment
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      out.codes[m][f] = *reinterpret_cast<const uint4*>(wrow[m][f] + min(c * 64 + kg * 16, row_bytes - 16));
+      const int blk = 4 * c + kg;
+      // blocks past K meet zero activations: any finite scale (raw 127 = 1.0)
+      out.sc[m][f] = blk < blocks ? (uint32_t)srow[m][f][blk] : 127u;
+    }
+}
+
+// ntb: token fragments holding rows of the tile (the rest are skipped, uniformly).
+template <int NM>
+__device__ __forceinline__ void g2_compute(const uint8_t* ab, const G2Chunk<NM>& ch, int i, int kg, int ntb,
+                                           f32x4_t (&acc)[NM][2][G2_TB]) {
+  float scale[NM][2];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) scale[m][f] = e8m0_to_f32(ch.sc[m][f]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    bf16x8_t bv[NM][2];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) bv[m][f] = fp4_codes_to_b(word_of(ch.codes[m][f], s), scale[m][f]);
+#pragma unroll
+    for (int tb = 0; tb < G2_TB; ++tb) {
+      if (tb >= ntb) break;
+      const bf16x8_t a = lds_a(ab, g2_aoff(tb * 16 + i, 4 * kg + s));
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) acc[m][f][tb] = mfma(a, bv[m][f], acc[m][f][tb]);
+    }
+  }
+}
+
+// grid = (max tiles, ceil(N / 256)).  NM = 2: gate/up (W1, W3) -> h; NM = 1: down (W2) -> y.
+template <int NM>
+__global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const uint8_t* __restrict__ zeros) {
+  __shared__ __align__(16) uint8_t abuf[G2_STAGES][G2_ABYTES];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, kg = lane >> 4;
+  if ((int)blockIdx.x >= g.tiles_n[0]) return;
+  const int2 tl = g.tiles[blockIdx.x];
+  const int e = tl.x, row0 = tl.y;
+  const int rows = min(G2_MT, g.offsets[e + 1] - row0);
+  const int ntb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
+  const int slot = g.slot_table[e];
+  f32x4_t acc[NM][2][G2_TB];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int tb = 0; tb < G2_TB; ++tb) acc[m][f][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int nw0 = blockIdx.y * G2_NT + 32 * wave;   // the wave's first weight row
+  if (slot >= 0) {
+    const int nch = (g.K + 127) / 128;
+    const int row_bytes = g.K / 2, blocks = g.K / 32;
+    // A sources of the lane's two slots per chunk
+    const uint8_t* arow[G2_ASLICES];
+    int ak16[G2_ASLICES];
+#pragma unroll
+    for (int q = 0; q < G2_ASLICES; ++q) {
+      const int S = 64 * (G2_ASLICES * wave + q) + lane;
+      const int r = S >> 4;
+      ak16[q] = (S & 15) ^ (r & 15);
+      const int rr = min(r, rows - 1);   // rows past the tile's end: any valid row (discarded)
+      const int src = g.a_gather ? g.a_gather[row0 + rr] : row0 + rr;
+      arow[q] = reinterpret_cast<const uint8_t*>(g.a + (size_t)src * g.a_stride);
+    }
+    const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
+    const int tq[2] = {NM == 2 ? 0 : 3, 6};   // w1, w3 (gate/up) or w2 (down)
+    const uint8_t* wrow[NM][2];
+    const uint8_t* srow[NM][2];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int n = min(nw0 + 16 * f + i, g.N - 1);   // rows past N: clamped (discarded)
+        wrow[m][f] = base + g.L.off[tq[m]] + (int64_t)n * row_bytes;
+        srow[m][f] = base + g.L.off[tq[m] + 1] + (int64_t)n * blocks;
+      }
+    G2Chunk<NM> ring[G2_STAGES];
+    g2_issue<NM>(g, abuf[0], arow, ak16, zeros, wrow, srow, 0, kg, wave, lane, row_bytes, blocks, ring[0]);
+    if (nch > 1)
+      g2_issue<NM>(g, abuf[1], arow, ak16, zeros, wrow, srow, 1, kg, wave, lane, row_bytes, blocks, ring[1]);
+    // three chunks per trip so every ring index is a compile-time constant
+    for (int c0 = 0; c0 < nch; c0 += G2_STAGES) {
+#pragma unroll
+      for (int u = 0; u < G2_STAGES; ++u) {
+        const int c = c0 + u;
+        if (c < nch) {
+          // this wave's loads of chunk c have landed (its codes are consumed here, and
+          // its earlier direct-to-LDS loads complete first); then every wave's
+          lds_sync_after(ring[u].codes[NM - 1][1].w);
+          if (c + 2 < nch)   // into the stage chunk c - 1 used: every wave is past it
+            g2_issue<NM>(g, abuf[(u + 2) % G2_STAGES], arow, ak16, zeros, wrow, srow, c + 2, kg, wave, lane,
+                         row_bytes, blocks, ring[(u + 2) % G2_STAGES]);
+          g2_compute<NM>(abuf[u], ring[u], i, kg, ntb, acc);
+        }
+      }
+    }
+  }
+  // epilogue: lane holds rows tb*16 + 4kg + r (tokens) x column nw0 + 16f + i
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int n = nw0 + 16 * f + i;
+    if (n >= g.N) continue;
+#pragma unroll
+    for (int tb = 0; tb < G2_TB; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tr = tb * 16 + 4 * kg + r;
+        if (tr >= rows) continue;
+        const int rr = row0 + tr;
+        if constexpr (NM == 2) {
+          float gv = round_bf16(acc[0][f][tb][r]);
+          float uv = round_bf16(acc[1][f][tb][r]);
+          if (g.limit > 0.0f) {
+            uv = fminf(fmaxf(uv, -g.limit), g.limit);
+            gv = fminf(gv, g.limit);
+          }
+          g.out[(size_t)rr * g.N + n] = f32_to_bf16((silu_f32(gv) * uv) * g.row_w[rr]);
+        } else {
+          g.out[((size_t)g.row_token[rr] * g.k + g.row_slot[rr]) * g.N + n] = f32_to_bf16(acc[0][f][tb][r]);
+        }
+      }
+  }
+}
+
 // out[t, d] = bf16(0 + y[t,0,d] + ... + y[t,k-1,d] (+ addend[t,d])); routed likewise in fp32.
 __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ y, const uint16_t* __restrict__ addend,
                                                       int T, int k, int D, float* __restrict__ routed,
@@ -483,6 +672,12 @@ int launch_grouped_mt(const GroupedArgs& gu, const GroupedArgs& dn, int max_tile
   return check_launch("grouped_down_kernel");
 }
 
+// The 64-row-tile kernels stay selectable for FP4 (CACHALOT_GROUPED_SMALL=1) for comparison.
+inline bool small_tiles_requested() {
+  const char* env = getenv("CACHALOT_GROUPED_SMALL");
+  return env && env[0] == '1';
+}
+
 template <int KIND>
 int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
                    const int32_t* slot_table, const int32_t* offsets, const int32_t* row_token,
@@ -512,7 +707,10 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   uint16_t* hidden = reinterpret_cast<uint16_t*>(ws + wo.hidden);
   // tiles of 64 rows when experts see many tokens, 16 for batched decode
   const int MT = T * k >= 4 * E ? 64 : 16;
-  hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, MT, tiles, tiles_n);
+  uint32_t* zeros = reinterpret_cast<uint32_t*>(ws + wo.tiles_n + 128);
+  const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested();
+  hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, large ? G2_MT : MT, tiles, tiles_n,
+                     zeros);
   rc = check_launch("tile_list_kernel");
   if (rc) return rc;
   const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
@@ -520,6 +718,15 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
                  D, F, k, limit, hidden};
   GroupedArgs dn{hidden, F, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
                  F, D, k, limit, y};
+  if (large) {
+    hipLaunchKernelGGL(g2_fp4_kernel<2>, dim3(max_tiles, (F + G2_NT - 1) / G2_NT), dim3(G2_THREADS), 0, s, gu,
+                       reinterpret_cast<const uint8_t*>(zeros));
+    rc = check_launch("g2_fp4_kernel<2>");
+    if (rc) return rc;
+    hipLaunchKernelGGL(g2_fp4_kernel<1>, dim3(max_tiles, (D + G2_NT - 1) / G2_NT), dim3(G2_THREADS), 0, s, dn,
+                       reinterpret_cast<const uint8_t*>(zeros));
+    return check_launch("g2_fp4_kernel<1>");
+  }
   const size_t lds_gu = grouped_lds_bytes(KIND, MT, 2, D), lds_dn = grouped_lds_bytes(KIND, MT, 1, F);
   return MT == 64 ? launch_grouped_mt<KIND, 64>(gu, dn, max_tiles, lds_gu, lds_dn, s)
                   : launch_grouped_mt<KIND, 16>(gu, dn, max_tiles, lds_gu, lds_dn, s);

@@ -99,6 +99,139 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict
   if (threadIdx.x == 0) normalise_weights(top_v, k, route_scale, norm, w + (size_t)t * k);
 }
 
+// Many tokens: one 256-thread workgroup = 32 tokens x 64 experts, each thread 2
+// tokens x 4 experts.  The same arithmetic as router_row: chunk c (of 64) of every
+// dot product is a sequential fp32 sum of its D/64 products, and the 64 chunk sums
+// meet in the pairwise tree (left + right) the xor butterfly forms.  Chunk by chunk,
+// x and W slices are staged in LDS as fp32; the tree is kept as a binary-counter
+// stack of six partial nodes per dot product.  fma(x, w, s) equals s + x * w here:
+// the product of two bf16 values is exact in fp32 (16 significant bits) unless it is
+// below 2^-133 in magnitude.
+constexpr int RT_T = 32;             // tokens per workgroup
+constexpr int RT_E = 64;             // experts per workgroup
+constexpr int RT_MAXCH = 80;         // D / 64 <= 80 (D <= 5120)
+constexpr int RT_PAD = 4;            // floats of padding per staged row (bank spread)
+
+__global__ void __launch_bounds__(256) router_tiled_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ W, int T, int D, int E,
+                                                           float gate_temp, int fn, float* __restrict__ scores) {
+  __shared__ __align__(16) float xs[RT_T][RT_MAXCH + RT_PAD];
+  __shared__ __align__(16) float ws[RT_E][RT_MAXCH + RT_PAD];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int eq = lane & 15;                   // experts 4 eq .. 4 eq + 3
+  const int tp = (lane >> 4) + 4 * wave;      // tokens 2 tp, 2 tp + 1
+  const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
+  const int ch = D / CHUNKS;                  // a multiple of 8
+  const int xq = RT_T * ch / 8, wq = RT_E * ch / 8;   // 8-value items per chunk
+  // staging: item -> (row, 8 values); rows past T / E read row 0 (results unused)
+  auto load_chunk = [&](int c, uint4 (&xv)[2], uint4 (&wv)[3]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int it = tid + 256 * j;
+      const int r = it / (ch / 8), q = it - r * (ch / 8);
+      const int t = min(t0 + r, T - 1);
+      xv[j] = it < xq ? *reinterpret_cast<const uint4*>(x + (size_t)t * D + c * ch + 8 * q) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int it = tid + 256 * j;
+      const int r = it / (ch / 8), q = it - r * (ch / 8);
+      const int e = min(e0 + r, E - 1);
+      wv[j] = it < wq ? *reinterpret_cast<const uint4*>(W + (size_t)e * D + c * ch + 8 * q) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_chunk = [&](const uint4 (&xv)[2], const uint4 (&wv)[3]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int it = tid + 256 * j;
+      if (it < xq) {
+        const int r = it / (ch / 8), q = it - r * (ch / 8);
+        const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        float4* d = reinterpret_cast<float4*>(&xs[r][8 * q]);
+        d[0] = make_float4(__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u),
+                           __uint_as_float(u[1] << 16), __uint_as_float(u[1] & 0xffff0000u));
+        d[1] = make_float4(__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xffff0000u),
+                           __uint_as_float(u[3] << 16), __uint_as_float(u[3] & 0xffff0000u));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int it = tid + 256 * j;
+      if (it < wq) {
+        const int r = it / (ch / 8), q = it - r * (ch / 8);
+        const uint32_t u[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+        float4* d = reinterpret_cast<float4*>(&ws[r][8 * q]);
+        d[0] = make_float4(__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u),
+                           __uint_as_float(u[1] << 16), __uint_as_float(u[1] & 0xffff0000u));
+        d[1] = make_float4(__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xffff0000u),
+                           __uint_as_float(u[3] << 16), __uint_as_float(u[3] & 0xffff0000u));
+      }
+    }
+  };
+  float stk[6][8];
+  float node[8];
+  uint4 xv[2], wv[3];
+  load_chunk(0, xv, wv);
+  store_chunk(xv, wv);
+  __syncthreads();
+  for (int c = 0; c < CHUNKS; ++c) {
+    if (c + 1 < CHUNKS) load_chunk(c + 1, xv, wv);
+    float acc[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) acc[p] = 0.0f;
+    for (int k = 0; k < ch; k += 4) {
+      float4 xa[2], wa[4];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) xa[a] = *reinterpret_cast<const float4*>(&xs[2 * tp + a][k]);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) wa[b] = *reinterpret_cast<const float4*>(&ws[4 * eq + b][k]);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float v = acc[4 * a + b];
+          v = __builtin_fmaf(xa[a].x, wa[b].x, v);
+          v = __builtin_fmaf(xa[a].y, wa[b].y, v);
+          v = __builtin_fmaf(xa[a].z, wa[b].z, v);
+          v = __builtin_fmaf(xa[a].w, wa[b].w, v);
+          acc[4 * a + b] = v;
+        }
+    }
+    // merge chunk c into the tree (c is uniform: every branch below is too)
+#pragma unroll
+    for (int p = 0; p < 8; ++p) node[p] = acc[p];
+    // chunk c closes the nodes of the levels below its lowest zero bit
+    const int up = __builtin_ctz(~c);   // levels merged (6 after the last chunk)
+#pragma unroll
+    for (int L = 0; L < 6; ++L) {
+      if (L < up) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) node[p] = stk[L][p] + node[p];
+      } else if (L == up) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) stk[L][p] = node[p];
+      }
+    }
+    __syncthreads();
+    if (c + 1 < CHUNKS) {
+      store_chunk(xv, wv);
+      __syncthreads();
+    }
+  }
+  // after chunk 63 every level merged: node holds the root
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int t = t0 + 2 * tp + a;
+    if (t >= T) continue;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int e = e0 + 4 * eq + b;
+      if (e < E) scores[(size_t)t * E + e] = score_of(node[4 * a + b] / gate_temp, fn);
+    }
+  }
+}
+
 }  // namespace
 
 template <int TT>
@@ -116,6 +249,11 @@ static void launch_scores_tt(const uint16_t* x, const uint16_t* W, int T, int D,
 int launch_router_scores(const uint16_t* x, const uint16_t* W, int T, int D, int E, float gate_temp, int fn,
                          float* scores, hipStream_t s, const decode::RouteTail* tail, uint8_t* xplanes) {
   decode::RouteTail none{};
+  if (T >= RT_T && D % 512 == 0 && D / CHUNKS <= RT_MAXCH) {
+    hipLaunchKernelGGL(router_tiled_kernel, dim3((T + RT_T - 1) / RT_T, (E + RT_E - 1) / RT_E), dim3(256), 0, s, x,
+                       W, T, D, E, gate_temp, fn, scores);
+    return check_launch("router_tiled_kernel");
+  }
   if (T >= 4) launch_scores_tt<4>(x, W, T, D, E, gate_temp, fn, scores, s, none, nullptr);
   else launch_scores_tt<1>(x, W, T, D, E, gate_temp, fn, scores, s, tail && T == 1 ? *tail : none, xplanes);
   return check_launch("router_scores_kernel");
