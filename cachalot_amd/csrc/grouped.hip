@@ -497,14 +497,21 @@ __device__ __forceinline__ void g2_compute(const uint8_t* ab, const G2Chunk<NM>&
     for (int m = 0; m < NM; ++m)
 #pragma unroll
       for (int f = 0; f < 2; ++f) bv[m][f] = fp4_codes_to_b(word_of(ch.codes[m][f], s), scale[m][f]);
+    // token fragments in pairs: both A reads issue before the pair's MFMAs (one LDS
+    // round trip per 4 NM MFMAs); a fragment past the tile's rows is computed on
+    // stale rows and discarded
 #pragma unroll
-    for (int tb = 0; tb < G2_TB; ++tb) {
-      if (tb >= ntb) break;
-      const bf16x8_t a = lds_a(ab, g2_aoff(tb * 16 + i, 4 * kg + s));
+    for (int tp = 0; tp < G2_TB; tp += 2) {
+      if (tp >= ntb) break;
+      const bf16x8_t a0 = lds_a(ab, g2_aoff(tp * 16 + i, 4 * kg + s));
+      const bf16x8_t a1 = lds_a(ab, g2_aoff((tp + 1) * 16 + i, 4 * kg + s));
 #pragma unroll
       for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int f = 0; f < 2; ++f) acc[m][f][tb] = mfma(a, bv[m][f], acc[m][f][tb]);
+        for (int f = 0; f < 2; ++f) {
+          acc[m][f][tp] = mfma(a0, bv[m][f], acc[m][f][tp]);
+          acc[m][f][tp + 1] = mfma(a1, bv[m][f], acc[m][f][tp + 1]);
+        }
     }
   }
 }
