@@ -379,6 +379,268 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   }
 }
 
+// ------------------------------------------------------ batched (expert-major) ---
+// Few tokens per expert (batched decode, speculative verify): the rows of one expert
+// (permuted expert-major, grouped.hip) share one load of its codes.  The same tiles,
+// items and arithmetic as the one-token kernels above, run once per row with that
+// row's activation planes; the next row's planes are copied into LDS while the
+// current row computes.
+//   q2mx_bgu_kernel  grid (active experts, F / 16): h planes of every row, [rows][GK]
+//   q2mx_bdn_kernel  grid (active experts, D / 16): y = bf16(h W2) of every row, to
+//                    its (token, route slot) place of y [T, k, D]
+struct BatchArgs {
+  const uint8_t* xplanes;   // [T][D / 128] plane blocks
+  const uint8_t* pool;
+  Layout L;
+  const int32_t* slot_table;
+  const int32_t* offsets;   // [E + 1] expert-major rows
+  const int2* tiles;        // (expert, first row) of every expert with rows
+  const int32_t* tiles_n;
+  const int32_t* row_token;
+  const int32_t* row_slot;
+  const float* row_w;
+  int D, F, k;
+  float limit;
+  uint8_t* hid;             // [rows][GK] plane blocks
+  uint16_t* y;              // [T, k, D]
+};
+
+struct BGuLds {
+  uint8_t planes[2][MAX_GT * PB_BYTES];
+  uint8_t scl[GU_WAVES][GU_MAXM][1024];
+  float red[MAX_NQ][2][16];
+};
+
+// x (T tokens) as plane blocks: grid (T, ceil(D / 1024)).
+__global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __restrict__ x, int D,
+                                                            uint8_t* __restrict__ xplanes) {
+  const int t = blockIdx.x;
+  const int t4 = blockIdx.y * 256 + threadIdx.x;
+  if (4 * t4 < D)
+    mx::encode_x_quad(xplanes + (size_t)t * (D / 128) * PB_BYTES, t4,
+                      reinterpret_cast<const uint2*>(x + (size_t)t * D)[t4]);   // whole quads
+}
+
+template <int MAXM>
+__global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
+  __shared__ __align__(16) BGuLds s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kg = lane >> 4;
+  if ((int)blockIdx.x >= a.tiles_n[0]) return;
+  const int2 et = a.tiles[blockIdx.x];
+  const int e = __builtin_amdgcn_readfirstlane(et.x), r0 = __builtin_amdgcn_readfirstlane(et.y);
+  const int r1 = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
+  const int D = a.D, F = a.F;
+  const int GT = D / 128, NQ = GT / 4;
+  const int GK = (F + 127) / 128, FT = F / 16;
+  const int tile = blockIdx.y;
+  const int row0 = tile * 16;
+  const int slot = a.slot_table[e];
+  const bool live = slot >= 0;
+  const int pbytes = GT * PB_BYTES;
+
+  // the first row's planes, then the tile's scale chunks and codes
+  copy_to_lds_untracked(a.xplanes + (size_t)a.row_token[r0] * pbytes, s.planes[0], pbytes, wave, GU_WAVES, lane);
+  uint4 c1[MAXM][2], c3[MAXM][2];
+  int gsb[MAXM];
+  if (live) {
+    const uint8_t* base = a.pool + (int64_t)slot * a.L.record_bytes;
+    const int t = lane >> 4, r = lane & 15;
+    const int64_t toff = t == 0 ? a.L.off[1] : t == 1 ? a.L.off[2] : t == 2 ? a.L.off[7] : a.L.off[8];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int q = min(wave + GU_WAVES * m, NQ - 1);
+      const int o = ((row0 + r) * GT + 4 * q) * 2;
+      tile::lds_load16_untracked(base + toff + (o & ~15), s.scl[wave][m]);
+      gsb[m] = (8 * q) & 15;
+      const int64_t off = (int64_t)(row0 + j) * (D / 4) + (4 * q + kg) * 32;
+      const uint4* w1 = reinterpret_cast<const uint4*>(base + a.L.off[0] + off);
+      const uint4* w3 = reinterpret_cast<const uint4*>(base + a.L.off[6] + off);
+      c1[m][0] = w1[0];
+      c1[m][1] = w1[1];
+      c3[m][0] = w3[0];
+      c3[m][1] = w3[1];
+    }
+  }
+  tile::wait_vmem();
+  lds_sync();
+  const ARole ro = a_role(lane);
+  Chain ch;
+  chain_init(ch);
+  for (int r = r0; r < r1; ++r) {
+    const int buf = __builtin_amdgcn_readfirstlane((r - r0) & 1);
+    if (r + 1 < r1)   // the next row's planes, into the other buffer
+      copy_to_lds_untracked(a.xplanes + (size_t)a.row_token[r + 1] * pbytes, s.planes[buf ^ 1], pbytes, wave,
+                            GU_WAVES, lane);
+    const uint8_t* planes = s.planes[buf];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int q = wave + GU_WAVES * m;
+      if (!live || q >= NQ) break;
+      f32x4_t a1 = mx::zero_acc(), a3 = mx::zero_acc();
+      chain_load(ch, planes + (4 * q + ro.kgR) * PB_BYTES, ro);
+      a1 = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c1[m][0].x, c1[m][0].y), a1, ch.sa, mx::E8M0_TWO);
+      a3 = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c3[m][0].x, c3[m][0].y), a3, ch.sa, mx::E8M0_TWO);
+      a1 = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c1[m][0].z, c1[m][0].w), a1, ch.sa, mx::E8M0_TWO);
+      a3 = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c3[m][0].z, c3[m][0].w), a3, ch.sa, mx::E8M0_TWO);
+      a1 = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c1[m][1].x, c1[m][1].y), a1, ch.sa, mx::E8M0_TWO);
+      a3 = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c3[m][1].x, c3[m][1].y), a3, ch.sa, mx::E8M0_TWO);
+      a1 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c1[m][1].z, c1[m][1].w), a1, ch.sa, mx::E8M0_TWO);
+      a3 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c3[m][1].z, c3[m][1].w), a3, ch.sa, mx::E8M0_TWO);
+      const float sx = piece_sums(planes + (4 * q + kg) * PB_BYTES, mx::PIECES);
+      const uint16_t* sc = reinterpret_cast<const uint16_t*>(s.scl[wave][m]) + (j * 16 + gsb[m] + 2 * kg) / 2;
+      const float v1 = bf16_to_f32(sc[0]) * dot4(a1) + bf16_to_f32(sc[128]) * sx;
+      const float v3 = bf16_to_f32(sc[256]) * dot4(a3) + bf16_to_f32(sc[384]) * sx;
+      const float s1 = tile::sum_lane_groups(v1);
+      const float s3 = tile::sum_lane_groups(v3);
+      if (lane < 16) {
+        s.red[q][0][lane] = s1;
+        s.red[q][1][lane] = s3;
+      }
+    }
+    lds_sync();
+    if (tid < 16) {
+      float hv = 0.0f;
+      if (live) {
+        float rg[MAX_NQ], ru[MAX_NQ];
+#pragma unroll
+        for (int q = 0; q < MAX_NQ; ++q) {
+          rg[q] = s.red[q][0][tid];
+          ru[q] = s.red[q][1][tid];
+        }
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int q = 0; q < MAX_NQ; ++q) {
+          if (q < NQ) {
+            g = g + rg[q];
+            u = u + ru[q];
+          }
+        }
+        g = round_bf16(g);
+        u = round_bf16(u);
+        if (a.limit > 0.0f) {
+          u = fminf(fmaxf(u, -a.limit), a.limit);
+          g = fminf(g, a.limit);
+        }
+        hv = round_bf16((silu_f32(g) * u) * a.row_w[r]);
+      }
+      const mx::PieceCode pc = mx::encode_piece(hv);
+      const int pp = tile & 7;
+      uint8_t* blk = a.hid + ((int64_t)r * GK + (tile >> 3)) * PB_BYTES;
+      blk[mx::pb_data(pp, 0) + mx::piece_pos(tid)] = (uint8_t)pc.hi;
+      blk[mx::pb_data(pp, 1) + mx::piece_pos(tid)] = (uint8_t)pc.lo;
+      if (tid == 0) {
+        blk[mx::pb_scale(pp, 0)] = (uint8_t)pc.scales;
+        blk[mx::pb_scale(pp, 1)] = (uint8_t)(pc.scales >> 8);
+        *reinterpret_cast<float*>(blk + PB_SUM + 4 * pp) = pc.sum;
+      }
+      if (tile == FT - 1) {
+        for (int z = pp + 1; z < mx::PIECES; ++z) {
+          blk[mx::pb_data(z, 0) + tid] = 0;
+          blk[mx::pb_data(z, 1) + tid] = 0;
+          if (tid == 0) {
+            blk[mx::pb_scale(z, 0)] = 127;
+            blk[mx::pb_scale(z, 1)] = 127;
+            *reinterpret_cast<float*>(blk + PB_SUM + 4 * z) = 0.0f;
+          }
+        }
+      }
+    }
+    // the next row's planes have landed (this wave's copy) and every wave is past
+    // this row's reads of red and of the current planes
+    tile::wait_vmem();
+    lds_sync();
+  }
+}
+
+struct BDnLds {
+  uint8_t planes[2][MAX_GK * PB_BYTES];
+  uint16_t sc[2][16 * MAX_GK];   // s2, b2 runs of the tile's rows
+  float red[MAX_NQ2][16];
+};
+
+template <int MAXM>
+__global__ void __launch_bounds__(GU_THREADS) q2mx_bdn_kernel(BatchArgs a) {
+  __shared__ __align__(16) BDnLds s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kg = lane >> 4;
+  if ((int)blockIdx.x >= a.tiles_n[0]) return;
+  const int2 et = a.tiles[blockIdx.x];
+  const int e = __builtin_amdgcn_readfirstlane(et.x), r0 = __builtin_amdgcn_readfirstlane(et.y);
+  const int r1 = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
+  const int D = a.D, F = a.F;
+  const int GK = (F + 127) / 128, NQ2 = (GK + 3) / 4, FT = F / 16;
+  const int n0 = blockIdx.y * 16;
+  const int slot = a.slot_table[e];
+  const bool live = slot >= 0;
+  const int hbytes = GK * PB_BYTES;
+
+  copy_to_lds_untracked(a.hid + (size_t)r0 * hbytes, s.planes[0], hbytes, wave, GU_WAVES, lane);
+  uint4 c2[MAXM][2];
+  if (live) {
+    const uint8_t* base = a.pool + (int64_t)slot * a.L.record_bytes;
+    const int run = 32 * GK;
+    if (wave < 2)
+      copy_to_lds_untracked(base + (wave ? a.L.off[5] : a.L.off[4]) + (int64_t)n0 * GK * 2,
+                            reinterpret_cast<uint8_t*>(s.sc[wave]), run, 0, 1, lane);
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int q2 = min(wave + GU_WAVES * m, NQ2 - 1);
+      const int g2 = min(4 * q2 + kg, GK - 1);
+      const uint4* w2 = reinterpret_cast<const uint4*>(base + a.L.off[3] + (int64_t)(n0 + j) * (GK * 32) + g2 * 32);
+      c2[m][0] = w2[0];
+      c2[m][1] = w2[1];
+    }
+  }
+  tile::wait_vmem();
+  lds_sync();
+  const ARole ro = a_role(lane);
+  Chain ch;
+  chain_init(ch);
+  for (int r = r0; r < r1; ++r) {
+    const int buf = __builtin_amdgcn_readfirstlane((r - r0) & 1);
+    if (r + 1 < r1)
+      copy_to_lds_untracked(a.hid + (size_t)(r + 1) * hbytes, s.planes[buf ^ 1], hbytes, wave, GU_WAVES, lane);
+    const uint8_t* planes = s.planes[buf];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+      const int q2 = wave + GU_WAVES * m;
+      if (!live || q2 >= NQ2) break;
+      const int g2 = 4 * q2 + kg;
+      f32x4_t acc = mx::zero_acc();
+      chain_load(ch, planes + min(4 * q2 + ro.kgR, GK - 1) * PB_BYTES, ro);
+      acc = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c2[m][0].x, c2[m][0].y), acc, ch.sa, mx::E8M0_TWO);
+      acc = mx::mfma_fp8_fp4<1>(ch.a[1], mx::q2_spread(c2[m][0].z, c2[m][0].w), acc, ch.sa, mx::E8M0_TWO);
+      acc = mx::mfma_fp8_fp4<2>(ch.a[2], mx::q2_spread(c2[m][1].x, c2[m][1].y), acc, ch.sa, mx::E8M0_TWO);
+      acc = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c2[m][1].z, c2[m][1].w), acc, ch.sa, mx::E8M0_TWO);
+      const float sh = g2 < GK ? piece_sums(planes + g2 * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
+      const int si = j * GK + min(g2, GK - 1);
+      float v = g2 < GK ? bf16_to_f32(s.sc[0][si]) * dot4(acc) + bf16_to_f32(s.sc[1][si]) * sh : 0.0f;
+      v = tile::sum_lane_groups(v);
+      if (lane < 16) s.red[q2][lane] = v;
+    }
+    lds_sync();
+    if (tid < 16) {
+      float part[MAX_NQ2];
+#pragma unroll
+      for (int q2 = 0; q2 < MAX_NQ2; ++q2) part[q2] = s.red[q2][tid];
+      float yv = 0.0f;
+      if (live) {
+#pragma unroll
+        for (int q2 = 0; q2 < MAX_NQ2; ++q2)
+          if (q2 < NQ2) yv = yv + part[q2];
+      }
+      a.y[((size_t)a.row_token[r] * a.k + a.row_slot[r]) * D + n0 + tid] = f32_to_bf16(yv);
+    }
+    tile::wait_vmem();
+    lds_sync();
+  }
+}
+
 }  // namespace
 
 // The shapes the matrix-core path takes (the rest use the bf16 kernels).
@@ -417,6 +679,34 @@ int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, c
   else CACHALOT_DN(4);
 #undef CACHALOT_DN
   return check_launch("q2mx_down_kernel");
+}
+
+// Batched decode over expert-major rows (grouped.hip's permutation): x planes of the
+// T tokens, then gate/up and down over the active experts.  tiles / tiles_n list the
+// active experts (one entry each, first row); hid holds rows x GK plane blocks and
+// xplanes T x D / 128.
+int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const Layout& L, const int32_t* slot_table,
+                        const int32_t* offsets, const int2* tiles, const int32_t* tiles_n, int max_active,
+                        const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k,
+                        float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s) {
+  hipLaunchKernelGGL(x_planes_rows_kernel, dim3(T, (D + 1023) / 1024), dim3(256), 0, s, x, D, xplanes);
+  int rc = check_launch("x_planes_rows_kernel");
+  if (rc) return rc;
+  BatchArgs a{xplanes, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w, D, F, k, limit,
+              hid, y};
+  const int NQ = D / 512;
+  const int mg = (NQ + GU_WAVES - 1) / GU_WAVES;
+  const dim3 grid_gu(max_active, F / 16);
+  if (mg <= 2) hipLaunchKernelGGL(q2mx_bgu_kernel<2>, grid_gu, dim3(GU_THREADS), 0, s, a);
+  else hipLaunchKernelGGL(q2mx_bgu_kernel<3>, grid_gu, dim3(GU_THREADS), 0, s, a);
+  rc = check_launch("q2mx_bgu_kernel");
+  if (rc) return rc;
+  const int NQ2 = ((F + 127) / 128 + 3) / 4;
+  const int md = (NQ2 + GU_WAVES - 1) / GU_WAVES;
+  const dim3 grid_dn(max_active, D / 16);
+  if (md <= 1) hipLaunchKernelGGL(q2mx_bdn_kernel<1>, grid_dn, dim3(GU_THREADS), 0, s, a);
+  else hipLaunchKernelGGL(q2mx_bdn_kernel<2>, grid_dn, dim3(GU_THREADS), 0, s, a);
+  return check_launch("q2mx_bdn_kernel");
 }
 
 }  // namespace cachalot

@@ -33,6 +33,14 @@
 #include <algorithm>
 
 namespace cachalot {
+
+// matrix-core batched decode (decode_q2_mx.hip)
+bool q2mx_supported(int D, int F, int k);
+int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
+                        const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
+                        int max_active, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
+                        int F, int k, float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s);
+
 namespace {
 
 using namespace decode;
@@ -642,22 +650,27 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   }
 }
 
-// Workspace of a grouped call: [tiles_n][tiles][hidden rows x F bf16], 256-byte aligned regions.
+// Workspace of a grouped call: [tiles_n][tiles][hidden][x planes], 256-byte aligned regions.
+// hidden: rows x F bf16, or rows x ceil(F / 128) plane blocks (matrix-core batched decode);
+// x planes: T x D / 128 plane blocks (same).
 struct GroupedWs {
-  size_t tiles_n, tiles, hidden, total;
+  size_t tiles_n, tiles, hidden, xplanes, total;
   int max_tiles;
 };
 
-inline GroupedWs grouped_ws(int T, int k, int E, int F) {
+inline GroupedWs grouped_ws(int T, int k, int E, int D, int F) {
   GroupedWs w;
   const int rows = T * k;
   w.max_tiles = rows / 16 + std::min(E, rows) + 1;   // bound for MT >= 16
   w.tiles_n = 0;
   w.tiles = 256;
   w.hidden = w.tiles + align256((size_t)w.max_tiles * sizeof(int2));
-  w.total = w.hidden + align256((size_t)rows * F * sizeof(uint16_t));
+  const size_t hid = std::max((size_t)rows * F * sizeof(uint16_t), (size_t)rows * ((F + 127) / 128) * 320);
+  w.xplanes = w.hidden + align256(hid);
+  w.total = w.xplanes + align256((size_t)T * ((D + 127) / 128) * 320);
   return w;
 }
+
 
 template <int KIND, int MT>
 int launch_grouped_mt(const GroupedArgs& gu, const GroupedArgs& dn, int max_tiles, size_t lds_gu, size_t lds_dn,
@@ -679,7 +692,8 @@ int launch_grouped_mt(const GroupedArgs& gu, const GroupedArgs& dn, int max_tile
   return check_launch("grouped_down_kernel");
 }
 
-// The 64-row-tile kernels stay selectable for FP4 (CACHALOT_GROUPED_SMALL=1) for comparison.
+// The earlier kernels stay selectable (CACHALOT_GROUPED_SMALL=1) for comparison: 64-row
+// tiles for FP4 prefill, bf16 MFMA for 2-bit batched decode.
 inline bool small_tiles_requested() {
   const char* env = getenv("CACHALOT_GROUPED_SMALL");
   return env && env[0] == '1';
@@ -700,7 +714,7 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   CACHALOT_REQUIRE(F % NT == 0 && F >= 64 && F <= KC * MAX_GROUPS, "%s: F=%d must be a multiple of 64 in 64..8192",
                    who, F);
   if (KIND == KIND_Q2) CACHALOT_REQUIRE(D % KC == 0, "%s: D=%d must be a multiple of the 128-code group", who, D);
-  const GroupedWs wo = grouped_ws(T, k, E, F);
+  const GroupedWs wo = grouped_ws(T, k, E, D, F);
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "%s: workspace %zu < %zu bytes", who, workspace_bytes, wo.total);
   Layout L;
@@ -715,6 +729,14 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   // tiles of 64 rows when experts see many tokens, 16 for batched decode
   const int MT = T * k >= 4 * E ? 64 : 16;
   uint32_t* zeros = reinterpret_cast<uint32_t*>(ws + wo.tiles_n + 128);
+  if (KIND == KIND_Q2 && MT == 16 && q2mx_supported(D, F, k) && !small_tiles_requested()) {
+    // few rows per expert: the matrix-core batched decode, one entry per active expert
+    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, 1 << 30, tiles, tiles_n, zeros);
+    rc = check_launch("tile_list_kernel");
+    if (rc) return rc;
+    return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, tiles, tiles_n, std::min(E, T * k), row_token,
+                               row_slot, row_w, D, F, k, limit, ws + wo.hidden, ws + wo.xplanes, y, s);
+  }
   const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested();
   hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, large ? G2_MT : MT, tiles, tiles_n,
                      zeros);
@@ -760,7 +782,7 @@ extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k
 extern "C" size_t cachalot_grouped_experts_workspace_bytes(int T, int k, int E, int D, int F) {
   (void)D;
   if (T <= 0 || k <= 0 || E <= 0 || F <= 0) return 0;
-  return cachalot::grouped_ws(T, k, E, F).total;
+  return cachalot::grouped_ws(T, k, E, D, F).total;
 }
 
 extern "C" int cachalot_grouped_experts_q2(const uint16_t* x, const uint8_t* pool,

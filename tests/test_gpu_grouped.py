@@ -156,6 +156,30 @@ def test_grouped_experts_batched_decode(cuda, kind):
                   + bf16_ulp(want + a))
 
 
+@pytest.mark.parametrize("path", ["matrix_core", "bf16"])
+@pytest.mark.parametrize("shape", [(4096, 2880), (5120, 2304)])
+def test_grouped_batched_decode_many_rows(cuda, path, shape, monkeypatch):
+    """2-bit batched decode with several rows per expert (B = 32 tokens over 40 experts):
+    the matrix-core batched kernels (default) and the bf16 grouped kernels
+    (CACHALOT_GROUPED_SMALL=1) against the oracle."""
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.storage.index import affine_format
+
+    monkeypatch.setenv("CACHALOT_GROUPED_SMALL", "1" if path == "bf16" else "0")
+    D, F = shape
+    fmt = affine_format(D, F)
+    rng = np.random.default_rng(13)
+    t, k = 32, 6
+    experts = list(rng.choice(384, size=40, replace=False))
+    idx, w = _zipf_routes(rng, t, k, experts)
+    store = make_store(fmt, n_layers=1, n_experts=384, keys=[(0, int(e)) for e in experts], n_slots=len(experts))
+    xb = osynth.activations(SEED, 700, t, D)
+    routed, out = grouped_experts(_bf16(xb, cuda), torch.from_numpy(idx).to(cuda), torch.from_numpy(w).to(cuda),
+                                  store.pool, store.layer_table(0), want_routed=True)
+    want, ys = _oracle_grouped(fmt, 0, bf16_bits_to_f32(xb), idx, w)
+    _check_rows(_np(routed), want, ys, path)
+
+
 def test_grouped_is_deterministic(cuda):
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format
