@@ -118,20 +118,26 @@ __global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __r
 __global__ void __launch_bounds__(1024) tile_list_kernel(const int32_t* __restrict__ offsets, int E, int MT,
                                                          int2* __restrict__ tiles, int32_t* __restrict__ tiles_n,
                                                          uint32_t* __restrict__ zeros) {
-  __shared__ int first[1024 + 1];
+  __shared__ int sc[1024];
   if (threadIdx.x < ZERO_WORDS) zeros[threadIdx.x] = 0u;   // source of the zero A columns past K
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      first[e] = run;
-      run += (offsets[e + 1] - offsets[e] + MT - 1) / MT;
-    }
-    first[E] = run;
-    tiles_n[0] = run;
+  // one thread per expert (E <= 1024): its tile count, then an inclusive scan (Hillis-Steele)
+  const int e = threadIdx.x;
+  int cnt = 0;
+  if (e < E) {
+    const int rows = offsets[e + 1] - offsets[e];
+    cnt = rows > 0 ? 1 + (rows - 1) / MT : 0;
   }
+  sc[e] = cnt;
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x)
-    for (int t = first[e]; t < first[e + 1]; ++t) tiles[t] = make_int2(e, offsets[e] + (t - first[e]) * MT);
+  for (int off = 1; off < 1024; off *= 2) {
+    const int v = e >= off ? sc[e - off] : 0;
+    __syncthreads();
+    sc[e] += v;
+    __syncthreads();
+  }
+  const int first = sc[e] - cnt;
+  if (e == 1023) tiles_n[0] = sc[1023];
+  for (int t = 0; t < cnt; ++t) tiles[first + t] = make_int2(e, offsets[e] + t * MT);
 }
 
 // ------------------------------------------------------------ grouped GEMM ---

@@ -111,6 +111,7 @@ constexpr int RT_T = 32;             // tokens per workgroup
 constexpr int RT_E = 64;             // experts per workgroup
 constexpr int RT_MAXCH = 80;         // D / 64 <= 80 (D <= 5120)
 constexpr int RT_PAD = 4;            // floats of padding per staged row (bank spread)
+constexpr int RT_MIN_T = 1024;       // fewer tokens: the 4-token kernel fills the chip better
 
 __global__ void __launch_bounds__(256) router_tiled_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ W, int T, int D, int E,
@@ -249,7 +250,8 @@ static void launch_scores_tt(const uint16_t* x, const uint16_t* W, int T, int D,
 int launch_router_scores(const uint16_t* x, const uint16_t* W, int T, int D, int E, float gate_temp, int fn,
                          float* scores, hipStream_t s, const decode::RouteTail* tail, uint8_t* xplanes) {
   decode::RouteTail none{};
-  if (T >= RT_T && D % 512 == 0 && D / CHUNKS <= RT_MAXCH) {
+  // the tiled kernel needs enough tiles to fill the chip (32 x 64 per workgroup)
+  if (T >= RT_MIN_T && D % 512 == 0 && D / CHUNKS <= RT_MAXCH) {
     hipLaunchKernelGGL(router_tiled_kernel, dim3((T + RT_T - 1) / RT_T, (E + RT_E - 1) / RT_E), dim3(256), 0, s, x,
                        W, T, D, E, gate_temp, fn, scores);
     return check_launch("router_tiled_kernel");

@@ -139,9 +139,10 @@ ROUTER_CASES = [
     (5, 128, 100, 1, "sigmoid", "ascending", 1.0, 1.0, True),
     (3, 256, 64, 64, "sqrt_softplus", "rank", 1.0, 1.0, True),
     (9, 5120, 384, 6, "sqrt_softplus", "ascending", 1.0, 1.5, True),
-    # many tokens: the tiled router kernel (partial token and expert tiles, D/64 = 16 and 80)
     (40, 5120, 384, 6, "sigmoid", "ascending", 1.0, 1.0, True),
-    (33, 1024, 100, 4, "sqrt_softplus", "rank", 1.3, 1.5, True),
+    # many tokens: the tiled router kernel (partial token and expert tiles, D/64 = 16 and 80)
+    (1030, 1024, 100, 4, "sqrt_softplus", "rank", 1.3, 1.5, True),
+    (1024, 5120, 64, 6, "sigmoid", "ascending", 1.0, 1.0, True),
 ]
 
 
