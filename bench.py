@@ -153,6 +153,66 @@ def batched_decode(args, store, gates, log_fn):
     return out
 
 
+def fp4_decode_config0(args, dev, log_fn):
+    """one token through one FP4 MoE layer (router + 6 FP4 experts), chained over 8
+    resident FP4 layers (58 GB, so the 256 MB MALL holds nothing between visits)."""
+    import torch
+
+    from cachalot_amd import synth
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+    from cachalot_amd.moe_decode import moe_layer_decode
+    from cachalot_amd.storage.index import fp4_format
+
+    D, F, E, K, L = 4096, 2880, 384, 6, 8
+    fmt = fp4_format(D, F)
+    loader = SyntheticLoader(fmt, args.seed + 11)
+    store = ResidentExpertStore(fmt=fmt, n_slots=L * E, n_layers=L, n_experts=E, device=dev)
+    store.preload([(la, e) for la in range(L) for e in range(E)], loader.fill_key)
+    table = store.track_slots()
+    gates = [synth.router_weights(args.seed + 11, la, E, D, dev) for la in range(L)]
+    x0 = synth.activations(args.seed + 11, 0, 1, D, dev)[0]
+
+    def step(x, s):
+        w, b = gates[s % L]
+        _, out, _ = moe_layer_decode(x, w, b, store.pool, table[s % L], topk=K, route_scale=1.0,
+                                     score_fn="sigmoid", swiglu_limit=10.0, addend=x)
+        return out
+
+    G = 8 * L
+    xbuf = x0.clone()
+    warm = xbuf
+    for s in range(G):
+        warm = step(warm, s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        xg = xbuf
+        for s in range(G):
+            xg = step(xg, s)
+        xbuf.copy_(xg)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = 8
+    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(e) * 1e3 / (reps * G)
+    expert_bytes = K * fmt.algorithmic_bytes
+    step_bytes = expert_bytes + E * D * 2 + E * 4
+    res = {"us_per_step": round(us, 2), "tok_per_s": round(1e6 / us, 1),
+           "expert_GBps": round(expert_bytes / (us * 1e-6) / 1e9, 1),
+           "hbm_frac_step": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+           "note": "chained layer steps (router + FP4 gate/up + down), graph replays; FP4 decode computes in fp32 "
+                   "(bf16 hi/lo MFMA), the reference's FP4 rounding points"}
+    log_fn(f"config 0 FP4 decode: {us:.2f} us/step, {res['expert_GBps']:.0f} GB/s expert bytes")
+    del store
+    torch.cuda.empty_cache()
+    return res
+
+
 def prefill_config3(args, dev, log_fn):
     """4096 tokens, FP4 bank, Zipf(1.1)-skewed router bias; one MoE layer."""
     import torch
@@ -391,6 +451,7 @@ def main() -> int:
                          "note": "the chained decode above walks all resident layers in order: one token through "
                                  f"the {L}-layer stack = {L} steps"}
     if not args.no_extra:
+        result["config0_fp4_decode"] = fp4_decode_config0(args, dev, log)
         result["config2_batched_decode"] = batched_decode(args, store, gates, log)
         result["config3_prefill"] = prefill_config3(args, dev, log)
     if not args.no_cpu:
