@@ -7,6 +7,8 @@ mirror the reference's call sites:
 * routing: ``route_topk``, ``route_topk_fused``, ``route_topk_batch``, ``route_topk_rows``
 * decode:  ``moe_layer_forward``, ``fused_routed_experts``, ``affine_routed_experts``
 * prefill / batched decode: ``moe_prefill_grouped``, ``grouped_experts``
+* shared FP8 expert: ``shared_expert_forward``, ``shared_expert_forward_fused``,
+  ``shared_expert_forward_batched``, ``fp8_linear``, ``quantize_fp8_activation``
 * store:   ``ResidentExpertStore`` over an ``HBMSlotPool``; formats in ``storage.index``
 """
 from __future__ import annotations
@@ -16,6 +18,8 @@ __version__ = "0.1.0"
 __all__ = [
     "RouterResult", "route_topk", "route_topk_fused", "route_topk_batch", "route_topk_rows",
     "moe_layer_forward", "moe_prefill_grouped", "grouped_experts", "fused_routed_experts", "affine_routed_experts", "affine_expert_forward",
+    "shared_expert_forward", "shared_expert_forward_fused", "shared_expert_forward_batched", "fp8_linear",
+    "fp8_linear_quantized", "quantize_fp8_activation",
     "ResidentExpertStore", "HBMSlotPool", "ExpertFormat", "FP4_FORMAT", "affine_format", "fp4_format",
 ]
 
@@ -30,6 +34,10 @@ def __getattr__(name):  # lazy: importing the package does not load torch or the
     if name in ("moe_prefill_grouped", "grouped_experts"):
         from . import moe_prefill
         return getattr(moe_prefill, name)
+    if name in ("shared_expert_forward", "shared_expert_forward_fused", "shared_expert_forward_batched",
+                "fp8_linear", "fp8_linear_quantized", "quantize_fp8_activation"):
+        from . import shared_expert
+        return getattr(shared_expert, name)
     if name == "moe_layer_forward":
         from .moe_layer import moe_layer_forward
         return moe_layer_forward

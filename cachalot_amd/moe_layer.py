@@ -13,9 +13,11 @@ launches (router scores; top-k + slot lookup + gate/up; down + route-order
 combine), no host synchronisation.  When a layer is not fully resident the host path is taken:
 one synchronisation, ``get_many`` (which loads misses), then the same kernels.
 
-The FP8 shared expert the reference adds into the combine
-(``moe_layer_metal.py:381-397``) is not built yet; ``shared_*`` must be None,
-and ``addend`` (bf16 [D], optional) is added before the final cast instead.
+The FP8 shared expert (``shared_*``, ``moe_layer_metal.py:381-397``) runs
+first, on the same stream, and its bf16 output is added in the combine:
+``out = bf16(routed + shared)``.  ``addend`` (bf16 [D]) is the same hook for a
+caller that computes the shared branch itself; it cannot be combined with
+``shared_*``.
 """
 from __future__ import annotations
 
@@ -24,6 +26,7 @@ import torch
 from .cache.resident_store import ResidentExpertStore
 from .moe_decode import decode_experts, moe_layer_decode
 from .router import RouterResult, route_topk, route_topk_fused
+from .shared_expert import shared_args, shared_expert_forward
 from .storage.index import ExpertEntry
 
 
@@ -53,9 +56,11 @@ def moe_layer_forward(
 ) -> tuple[torch.Tensor, RouterResult]:
     if x.ndim != 1:
         raise ValueError(f"x must be 1D for decode, got {tuple(x.shape)}")
-    if any(t is not None for t in (shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3,
-                                   shared_w3_scales)):
-        raise NotImplementedError("the FP8 shared expert is not part of this build yet")
+    shared = shared_args(shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3, shared_w3_scales)
+    if shared is not None:
+        if addend is not None:
+            raise ValueError("pass either the shared expert weights or addend, not both")
+        addend = shared_expert_forward(x.to(torch.bfloat16), **shared, swiglu_limit=swiglu_limit)
     pool = expert_store.pool
     if expert_store.layer_fully_resident(layer_id) and x.dtype == torch.bfloat16 and topk <= 8:
         # routing, slot lookup and experts on the device, no host round trip

@@ -14,9 +14,10 @@ route slots in decode order (``:526-545``).  The host reads nothing back when
 the layer is fully resident in HBM; otherwise one synchronisation fetches the
 routed expert ids so that ``get_many`` can load the misses first.
 
-The FP8 shared expert of the reference (``:532-545``) is not built yet:
-``shared_*`` must be None; ``addend`` ([T, D] bf16, optional) is added before
-the final cast instead.
+The FP8 shared expert (``shared_*``, ``:532-545``) runs over all rows and its
+bf16 output is added in the combine: ``out = bf16(routed + shared)``.
+``addend`` ([T, D] bf16) is the same hook for a caller that computes the
+shared branch itself; it cannot be combined with ``shared_*``.
 """
 from __future__ import annotations
 
@@ -26,6 +27,7 @@ from . import _lib
 from .cache.resident_store import ResidentExpertStore
 from .cache.slots import HBMSlotPool
 from .router import RouterResult, route_topk_batch, route_topk_rows
+from .shared_expert import shared_args, shared_expert_forward_batched
 from .storage.index import ExpertEntry
 
 _WORKSPACES: dict[int, torch.Tensor] = {}
@@ -143,9 +145,11 @@ def moe_prefill_grouped(
         raise NotImplementedError(
             "per-token bias_vl selection is only wired for the batched (route_topk_rows) path; "
             "batched=False has no image_mask support")
-    if any(t is not None for t in (shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3,
-                                   shared_w3_scales)):
-        raise NotImplementedError("the FP8 shared expert is not part of this build yet")
+    shared = shared_args(shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3, shared_w3_scales)
+    if shared is not None:
+        if addend is not None:
+            raise ValueError("pass either the shared expert weights or addend, not both")
+        addend = shared_expert_forward_batched(x.to(torch.bfloat16), **shared, swiglu_limit=swiglu_limit)
     if batched:
         indices, weights, scores = route_topk_rows(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp,
                                                    route_scale=route_scale, norm_topk_prob=norm_topk_prob,

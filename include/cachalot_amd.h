@@ -183,6 +183,45 @@ int cachalot_grouped_experts_fp4(const uint16_t* x, const uint8_t* pool,
 int cachalot_unpermute_combine(const uint16_t* y, const uint16_t* addend, int T, int k, int D, float* routed,
                                uint16_t* out, cachalot_stream_t stream);
 
+/* FP8 (E4M3FN values, E8M0 power-of-two scales per 32-element block).
+ *
+ * cachalot_fp8_act_quant: per 32-element block of each row of x [M, K] bf16,
+ * amax = max(max|x|, 1e-4), e = ceil(log2(fl32(amax / 448))),
+ * q = E4M3(clip(x / 2^e, -448, 448)) rounded to nearest even -> q [M, K] u8,
+ * scales [M, K/32] u8 (E8M0, e + 127).  K a multiple of 32.  Replaces
+ * quantize_fp8_activation / quantize_activation_fp8
+ * (src/cachalot/model/fp8_linear_metal.py:30-53, fp8_ref.py:28-93).
+ *
+ * cachalot_fp8_linear_quantized: y[t, n] = bf16(sum_kb dot(q[t, kb], w[n, kb])
+ * * 2^(q_scales[t, kb]-127) * 2^(w_scales[n/32, kb]-127)), fp32 accumulation;
+ * w [N, K] u8 E4M3, w_scales [ceil(N/32), K/32] u8; N a multiple of 16.
+ * Replaces fp8_linear_quantized (fp8_linear_metal.py:56-89) and
+ * fp8_gemv_reference (fp8_ref.py:96-231).
+ *
+ * cachalot_shared_expert_fp8: the shared expert for M tokens x [M, D] bf16:
+ * q = act_quant(x); g = bf16(w1 q), u = bf16(w3 q); if swiglu_limit > 0,
+ * u = clip(u, -L, L), g = min(g, L); h = bf16(silu(g) * u);
+ * y = bf16(w2 act_quant(h)) [M, D] bf16.  w1, w3 [F, D] with scales
+ * [ceil(F/32), D/32]; w2 [D, F] with scales [ceil(D/32), F/32].  D and F
+ * multiples of 32 and of 16.  Workspace from
+ * cachalot_shared_expert_fp8_workspace_bytes (scratch only).  The layer
+ * combine adds y through the `addend` argument of the decode / combine calls:
+ * out = bf16(routed + y), the reference's order (moe_layer_metal.py:381-397,
+ * moe_prefill_grouped.py:532-545).  Replaces shared_expert_forward /
+ * shared_expert_forward_fused (shared_expert_metal.py:44-188) and
+ * shared_expert_forward_batched (moe_prefill_batched.py:104-125). */
+int cachalot_fp8_act_quant(const uint16_t* x, int M, int K, uint8_t* q, uint8_t* scales,
+                           cachalot_stream_t stream);
+int cachalot_fp8_linear_quantized(const uint8_t* q, const uint8_t* q_scales, const uint8_t* w,
+                                  const uint8_t* w_scales, int M, int K, int N, uint16_t* y,
+                                  cachalot_stream_t stream);
+size_t cachalot_shared_expert_fp8_workspace_bytes(int M, int D, int F);
+int cachalot_shared_expert_fp8(const uint16_t* x, const uint8_t* w1, const uint8_t* w1_scales,
+                               const uint8_t* w3, const uint8_t* w3_scales, const uint8_t* w2,
+                               const uint8_t* w2_scales, int M, int D, int F, float swiglu_limit,
+                               uint16_t* y, void* workspace, size_t workspace_bytes,
+                               cachalot_stream_t stream);
+
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32
  *   (replaces dequantize_fp4_weight / dequantize_fp4_dense,

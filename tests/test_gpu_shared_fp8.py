@@ -1,0 +1,157 @@
+"""GPU parity of the FP8 shared expert against oracle/fp8.py.
+
+Bar: act_quant codes and block exponents bit-exact; the FP8 linear within one
+bf16 ulp of the exact block-scaled sum, plus 2^-20 of the sum of the terms'
+magnitudes for the fp32 accumulation order (the reference accumulates in fp32
+too, in another order); the
+shared expert's output within max relative error 2e-3 (max |got - want| /
+max |want|) plus one bf16 ulp per element for its final cast.  Weights follow
+the reference's own test generator (tests/test_shared_expert_fused.py:31-38:
+random E4M3 bytes, E8M0 scales in [120, 130]), NaN codes excluded.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import SEED, bf16_ulp, make_store, rel_err
+from oracle import fp8 as ofp8
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _bf16_np(t):
+    return bf16_bits_to_f32(_np(t.contiguous().view(torch.int16)).view(np.uint16))
+
+
+def _to_dev_bf16(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(f32_to_bf16_bits(np.asarray(a, np.float32)).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _weights(rng, n, k):
+    w = rng.integers(0, 256, size=(n, k), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x3F
+    s = rng.integers(120, 131, size=(-(-n // 32), k // 32), dtype=np.uint8)
+    return w, s
+
+
+def _expert(rng, d, f):
+    return _weights(rng, f, d), _weights(rng, f, d), _weights(rng, d, f)
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_act_quant_bit_exact(cuda):
+    from cachalot_amd.shared_expert import quantize_fp8_activation
+
+    rng = np.random.default_rng(SEED)
+    m, k = 37, 4096
+    x = rng.standard_normal((m, k)) * np.exp2(rng.integers(-30, 30, size=(m, 1)))
+    x[0, :32] = 0.0                                               # amax floor 1e-4
+    x[1, :32] = -1e-30                                            # negative underflow -> -0 codes
+    x[2, :32] = 448.0 * 2.0 ** -5                                 # amax / 448 a power of two
+    vals = ofp8.e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = (vals[1:] + vals[:-1]) / 2                             # ties: RNE picks the even code
+    x[3, :32] = np.concatenate([[448.0], mids[-31:]]) * 2.0 ** 3
+    x[4, :32] = np.concatenate([[448.0], mids[:31]]) * 2.0 ** -2
+    x[5, :64] = np.concatenate([[448.0], -mids[40:71]] * 2) * 2.0 ** 7
+    x = round_bf16(x.astype(np.float32))
+    q = quantize_fp8_activation(_to_dev_bf16(x, cuda))
+    wq, we = ofp8.act_quant(x)
+    assert np.array_equal(_np(q.values), wq)
+    assert np.array_equal(_np(q.scales).astype(np.int32), we + 127)
+    # 1-D input (the decode shape)
+    q1 = quantize_fp8_activation(_to_dev_bf16(x[7], cuda))
+    assert np.array_equal(_np(q1.values), wq[7])
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 2880), (3, 2880, 4096), (16, 320, 96), (200, 1024, 640)])
+def test_fp8_linear_within_one_bf16_ulp(cuda, m, k, n):
+    from cachalot_amd.shared_expert import fp8_linear
+
+    rng = np.random.default_rng(SEED + m)
+    w, s = _weights(rng, n, k)
+    x = round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    y = fp8_linear(_to_dev_bf16(x, cuda), _dev(w, cuda), _dev(s, cuda))
+    torch.cuda.synchronize()
+    q, e = ofp8.act_quant(x)
+    exact = ofp8.linear(q, e, w, s)
+    mag = ofp8.linear(q & 0x7F, e, w & 0x7F, s)                  # sum of |terms|: fp32 summation-order slack
+    got = _bf16_np(y)
+    assert np.all(np.abs(got - exact) <= bf16_ulp(exact) + 2.0 ** -20 * mag), (m, k, n)
+    assert np.mean(got == round_bf16(exact.astype(np.float32))) > 0.99
+
+
+@pytest.mark.parametrize("m,d,f", [(1, 4096, 2880), (1, 5120, 2304), (5, 256, 192), (130, 1024, 640)])
+def test_shared_expert_matches_oracle(cuda, m, d, f):
+    from cachalot_amd.shared_expert import shared_expert_forward, shared_expert_forward_batched
+
+    rng = np.random.default_rng(SEED + d + m)
+    (w1, s1), (w3, s3), (w2, s2) = _expert(rng, d, f)
+    x = round_bf16(rng.standard_normal((m, d)).astype(np.float32))
+    dev = {n: _dev(a, cuda) for n, a in dict(w1=w1, w1_scales=s1, w3=w3, w3_scales=s3, w2=w2, w2_scales=s2).items()}
+    xd = _to_dev_bf16(x, cuda)
+    for limit in (10.0, 0.25):
+        y = shared_expert_forward(xd[0], **dev, swiglu_limit=limit)[None] if m == 1 else \
+            shared_expert_forward_batched(xd, **dev, swiglu_limit=limit)
+        got = _bf16_np(y)
+        want = ofp8.shared_expert(x, w1, s1, w3, s3, w2, s2, limit=limit)
+        assert rel_err(got, want) <= TOL + 2.0 ** -8, (m, d, f, limit)
+        assert np.all(np.abs(got - want) <= TOL * np.abs(want).max() + bf16_ulp(want)), (m, d, f, limit)
+
+
+def test_shared_expert_fused_w13_is_identical(cuda):
+    from cachalot_amd.shared_expert import shared_expert_forward, shared_expert_forward_fused
+
+    rng = np.random.default_rng(SEED + 1)
+    (w1, s1), (w3, s3), (w2, s2) = _expert(rng, 1024, 640)
+    x = _to_dev_bf16(round_bf16(rng.standard_normal(1024).astype(np.float32)), cuda)
+    a = shared_expert_forward(x, w1=_dev(w1, cuda), w1_scales=_dev(s1, cuda), w3=_dev(w3, cuda),
+                              w3_scales=_dev(s3, cuda), w2=_dev(w2, cuda), w2_scales=_dev(s2, cuda))
+    b = shared_expert_forward_fused(x, w13=_dev(np.concatenate([w1, w3]), cuda),
+                                    w13_scales=_dev(np.concatenate([s1, s3]), cuda), w2=_dev(w2, cuda),
+                                    w2_scales=_dev(s2, cuda))
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_layer_entries_add_the_shared_expert(cuda):
+    """moe_layer_forward / moe_prefill_grouped with shared_* give exactly the
+    output of the same call with the shared expert's output as the addend, the
+    reference's bf16(routed + shared) (moe_layer_metal.py:381-397,
+    moe_prefill_grouped.py:532-545)."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_layer import moe_layer_forward
+    from cachalot_amd.moe_prefill import moe_prefill_grouped
+    from cachalot_amd.shared_expert import shared_expert_forward, shared_expert_forward_batched
+    from cachalot_amd.storage.index import affine_format
+
+    d, f, e = 4096, 2880, 16
+    store = make_store(affine_format(d, f), n_layers=1, n_experts=e)
+    w, b = synth.router_weights(SEED, 0, e, d, cuda)
+    rng = np.random.default_rng(SEED + 2)
+    (w1, s1), (w3, s3), (w2, s2) = _expert(rng, d, 2304)
+    shared = dict(shared_w1=_dev(w1, cuda), shared_w1_scales=_dev(s1, cuda), shared_w2=_dev(w2, cuda),
+                  shared_w2_scales=_dev(s2, cuda), shared_w3=_dev(w3, cuda), shared_w3_scales=_dev(s3, cuda))
+    plain = {k[len("shared_"):]: v for k, v in shared.items()}
+    kw = dict(layer_id=0, gate_weight=w, gate_bias=b, expert_index=None, expert_store=store, topk=6,
+              route_scale=1.0, score_fn="sigmoid")
+    x = synth.activations(SEED, 90, 8, d, cuda)
+    out, route = moe_layer_forward(x[0], **kw, **shared)
+    ref, route2 = moe_layer_forward(x[0], **kw, addend=shared_expert_forward(x[0], **plain))
+    assert torch.equal(route.indices, route2.indices)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    outp, _ = moe_prefill_grouped(x, **kw, **shared)
+    refp, _ = moe_prefill_grouped(x, **kw, addend=shared_expert_forward_batched(x, **plain))
+    assert torch.equal(outp.view(torch.int16), refp.view(torch.int16))
+    with pytest.raises(ValueError):
+        moe_layer_forward(x[0], **kw, **shared, addend=refp[0])
