@@ -35,60 +35,57 @@ constexpr float MIN_AMAX = 1e-4f;
 constexpr uint32_t E8M0_ONE = 127u;
 
 // ------------------------------------------------------------ act_quant ---
-// float -> E4M3FN byte, round to nearest even, for |v| <= 448 (callers clip).
-// Normal range (|v| >= 2^-6): round the fp32 significand to 3 bits by adding
-// half an E4M3 ulp minus one plus the kept lsb, then rebias the exponent
-// (fp32 bias 127, E4M3 bias 7: field 120 << 3 = 960).  Below 2^-6 the E4M3
-// value is m * 2^-9 with m = rint(|v| * 512) in 0..8 (8 is the smallest
-// normal, code 0x08, so the same m is the code).  The sign is kept for zeros.
-__host__ __device__ inline uint32_t e4m3_encode(float v) {
-  uint32_t bits;
-  __builtin_memcpy(&bits, &v, 4);
-  const uint32_t sign = (bits >> 24) & 0x80u;
-  const uint32_t mag = bits & 0x7fffffffu;
-  uint32_t code;
-  if (mag < 0x3c800000u) {   // 2^-6
-    float a;
-    __builtin_memcpy(&a, &mag, 4);
-    code = (uint32_t)__builtin_rintf(a * 512.0f);
-  } else {
-    code = ((mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20) - 960u;
-  }
-  return code | sign;
-}
-
 // Block exponent e = ceil(log2(r)) of r = fl32(amax / 448) >= 2^-23 (a normal
 // float): the unbiased exponent, plus one unless the significand is exactly 1.
-__host__ __device__ inline int block_exponent(float amax) {
-  const float r = amax / FP8_MAX;
-  uint32_t bits;
-  __builtin_memcpy(&bits, &r, 4);
+__device__ __forceinline__ int block_exponent(float amax) {
+  const uint32_t bits = __float_as_uint(amax / FP8_MAX);
   return (int)((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0u ? 1 : 0);
 }
 
-// 2^-e as a float (e in [-23, 126]).
+// 2^e and 2^-e as floats (e in [-23, 126]).
+__device__ __forceinline__ float pow2(int e) { return __uint_as_float((uint32_t)(127 + e) << 23); }
 __device__ __forceinline__ float pow2_neg(int e) { return __uint_as_float((uint32_t)(127 - e) << 23); }
 
-// Quantize one 32-element block: codes (8 words, element i in byte i % 4 of
-// word i / 4) and the E8M0 exponent byte.
-__device__ __forceinline__ uint32_t quant_block(const float (&v)[BLOCK], uint32_t (&codes)[8]) {
+__device__ __forceinline__ float clip448(float v) { return fminf(fmaxf(v, -FP8_MAX), FP8_MAX); }
+
+// One quarter (8 consecutive values) of a 32-element block whose four quarters
+// sit in an aligned group of 4 lanes (quarter q in lane 4 g + q): the block's
+// exponent (amax over the 4 lanes by two quad swaps) and this quarter's E4M3
+// codes, element i in byte i % 4 of word i / 4, converted by the hardware
+// round-to-nearest-even fp32 -> E4M3 converter after the exact power-of-two
+// scaling and the clip.  Every lane of the wave must execute it.
+__device__ __forceinline__ uint2 quant_quarter(const float (&v)[8], int& e) {
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < BLOCK; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, MIN_AMAX);
-  const int e = block_exponent(amax);
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __uint_as_float(xor1_u32(__float_as_uint(amax))));
+  amax = fmaxf(amax, __uint_as_float(xor2_u32(__float_as_uint(amax))));
+  e = block_exponent(fmaxf(amax, MIN_AMAX));
   const float inv = pow2_neg(e);
+  uint2 w;
+  int t = __builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[0] * inv), clip448(v[1] * inv), 0, false);
+  w.x = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[2] * inv), clip448(v[3] * inv), t, true);
+  t = __builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[4] * inv), clip448(v[5] * inv), 0, false);
+  w.y = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[6] * inv), clip448(v[7] * inv), t, true);
+  return w;
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& w, float (&v)[8]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float s = fminf(fmaxf(v[4 * w + b] * inv, -FP8_MAX), FP8_MAX);
-      word |= e4m3_encode(s) << (8 * b);
-    }
-    codes[w] = word;
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(ws[i] << 16);
+    v[2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
   }
-  return (uint32_t)(e + 127);
+}
+
+// h = bf16(silu(min(g, L)) * clip(u, -L, L)) from bf16 g and u (L <= 0: no clamp).
+__device__ __forceinline__ float swiglu_h(float g, float u, float limit) {
+  if (limit > 0.0f) {
+    u = fminf(fmaxf(u, -limit), limit);
+    g = fminf(g, limit);
+  }
+  return round_bf16(decode::silu_f32(g) * u);
 }
 
 struct QuantArgs {
@@ -100,52 +97,33 @@ struct QuantArgs {
   uint8_t* e;             // [M, K / 32] E8M0
 };
 
-__device__ __forceinline__ void load_bf16x32(const uint16_t* src, float (&v)[BLOCK]) {
-  const uint4* p = reinterpret_cast<const uint4*>(src);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint4 w = p[j];
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[8 * j + 2 * i] = __uint_as_float(ws[i] << 16);
-      v[8 * j + 2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
-    }
-  }
-}
-
-// One thread per 32-element block.  SWIGLU: the block's h values first,
-// h = bf16(silu(min(g, L)) * clip(u, -L, L)) from the bf16 g and u.
+// Four lanes per 32-element block, 8 values (one 16-byte load) each.  SWIGLU:
+// the values are h = swiglu(g, u) from the bf16 g | u rows.
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void quant_kernel(QuantArgs p) {
-  const int nb = p.K / BLOCK;
-  const long blk = (long)blockIdx.x * 256 + threadIdx.x;
-  if (blk >= (long)p.M * nb) return;
-  const int t = (int)(blk / nb), b = (int)(blk % nb);
-  float v[BLOCK];
-  if constexpr (SWIGLU) {
-    float u[BLOCK];
-    const uint16_t* row = p.x + (size_t)t * p.ldx;
-    load_bf16x32(row + b * BLOCK, v);
-    load_bf16x32(row + p.K + b * BLOCK, u);
+  const int nq = p.K / 8;                                   // quarters per row
+  const long qi = (long)blockIdx.x * 256 + threadIdx.x;
+  const bool ok = qi < (long)p.M * nq;
+  const int t = ok ? (int)(qi / nq) : 0, k8 = ok ? (int)(qi % nq) * 8 : 0;
+  const uint16_t* row = p.x + (size_t)t * p.ldx;
+  float v[8];
+  if (ok) {
+    unpack_bf16x8(*reinterpret_cast<const uint4*>(row + k8), v);
+    if constexpr (SWIGLU) {
+      float u[8];
+      unpack_bf16x8(*reinterpret_cast<const uint4*>(row + p.K + k8), u);
 #pragma unroll
-    for (int i = 0; i < BLOCK; ++i) {
-      float g = v[i], uu = u[i];
-      if (p.limit > 0.0f) {
-        uu = fminf(fmaxf(uu, -p.limit), p.limit);
-        g = fminf(g, p.limit);
-      }
-      v[i] = round_bf16(decode::silu_f32(g) * uu);
+      for (int i = 0; i < 8; ++i) v[i] = swiglu_h(v[i], u[i], p.limit);
     }
   } else {
-    load_bf16x32(p.x + (size_t)t * p.ldx + b * BLOCK, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
   }
-  uint32_t codes[8];
-  const uint32_t eb = quant_block(v, codes);
-  uint4* dst = reinterpret_cast<uint4*>(p.q + (size_t)t * p.K + b * BLOCK);
-  dst[0] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
-  dst[1] = make_uint4(codes[4], codes[5], codes[6], codes[7]);
-  p.e[(size_t)t * nb + b] = (uint8_t)eb;
+  int e;
+  const uint2 w = quant_quarter(v, e);
+  if (!ok) return;
+  *reinterpret_cast<uint2*>(p.q + (size_t)t * p.K + k8) = w;
+  if ((k8 & 31) == 0) p.e[(size_t)t * (p.K / BLOCK) + k8 / BLOCK] = (uint8_t)(e + 127);
 }
 
 // --------------------------------------------------------------- linear ---
@@ -167,18 +145,22 @@ struct Operand {
   uint32_t s;
 };
 
+// Branch-free: out-of-range lanes load from the row start and are zeroed after,
+// so every load is issued unconditionally and the compiler can wait for exactly
+// the loads a use needs (loads under a branch make it wait for all of them).
 __device__ __forceinline__ Operand load_operand(const uint8_t* base, const uint8_t* scales, int K, int c, int kg,
                                                 bool row_ok) {
   Operand o;
   const int k0 = c * CHUNK + BLOCK * kg;
-  o.lo = make_uint4(0, 0, 0, 0);
-  o.hi = make_uint4(0, 0, 0, 0);
-  if (row_ok && k0 < K) {
-    o.lo = *reinterpret_cast<const uint4*>(base + k0);
-    o.hi = *reinterpret_cast<const uint4*>(base + k0 + 16);
-  }
-  const int blk = 4 * c + kg;
-  o.s = blk < K / BLOCK ? (uint32_t)scales[blk] : E8M0_ONE;
+  const bool ok = row_ok && k0 < K;
+  const int kk = ok ? k0 : 0, blk = ok ? 4 * c + kg : 0;
+  const uint4 lo = *reinterpret_cast<const uint4*>(base + kk);
+  const uint4 hi = *reinterpret_cast<const uint4*>(base + kk + 16);
+  const uint32_t sc = scales[blk];
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  o.lo = ok ? lo : z;
+  o.hi = ok ? hi : z;
+  o.s = ok ? sc : E8M0_ONE;
   return o;
 }
 
@@ -304,6 +286,155 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs p) {
   }
 }
 
+// ---------------------------------------------------------- decode GEMV ---
+// Few tokens (M <= DEC_MT per workgroup tile): the activation rows are
+// quantized by the workgroup itself into LDS (E4M3 codes + E8M0 exponents, the
+// act_quant above), so a decode call is two launches:
+//   gate/up (PAIRED): a 16-column tile = 8 rows of w1 and the same 8 rows of w3;
+//     the epilogue forms h = bf16(silu(min(g, L)) * clip(u, -L, L)) from the
+//     bf16-rounded g and u of each row and writes h [M, F] bf16;
+//   down: 16 rows of w2 over act_quant(h), y [M, D] bf16.
+// The waves split the K chunks; a wave's first PF chunks of weights are
+// requested before the activation rows are quantized, so the HBM stream starts
+// at once (the activation loads are issued first, so waiting for them leaves
+// the weight loads in flight).
+constexpr int DEC_MT = 4;
+constexpr int DEC_MAX_K = 5120;
+#ifndef CACHALOT_DEC_WAVES
+#define CACHALOT_DEC_WAVES 8
+#endif
+constexpr int DEC_WAVES = CACHALOT_DEC_WAVES;      // waves per workgroup (they split K)
+constexpr int DEC_PF = 32 / DEC_WAVES;             // chunks of weights in flight per wave
+
+struct DecodeArgs {
+  const uint16_t* a;         // bf16 activation rows [M, K], row stride lda
+  int lda;
+  const uint8_t* w[2];       // w1, w3 (PAIRED) or w2
+  const uint8_t* ws[2];
+  int M, N, K;               // N = rows per matrix
+  float limit;
+  uint16_t* out;             // PAIRED: h [M, N]; else y [M, N]; row stride ldo
+  int ldo;
+};
+
+__host__ __device__ inline int dec_stride(int K) { return K + 16; }
+__host__ __device__ inline int dec_lds_bytes(int K, int waves) {
+  const int codes = DEC_MT * dec_stride(K), scales = DEC_MT * (K / BLOCK);
+  return ((codes + scales + 15) & ~15) + waves * 64 * 4 * 4;
+}
+
+template <bool PAIRED, int WAVES, int PF>
+__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs p) {
+  constexpr int NT = WAVES * 64;
+  constexpr int XP = (DEC_MT * DEC_MAX_K / 8 + NT - 1) / NT;   // activation quarters per thread
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, kg = lane >> 4;
+  const int K = p.K, nkb = K / BLOCK, nch = (K + CHUNK - 1) / CHUNK, stride = dec_stride(K);
+  const int t0 = blockIdx.y * DEC_MT, mt = min(DEC_MT, p.M - t0);
+  uint8_t* codes = lds;
+  uint8_t* scl = lds + DEC_MT * stride;
+  float* red = reinterpret_cast<float*>(lds + ((DEC_MT * stride + DEC_MT * nkb + 15) & ~15));
+
+  // 1. the activation quarters this thread quantizes (loads first in program order)
+  const int nq = K / 8, total = mt * nq;
+  uint4 xv[XP];
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    const int q = min(threadIdx.x + NT * i, total - 1);     // unconditional load; extra lanes are unused
+    const int r = q / nq, k8 = (q - r * nq) * 8;
+    xv[i] = *reinterpret_cast<const uint4*>(p.a + (size_t)(t0 + r) * p.lda + k8);
+  }
+  __builtin_amdgcn_sched_barrier(0);   // keep the activation loads ahead of the weight loads
+
+  // 2. this wave's first PF chunks of weights
+  int mat, n;
+  if constexpr (PAIRED) {
+    mat = c16 >> 3;
+    n = blockIdx.x * 8 + (c16 & 7);
+  } else {
+    mat = 0;
+    n = blockIdx.x * 16 + c16;
+  }
+  // (select, not index: a lane-dependent index into the argument block would be a
+  // vector memory load, ordered behind the activation loads above)
+  const uint8_t* brow = (mat ? p.w[1] : p.w[0]) + (size_t)n * K;
+  const uint8_t* bsc = (mat ? p.ws[1] : p.ws[0]) + (size_t)(n / 32) * nkb;
+  Operand B[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    const int c = wave + WAVES * i;
+    B[i] = load_operand(brow, bsc, c < nch ? K : 0, c, kg, true);
+  }
+
+  // 3. quantize the activation rows into LDS
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    if (NT * i >= total) break;                        // uniform
+    const int q = threadIdx.x + NT * i;
+    float v[8];
+    unpack_bf16x8(q < total ? xv[i] : make_uint4(0, 0, 0, 0), v);
+    int e;
+    const uint2 w = quant_quarter(v, e);
+    if (q < total) {
+      const int r = q / nq, k8 = (q - r * nq) * 8;
+      *reinterpret_cast<uint2*>(codes + r * stride + k8) = w;
+      if ((k8 & 31) == 0) scl[r * nkb + k8 / BLOCK] = (uint8_t)(e + 127);
+    }
+  }
+  lds_sync();
+
+  // 4. chunks: A from LDS (rows >= mt are zero), B from registers
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = wave;; c0 += WAVES * PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int c = c0 + WAVES * i;
+      if (c >= nch) break;
+      const int k0 = c * CHUNK + BLOCK * kg;
+      Operand A;
+      A.lo = make_uint4(0, 0, 0, 0);
+      A.hi = make_uint4(0, 0, 0, 0);
+      A.s = E8M0_ONE;
+      if (c16 < mt && k0 < K) {
+        A.lo = *reinterpret_cast<const uint4*>(codes + c16 * stride + k0);
+        A.hi = *reinterpret_cast<const uint4*>(codes + c16 * stride + k0 + 16);
+        A.s = scl[c16 * nkb + 4 * c + kg];
+      }
+      const float sa = e8m0_to_f32(A.s), sb = e8m0_to_f32(B[i].s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma_bf16(step_values(A, j, sa), step_values(B[i], j, sb), acc);
+    }
+    if (c0 + WAVES * PF >= nch) break;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int c = c0 + WAVES * PF + WAVES * i;
+      B[i] = load_operand(brow, bsc, c < nch ? K : 0, c, kg, true);
+    }
+  }
+
+  // 5. sum the waves' tiles in wave order; D[i][j] is lane j + 16 (i / 4), register i % 4
+#pragma unroll
+  for (int j = 0; j < 4; ++j) red[(wave * 64 + lane) * 4 + j] = acc[j];
+  __syncthreads();
+  const int j = threadIdx.x & 15, i = threadIdx.x >> 4;
+  if (i >= mt) return;
+  auto total_of = [&](int col) {
+    const int idx = ((col + 16 * (i >> 2)) * 4) + (i & 3);
+    float t = red[idx];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += red[256 * w + idx];
+    return t;
+  };
+  if constexpr (PAIRED) {
+    if (j >= 8) return;
+    const float g = round_bf16(total_of(j)), u = round_bf16(total_of(j + 8));
+    p.out[(size_t)(t0 + i) * p.ldo + blockIdx.x * 8 + j] = f32_to_bf16(swiglu_h(g, u, p.limit));
+  } else {
+    p.out[(size_t)(t0 + i) * p.ldo + blockIdx.x * 16 + j] = f32_to_bf16(total_of(j));
+  }
+}
+
 // ------------------------------------------------------------------ host ---
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
@@ -331,8 +462,8 @@ inline Workspace carve(void* base, int M, int D, int F) {
 int launch_quant(const uint16_t* x, int ldx, int M, int K, bool swiglu, float limit, uint8_t* q, uint8_t* e,
                  hipStream_t s) {
   QuantArgs a{x, ldx, M, K, limit, q, e};
-  const long blocks = (long)M * (K / BLOCK);
-  const dim3 grid((unsigned)((blocks + 255) / 256));
+  const long quarters = (long)M * (K / 8);
+  const dim3 grid((unsigned)((quarters + 255) / 256));
   if (swiglu)
     hipLaunchKernelGGL(quant_kernel<true>, grid, dim3(256), 0, s, a);
   else
@@ -351,6 +482,22 @@ int launch_linear(const LinearArgs& a, int nmat, hipStream_t s) {
     hipLaunchKernelGGL((linear_kernel<1, 1, 8>), grid, dim3(256), 0, s, a);
   }
   return check_launch("fp8 linear");
+}
+
+// Decode (M <= DEC_MT): gate/up + SwiGLU -> h [M, F] bf16 (in the gu region), down -> y.
+int launch_decode(const uint16_t* x, const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, const uint8_t* s3,
+                  const uint8_t* w2, const uint8_t* s2, int M, int D, int F, float limit, uint16_t* h, uint16_t* y,
+                  hipStream_t s) {
+  DecodeArgs gu{x, D, {w1, w3}, {s1, s3}, M, F, D, limit, h, F};
+  const dim3 grid_gu((unsigned)(F / 8), (unsigned)((M + DEC_MT - 1) / DEC_MT));
+  hipLaunchKernelGGL((decode_kernel<true, DEC_WAVES, DEC_PF>), grid_gu, dim3(64 * DEC_WAVES), dec_lds_bytes(D, DEC_WAVES),
+                     s, gu);
+  if (int rc = check_launch("fp8 decode gate/up")) return rc;
+  DecodeArgs dn{h, F, {w2, w2}, {s2, s2}, M, D, F, limit, y, D};
+  const dim3 grid_dn((unsigned)(D / 16), (unsigned)((M + DEC_MT - 1) / DEC_MT));
+  hipLaunchKernelGGL((decode_kernel<false, DEC_WAVES, DEC_PF>), grid_dn, dim3(64 * DEC_WAVES),
+                     dec_lds_bytes(F, DEC_WAVES), s, dn);
+  return check_launch("fp8 decode down");
 }
 
 int check_shapes(const char* who, int M, int K, int N) {
@@ -404,6 +551,8 @@ extern "C" int cachalot_shared_expert_fp8(const uint16_t* x, const uint8_t* w1, 
     return fail(CACHALOT_ESPACE, "shared_expert_fp8: workspace %zu bytes < %zu", workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
   const fp8::Workspace ws = fp8::carve(workspace, M, D, F);
+  if (M <= fp8::DEC_MT && D <= fp8::DEC_MAX_K && F <= fp8::DEC_MAX_K && F % 8 == 0)
+    return fp8::launch_decode(x, w1, w1_scales, w3, w3_scales, w2, w2_scales, M, D, F, swiglu_limit, ws.gu, y, s);
   if (int rc = fp8::launch_quant(x, D, M, D, false, 0.0f, ws.xq, ws.xe, s)) return rc;
   fp8::LinearArgs gu{ws.xq, ws.xe, {w1, w3}, {w1_scales, w3_scales}, M, F, D, ws.gu, 2 * F};
   if (int rc = fp8::launch_linear(gu, 2, s)) return rc;

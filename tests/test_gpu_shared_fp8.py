@@ -92,7 +92,8 @@ def test_fp8_linear_within_one_bf16_ulp(cuda, m, k, n):
     assert np.mean(got == round_bf16(exact.astype(np.float32))) > 0.99
 
 
-@pytest.mark.parametrize("m,d,f", [(1, 4096, 2880), (1, 5120, 2304), (5, 256, 192), (130, 1024, 640)])
+@pytest.mark.parametrize("m,d,f", [(1, 4096, 2880), (1, 5120, 2304), (3, 4096, 2880), (4, 1024, 2304),
+                                   (5, 256, 192), (130, 1024, 640)])
 def test_shared_expert_matches_oracle(cuda, m, d, f):
     from cachalot_amd.shared_expert import shared_expert_forward, shared_expert_forward_batched
 
