@@ -20,6 +20,9 @@ extension of the layout, needed for the configured shapes).
 """
 from __future__ import annotations
 
+import json
+import re
+import struct
 from dataclasses import dataclass, field
 from pathlib import Path
 
@@ -32,6 +35,8 @@ class TensorRange:
     shard: Path | None
     start: int
     end: int
+    dtype: str | None = None                 # safetensors dtype of the source tensor, when indexed from a header
+    shape: tuple[int, ...] | None = None     # this expert's slice shape
 
     @property
     def size(self) -> int:
@@ -138,3 +143,136 @@ def kernel_tensor_name(fmt: ExpertFormat, canonical: str) -> str | None:
             return None
         return canonical.replace(".scales", ".scale")
     return canonical
+
+
+# ------------------------------------------------------------------ banks on disk
+# Checkpoint tensor names (``storage/index.py:9-16``): the shipped FP4 checkpoint
+# names every expert's tensors; oMLX-converted banks stack a layer's experts in
+# one tensor per projection field, [n_experts, rows, cols].
+_EXPERT_RE = re.compile(r"^layers\.(\d+)\.ffn\.experts\.(\d+)\.(w[123])\.(weight|scale)$")
+_STACKED_RE = re.compile(r"^language_model\.layers\.(\d+)\.ffn\.experts\.(w[123])\.(weight|scales|biases)$")
+_ST_ITEM_BYTES = {"U32": 4, "F32": 4, "F16": 2, "BF16": 2, "U8": 1, "I8": 1, "F8_E4M3": 1, "F8_E8M0": 1}
+_ST_DTYPE = {"U32": "uint32", "F32": "float32", "F16": "float16", "BF16": "bfloat16", "U8": "uint8"}
+
+
+def read_safetensors_header(path: Path) -> tuple[dict, int]:
+    """(header dict, byte offset of the data section) of a safetensors file (``storage/index.py:70-76``)."""
+    with Path(path).open("rb") as f:
+        header_len = struct.unpack("<Q", f.read(8))[0]
+        header = json.loads(f.read(header_len))
+    return header, 8 + header_len
+
+
+def build_expert_index(model_path: str | Path) -> dict[tuple[int, int], ExpertEntry]:
+    """Per-expert tensors of the shipped FP4 checkpoint -> {(layer, expert): entry}, tensors in file
+    order; unreadable shards are skipped (``storage/index.py:79-117``)."""
+    root = Path(model_path)
+    entries: dict[tuple[int, int], list[TensorRange]] = {}
+    for shard in sorted(root.glob("model-*.safetensors")):
+        try:
+            header, data_start = read_safetensors_header(shard)
+        except (OSError, json.JSONDecodeError, struct.error):
+            continue
+        for name, meta in header.items():
+            m = _EXPERT_RE.match(name)
+            if not m:
+                continue
+            a, b = meta["data_offsets"]
+            entries.setdefault((int(m.group(1)), int(m.group(2))), []).append(
+                TensorRange(name, shard, data_start + a, data_start + b, meta.get("dtype"),
+                            tuple(meta.get("shape", ()))))
+    return {k: ExpertEntry(k[0], k[1], tuple(sorted(v, key=lambda t: t.start))) for k, v in entries.items()}
+
+
+def build_stacked_expert_index(model_path: str | Path, quantized_modules: dict) -> tuple[ExpertFormat, dict]:
+    """oMLX-converted stacked affine bank -> (format, index); every expert's nine tensors are rows of
+    the layer's stacked tensors (``storage/index.py:120-179``).  Mixed quantization, non-affine
+    modules and inconsistent shapes raise ValueError."""
+    root = Path(model_path)
+    entries: dict[tuple[int, int], list[TensorRange]] = {}
+    shapes: dict[str, tuple[int, int]] = {}
+    dtypes: dict[str, str] = {}
+    bits = group = None
+    for shard in sorted(root.glob("model-*.safetensors")):
+        try:
+            header, data_start = read_safetensors_header(shard)
+        except (OSError, json.JSONDecodeError, struct.error):
+            continue
+        for name, meta in header.items():
+            m = _STACKED_RE.match(name)
+            if not m:
+                continue
+            layer, proj, fld = int(m.group(1)), m.group(2), m.group(3)
+            spec = quantized_modules.get(f"language_model.layers.{layer}.ffn.experts.{proj}")
+            if spec is None or spec.get("mode") != "affine":
+                raise ValueError(f"{name}: routed experts must be affine-quantized, got {spec}")
+            this = (int(spec["bits"]), int(spec.get("group_size", 64)))
+            if bits is None:
+                bits, group = this
+            elif this != (bits, group):
+                raise ValueError(f"{name}: mixed expert quantization ({spec} vs {bits}-bit/{group})")
+            n_exp, rows, cols = (int(v) for v in meta["shape"])
+            short = f"{proj}.{fld}"
+            if shapes.setdefault(short, (rows, cols)) != (rows, cols):
+                raise ValueError(f"{name}: shape {(rows, cols)} differs from {shapes[short]}")
+            dtypes[short] = _ST_DTYPE[meta["dtype"]]
+            per = rows * cols * _ST_ITEM_BYTES[meta["dtype"]]
+            base = data_start + meta["data_offsets"][0]
+            for e in range(n_exp):
+                entries.setdefault((layer, e), []).append(
+                    TensorRange(f"layers.{layer}.ffn.experts.{e}.{short}", shard, base + e * per,
+                                base + (e + 1) * per, meta["dtype"], (rows, cols)))
+    if bits is None:
+        raise ValueError(f"no stacked routed-expert tensors under {root}")
+    rows1, cols1 = shapes["w1.weight"]
+    d_model, d_ff = cols1 * 32 // bits, rows1
+    fmt = ExpertFormat("affine", bits, group, tuple(sorted(shapes)), shapes, dtypes, d_model, d_ff)
+    index = {k: ExpertEntry(k[0], k[1], tuple(sorted(v, key=lambda t: t.start))) for k, v in entries.items()}
+    return fmt, index
+
+
+def detect_expert_bank(model_path: str | Path) -> tuple[ExpertFormat, dict[tuple[int, int], ExpertEntry]]:
+    """(format, index) of the routed experts under `model_path`: a stacked affine bank when
+    config.json carries ``omlx_deepseek_v41``, else the shipped FP4 layout (``storage/index.py:182-194``).
+    The FP4 format's shapes come from the first expert's w1 / w2 headers."""
+    root = Path(model_path)
+    config = root / "config.json"
+    if config.exists():
+        try:
+            spec = json.loads(config.read_text()).get("omlx_deepseek_v41")
+        except (OSError, json.JSONDecodeError):
+            spec = None
+        if spec:
+            return build_stacked_expert_index(root, spec.get("quantized_modules", {}))
+    index = build_expert_index(root)
+    if not index:
+        return FP4_FORMAT, index
+    first = index[min(index)]
+    by = {".".join(t.name.rsplit(".", 2)[-2:]): t for t in first.tensors}
+    if "w1.weight" not in by or by["w1.weight"].shape is None or len(by["w1.weight"].shape) != 2:
+        return FP4_FORMAT, index
+    d_ff, half_d = by["w1.weight"].shape
+    return fp4_format(half_d * 2, d_ff), index
+
+
+@dataclass(frozen=True)
+class ReadRange:
+    shard: Path
+    start: int
+    end: int
+    tensors: tuple[TensorRange, ...]
+
+    @property
+    def size(self) -> int:
+        return self.end - self.start
+
+
+def merge_contiguous_ranges(entry: ExpertEntry) -> tuple[ReadRange, ...]:
+    """Runs of an entry's tensors that are adjacent in one shard, one read each (``storage/index.py:208-233``)."""
+    groups: list[list[TensorRange]] = []
+    for t in entry.tensors:
+        if groups and groups[-1][-1].shard == t.shard and groups[-1][-1].end == t.start:
+            groups[-1].append(t)
+        else:
+            groups.append([t])
+    return tuple(ReadRange(g[0].shard, g[0].start, g[-1].end, tuple(g)) for g in groups)

@@ -222,6 +222,16 @@ int cachalot_shared_expert_fp8(const uint16_t* x, const uint8_t* w1, const uint8
                                uint16_t* y, void* workspace, size_t workspace_bytes,
                                cachalot_stream_t stream);
 
+/* Bank loading: n experts' bytes of one tensor ([n, tensor_bytes] contiguous at
+ * src, pinned host or device memory) into the slot records first_slot ..
+ * first_slot + n - 1 of a pool (record stride record_bytes), at byte `offset`
+ * inside each record, as one asynchronous 2-D copy on `stream`.  Replaces the
+ * per-expert read_expert_into(entry, slot.views) scatter into slab memory
+ * (src/cachalot/storage/reader.py:182-250, cache/slots.py:240-251) for a
+ * stacked bank tensor [n_experts, rows, cols] (storage/index.py:120-179). */
+int cachalot_copy_records(uint8_t* pool, int64_t record_bytes, int64_t offset, int64_t first_slot,
+                          const void* src, int64_t tensor_bytes, int64_t n, cachalot_stream_t stream);
+
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32
  *   (replaces dequantize_fp4_weight / dequantize_fp4_dense,
