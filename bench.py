@@ -323,6 +323,46 @@ def shared_expert_fp8(args, dev, log_fn):
     return out
 
 
+def requant_bank(args, dev, log_fn):
+    """FP4 -> 2-bit g128 requantization (searched fit) of whole experts at the layer's shape, on the GPU:
+    time per expert and the implied time for the 40 x 384 bank (device work only, no disk)."""
+    import torch
+
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+    from cachalot_amd.requant import requantize_expert
+    from cachalot_amd.storage.index import affine_format, fp4_format
+
+    D, F, N = 4096, 2880, 8
+    sf, df = fp4_format(D, F), affine_format(D, F)
+    src = ResidentExpertStore(fmt=sf, n_slots=N, n_layers=1, n_experts=N, device=dev)
+    src.preload([(0, e) for e in range(N)], SyntheticLoader(sf, args.seed + 5).fill_key)
+    dst = ResidentExpertStore(fmt=df, n_slots=N, n_layers=1, n_experts=N, device=dev)
+    slots = [dst.pool.acquire_index(e) for e in range(N)]
+
+    def run():
+        for e in range(N):
+            requantize_expert(src._items[(0, e)].arrays, sf, slots[e].arrays, df)
+
+    run()
+    torch.cuda.synchronize()
+    reps = 3
+    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        run()
+    e.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(e) / (reps * N)
+    res = {"ms_per_expert": round(ms, 3), "experts_per_s": round(1e3 / ms, 1),
+           "bank_40x384_s": round(ms * 40 * 384 / 1e3, 1),
+           "note": "per expert: three matrices, 3 x 2880 x 32 groups of 128 (w2 23 groups per row), 25 fit "
+                   "candidates each; device work only"}
+    log_fn(f"requant FP4 -> 2-bit: {ms:.3f} ms/expert, bank {res['bank_40x384_s']} s")
+    del src, dst
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -512,6 +552,7 @@ def main() -> int:
         result["config2_batched_decode"] = batched_decode(args, store, gates, log)
         result["config3_prefill"] = prefill_config3(args, dev, log)
         result["shared_fp8_expert"] = shared_expert_fp8(args, dev, log)
+        result["requant_fp4_to_q2"] = requant_bank(args, dev, log)
     if not args.no_cpu:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_seconds)

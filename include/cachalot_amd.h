@@ -232,6 +232,19 @@ int cachalot_shared_expert_fp8(const uint16_t* x, const uint8_t* w1, const uint8
 int cachalot_copy_records(uint8_t* pool, int64_t record_bytes, int64_t offset, int64_t first_slot,
                           const void* src, int64_t tensor_bytes, int64_t n, cachalot_stream_t stream);
 
+/* FP4 -> 2-bit affine g128 requantization (the searched fit) of one weight
+ * matrix: w_fp4 [N, K/2] packed E2M1 + s_fp4 [N, K/32] E8M0 -> q [N, Kp/16] u32
+ * codes (16 per word, low field first), scales / biases [N, Kp/128] bf16,
+ * Kp = K rounded up to 128.  Per group: the min/max fit, then 24 shrunk ranges
+ * (SHRINKS x SHRINKS), the least squared error kept (strictly smaller wins,
+ * error summed in index order), scale and bias rounded to bf16, codes
+ * recomputed against them; a partial last group fits its real elements and
+ * pads with code 0.  Replaces quantize_affine(fit=fit_search) over the FP4
+ * checkpoint (benchmarks/quant_affine.py:157-205,330-359,
+ * build_affine_bank.py:165-189). */
+int cachalot_requant_fp4_to_q2(const uint8_t* w_fp4, const uint8_t* s_fp4, int N, int K, uint32_t* q,
+                               uint16_t* scales, uint16_t* biases, cachalot_stream_t stream);
+
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32
  *   (replaces dequantize_fp4_weight / dequantize_fp4_dense,

@@ -1,0 +1,94 @@
+"""GPU requantizer (FP4 -> 2-bit affine g128, searched fit) against oracle/requant.py.
+
+The oracle evaluates the fit in float32 with the error summed in index order,
+the order the kernel uses, so codes, scales and biases must match bit for bit.
+Sources are the seeded synthetic FP4 experts (uniform nibbles, many exact ties
+between candidates) and FP4-rounded Gaussian weights.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import oracle_tensors
+from oracle import requant as orq
+from oracle.fp4 import dequantize_fp4_weight
+from cachalot_amd.storage import index as I
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _check_matrix(cuda, w, s):
+    from cachalot_amd.requant import requantize_fp4_matrix
+
+    k = w.shape[1] * 2
+    q, sc, bi = requantize_fp4_matrix(torch.from_numpy(w).to(cuda), torch.from_numpy(s).to(cuda), k)
+    wq, ws, wb = orq.requantize(dequantize_fp4_weight(w, s).astype(np.float32))
+    assert np.array_equal(_np(q).view(np.uint32), wq)
+    assert np.array_equal(_np(sc).view(np.uint16), ws)
+    assert np.array_equal(_np(bi).view(np.uint16), wb)
+
+
+@pytest.mark.parametrize("proj", ["w1", "w2"])
+def test_requant_matrix_bit_exact_synthetic(cuda, proj):
+    fmt = I.fp4_format(1024, 2880)                   # w2: K = 2880, a partial last group
+    t = oracle_tensors(fmt, 0, 3)
+    rows = 640 if proj == "w1" else 512
+    _check_matrix(cuda, t[f"{proj}.weight"][:rows], t[f"{proj}.scale"][:rows])
+
+
+def test_requant_matrix_bit_exact_gaussian(cuda):
+    rng = np.random.default_rng(9)
+    n, k = 256, 1024
+    # FP4-encode Gaussian weights: per 32-block scale 2^ceil(log2(amax/6)), nearest E2M1 code
+    dense = rng.standard_normal((n, k)) * rng.uniform(0.01, 1.0, size=(n, 1))
+    blocks = dense.reshape(n, k // 32, 32)
+    e = np.ceil(np.log2(np.abs(blocks).max(-1) / 6.0)).astype(np.int32)
+    grid = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6])
+    mag = np.abs(blocks) / np.exp2(e)[..., None]
+    code = np.abs(mag[..., None] - grid).argmin(-1) | (np.signbit(blocks) << 3)
+    code = code.reshape(n, k).astype(np.uint8)
+    w = (code[:, 0::2] | (code[:, 1::2] << 4)).astype(np.uint8)
+    s = (e + 127).astype(np.uint8)
+    _check_matrix(cuda, w, s)
+
+
+def test_requantize_store_and_bank_file(cuda, tmp_path):
+    from cachalot_amd.requant import build_affine_bank, requantize_store
+    from cachalot_amd.storage.reader import preload_bank
+    from cachalot_amd.storage.writer import write_fp4_shard
+    from cachalot_amd.cache.resident_store import ResidentExpertStore
+    from helpers import make_store
+
+    src_fmt = I.fp4_format(1024, 640)
+    src = make_store(src_fmt, n_layers=1, n_experts=4)
+    dst = ResidentExpertStore(fmt=I.affine_format(1024, 640), n_slots=4, n_layers=1, n_experts=4, device=cuda)
+    requantize_store(src, dst)
+    torch.cuda.synchronize()
+    want = {}
+    for e in range(4):
+        t = oracle_tensors(src_fmt, 0, e)
+        want[e] = {}
+        for p in ("w1", "w2", "w3"):
+            q, sb, bb = orq.requantize(dequantize_fp4_weight(t[f"{p}.weight"], t[f"{p}.scale"]).astype(np.float32))
+            want[e].update({f"{p}.weight": q, f"{p}.scales": sb, f"{p}.biases": bb})
+        slot = dst.pool.slot(dst.layer_table(0)[e].item())
+        for name, arr in want[e].items():
+            assert np.array_equal(_np(slot.arrays[name]), arr.view(np.uint8).reshape(-1)), (e, name)
+    # the same through files: FP4 shard -> build_affine_bank -> detect -> preload
+    (tmp_path / "fp4").mkdir()
+    write_fp4_shard(tmp_path / "fp4" / "model-00001-of-00001.safetensors",
+                    {(0, e): oracle_tensors(src_fmt, 0, e) for e in range(4)})
+    build_affine_bank(tmp_path / "fp4", tmp_path / "q2", device=cuda)
+    fmt, index = I.detect_expert_bank(tmp_path / "q2")
+    store = ResidentExpertStore(fmt=fmt, n_slots=4, n_layers=1, n_experts=4, device=cuda)
+    preload_bank(store, index)
+    for e in range(4):
+        slot = store.pool.slot(store.layer_table(0)[e].item())
+        for name, arr in want[e].items():
+            assert np.array_equal(_np(slot.arrays[name]), arr.view(np.uint8).reshape(-1)), (e, name)
