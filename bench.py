@@ -363,6 +363,69 @@ def requant_bank(args, dev, log_fn):
     return res
 
 
+def layer_with_shared(args, store, gates, log_fn):
+    """Config 1's layer as the reference's call site runs it: routed experts + the FP8 shared expert
+    (moe_layer_forward with shared_*), against the routed experts alone.  Steps rotate through the
+    resident layers and 8 shared weight sets (283 MB, beyond the MALL)."""
+    import torch
+
+    from cachalot_amd.moe_layer import moe_layer_forward
+
+    D, F, S = 4096, 2880, 8
+    dev = store.pool.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 31)
+
+    def wt(n, k):
+        w = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev, generator=g)
+        w[(w & 0x7F) == 0x7F] = 0x3F
+        return w, torch.randint(120, 131, ((n + 31) // 32, k // 32), dtype=torch.uint8, device=dev, generator=g)
+
+    sets = []
+    for _ in range(S):
+        (w1, s1), (w3, s3), (w2, s2) = wt(F, D), wt(F, D), wt(D, F)
+        sets.append(dict(shared_w1=w1, shared_w1_scales=s1, shared_w3=w3, shared_w3_scales=s3, shared_w2=w2,
+                         shared_w2_scales=s2))
+    x = torch.randn(D, device=dev, generator=g).to(torch.bfloat16)
+    L = len(gates)
+
+    def kw(i):
+        w, b = gates[i % L]
+        return dict(layer_id=i % L, gate_weight=w, gate_bias=b, expert_index=None, expert_store=store, topk=6,
+                    route_scale=1.0, score_fn="sigmoid")
+
+    variants = {
+        "routed_only": lambda i: moe_layer_forward(x, **kw(i)),
+        "routed_plus_shared": lambda i: moe_layer_forward(x, **kw(i), **sets[i % S]),
+    }
+    G = 2 * L
+    out = {}
+    for name, fn in variants.items():
+        for i in range(G):
+            fn(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(G):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(4):
+            graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        out[name] = {"us_per_layer": round(a.elapsed_time(e) * 1e3 / (4 * G), 2)}
+        log_fn(f"layer {name}: {out[name]['us_per_layer']} us")
+        del graph
+    out["note"] = ("moe_layer_forward graph-captured, independent steps over the resident layers; the shared "
+                   "expert D 4096 x F 2880 FP8")
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -550,6 +613,7 @@ def main() -> int:
     if not args.no_extra:
         result["config0_fp4_decode"] = fp4_decode_config0(args, dev, log)
         result["config2_batched_decode"] = batched_decode(args, store, gates, log)
+        result["config1_layer_with_shared_expert"] = layer_with_shared(args, store, gates, log)
         result["config3_prefill"] = prefill_config3(args, dev, log)
         result["shared_fp8_expert"] = shared_expert_fp8(args, dev, log)
         result["requant_fp4_to_q2"] = requant_bank(args, dev, log)

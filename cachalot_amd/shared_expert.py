@@ -30,14 +30,16 @@ from . import _lib
 
 BLOCK = 32
 
-_WORKSPACES: dict[int, torch.Tensor] = {}
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    ws = _WORKSPACES.get(device.index)
+    """Scratch per (device, stream): calls on one stream are ordered, calls on two streams may overlap."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-        _WORKSPACES[device.index] = ws
+        _WORKSPACES[key] = ws
     return ws
 
 
