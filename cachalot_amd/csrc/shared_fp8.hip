@@ -42,8 +42,7 @@ __device__ __forceinline__ int block_exponent(float amax) {
   return (int)((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0u ? 1 : 0);
 }
 
-// 2^e and 2^-e as floats (e in [-23, 126]).
-__device__ __forceinline__ float pow2(int e) { return __uint_as_float((uint32_t)(127 + e) << 23); }
+// 2^-e as a float (e in [-23, 126]).
 __device__ __forceinline__ float pow2_neg(int e) { return __uint_as_float((uint32_t)(127 - e) << 23); }
 
 __device__ __forceinline__ float clip448(float v) { return fminf(fmaxf(v, -FP8_MAX), FP8_MAX); }
