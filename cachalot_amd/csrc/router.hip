@@ -99,136 +99,138 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float* __restrict
   if (threadIdx.x == 0) normalise_weights(top_v, k, route_scale, norm, w + (size_t)t * k);
 }
 
-// Many tokens: one 256-thread workgroup = 32 tokens x 64 experts, each thread 2
-// tokens x 4 experts.  The same arithmetic as router_row: chunk c (of 64) of every
-// dot product is a sequential fp32 sum of its D/64 products, and the 64 chunk sums
-// meet in the pairwise tree (left + right) the xor butterfly forms.  Chunk by chunk,
-// x and W slices are staged in LDS as fp32; the tree is kept as a binary-counter
-// stack of six partial nodes per dot product.  fma(x, w, s) equals s + x * w here:
-// the product of two bf16 values is exact in fp32 (16 significant bits) unless it is
-// below 2^-133 in magnitude.
-constexpr int RT_T = 32;             // tokens per workgroup
-constexpr int RT_E = 64;             // experts per workgroup
+// Many tokens: one 256-thread workgroup = 64 tokens x 32 experts, each thread 4
+// tokens (tq + 16 a) x 2 experts (eq + 16 b).  The same arithmetic as router_row:
+// chunk c (of 64) of every dot product is a sequential fp32 sum of its D/64
+// products in k order, and the 64 chunk sums meet in the pairwise tree (left +
+// right) the xor butterfly forms, kept as a binary-counter stack of six partial
+// nodes per dot product.  Chunk by chunk, the x and W slices are staged in LDS as
+// bf16 (double-buffered, one barrier per chunk) and read as 8-value runs (one
+// 16-byte read per token or expert feeds 8 x 4 products); rows are padded to an
+// odd number of 16-byte slots so the 16 experts a wave row reads hit distinct
+// bank groups.  fma(x, w, s) equals s + x * w here: the product of two bf16
+// values is exact in fp32 (16 significant bits) unless it is below 2^-133.
+constexpr int RT_TA = 4;             // tokens per thread (tq + 16 a)
+constexpr int RT_TB = 2;             // experts per thread (eq + 16 b)
+constexpr int RT_T = 16 * RT_TA;     // tokens per workgroup
+constexpr int RT_E = 16 * RT_TB;     // experts per workgroup
 constexpr int RT_MAXCH = 80;         // D / 64 <= 80 (D <= 5120)
-constexpr int RT_PAD = 4;            // floats of padding per staged row (bank spread)
+constexpr int RT_MAXS = RT_MAXCH * 2 + 32;   // staged row bytes, padding included
 constexpr int RT_MIN_T = 1024;       // fewer tokens: the 4-token kernel fills the chip better
+
+__host__ __device__ inline int rt_stride(int ch) { return ch * 2 + ((ch / 8) % 2 == 0 ? 16 : 32); }
+
+// Chunk c of a tile's x rows, then its W rows, as 16-byte items (rows past T / E:
+// clamped, unused), and the store of those items into a staged buffer.
+template <int N>
+__device__ __forceinline__ void rt_load(uint4 (&v)[N], const uint16_t* __restrict__ x, const uint16_t* __restrict__ W,
+                                        int T, int D, int E, int t0, int e0, int c, int tid, int items, int per_row) {
+  const int ch = 8 * per_row;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int it = min(tid + 256 * j, items - 1);
+    const int r = it / per_row, q = it - r * per_row;
+    const uint16_t* src = r < RT_T ? x + (size_t)min(t0 + r, T - 1) * D : W + (size_t)min(e0 + r - RT_T, E - 1) * D;
+    v[j] = *reinterpret_cast<const uint4*>(src + c * ch + 8 * q);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void rt_store(uint8_t* buf, const uint4 (&v)[N], int tid, int items, int per_row, int S) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int it = tid + 256 * j;
+    const int r = it / per_row, q = it - r * per_row;
+    if (it < items) *reinterpret_cast<uint4*>(buf + r * S + 16 * q) = v[j];
+  }
+}
 
 __global__ void __launch_bounds__(256) router_tiled_kernel(const uint16_t* __restrict__ x,
                                                            const uint16_t* __restrict__ W, int T, int D, int E,
                                                            float gate_temp, int fn, float* __restrict__ scores) {
-  __shared__ __align__(16) float xs[RT_T][RT_MAXCH + RT_PAD];
-  __shared__ __align__(16) float ws[RT_E][RT_MAXCH + RT_PAD];
+  __shared__ __align__(16) uint8_t st[2][(RT_T + RT_E) * RT_MAXS];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int eq = lane & 15;                   // experts 4 eq .. 4 eq + 3
-  const int tp = (lane >> 4) + 4 * wave;      // tokens 2 tp, 2 tp + 1
+  const int eq = tid & 15, tq = tid >> 4;
   const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
-  const int ch = D / CHUNKS;                  // a multiple of 8
-  const int xq = RT_T * ch / 8, wq = RT_E * ch / 8;   // 8-value items per chunk
-  // staging: item -> (row, 8 values); rows past T / E read row 0 (results unused)
-  auto load_chunk = [&](int c, uint4 (&xv)[2], uint4 (&wv)[3]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int it = tid + 256 * j;
-      const int r = it / (ch / 8), q = it - r * (ch / 8);
-      const int t = min(t0 + r, T - 1);
-      xv[j] = it < xq ? *reinterpret_cast<const uint4*>(x + (size_t)t * D + c * ch + 8 * q) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int it = tid + 256 * j;
-      const int r = it / (ch / 8), q = it - r * (ch / 8);
-      const int e = min(e0 + r, E - 1);
-      wv[j] = it < wq ? *reinterpret_cast<const uint4*>(W + (size_t)e * D + c * ch + 8 * q) : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_chunk = [&](const uint4 (&xv)[2], const uint4 (&wv)[3]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int it = tid + 256 * j;
-      if (it < xq) {
-        const int r = it / (ch / 8), q = it - r * (ch / 8);
-        const uint32_t u[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-        float4* d = reinterpret_cast<float4*>(&xs[r][8 * q]);
-        d[0] = make_float4(__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u),
-                           __uint_as_float(u[1] << 16), __uint_as_float(u[1] & 0xffff0000u));
-        d[1] = make_float4(__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xffff0000u),
-                           __uint_as_float(u[3] << 16), __uint_as_float(u[3] & 0xffff0000u));
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int it = tid + 256 * j;
-      if (it < wq) {
-        const int r = it / (ch / 8), q = it - r * (ch / 8);
-        const uint32_t u[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-        float4* d = reinterpret_cast<float4*>(&ws[r][8 * q]);
-        d[0] = make_float4(__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u),
-                           __uint_as_float(u[1] << 16), __uint_as_float(u[1] & 0xffff0000u));
-        d[1] = make_float4(__uint_as_float(u[2] << 16), __uint_as_float(u[2] & 0xffff0000u),
-                           __uint_as_float(u[3] << 16), __uint_as_float(u[3] & 0xffff0000u));
-      }
-    }
-  };
-  float stk[6][8];
-  float node[8];
-  uint4 xv[2], wv[3];
-  load_chunk(0, xv, wv);
-  store_chunk(xv, wv);
+  const int per_row = D / 512;                // 16-byte items per staged row
+  const int ch = 8 * per_row;                 // D / 64
+  const int S = rt_stride(ch);
+  const int items = (RT_T + RT_E) * per_row;  // x rows first, then W rows
+  constexpr int MAXIT = ((RT_T + RT_E) * RT_MAXCH / 8 + 255) / 256;
+
+  float stk[6][RT_TA * RT_TB];
+  float node[RT_TA * RT_TB];
+  uint4 v[MAXIT];
+  rt_load(v, x, W, T, D, E, t0, e0, 0, tid, items, per_row);
+  rt_store(st[0], v, tid, items, per_row, S);
   __syncthreads();
   for (int c = 0; c < CHUNKS; ++c) {
-    if (c + 1 < CHUNKS) load_chunk(c + 1, xv, wv);
-    float acc[8];
+    if (c + 1 < CHUNKS) rt_load(v, x, W, T, D, E, t0, e0, c + 1, tid, items, per_row);
+    const uint8_t* buf = st[c & 1];
+    float acc[RT_TA * RT_TB];
 #pragma unroll
-    for (int p = 0; p < 8; ++p) acc[p] = 0.0f;
-    for (int k = 0; k < ch; k += 4) {
-      float4 xa[2], wa[4];
+    for (int p = 0; p < RT_TA * RT_TB; ++p) acc[p] = 0.0f;
+    // (a runtime loop: unrolled, the scheduled-ahead reads push the kernel to one wave per SIMD)
+    for (int k8 = 0; k8 < per_row; ++k8) {
+      uint4 xa[RT_TA], wb[RT_TB];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) xa[a] = *reinterpret_cast<const float4*>(&xs[2 * tp + a][k]);
+      for (int a = 0; a < RT_TA; ++a) xa[a] = *reinterpret_cast<const uint4*>(buf + (tq + 16 * a) * S + 16 * k8);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) wa[b] = *reinterpret_cast<const float4*>(&ws[4 * eq + b][k]);
+      for (int b = 0; b < RT_TB; ++b)
+        wb[b] = *reinterpret_cast<const uint4*>(buf + (RT_T + eq + 16 * b) * S + 16 * k8);
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int h = 0; h < 4; ++h) {            // the 8 values in k order: word h, low then high half
+        float xl[RT_TA], xh[RT_TA], wl[RT_TB], wh[RT_TB];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          float v = acc[4 * a + b];
-          v = __builtin_fmaf(xa[a].x, wa[b].x, v);
-          v = __builtin_fmaf(xa[a].y, wa[b].y, v);
-          v = __builtin_fmaf(xa[a].z, wa[b].z, v);
-          v = __builtin_fmaf(xa[a].w, wa[b].w, v);
-          acc[4 * a + b] = v;
+        for (int a = 0; a < RT_TA; ++a) {
+          const uint32_t u = h == 0 ? xa[a].x : h == 1 ? xa[a].y : h == 2 ? xa[a].z : xa[a].w;
+          xl[a] = __uint_as_float(u << 16);
+          xh[a] = __uint_as_float(u & 0xffff0000u);
         }
+#pragma unroll
+        for (int b = 0; b < RT_TB; ++b) {
+          const uint32_t u = h == 0 ? wb[b].x : h == 1 ? wb[b].y : h == 2 ? wb[b].z : wb[b].w;
+          wl[b] = __uint_as_float(u << 16);
+          wh[b] = __uint_as_float(u & 0xffff0000u);
+        }
+#pragma unroll
+        for (int a = 0; a < RT_TA; ++a)
+#pragma unroll
+          for (int b = 0; b < RT_TB; ++b) {
+            float t = acc[RT_TB * a + b];
+            t = __builtin_fmaf(xl[a], wl[b], t);
+            t = __builtin_fmaf(xh[a], wh[b], t);
+            acc[RT_TB * a + b] = t;
+          }
+      }
     }
+    if (c + 1 < CHUNKS) rt_store(st[(c + 1) & 1], v, tid, items, per_row, S);
     // merge chunk c into the tree (c is uniform: every branch below is too)
 #pragma unroll
-    for (int p = 0; p < 8; ++p) node[p] = acc[p];
+    for (int p = 0; p < RT_TA * RT_TB; ++p) node[p] = acc[p];
     // chunk c closes the nodes of the levels below its lowest zero bit
     const int up = __builtin_ctz(~c);   // levels merged (6 after the last chunk)
 #pragma unroll
     for (int L = 0; L < 6; ++L) {
       if (L < up) {
 #pragma unroll
-        for (int p = 0; p < 8; ++p) node[p] = stk[L][p] + node[p];
+        for (int p = 0; p < RT_TA * RT_TB; ++p) node[p] = stk[L][p] + node[p];
       } else if (L == up) {
 #pragma unroll
-        for (int p = 0; p < 8; ++p) stk[L][p] = node[p];
+        for (int p = 0; p < RT_TA * RT_TB; ++p) stk[L][p] = node[p];
       }
     }
     __syncthreads();
-    if (c + 1 < CHUNKS) {
-      store_chunk(xv, wv);
-      __syncthreads();
-    }
   }
   // after chunk 63 every level merged: node holds the root
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
-    const int t = t0 + 2 * tp + a;
+  for (int a = 0; a < RT_TA; ++a) {
+    const int t = t0 + tq + 16 * a;
     if (t >= T) continue;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int e = e0 + 4 * eq + b;
-      if (e < E) scores[(size_t)t * E + e] = score_of(node[4 * a + b] / gate_temp, fn);
+    for (int b = 0; b < RT_TB; ++b) {
+      const int e = e0 + eq + 16 * b;
+      if (e < E) scores[(size_t)t * E + e] = score_of(node[RT_TB * a + b] / gate_temp, fn);
     }
   }
 }
