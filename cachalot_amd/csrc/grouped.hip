@@ -467,7 +467,8 @@ __device__ __forceinline__ uint32_t g2_aoff(int r, int k16) { return (uint32_t)(
 template <int NM>
 struct G2Chunk {
   uint4 codes[NM][2];
-  uint32_t sc[NM][2];
+  uint32_t sc[NM][2];    // raw E8M0 bytes as loaded (a block past K: any byte)
+  bool in_k;             // the lane's block of this chunk lies inside K
 };
 
 template <int NM>
@@ -476,6 +477,7 @@ __device__ __forceinline__ void g2_issue(const GroupedArgs& g, uint8_t* stage, c
                                          const uint8_t* (&wrow)[NM][2],
                                          const uint8_t* (&srow)[NM][2], int c, int kg, int wave, int lane,
                                          int row_bytes, int blocks, G2Chunk<NM>& out) {
+  out.in_k = 4 * c + kg < blocks;
   // A: this wave's 1 KiB slices of the chunk (slot = 64 * (G2_ASLICES wave + q) + lane)
 #pragma unroll
   for (int q = 0; q < G2_ASLICES; ++q) {
@@ -489,9 +491,9 @@ __device__ __forceinline__ void g2_issue(const GroupedArgs& g, uint8_t* stage, c
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       out.codes[m][f] = *reinterpret_cast<const uint4*>(wrow[m][f] + min(c * 64 + kg * 16, row_bytes - 16));
-      const int blk = 4 * c + kg;
-      // blocks past K meet zero activations: any finite scale (raw 127 = 1.0)
-      out.sc[m][f] = blk < blocks ? (uint32_t)srow[m][f][blk] : 127u;
+      // unconditional (clamped) load: the compiler then counts this wave's loads exactly;
+      // the value is checked where it is used, so nothing here waits for it
+      out.sc[m][f] = srow[m][f][min(4 * c + kg, blocks - 1)];
     }
 }
 
@@ -499,11 +501,12 @@ __device__ __forceinline__ void g2_issue(const GroupedArgs& g, uint8_t* stage, c
 template <int NM>
 __device__ __forceinline__ void g2_compute(const uint8_t* ab, const G2Chunk<NM>& ch, int i, int kg, int ntb,
                                            f32x4_t (&acc)[NM][2][G2_TB]) {
+  // blocks past K meet zero activations: any finite scale (raw 127 = 1.0)
   float scale[NM][2];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int f = 0; f < 2; ++f) scale[m][f] = e8m0_to_f32(ch.sc[m][f]);
+    for (int f = 0; f < 2; ++f) scale[m][f] = e8m0_to_f32(ch.in_k ? ch.sc[m][f] : 127u);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     bf16x8_t bv[NM][2];
@@ -579,23 +582,24 @@ __global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const
         srow[m][f] = base + g.L.off[tq[m] + 1] + (int64_t)n * blocks;
       }
     G2Chunk<NM> ring[G2_STAGES];
+    // Every issue is unconditional (a chunk past the end re-reads the last one into a
+    // stage nothing reads again), so each wait below is for exactly the loads it needs
+    // and two chunks stay in flight; a load under a branch makes the compiler wait for all.
     g2_issue<NM>(g, abuf[0], arow, ak16, zeros, wrow, srow, 0, kg, wave, lane, row_bytes, blocks, ring[0]);
-    if (nch > 1)
-      g2_issue<NM>(g, abuf[1], arow, ak16, zeros, wrow, srow, 1, kg, wave, lane, row_bytes, blocks, ring[1]);
+    g2_issue<NM>(g, abuf[1], arow, ak16, zeros, wrow, srow, min(1, nch - 1), kg, wave, lane, row_bytes, blocks,
+                 ring[1]);
     // three chunks per trip so every ring index is a compile-time constant
     for (int c0 = 0; c0 < nch; c0 += G2_STAGES) {
 #pragma unroll
       for (int u = 0; u < G2_STAGES; ++u) {
         const int c = c0 + u;
-        if (c < nch) {
-          // this wave's loads of chunk c have landed (its codes are consumed here, and
-          // its earlier direct-to-LDS loads complete first); then every wave's
-          lds_sync_after(ring[u].codes[NM - 1][1].w);
-          if (c + 2 < nch)   // into the stage chunk c - 1 used: every wave is past it
-            g2_issue<NM>(g, abuf[(u + 2) % G2_STAGES], arow, ak16, zeros, wrow, srow, c + 2, kg, wave, lane,
-                         row_bytes, blocks, ring[(u + 2) % G2_STAGES]);
-          g2_compute<NM>(abuf[u], ring[u], i, kg, ntb, acc);
-        }
+        // this wave's loads of chunk c have landed (its codes are consumed here, and
+        // its earlier direct-to-LDS loads complete first); then every wave's
+        lds_sync_after(ring[u].codes[NM - 1][1].w);
+        // into the stage chunk c - 1 used: every wave is past it
+        g2_issue<NM>(g, abuf[(u + 2) % G2_STAGES], arow, ak16, zeros, wrow, srow, min(c + 2, nch - 1), kg, wave,
+                     lane, row_bytes, blocks, ring[(u + 2) % G2_STAGES]);
+        if (c < nch) g2_compute<NM>(abuf[u], ring[u], i, kg, ntb, acc);
       }
     }
   }
