@@ -156,3 +156,27 @@ def test_layer_entries_add_the_shared_expert(cuda):
     assert torch.equal(outp.view(torch.int16), refp.view(torch.int16))
     with pytest.raises(ValueError):
         moe_layer_forward(x[0], **kw, **shared, addend=refp[0])
+
+
+def test_shared_expert_argument_errors_and_no_limit(cuda):
+    """Contract errors (the reference's ValueErrors for shapes, fp8_ref.py:48-58,140-170) and
+    swiglu_limit <= 0 (no clamp, shared_expert_metal.py:99-108)."""
+    from cachalot_amd.shared_expert import fp8_linear, quantize_fp8_activation, shared_expert_forward
+
+    rng = np.random.default_rng(SEED + 7)
+    (w1, s1), (w3, s3), (w2, s2) = _expert(rng, 256, 192)
+    dev = {n: _dev(a, cuda) for n, a in dict(w1=w1, w1_scales=s1, w3=w3, w3_scales=s3, w2=w2, w2_scales=s2).items()}
+    x = round_bf16((rng.standard_normal(256) * 4).astype(np.float32))
+    got = _bf16_np(shared_expert_forward(_to_dev_bf16(x, cuda), **dev, swiglu_limit=0.0))
+    want = ofp8.shared_expert(x[None], w1, s1, w3, s3, w2, s2, limit=0.0)[0]
+    assert np.all(np.abs(got - want) <= TOL * np.abs(want).max() + bf16_ulp(want))
+    with pytest.raises(ValueError):
+        quantize_fp8_activation(_to_dev_bf16(np.zeros(40, np.float32), cuda))          # K not a multiple of 32
+    with pytest.raises(ValueError):
+        fp8_linear(_to_dev_bf16(x, cuda), dev["w1"], dev["w1_scales"][:-1])            # scale shape
+    with pytest.raises(ValueError):
+        fp8_linear(_to_dev_bf16(x[:128], cuda), dev["w1"], dev["w1_scales"])           # K mismatch
+    with pytest.raises(ValueError):
+        shared_expert_forward(_to_dev_bf16(x, cuda)[None], **dev)                       # decode takes 1-D x
+    with pytest.raises(ValueError):
+        shared_expert_forward(_to_dev_bf16(x, cuda), **{**dev, "w2": dev["w1"]})       # w2 shape
