@@ -127,7 +127,9 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
     routed = torch.empty((d,), dtype=torch.float32, device=dev) if want_routed else None
     out = torch.empty((d,), dtype=torch.bfloat16, device=dev) if want_out else None
     L = _lib.lib()
-    args_route = (x.contiguous().data_ptr(), gate_weight.contiguous().data_ptr(), gate_bias.data_ptr(), n_experts,
+    x = x.contiguous()                      # bound to names: a temporary could be freed and its
+    gate_weight = gate_weight.contiguous()  # memory reused before the kernels read it
+    args_route = (x.data_ptr(), gate_weight.data_ptr(), gate_bias.data_ptr(), n_experts,
                   topk, _lib.SCORE_FNS[score_fn], float(gate_temp), float(route_scale),
                   1 if norm_topk_prob else 0, _lib.ORDERS[order], pool.storage.data_ptr(), pool.layout(),
                   slot_table.data_ptr(), d, f)
