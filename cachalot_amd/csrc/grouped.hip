@@ -533,15 +533,17 @@ __device__ __forceinline__ void g2_compute(const uint8_t* ab, const G2Chunk<NM>&
   }
 }
 
-// grid = (max tiles, ceil(N / 256)).  NM = 2: gate/up (W1, W3) -> h; NM = 1: down (W2) -> y.
+// grid = (ceil(N / 256), max tiles).  NM = 2: gate/up (W1, W3) -> h; NM = 1: down (W2) -> y.
 template <int NM>
 __global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const uint8_t* __restrict__ zeros) {
   __shared__ __align__(16) uint8_t abuf[G2_STAGES][G2_ABYTES];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, kg = lane >> 4;
-  if ((int)blockIdx.x >= g.tiles_n[0]) return;
-  const int2 tl = g.tiles[blockIdx.x];
+  // grid = (N slices, tiles): the slices of one M tile are dispatched together, so its
+  // gathered A rows are read from HBM once and then hit in cache
+  if ((int)blockIdx.y >= g.tiles_n[0]) return;
+  const int2 tl = g.tiles[blockIdx.y];
   const int e = tl.x, row0 = tl.y;
   const int rows = min(G2_MT, g.offsets[e + 1] - row0);
   const int ntb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
@@ -553,7 +555,7 @@ __global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const
     for (int f = 0; f < 2; ++f)
 #pragma unroll
       for (int tb = 0; tb < G2_TB; ++tb) acc[m][f][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const int nw0 = blockIdx.y * G2_NT + 32 * wave;   // the wave's first weight row
+  const int nw0 = blockIdx.x * G2_NT + 32 * wave;   // the wave's first weight row
   if (slot >= 0) {
     const int nch = (g.K + 127) / 128;
     const int row_bytes = g.K / 2, blocks = g.K / 32;
@@ -747,22 +749,24 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
     return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, tiles, tiles_n, std::min(E, T * k), row_token,
                                row_slot, row_w, D, F, k, limit, ws + wo.hidden, ws + wo.xplanes, y, s);
   }
-  const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested();
+  const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
+  // (the 128-row kernel puts the tiles on grid.y, at most 65535)
+  const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested() &&
+                     max_tiles <= 65535;
   hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, large ? G2_MT : MT, tiles, tiles_n,
                      zeros);
   rc = check_launch("tile_list_kernel");
   if (rc) return rc;
-  const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
   GroupedArgs gu{x, D, row_token, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
                  D, F, k, limit, hidden};
   GroupedArgs dn{hidden, F, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
                  F, D, k, limit, y};
   if (large) {
-    hipLaunchKernelGGL(g2_fp4_kernel<2>, dim3(max_tiles, (F + G2_NT - 1) / G2_NT), dim3(G2_THREADS), 0, s, gu,
+    hipLaunchKernelGGL(g2_fp4_kernel<2>, dim3((F + G2_NT - 1) / G2_NT, max_tiles), dim3(G2_THREADS), 0, s, gu,
                        reinterpret_cast<const uint8_t*>(zeros));
     rc = check_launch("g2_fp4_kernel<2>");
     if (rc) return rc;
-    hipLaunchKernelGGL(g2_fp4_kernel<1>, dim3(max_tiles, (D + G2_NT - 1) / G2_NT), dim3(G2_THREADS), 0, s, dn,
+    hipLaunchKernelGGL(g2_fp4_kernel<1>, dim3((D + G2_NT - 1) / G2_NT, max_tiles), dim3(G2_THREADS), 0, s, dn,
                        reinterpret_cast<const uint8_t*>(zeros));
     return check_launch("g2_fp4_kernel<1>");
   }
