@@ -134,6 +134,8 @@ extern "C" int cachalot_requant_fp4_to_q2(const uint8_t* w_fp4, const uint8_t* s
                                           uint16_t* scales, uint16_t* biases, cachalot_stream_t stream) {
   CACHALOT_REQUIRE(w_fp4 && s_fp4 && q && scales && biases, "requant_fp4_to_q2: null pointer");
   CACHALOT_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "requant_fp4_to_q2: N=%d, K=%d (K a positive multiple of 32)", N, K);
+  CACHALOT_REQUIRE(((uintptr_t)w_fp4 & 15u) == 0 && ((uintptr_t)q & 15u) == 0,
+                   "requant_fp4_to_q2: w_fp4 and q must be 16-byte aligned");
   const long groups = (long)N * ((K + requant::GROUP - 1) / requant::GROUP);
   requant::Args a{w_fp4, s_fp4, N, K, q, scales, biases};
   hipLaunchKernelGGL(requant::requant_fp4_q2_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0,

@@ -499,6 +499,8 @@ int launch_decode(const uint16_t* x, const uint8_t* w1, const uint8_t* s1, const
   return check_launch("fp8 decode down");
 }
 
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 int check_shapes(const char* who, int M, int K, int N) {
   CACHALOT_REQUIRE(M >= 0, "%s: M=%d must be >= 0", who, M);
   CACHALOT_REQUIRE(K > 0 && K % BLOCK == 0, "%s: K=%d must be a positive multiple of %d", who, K, BLOCK);
@@ -516,6 +518,7 @@ extern "C" int cachalot_fp8_act_quant(const uint16_t* x, int M, int K, uint8_t* 
   CACHALOT_REQUIRE(M >= 0, "fp8_act_quant: M=%d must be >= 0", M);
   CACHALOT_REQUIRE(K > 0 && K % fp8::BLOCK == 0, "fp8_act_quant: K=%d must be a positive multiple of 32", K);
   CACHALOT_REQUIRE(x && q && scales, "fp8_act_quant: null pointer");
+  CACHALOT_REQUIRE(fp8::aligned16(x) && fp8::aligned16(q), "fp8_act_quant: x and q must be 16-byte aligned");
   if (M == 0) return CACHALOT_OK;
   return fp8::launch_quant(x, K, M, K, false, 0.0f, q, scales, (hipStream_t)stream);
 }
@@ -525,6 +528,7 @@ extern "C" int cachalot_fp8_linear_quantized(const uint8_t* q, const uint8_t* q_
                                              cachalot_stream_t stream) {
   if (int rc = fp8::check_shapes("fp8_linear_quantized", M, K, N)) return rc;
   CACHALOT_REQUIRE(q && q_scales && w && w_scales && y, "fp8_linear_quantized: null pointer");
+  CACHALOT_REQUIRE(fp8::aligned16(q) && fp8::aligned16(w), "fp8_linear_quantized: q and w must be 16-byte aligned");
   if (M == 0) return CACHALOT_OK;
   fp8::LinearArgs a{q, q_scales, {w, w}, {w_scales, w_scales}, M, N, K, y, N};
   return fp8::launch_linear(a, 1, (hipStream_t)stream);
@@ -544,6 +548,9 @@ extern "C" int cachalot_shared_expert_fp8(const uint16_t* x, const uint8_t* w1, 
   if (int rc = fp8::check_shapes("shared_expert_fp8 (w2)", M, F, D)) return rc;
   CACHALOT_REQUIRE(x && w1 && w1_scales && w3 && w3_scales && w2 && w2_scales && y,
                    "shared_expert_fp8: null pointer");
+  CACHALOT_REQUIRE(fp8::aligned16(x) && fp8::aligned16(w1) && fp8::aligned16(w3) && fp8::aligned16(w2) &&
+                       fp8::aligned16(workspace),
+                   "shared_expert_fp8: x, the weights and the workspace must be 16-byte aligned");
   if (M == 0) return CACHALOT_OK;
   const size_t need = fp8::workspace_bytes(M, D, F);
   if (workspace_bytes < need || !workspace)
