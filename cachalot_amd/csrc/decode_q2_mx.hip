@@ -124,8 +124,15 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
     tile::wait_vmem();
   }
   lds_sync();
-  const int slot = s.slot;
+  // uniform (one value per workgroup): the loads below then take a scalar base and a
+  // 32-bit vector offset, so no 64-bit address pair per load stays live
+  const int slot = __builtin_amdgcn_readfirstlane(s.slot);
   const bool live = slot >= 0;
+
+  // (set up before the loads, so these registers are not taken from the loads' addresses)
+  const ARole ro = a_role(lane);
+  Chain ch;
+  chain_init(ch);
 
   // ---- 1. loads: per item the scale / bias chunk copy (lane = tensor x row), then the codes
   uint4 c1[MAXM][2], c3[MAXM][2];
@@ -140,7 +147,7 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
       const int o = ((row0 + r) * GT + 4 * q) * 2;
       tile::lds_load16_untracked(base + toff + (o & ~15), s.scl[wave][m]);
       gsb[m] = (8 * q) & 15;
-      const int64_t off = (int64_t)(row0 + j) * (D / 4) + (4 * q + kg) * 32;
+      const int off = (row0 + j) * (D / 4) + (4 * q + kg) * 32;   // < 2^31: a 16-row tile of one tensor
       const uint4* r1 = reinterpret_cast<const uint4*>(base + L.off[0] + off);
       const uint4* r3 = reinterpret_cast<const uint4*>(base + L.off[6] + off);
       c1[m][0] = r1[0];
@@ -151,9 +158,6 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
   }
 
   // ---- 2. items
-  const ARole ro = a_role(lane);
-  Chain ch;
-  chain_init(ch);
 #pragma unroll
   for (int m = 0; m < MAXM; ++m) {
     const int q = wave + GU_WAVES * m;
