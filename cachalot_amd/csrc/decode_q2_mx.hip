@@ -396,10 +396,8 @@ struct BatchArgs {
   const uint8_t* xplanes;   // [T][D / 128] plane blocks
   const uint8_t* pool;
   Layout L;
-  const int32_t* slot_table;
-  const int32_t* offsets;   // [E + 1] expert-major rows
-  const int2* tiles;        // (expert, first row) of every expert with rows
-  const int32_t* tiles_n;
+  const int4* recs;         // (expert, first row, end row, slot) of every expert with rows
+  const int32_t* n_recs;
   const int32_t* row_token;
   const int32_t* row_slot;
   const float* row_w;
@@ -409,39 +407,79 @@ struct BatchArgs {
   uint16_t* y;              // [T, k, D]
 };
 
+// sized for D <= 2048 * MAXM, so that more workgroups fit a CU at the smaller widths
+template <int MAXM>
 struct BGuLds {
-  uint8_t planes[2][MAX_GT * PB_BYTES];
-  uint8_t scl[GU_WAVES][GU_MAXM][1024];
-  float red[MAX_NQ][2][16];
+  uint8_t planes[2][4 * GU_WAVES * MAXM * PB_BYTES];
+  uint8_t scl[GU_WAVES][MAXM][1024];
+  float red[GU_WAVES * MAXM][2][16];
 };
 
-// x (T tokens) as plane blocks: grid (T, ceil(D / 1024)).
-__global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __restrict__ x, int D,
-                                                            uint8_t* __restrict__ xplanes) {
-  const int t = blockIdx.x;
-  const int t4 = blockIdx.y * 256 + threadIdx.x;
-  if (4 * t4 < D)
-    mx::encode_x_quad(xplanes + (size_t)t * (D / 128) * PB_BYTES, t4,
-                      reinterpret_cast<const uint2*>(x + (size_t)t * D)[t4]);   // whole quads
+// One launch before the batched kernels, grid 1 + T * ceil(D / 4096), 1024 threads:
+//   workgroup 0: the record (expert, first row, end row, slot) of every expert with
+//     rows, experts ascending, and their count -- so a batched workgroup reads one
+//     record and issues its weight loads, with no dependent lookup in between;
+//   the others: x (T tokens) as plane blocks, 1024 quads each.
+constexpr int PREP_THREADS = 1024;
+__global__ void __launch_bounds__(PREP_THREADS) batch_prep_kernel(const uint16_t* __restrict__ x, int T, int D,
+                                                                  uint8_t* __restrict__ xplanes,
+                                                                  const int32_t* __restrict__ offsets, int E,
+                                                                  const int32_t* __restrict__ slot_table,
+                                                                  int4* __restrict__ recs, int32_t* __restrict__ n_recs) {
+  const int tid = threadIdx.x;
+  if (blockIdx.x > 0) {
+    const int per_row = (D + 4095) / 4096;
+    const int t = (blockIdx.x - 1) / per_row;
+    const int t4 = ((blockIdx.x - 1) - t * per_row) * PREP_THREADS + tid;
+    if (4 * t4 < D)
+      mx::encode_x_quad(xplanes + (size_t)t * (D / 128) * PB_BYTES, t4,
+                        reinterpret_cast<const uint2*>(x + (size_t)t * D)[t4]);   // whole quads
+    return;
+  }
+  __shared__ int wave_n[PREP_THREADS / 64];
+  const int lane = tid & 63, wave = tid >> 6;
+  int base = 0;
+  for (int e0 = 0; e0 < E; e0 += PREP_THREADS) {   // E <= 1024: one trip
+    const int e = e0 + tid;
+    int r0 = 0, r1 = 0;
+    if (e < E) {
+      r0 = offsets[e];
+      r1 = offsets[e + 1];
+    }
+    const bool active = r1 > r0;
+    const uint64_t m = __ballot(active);
+    if (lane == 0) wave_n[wave] = __popcll(m);
+    __syncthreads();
+    int before = base, total = base;
+    for (int w = 0; w < PREP_THREADS / 64; ++w) {
+      before += w < wave ? wave_n[w] : 0;
+      total += wave_n[w];
+    }
+    if (active) recs[before + __popcll(m & ((1ull << lane) - 1ull))] = make_int4(e, r0, r1, slot_table[e]);
+    base = total;
+    __syncthreads();
+  }
+  if (tid == 0) n_recs[0] = base;
 }
 
 template <int MAXM>
 __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
-  __shared__ __align__(16) BGuLds s;
+  __shared__ __align__(16) BGuLds<MAXM> s;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
-  if ((int)blockIdx.x >= a.tiles_n[0]) return;
-  const int2 et = a.tiles[blockIdx.x];
-  const int e = __builtin_amdgcn_readfirstlane(et.x), r0 = __builtin_amdgcn_readfirstlane(et.y);
-  const int r1 = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
+  // the record and the count load together (grid.x = the records allocated)
+  const int4 rec = a.recs[blockIdx.x];
+  if ((int)blockIdx.x >= a.n_recs[0]) return;
+  const int r0 = __builtin_amdgcn_readfirstlane(rec.y);
+  const int r1 = __builtin_amdgcn_readfirstlane(rec.z);
+  const int slot = __builtin_amdgcn_readfirstlane(rec.w);
   const int D = a.D, F = a.F;
   const int GT = D / 128, NQ = GT / 4;
   const int GK = (F + 127) / 128, FT = F / 16;
   const int tile = blockIdx.y;
   const int row0 = tile * 16;
-  const int slot = a.slot_table[e];
   const bool live = slot >= 0;
   const int pbytes = GT * PB_BYTES;
 
@@ -475,9 +513,11 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
   chain_init(ch);
   for (int r = r0; r < r1; ++r) {
     const int buf = __builtin_amdgcn_readfirstlane((r - r0) & 1);
-    if (r + 1 < r1)   // the next row's planes, into the other buffer
-      copy_to_lds_untracked(a.xplanes + (size_t)a.row_token[r + 1] * pbytes, s.planes[buf ^ 1], pbytes, wave,
-                            GU_WAVES, lane);
+    // the next row's planes, into the other buffer, by waves 1.. (wave 0 stores this
+    // row's h below and then need not wait for its own stores)
+    if (r + 1 < r1 && wave > 0)
+      copy_to_lds_untracked(a.xplanes + (size_t)a.row_token[r + 1] * pbytes, s.planes[buf ^ 1], pbytes, wave - 1,
+                            GU_WAVES - 1, lane);
     const uint8_t* planes = s.planes[buf];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
@@ -508,15 +548,15 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
     if (tid < 16) {
       float hv = 0.0f;
       if (live) {
-        float rg[MAX_NQ], ru[MAX_NQ];
+        float rg[GU_WAVES * MAXM], ru[GU_WAVES * MAXM];
 #pragma unroll
-        for (int q = 0; q < MAX_NQ; ++q) {
+        for (int q = 0; q < GU_WAVES * MAXM; ++q) {
           rg[q] = s.red[q][0][tid];
           ru[q] = s.red[q][1][tid];
         }
         float g = 0.0f, u = 0.0f;
 #pragma unroll
-        for (int q = 0; q < MAX_NQ; ++q) {
+        for (int q = 0; q < GU_WAVES * MAXM; ++q) {
           if (q < NQ) {
             g = g + rg[q];
             u = u + ru[q];
@@ -552,10 +592,13 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
         }
       }
     }
-    // the next row's planes have landed (this wave's copy) and every wave is past
-    // this row's reads of red and of the current planes
-    tile::wait_vmem();
-    lds_sync();
+    // before the next row: its planes have landed (the copying waves' loads) and
+    // every wave is past this row's reads of red and of the current planes.  After
+    // the last row nothing waits, so the workgroup ends while its stores drain.
+    if (r + 1 < r1) {
+      if (wave > 0) tile::wait_vmem();
+      lds_sync();
+    }
   }
 }
 
@@ -572,14 +615,14 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn_kernel(BatchArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
-  if ((int)blockIdx.x >= a.tiles_n[0]) return;
-  const int2 et = a.tiles[blockIdx.x];
-  const int e = __builtin_amdgcn_readfirstlane(et.x), r0 = __builtin_amdgcn_readfirstlane(et.y);
-  const int r1 = __builtin_amdgcn_readfirstlane(a.offsets[e + 1]);
+  const int4 rec = a.recs[blockIdx.x];
+  if ((int)blockIdx.x >= a.n_recs[0]) return;
+  const int r0 = __builtin_amdgcn_readfirstlane(rec.y);
+  const int r1 = __builtin_amdgcn_readfirstlane(rec.z);
+  const int slot = __builtin_amdgcn_readfirstlane(rec.w);
   const int D = a.D, F = a.F;
   const int GK = (F + 127) / 128, NQ2 = (GK + 3) / 4, FT = F / 16;
   const int n0 = blockIdx.y * 16;
-  const int slot = a.slot_table[e];
   const bool live = slot >= 0;
   const int hbytes = GK * PB_BYTES;
 
@@ -607,8 +650,9 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn_kernel(BatchArgs a) {
   chain_init(ch);
   for (int r = r0; r < r1; ++r) {
     const int buf = __builtin_amdgcn_readfirstlane((r - r0) & 1);
-    if (r + 1 < r1)
-      copy_to_lds_untracked(a.hid + (size_t)(r + 1) * hbytes, s.planes[buf ^ 1], hbytes, wave, GU_WAVES, lane);
+    if (r + 1 < r1 && wave > 0)   // (as in q2mx_bgu_kernel: wave 0 stores, waves 1.. copy)
+      copy_to_lds_untracked(a.hid + (size_t)(r + 1) * hbytes, s.planes[buf ^ 1], hbytes, wave - 1, GU_WAVES - 1,
+                            lane);
     const uint8_t* planes = s.planes[buf];
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
@@ -640,8 +684,10 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn_kernel(BatchArgs a) {
       }
       a.y[((size_t)a.row_token[r] * a.k + a.row_slot[r]) * D + n0 + tid] = f32_to_bf16(yv);
     }
-    tile::wait_vmem();
-    lds_sync();
+    if (r + 1 < r1) {
+      if (wave > 0) tile::wait_vmem();
+      lds_sync();
+    }
   }
 }
 
@@ -686,18 +732,18 @@ int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, c
 }
 
 // Batched decode over expert-major rows (grouped.hip's permutation): x planes of the
-// T tokens, then gate/up and down over the active experts.  tiles / tiles_n list the
-// active experts (one entry each, first row); hid holds rows x GK plane blocks and
-// xplanes T x D / 128.
+// T tokens and the active experts' records (recs, n_recs: min(E, T k) entries of
+// workspace), then gate/up and down over the active experts.
+// hid holds rows x GK plane blocks and xplanes T x D / 128.
 int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const Layout& L, const int32_t* slot_table,
-                        const int32_t* offsets, const int2* tiles, const int32_t* tiles_n, int max_active,
+                        const int32_t* offsets, int E, int4* recs, int32_t* n_recs, int max_active,
                         const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k,
                         float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s) {
-  hipLaunchKernelGGL(x_planes_rows_kernel, dim3(T, (D + 1023) / 1024), dim3(256), 0, s, x, D, xplanes);
-  int rc = check_launch("x_planes_rows_kernel");
+  hipLaunchKernelGGL(batch_prep_kernel, dim3(1 + T * ((D + 4095) / 4096)), dim3(PREP_THREADS), 0, s, x, T, D, xplanes,
+                     offsets, E, slot_table, recs, n_recs);
+  int rc = check_launch("batch_prep_kernel");
   if (rc) return rc;
-  BatchArgs a{xplanes, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w, D, F, k, limit,
-              hid, y};
+  BatchArgs a{xplanes, pool, L, recs, n_recs, row_token, row_slot, row_w, D, F, k, limit, hid, y};
   const int NQ = D / 512;
   const int mg = (NQ + GU_WAVES - 1) / GU_WAVES;
   const dim3 grid_gu(max_active, F / 16);

@@ -37,7 +37,7 @@ namespace cachalot {
 // matrix-core batched decode (decode_q2_mx.hip)
 bool q2mx_supported(int D, int F, int k);
 int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
-                        const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
+                        const int32_t* slot_table, const int32_t* offsets, int E, int4* recs, int32_t* n_recs,
                         int max_active, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
                         int F, int k, float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s);
 
@@ -676,7 +676,8 @@ inline GroupedWs grouped_ws(int T, int k, int E, int D, int F) {
   w.max_tiles = rows / 16 + std::min(E, rows) + 1;   // bound for MT >= 16
   w.tiles_n = 0;
   w.tiles = 256;
-  w.hidden = w.tiles + align256((size_t)w.max_tiles * sizeof(int2));
+  // int2 tiles, or one int4 record per active expert (matrix-core batched decode)
+  w.hidden = w.tiles + align256(std::max((size_t)w.max_tiles * sizeof(int2), (size_t)std::min(E, rows) * sizeof(int4)));
   const size_t hid = std::max((size_t)rows * F * sizeof(uint16_t), (size_t)rows * ((F + 127) / 128) * 320);
   w.xplanes = w.hidden + align256(hid);
   w.total = w.xplanes + align256((size_t)T * ((D + 127) / 128) * 320);
@@ -743,11 +744,9 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   uint32_t* zeros = reinterpret_cast<uint32_t*>(ws + wo.tiles_n + 128);
   if (KIND == KIND_Q2 && MT == 16 && q2mx_supported(D, F, k) && !small_tiles_requested()) {
     // few rows per expert: the matrix-core batched decode, one entry per active expert
-    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, 1 << 30, tiles, tiles_n, zeros);
-    rc = check_launch("tile_list_kernel");
-    if (rc) return rc;
-    return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, tiles, tiles_n, std::min(E, T * k), row_token,
-                               row_slot, row_w, D, F, k, limit, ws + wo.hidden, ws + wo.xplanes, y, s);
+    return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, E, reinterpret_cast<int4*>(ws + wo.tiles),
+                               tiles_n, std::min(E, T * k), row_token, row_slot, row_w, D, F, k, limit,
+                               ws + wo.hidden, ws + wo.xplanes, y, s);
   }
   const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
   // (the 128-row kernel puts the tiles on grid.y, at most 65535)
