@@ -450,6 +450,7 @@ constexpr int G2_MT = 128;                 // token rows per workgroup (8 fragme
 constexpr int G2_TB = G2_MT / 16;
 constexpr int G2_NT = 32 * G2_WAVES;       // 256 weight rows per matrix
 constexpr int G2_STAGES = 3;
+constexpr int G2_GROUP = 1;                // M tiles per XCD block (workgroup order; 2 measured no faster)
 constexpr int G2_ABYTES = G2_MT * 256;     // one A chunk: 128 rows x 128 bf16
 constexpr int G2_ASLICES = G2_ABYTES / 1024 / G2_WAVES;   // 1 KiB direct-to-LDS slices per wave and chunk
 
@@ -533,17 +534,26 @@ __device__ __forceinline__ void g2_compute(const uint8_t* ab, const G2Chunk<NM>&
   }
 }
 
-// grid = (ceil(N / 256), max tiles).  NM = 2: gate/up (W1, W3) -> h; NM = 1: down (W2) -> y.
+// grid = slices * tiles rounded up to 8 G2_GROUP, one dimension, slices = ceil(N / 256).
+// Workgroups are dealt to the eight XCDs round-robin by launch index (b % 8).  XCD x takes
+// blocks of G2_GROUP consecutive tiles (block j of XCD x: tiles (8 j + x) G2_GROUP ..) and
+// runs a block's workgroups slice by slice, its tiles inside a slice, so the slices of an
+// M tile run on one XCD together and its gathered A rows are fetched into that XCD's L2
+// once instead of once per XCD (G2_GROUP > 1 would also share weight slices between a
+// block's tiles).  NM = 2: gate/up (W1, W3) -> h; NM = 1: down (W2) -> y.
 template <int NM>
-__global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const uint8_t* __restrict__ zeros) {
+__global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const uint8_t* __restrict__ zeros,
+                                                            int slices) {
   __shared__ __align__(16) uint8_t abuf[G2_STAGES][G2_ABYTES];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, kg = lane >> 4;
-  // grid = (N slices, tiles): the slices of one M tile are dispatched together, so its
-  // gathered A rows are read from HBM once and then hit in cache
-  if ((int)blockIdx.y >= g.tiles_n[0]) return;
-  const int2 tl = g.tiles[blockIdx.y];
+  const int b8 = blockIdx.x >> 3;                         // sequence number on this XCD
+  const int blk = b8 / (slices * G2_GROUP), w = b8 - blk * (slices * G2_GROUP);
+  const int slice = w / G2_GROUP;
+  const int tile_id = (blk * 8 + (int)(blockIdx.x & 7)) * G2_GROUP + (w - slice * G2_GROUP);
+  if (tile_id >= g.tiles_n[0]) return;
+  const int2 tl = g.tiles[tile_id];
   const int e = tl.x, row0 = tl.y;
   const int rows = min(G2_MT, g.offsets[e + 1] - row0);
   const int ntb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
@@ -555,7 +565,7 @@ __global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const
     for (int f = 0; f < 2; ++f)
 #pragma unroll
       for (int tb = 0; tb < G2_TB; ++tb) acc[m][f][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const int nw0 = blockIdx.x * G2_NT + 32 * wave;   // the wave's first weight row
+  const int nw0 = slice * G2_NT + 32 * wave;   // the wave's first weight row
   if (slot >= 0) {
     const int nch = (g.K + 127) / 128;
     const int row_bytes = g.K / 2, blocks = g.K / 32;
@@ -749,9 +759,8 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
                                ws + wo.hidden, ws + wo.xplanes, y, s);
   }
   const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
-  // (the 128-row kernel puts the tiles on grid.y, at most 65535)
   const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested() &&
-                     max_tiles <= 65535;
+                     max_tiles <= (1 << 20);
   hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, large ? G2_MT : MT, tiles, tiles_n,
                      zeros);
   rc = check_launch("tile_list_kernel");
@@ -761,12 +770,14 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   GroupedArgs dn{hidden, F, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
                  F, D, k, limit, y};
   if (large) {
-    hipLaunchKernelGGL(g2_fp4_kernel<2>, dim3((F + G2_NT - 1) / G2_NT, max_tiles), dim3(G2_THREADS), 0, s, gu,
-                       reinterpret_cast<const uint8_t*>(zeros));
+    const int tiles8 = (max_tiles + 8 * G2_GROUP - 1) / (8 * G2_GROUP) * (8 * G2_GROUP);
+    const int s_gu = (F + G2_NT - 1) / G2_NT, s_dn = (D + G2_NT - 1) / G2_NT;
+    hipLaunchKernelGGL(g2_fp4_kernel<2>, dim3(s_gu * tiles8), dim3(G2_THREADS), 0, s, gu,
+                       reinterpret_cast<const uint8_t*>(zeros), s_gu);
     rc = check_launch("g2_fp4_kernel<2>");
     if (rc) return rc;
-    hipLaunchKernelGGL(g2_fp4_kernel<1>, dim3((D + G2_NT - 1) / G2_NT, max_tiles), dim3(G2_THREADS), 0, s, dn,
-                       reinterpret_cast<const uint8_t*>(zeros));
+    hipLaunchKernelGGL(g2_fp4_kernel<1>, dim3(s_dn * tiles8), dim3(G2_THREADS), 0, s, dn,
+                       reinterpret_cast<const uint8_t*>(zeros), s_dn);
     return check_launch("g2_fp4_kernel<1>");
   }
   const size_t lds_gu = grouped_lds_bytes(KIND, MT, 2, D), lds_dn = grouped_lds_bytes(KIND, MT, 1, F);
