@@ -614,6 +614,9 @@ __global__ void __launch_bounds__(G2_THREADS) g2_fp4_kernel(GroupedArgs g, const
         if (c < nch) g2_compute<NM>(abuf[u], ring[u], i, kg, ntb, acc);
       }
     }
+    // the re-reads issued past the end (direct-to-LDS among them) land before the
+    // workgroup's LDS is released
+    tile::wait_vmem();
   }
   // epilogue: lane holds rows tb*16 + 4kg + r (tokens) x column nw0 + 16f + i
 #pragma unroll
