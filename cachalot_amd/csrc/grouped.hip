@@ -508,6 +508,36 @@ __device__ __forceinline__ void g2_compute(const uint8_t* ab, const G2Chunk<NM>&
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int f = 0; f < 2; ++f) scale[m][f] = e8m0_to_f32(ch.in_k ? ch.sc[m][f] : 127u);
+  if constexpr (NM == 1) {
+    // A fragments in pairs, double-buffered: the next pair's LDS reads are in flight
+    // while the current pair's MFMAs run (the next pair of the same step, or the first
+    // of the next step); pairs past the tile's rows are skipped (ntb uniform).  (Gate/up
+    // has no registers to spare for the second buffer.)
+    bf16x8_t cur0 = lds_a(ab, g2_aoff(i, 4 * kg)), cur1 = lds_a(ab, g2_aoff(16 + i, 4 * kg));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8_t bv[2];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) bv[f] = fp4_codes_to_b(word_of(ch.codes[0][f], s), scale[0][f]);
+#pragma unroll
+      for (int tp = 0; tp < G2_TB; tp += 2) {
+        if (tp >= ntb) break;
+        const bool last = tp + 2 >= ntb;
+        const int nt = last ? 0 : tp + 2;
+        const int ns = last ? min(s + 1, 3) : s;   // after the last step: a read nobody uses
+        const bf16x8_t nx0 = lds_a(ab, g2_aoff(nt * 16 + i, 4 * kg + ns));
+        const bf16x8_t nx1 = lds_a(ab, g2_aoff((nt + 1) * 16 + i, 4 * kg + ns));
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          acc[0][f][tp] = mfma(cur0, bv[f], acc[0][f][tp]);
+          acc[0][f][tp + 1] = mfma(cur1, bv[f], acc[0][f][tp + 1]);
+        }
+        cur0 = nx0;
+        cur1 = nx1;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     bf16x8_t bv[NM][2];
