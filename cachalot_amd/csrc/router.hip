@@ -63,7 +63,7 @@ __device__ __forceinline__ void route_tail(const float* __restrict__ scores, con
 }
 
 // One wave per expert row (lane l owns chunk l of D/64 elements), TT tokens per
-// wave, 4 waves per workgroup; optionally the top-k tail (one token).
+// wave, blockDim / 64 waves per workgroup; optionally the top-k tail (one token).
 template <int TT, int NV>
 __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ W, int T, int D,
@@ -71,9 +71,9 @@ __global__ void __launch_bounds__(256) router_scores_kernel(const uint16_t* __re
                                                             float* __restrict__ scores, decode::RouteTail tail,
                                                             uint8_t* __restrict__ xplanes) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (xplanes != nullptr && blockIdx.y == 0) {   // token 0 as fp8 planes for the matrix-core decode
-    for (int t4 = blockIdx.x * 256 + (int)threadIdx.x; 4 * t4 < D; t4 += gridDim.x * 256)
+    for (int t4 = blockIdx.x * blockDim.x + threadIdx.x; 4 * t4 < D; t4 += gridDim.x * blockDim.x)
       mx::encode_x_quad(xplanes, t4, reinterpret_cast<const uint2*>(x)[t4]);   // whole quads of lanes
   }
   if (row < E) router_row<TT, NV>(x, W, T, D, E, gate_temp, fn, scores, row, lane, tail.counter != nullptr);
@@ -240,12 +240,14 @@ __global__ void __launch_bounds__(256) router_tiled_kernel(const uint16_t* __res
 template <int TT>
 static void launch_scores_tt(const uint16_t* x, const uint16_t* W, int T, int D, int E, float temp, int fn,
                              float* scores, hipStream_t s, const decode::RouteTail& tail, uint8_t* xplanes) {
-  dim3 grid((E + 3) / 4, (T + TT - 1) / TT);
+  // one token: one wave per workgroup, so the E rows spread over every CU
+  const int wpb = TT == 1 ? 1 : 4;
+  const dim3 grid((E + wpb - 1) / wpb, (T + TT - 1) / TT), block(64 * wpb);
   switch (D) {
-    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
-    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
-    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
-    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, dim3(256), 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    case 4096: hipLaunchKernelGGL((router_scores_kernel<TT, 8>), grid, block, 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    case 5120: hipLaunchKernelGGL((router_scores_kernel<TT, 10>), grid, block, 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    case 7168: hipLaunchKernelGGL((router_scores_kernel<TT, 14>), grid, block, 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
+    default: hipLaunchKernelGGL((router_scores_kernel<TT, 0>), grid, block, 0, s, x, W, T, D, E, temp, fn, scores, tail, xplanes); break;
   }
 }
 
