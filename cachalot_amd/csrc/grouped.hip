@@ -67,15 +67,27 @@ __global__ void __launch_bounds__(PERMUTE_THREADS) permute_count_kernel(const in
     if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {   // E <= 1024: a serial scan is short
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = cnt[e];
-      offsets[e] = run;
-      run += c;
-    }
-    offsets[E] = run;
+  // exclusive scan over the E <= 1024 counts, one per thread: inclusive within each
+  // wave by shifted adds, then the wave totals
+  __shared__ int wave_tot[PERMUTE_THREADS / 64];
+  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
+  const int c = e < E ? cnt[e] : 0;
+  int v = c;
+#pragma unroll
+  for (int d = 1; d < 64; d *= 2) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
   }
+  if (lane == 63) wave_tot[wave] = v;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < PERMUTE_THREADS / 64; ++w) {
+    before += w < wave ? wave_tot[w] : 0;
+    total += wave_tot[w];
+  }
+  if (e < E) offsets[e] = before + v - c;
+  if (e == 0) offsets[E] = total;
 }
 
 // One workgroup per expert e: walk the routes in order, keep those that chose e.
