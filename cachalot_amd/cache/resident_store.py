@@ -152,9 +152,15 @@ class ResidentExpertStore:
                 misses.sort(key=lambda i: -priorities[i])
             budget = len(misses) if max_misses is None else max(0, int(max_misses))
             protect = set(keys)
-            for n, i in enumerate(misses):
-                if n >= budget:
-                    break
+            loaded = 0
+            for i in misses:
+                slot = self._items.get(keys[i])
+                if slot is not None:        # a repeated key, loaded earlier in this call
+                    out[i] = self._wrap(keys[i], slot)
+                    continue
+                if loaded >= budget:
+                    continue
+                loaded += 1
                 if self.loader is None:
                     raise KeyError(f"Missing routed expert layer={keys[i][0]}, expert={keys[i][1]}")
                 slot = self._take_slot(protect)

@@ -91,8 +91,11 @@ __global__ void __launch_bounds__(PERMUTE_THREADS) permute_count_kernel(const in
 }
 
 // One workgroup per expert e: walk the routes in order, keep those that chose e.
+// Workgroup E collects the routes whose id lies outside [0, E) into rows
+// [offsets[E], n), in route order, with weight 0: the dropped routes, whose y
+// rows drop_zero_kernel clears.
 __global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __restrict__ idx,
-                                                              const float* __restrict__ w, int n, int k,
+                                                              const float* __restrict__ w, int n, int k, int E,
                                                               const int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ row_token,
                                                               int32_t* __restrict__ row_slot,
@@ -101,11 +104,13 @@ __global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __r
   const int e = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const bool dropped = e == E;
   int base = offsets[e];
-  if (offsets[e + 1] == base) return;
+  if ((dropped ? n : offsets[e + 1]) == base) return;
   for (int i0 = 0; i0 < n; i0 += 256) {
     const int i = i0 + threadIdx.x;
-    const bool hit = i < n && idx[i] == e;
+    int id = i < n ? idx[i] : 0;
+    const bool hit = i < n && (dropped ? (id < 0 || id >= E) : id == e);
     const uint64_t mask = __ballot(hit);
     if (lane == 0) wave_count[wave] = __popcll(mask);
     __syncthreads();
@@ -119,10 +124,30 @@ __global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __r
       const int pos = base + before + __popcll(mask & ((1ull << lane) - 1ull));
       row_token[pos] = i / k;
       row_slot[pos] = i - (i / k) * k;
-      row_w[pos] = w[i];
+      row_w[pos] = dropped ? 0.0f : w[i];
     }
     base += total;
     __syncthreads();
+  }
+}
+
+// y rows of the dropped routes (rows [offsets[E], n) of the permutation) are
+// zero, so the combine adds nothing for them.  Runs before the expert kernels:
+// rows a caller's own permutation left undefined there are overwritten by the
+// expert kernels afterwards, and entries outside [0, T) x [0, k) are skipped.
+__global__ void __launch_bounds__(256) drop_zero_kernel(const int32_t* __restrict__ offsets, int E, int n, int T,
+                                                        int k, int D, const int32_t* __restrict__ row_token,
+                                                        const int32_t* __restrict__ row_slot,
+                                                        uint16_t* __restrict__ y) {
+  const int first = offsets[E];
+  const int per_row = D / 8;   // 16-byte stores
+  const int64_t total = (int64_t)max(n - first, 0) * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int r = first + (int)(i / per_row);
+    const int c = (int)(i - (int64_t)(r - first) * per_row);
+    const int t = row_token[r], sl = row_slot[r];
+    if (t < 0 || t >= T || sl < 0 || sl >= k) continue;
+    reinterpret_cast<uint4*>(y + ((int64_t)t * k + sl) * D)[c] = uint4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -797,6 +822,9 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   // tiles of 64 rows when experts see many tokens, 16 for batched decode
   const int MT = T * k >= 4 * E ? 64 : 16;
   uint32_t* zeros = reinterpret_cast<uint32_t*>(ws + wo.tiles_n + 128);
+  hipLaunchKernelGGL(drop_zero_kernel, dim3(16), dim3(256), 0, s, offsets, E, T * k, T, k, D, row_token, row_slot, y);
+  rc = check_launch("drop_zero_kernel");
+  if (rc) return rc;
   if (KIND == KIND_Q2 && MT == 16 && q2mx_supported(D, F, k) && !small_tiles_requested()) {
     // few rows per expert: the matrix-core batched decode, one entry per active expert
     return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, E, reinterpret_cast<int4*>(ws + wo.tiles),
@@ -843,8 +871,8 @@ extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k
   hipLaunchKernelGGL(permute_count_kernel, dim3(1), dim3(PERMUTE_THREADS), 0, s, idx, T * k, E, offsets);
   int rc = check_launch("permute_count_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(permute_scatter_kernel, dim3(E), dim3(256), 0, s, idx, w, T * k, k, offsets, row_token, row_slot,
-                     row_w);
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(E + 1), dim3(256), 0, s, idx, w, T * k, k, E, offsets, row_token,
+                     row_slot, row_w);
   return check_launch("permute_scatter_kernel");
 }
 

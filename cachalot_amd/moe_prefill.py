@@ -64,11 +64,14 @@ def permute(indices: torch.Tensor, weights: torch.Tensor, n_experts: int):
 
 def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, pool: HBMSlotPool,
                     slot_table: torch.Tensor, *, swiglu_limit: float = 10.0, addend: torch.Tensor | None = None,
-                    want_routed: bool = False, want_out: bool = True):
+                    want_routed: bool = False, want_out: bool = True, want_terms: bool = False):
     """x [T, D] bf16, routes [T, k] -> (routed fp32 [T, D] or None, out bf16 [T, D] or None).
 
     routed[t] = sum over route slots s (in order) of expert idx[t, s] applied to x[t]
-    with router weight w[t, s]; out = bf16(routed + addend)."""
+    with router weight w[t, s]; out = bf16(routed + addend).  A route whose expert
+    id lies outside [0, E), or whose expert has no slot, contributes zero.  With
+    ``want_terms`` the per-route expert outputs y [T, k, D] bf16 (each one the
+    reference's bf16 cast of its expert's output) come back as a third value."""
     fmt = pool.format
     d, f = fmt.d_model, fmt.d_ff
     if x.ndim != 2 or x.shape[1] != d:
@@ -107,7 +110,7 @@ def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tenso
     out = torch.empty((t, d), dtype=torch.bfloat16, device=dev) if want_out else None
     rc = L.cachalot_unpermute_combine(y.data_ptr(), _lib.ptr(addend), t, k, d, _lib.ptr(routed), _lib.ptr(out), stream)
     _lib.check(rc, "unpermute_combine")
-    return routed, out
+    return (routed, out, y) if want_terms else (routed, out)
 
 
 def moe_prefill_grouped(

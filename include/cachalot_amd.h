@@ -148,7 +148,10 @@ int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight
  * cachalot_permute: routes idx/w [T, k] -> rows grouped by expert id
  * (ascending), tokens ascending inside an expert: offsets [E+1] (rows of
  * expert e are offsets[e] .. offsets[e+1]-1), row_token / row_slot / row_w
- * [T*k].  Replaces the host-side assignment build of moe_prefill_grouped
+ * [T*k].  A route whose id lies outside [0, E) is dropped: such routes fill
+ * rows offsets[E] .. T*k-1, in route order, with row_w 0, and the grouped
+ * entry points write zero y rows for them (the decode entry points likewise
+ * give such an id zero rows).  Replaces the host-side assignment build of moe_prefill_grouped
  * (src/cachalot/model/moe_prefill_grouped.py:199-225) and the per-expert
  * x[token_idx] gather lists (:420-437).
  *
@@ -156,7 +159,8 @@ int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight
  * expert on its rows (x gathered by row_token): g = bf16(x W1), u = bf16(x W3),
  * h = bf16(silu(min(g,L)) * clip(u,-L,L) * row_w), y = bf16(h W2), written to
  * y[row_token, row_slot, :] ([T, k, D] bf16).  Experts whose slot_table entry
- * is negative give zero rows.  Workspace from
+ * is negative give zero rows, and so do the dropped routes (rows offsets[E]
+ * .. T*k-1, as cachalot_permute lays them out).  Workspace from
  * cachalot_grouped_experts_workspace_bytes (scratch, no state across calls).
  * Replaces affine_expert_forward_batched (expert_affine.py:84-99),
  * routed_expert_forward_sgmm (fp4_sgmm_metal.py:318-333) and

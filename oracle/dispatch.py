@@ -18,12 +18,17 @@ from .bf16 import round_bf16
 
 
 def permute(idx, n_experts: int):
-    """idx [T, k] -> dict(offsets [E+1], token [T*k], slot [T*k], pos [T, k])."""
+    """idx [T, k] -> dict(offsets [E+1], token [T*k], slot [T*k], pos [T, k]).
+
+    Ids outside [0, E) are dropped routes (the reference raises ``KeyError`` for a
+    missing expert, ``moe_layer_metal.py:279-283``; this build gives them zero
+    rows): they follow every expert's rows, in route order."""
     idx = np.asarray(idx, dtype=np.int64)
     t, k = idx.shape
     flat = idx.reshape(-1)
+    flat = np.where((flat >= 0) & (flat < n_experts), flat, n_experts)
     order = np.argsort(flat, kind="stable")           # (token, slot) row-major -> stable by expert
-    counts = np.bincount(flat, minlength=n_experts)
+    counts = np.bincount(flat, minlength=n_experts + 1)[:n_experts]
     offsets = np.zeros(n_experts + 1, dtype=np.int64)
     offsets[1:] = np.cumsum(counts)
     pos = np.empty(t * k, dtype=np.int64)

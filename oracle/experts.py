@@ -52,35 +52,45 @@ def fp4_decode(x, dense_experts, weights, limit: float = 10.0) -> np.ndarray:
     return out.astype(np.float32)
 
 
-def swiglu_rows(x, mm1, mm3, mm2, weights, limit: float = 10.0) -> np.ndarray:
+def swiglu_rows(x, mm1, mm3, mm2, weights, limit: float = 10.0, *, raw: bool = False):
     """Rows with the bf16 rounding points.
 
     x [M, K] bf16-exact values; mm1/mm3/mm2 map a float64 [M, K] array to its
     float64 product with W1^T / W3^T / W2^T; weights [M] fp32.  -> fp32 [M, D]
-    (each value bf16-exact)."""
+    (each value bf16-exact).  With ``raw`` also the float64 value of the last
+    product before its casts (fp32, then bf16), which tells how close each
+    output lies to a bf16 rounding boundary."""
     x = np.asarray(x, dtype=np.float64)
     g = round_bf16(mm1(x).astype(np.float32)).astype(np.float64)
     u = round_bf16(mm3(x).astype(np.float32)).astype(np.float64)
     g, u = _clamp(g, u, limit)
     w = np.asarray(weights, dtype=np.float32).astype(np.float64)[:, None]
     h = round_bf16((_silu64(g) * u * w).astype(np.float32)).astype(np.float64)
-    return round_bf16(mm2(h).astype(np.float32))
+    y64 = mm2(h)
+    y = round_bf16(y64.astype(np.float32))
+    return (y, y64) if raw else y
 
 
-def affine_decode(x, mats, weights, limit: float = 10.0, addend=None, *, terms: bool = False):
+def affine_decode(x, mats, weights, limit: float = 10.0, addend=None, *, terms: bool = False,
+                  raw: bool = False):
     """x [D] bf16-exact; mats: per expert (mm1, mm3, mm2) as in ``swiglu_rows``.
 
     -> (routed fp32 [D], out fp32 [D] holding bf16(routed + addend)), plus the
-    per-expert outputs y_e (bf16-exact fp32 [k, D]) when ``terms``."""
+    per-expert outputs y_e (bf16-exact fp32 [k, D]) when ``terms``, plus their
+    float64 values before the casts (``swiglu_rows(raw=True)``) when ``raw``."""
     x = np.asarray(x, dtype=np.float64)[None, :]
     routed = None
-    ys = []
+    ys, raws = [], []
     for (mm1, mm3, mm2), w in zip(mats, weights, strict=True):
-        y = swiglu_rows(x, mm1, mm3, mm2, np.asarray([w], np.float32), limit)[0]
-        ys.append(y)
-        routed = (np.float32(0.0) + y) if routed is None else (routed + y)
+        y, y64 = swiglu_rows(x, mm1, mm3, mm2, np.asarray([w], np.float32), limit, raw=True)
+        ys.append(y[0])
+        raws.append(y64[0])
+        routed = (np.float32(0.0) + y[0]) if routed is None else (routed + y[0])
     routed = routed.astype(np.float32)
     total = routed if addend is None else routed + np.asarray(addend, np.float32)
+    res = (routed, round_bf16(total))
     if terms:
-        return routed, round_bf16(total), np.stack(ys)
-    return routed, round_bf16(total)
+        res += (np.stack(ys),)
+    if raw:
+        res += (np.stack(raws),)
+    return res

@@ -93,8 +93,13 @@ def score_fn(z32: np.ndarray, kind: int) -> np.ndarray:
     raise ValueError(f"unknown score function {kind}")
 
 
-def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: int = 16) -> np.ndarray:
-    """x [T, D], w [E, D] (bf16-exact fp32 values) -> fp32 [T, E] in the fixed order."""
+def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: int = 16,
+           workers: int = 1) -> np.ndarray:
+    """x [T, D], w [E, D] (bf16-exact fp32 values) -> fp32 [T, E] in the fixed order.
+
+    ``workers`` > 1 evaluates blocks of tokens on that many threads (NumPy
+    releases the GIL inside the element-wise loops); every token's arithmetic is
+    the same either way."""
     x32 = np.asarray(x32, dtype=np.float32)
     w32 = np.asarray(w32, dtype=np.float32)
     t, d = x32.shape
@@ -106,7 +111,8 @@ def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: i
     xr = x32.reshape(t, N_CHUNKS, ch)
     wr = w32.reshape(e, N_CHUNKS, ch)
     lane = np.arange(N_CHUNKS)
-    for t0 in range(0, t, block):
+
+    def one(t0):
         xs = xr[t0:t0 + block]
         acc = np.zeros((xs.shape[0], e, N_CHUNKS), dtype=np.float32)
         for j in range(ch):
@@ -114,6 +120,16 @@ def logits(x32: np.ndarray, w32: np.ndarray, gate_temp: float = 1.0, *, block: i
         for s in (1, 2, 4, 8, 16, 32):
             acc = acc + acc[..., lane ^ s]
         out[t0:t0 + block] = acc[..., 0]
+
+    starts = range(0, t, block)
+    if workers > 1 and t > block:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=workers) as ex:
+            list(ex.map(one, starts))
+    else:
+        for t0 in starts:
+            one(t0)
     return out / np.float32(gate_temp)
 
 
@@ -141,10 +157,10 @@ def normalise(w: np.ndarray, route_scale: float, norm: bool) -> np.ndarray:
 
 def route(x32, w32, bias, *, topk: int = 6, gate_temp: float = 1.0, route_scale: float = 1.5,
           norm_topk_prob: bool = True, score: int = SCORE_SQRT_SOFTPLUS, order: int = ORDER_ASCENDING,
-          bias_vl=None, image_mask=None):
+          bias_vl=None, image_mask=None, workers: int = 1):
     """-> (indices int32 [T,k], weights fp32 [T,k], scores fp32 [T,E])."""
     x32 = np.atleast_2d(np.asarray(x32, dtype=np.float32))
-    scores = score_fn(logits(x32, w32, gate_temp), score)
+    scores = score_fn(logits(x32, w32, gate_temp, workers=workers), score)
     b = np.asarray(bias, dtype=np.float32)[None, :]
     if image_mask is not None:
         b = np.where(np.asarray(image_mask, bool)[:, None], np.asarray(bias_vl, np.float32)[None, :], b)

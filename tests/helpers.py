@@ -83,3 +83,58 @@ def bf16_terms_ok(got, want, terms, tol: float) -> bool:
     want = np.asarray(want, np.float64)
     slack = np.sum(bf16_ulp(np.asarray(terms, np.float64)), axis=0)
     return bool(np.all(np.abs(got - want) <= tol * np.abs(want).max() + slack))
+
+
+def term_flips(got, raw, tol: float = 2e-3, what: str = "") -> dict:
+    """Per-expert outputs y_e (bf16 values) against the oracle's float64 value of
+    the same product before its casts (``swiglu_rows(raw=True)``).
+
+    The reference rounds g, u, h and every y_e to bf16 (``expert_affine.py:65-81,
+    149-151``).  A different fp32 summation order can move a value across a
+    rounding boundary at any of those points: at y_e itself that is a one-step
+    "flip"; at g, u or h it moves every y_e of that expert by a fraction of a
+    step.  So each GPU term must lie within half a bf16 step of the raw value
+    (its own cast) plus ``tol`` * max|raw|.  Returned: how many terms equal the
+    oracle's cast exactly, how many are the adjacent bf16 value ("flips"), how
+    many are further ("moved"), and the largest excess over the half step in
+    units of max|raw| (``err``: the expert-output error the reference's own
+    bf16 cast does not explain)."""
+    from oracle.bf16 import round_bf16
+
+    got = np.asarray(got, np.float64)
+    raw = np.asarray(raw, np.float64)
+    want = round_bf16(raw.astype(np.float32)).astype(np.float64)
+    scale = max(float(np.abs(raw).max()), 1e-30)
+    excess = np.maximum(np.abs(got - raw) - 0.5 * bf16_ulp(raw), 0.0) / scale
+    diff = got != want
+    adjacent = np.abs(got - want) <= bf16_ulp(np.maximum(np.abs(got), np.abs(want))) * (1 + 1e-9)
+    bad = excess > tol
+    assert not bad.any(), (what, f"{int(bad.sum())} terms beyond half a step + {tol} of max|y|",
+                           float(excess.max()), got[bad][:4].tolist(), raw[bad][:4].tolist())
+    return {"exact": int((~diff).sum()), "flips": int((diff & adjacent).sum()), "moved": int((diff & ~adjacent).sum()),
+            "n": int(got.size), "err": float(excess.max())}
+
+
+def route_order_sum(terms) -> np.ndarray:
+    """0 + y_0 + ... + y_{k-1} in fp32 over the first axis (the reference's combine order)."""
+    terms = np.asarray(terms, np.float32)
+    acc = np.float32(0.0) + terms[0]
+    for t in terms[1:]:
+        acc = (acc + t).astype(np.float32)
+    return acc.astype(np.float32)
+
+
+def bf16_ulp_dist(a_bf16, b_bf16) -> np.ndarray:
+    """Distance in bf16 steps between two arrays of bf16 values (ordered-integer difference)."""
+    from oracle.bf16 import f32_to_bf16_bits
+
+    def key(v):
+        u = f32_to_bf16_bits(np.asarray(v, np.float32)).astype(np.int32)
+        return np.where(u & 0x8000, 0x8000 - (u & 0x7FFF), 0x8000 + u)
+
+    return np.abs(key(a_bf16) - key(b_bf16))
+
+
+def report(what: str, **fields) -> None:
+    """One parity line on stdout (seen with pytest -s and in the smoke output)."""
+    print(f"[parity] {what}: " + ", ".join(f"{k}={v}" for k, v in fields.items()), flush=True)

@@ -7,6 +7,8 @@ scores and weights, by the fixed reduction order both sides follow.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -21,17 +23,6 @@ from oracle.bf16 import bf16_bits_to_f32
 from oracle.fp4 import dequantize_fp4_weight
 
 pytestmark = pytest.mark.gpu
-
-
-@pytest.fixture(params=["two_kernel_mx", "two_kernel_bf16", "one_launch"])
-def q2_path(request, monkeypatch):
-    """The 2-bit decode runs as two kernels on the block-scaled fp8 x fp4 matrix
-    cores by default; the bf16-MFMA kernel pair is selected with
-    CACHALOT_DECODE_BF16=1 and the one-launch persistent kernel with
-    CACHALOT_DECODE_FUSED=1.  All three are pinned."""
-    monkeypatch.setenv("CACHALOT_DECODE_FUSED", "1" if request.param == "one_launch" else "0")
-    monkeypatch.setenv("CACHALOT_DECODE_BF16", "1" if request.param == "two_kernel_bf16" else "0")
-    return request.param
 
 
 TOL = 2e-3
@@ -143,6 +134,9 @@ ROUTER_CASES = [
     # many tokens: the tiled router kernel (partial token and expert tiles, D/64 = 16 and 80)
     (1030, 1024, 100, 4, "sqrt_softplus", "rank", 1.3, 1.5, True),
     (1024, 5120, 64, 6, "sigmoid", "ascending", 1.0, 1.0, True),
+    # the production shape of the tiled router (config 3: E = 384, D = 4096), both score functions
+    (1024, 4096, 384, 6, "sqrt_softplus", "ascending", 1.0, 1.5, True),
+    (1100, 4096, 384, 6, "sigmoid", "ascending", 1.0, 1.0, True),
 ]
 
 
@@ -164,7 +158,7 @@ def _check_router(cuda, x, w, b, *, k, score, order, temp, scale, norm, bias_vl=
                                 score=orouter.SCORE_SIGMOID if score == "sigmoid" else orouter.SCORE_SQRT_SOFTPLUS,
                                 order=orouter.ORDER_ASCENDING if order == "ascending" else orouter.ORDER_RANK,
                                 bias_vl=None if bias_vl is None else _np(bias_vl),
-                                image_mask=None if mask is None else _np(mask))
+                                image_mask=None if mask is None else _np(mask), workers=min(16, os.cpu_count() or 1))
     assert np.array_equal(_np(sc).view(np.uint32), osc.view(np.uint32)), "scores"
     assert np.array_equal(_np(idx), oi), "indices"
     assert np.array_equal(_np(wt).view(np.uint32), ow.view(np.uint32)), "weights"

@@ -127,3 +127,22 @@ def test_zipf_bias_is_a_permutation_of_ranks():
     ranks = sorted(b, reverse=True)
     assert ranks[0] == pytest.approx(0.5) and ranks[-1] == pytest.approx(0.5 * 384 ** -1.1)
     assert zipf_bias(384, seed=5) == b and zipf_bias(384, seed=6) != b
+
+
+def test_get_many_loads_a_repeated_key_once():
+    """A key named twice in one request is loaded once and both entries share its slot
+    (a host-memory pool: the store's bookkeeping needs no GPU)."""
+    from cachalot_amd.cache.resident_store import ResidentExpertStore
+    from cachalot_amd.storage.index import ExpertEntry, affine_format
+
+    loads = []
+    store = ResidentExpertStore(fmt=affine_format(256, 128), n_slots=3, n_layers=1, n_experts=8, device="cpu",
+                                loader=lambda entry, slot: loads.append((entry.layer, entry.expert, slot.index)))
+    got = store.get_many([ExpertEntry(0, 2), ExpertEntry(0, 5), ExpertEntry(0, 2)])
+    assert [g.expert for g in got] == [2, 5, 2] and got[0].slot is got[2].slot
+    assert len(loads) == 2 and store.stats.misses == 2
+    store.get_many([ExpertEntry(0, 6), ExpertEntry(0, 7)])        # both earlier slots can be reused now
+    assert store.stats.misses == 4 and store.stats.evictions >= 1
+    budget = store.get_many([ExpertEntry(0, 1), ExpertEntry(0, 1), ExpertEntry(0, 3)], max_misses=1)
+    assert budget[0] is not None and budget[1].slot is budget[0].slot
+    assert budget[2] is None
