@@ -24,6 +24,8 @@
 //                      value is rounded to bf16 (the reference's per-expert
 //                      cast) and the experts are summed in route order,
 //                      + addend, -> fp32 / bf16.
+#include <mutex>
+
 #include "decode_common.h"
 #include "mfma_tile.h"
 #include "router_launch.h"
@@ -485,4 +487,89 @@ extern "C" int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* g
                               route_scale};
   return launch_q2_decode(x, pool, layout, src, &rt, D, F, k, group, swiglu_limit, addend, routed, out, workspace,
                           workspace_bytes, (hipStream_t)stream);
+}
+
+// ------------------------------------------------- decode with no allocation ---
+// cachalot_moe_layer_decode_q2_static: cachalot_moe_layer_decode_q2 with its
+// workspace in a file-scope device array instead of a caller's buffer, for callers
+// that cannot allocate (code under HIP graph capture, serving loops, harnesses that
+// forbid hipMalloc).  Each GPU the library runs on holds its own copy of the array
+// (STATIC_SCRATCH_BYTES) until the process ends; every call on one GPU shares it,
+// so calls that overlap on one GPU race.  Nothing here allocates: the array's
+// device address comes from hipGetSymbolAddress, once per device, and the kernels
+// receive that address exactly as they receive a caller's workspace.
+//
+// What must start at zero: the counters at the head of the workspace.  The loader
+// zero-fills the array, the first call on each device clears it once more with a
+// fill kernel on the caller's stream, and every call leaves the counters at zero.
+namespace cachalot {
+namespace {
+constexpr size_t STATIC_SCRATCH_BYTES = 256 * 1024;
+constexpr int STATIC_MAX_DEVICES = 64;
+}  // namespace
+}  // namespace cachalot
+
+static __device__ __align__(256) uint8_t scratch[cachalot::STATIC_SCRATCH_BYTES];
+
+namespace cachalot {
+namespace {
+
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[STATIC_MAX_DEVICES] = {};
+
+__global__ void __launch_bounds__(256) scratch_clear_kernel(uint4* __restrict__ p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
+// The current device's copy of `scratch` (device address), set up on first use.
+int static_scratch(uint8_t** out, hipStream_t s) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= STATIC_MAX_DEVICES)
+    return fail(CACHALOT_EHIP, "moe_layer_decode_q2_static: no usable current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return fail(CACHALOT_EHIP, "moe_layer_decode_q2_static: hipGetSymbolAddress failed on device %d: %s", dev,
+                  hipGetErrorString(err));
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, s, static_cast<uint4*>(p),
+                       STATIC_SCRATCH_BYTES / 16);
+    const int rc = check_launch("scratch_clear_kernel");
+    if (rc) return rc;
+    g_scratch[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return CACHALOT_OK;
+}
+
+}  // namespace
+}  // namespace cachalot
+
+extern "C" size_t cachalot_moe_layer_decode_q2_static_max_bytes(void) { return cachalot::STATIC_SCRATCH_BYTES; }
+
+extern "C" int cachalot_moe_layer_decode_q2_static(const uint16_t* x, const uint16_t* gate_weight,
+                                                   const float* gate_bias, int E, int k, int score_fn,
+                                                   float gate_temp, float route_scale, int norm, int order,
+                                                   const uint8_t* pool, const cachalot_expert_layout* layout,
+                                                   const int32_t* slot_table, int D, int F, int group,
+                                                   float swiglu_limit, const uint16_t* addend, int32_t* idx_out,
+                                                   float* w_out, float* scores, float* routed, uint16_t* out,
+                                                   cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(D > 0 && F > 0 && k >= 1 && k <= decode::KMAX,
+                   "moe_layer_decode_q2_static: D=%d F=%d k=%d", D, F, k);
+  const size_t need = q2_workspace_bytes(D, F, k);
+  if (need > STATIC_SCRATCH_BYTES)
+    return fail(CACHALOT_ESPACE,
+                "moe_layer_decode_q2_static: D=%d F=%d k=%d needs %zu bytes of scratch, the static array holds %zu "
+                "(use cachalot_moe_layer_decode_q2 with a workspace)",
+                D, F, k, need, STATIC_SCRATCH_BYTES);
+  uint8_t* ws = nullptr;
+  const int rc = static_scratch(&ws, (hipStream_t)stream);
+  if (rc) return rc;
+  return cachalot_moe_layer_decode_q2(x, gate_weight, gate_bias, E, k, score_fn, gate_temp, route_scale, norm, order,
+                                      pool, layout, slot_table, D, F, group, swiglu_limit, addend, idx_out, w_out,
+                                      scores, routed, out, ws, STATIC_SCRATCH_BYTES, stream);
 }

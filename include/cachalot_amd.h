@@ -135,6 +135,23 @@ int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* gate_weight,
                                  const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
                                  float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
                                  cachalot_stream_t stream);
+/* cachalot_moe_layer_decode_q2_static: cachalot_moe_layer_decode_q2 with the
+ * same arguments minus the workspace, which allocates nothing.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its scratch is a file-scope device array of
+ * cachalot_moe_layer_decode_q2_static_max_bytes() bytes (256 KiB) that each GPU
+ * holds until the process ends; shapes whose workspace
+ * (cachalot_moe_decode_q2_workspace_bytes) exceeds it return CACHALOT_ESPACE.
+ * All calls on one GPU share that array: calls that overlap on one GPU race. */
+size_t cachalot_moe_layer_decode_q2_static_max_bytes(void);
+int cachalot_moe_layer_decode_q2_static(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                        int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                        int order, const uint8_t* pool,
+                                        const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                        int D, int F, int group, float swiglu_limit, const uint16_t* addend,
+                                        int32_t* idx_out, float* w_out, float* scores, float* routed, uint16_t* out,
+                                        cachalot_stream_t stream);
 int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
                                   int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
                                   int order, const uint8_t* pool, const cachalot_expert_layout* layout /* host */,
