@@ -34,16 +34,19 @@ METRIC = "MoE-layer decode tok/s + expert-byte HBM GB/s (B=1); prefill grouped-G
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=2560,
+                    help="chained decode steps timed for the headline (one step = one token through one layer)")
+    ap.add_argument("--warmup", type=int, default=320, help="untimed chained decode steps before the timed ones")
     ap.add_argument("--layers", type=int, default=40,
                     help="resident 2-bit layers the decode chain rotates through (40 = BASELINE config 4's stack)")
     ap.add_argument("--no-extra", action="store_true", help="skip the config 2 / config 3 measurements")
     ap.add_argument("--seed", type=int, default=20260917)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget for the CPU-baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget for the CPU-baseline samples")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager-only", action="store_true",
                     help="profiling aid: run --steps eager chained steps (no graphs, no JSON) and exit")
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -53,55 +56,201 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(seed: int, budget_s: float):
-    """oracle (NumPy) 2-bit decode of whole token-layers on the host: dequant + matvec per expert."""
-    import numpy as np
-
-    from cachalot_amd.storage.index import affine_format
-    from oracle import experts as oexperts
-    from oracle import router as orouter
-    from oracle import synth as osynth
-    from oracle.affine2 import qmv64
-    from oracle.bf16 import bf16_bits_to_f32
-
+def _blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        return max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:  # noqa: BLE001
-        threads = os.cpu_count() or 1
-    fmt = affine_format(4096, 2880)
-    specs = osynth.q2_tensor_specs(4096, 2880)
-    done, t_total = 0, 0.0
-    while t_total < budget_s and done < 64:
-        layer = done % 16
-        w_bits, bias = osynth.router_tensors(seed, layer, 384, 4096)
-        x_bits = osynth.activations(seed, 1000 + done, 1, 4096)
-        # expert bytes are generated outside the timed region (they are "resident")
-        xf = bf16_bits_to_f32(x_bits)
-        idx, wts, _ = orouter.route(xf, bf16_bits_to_f32(w_bits), bias, topk=6, route_scale=1.0,
-                                    score=orouter.SCORE_SIGMOID)
-        tens = [osynth.expert_tensors(seed, layer, int(e), specs) for e in idx[0]]
-        t0 = time.perf_counter()
-        idx, wts, _ = orouter.route(xf, bf16_bits_to_f32(w_bits), bias, topk=6, route_scale=1.0,
-                                    score=orouter.SCORE_SIGMOID)
-        mats = []
-        for t in tens:
-            def mm(p, k, t=t):
-                return lambda v: qmv64(v, t[f"{p}.weight"], t[f"{p}.scales"], t[f"{p}.biases"], k=k, group=128)
-            mats.append((mm("w1", 4096), mm("w3", 4096), mm("w2", 2880)))
-        oexperts.affine_decode(xf[0], mats, wts[0], 10.0, xf[0])
-        t_total += time.perf_counter() - t0
-        done += 1
-    per = t_total / max(done, 1)
+        return 1
+
+
+def _cpu_swiglu_f32(x, w1, w3, w2, wts, bf16_points: bool):
+    """The reference's CPU arithmetic in float32: dense float32 weights (NumPy dequant, ``model/fp4.py:67-109``),
+    float32 BLAS products, the bf16 rounding points of ``expert_affine.py:65-81`` when ``bf16_points``."""
+    import numpy as np
+
+    from oracle.bf16 import round_bf16
+
+    g = x @ w1.T
+    u = x @ w3.T
+    if bf16_points:
+        g, u = round_bf16(g), round_bf16(u)
+    u = np.clip(u, -10.0, 10.0)
+    g = np.minimum(g, 10.0)
+    with np.errstate(over="ignore"):
+        h = (g / (1.0 + np.exp(-g)) * u * wts[:, None]).astype(np.float32)
+    if bf16_points:
+        h = round_bf16(h)
+    y = h @ w2.T
+    return round_bf16(y) if bf16_points else y
+
+
+_LUT_Q2 = None
+_LUT_FP4 = None
+
+
+def _deq_q2_f32(w, scales_bits, biases_bits, k: int, group: int = 128):
+    """2-bit affine [N, K/16] u32 -> [N, k] float32, s * q + b per group (one byte -> four codes table)."""
+    import numpy as np
+
+    from oracle.bf16 import bf16_bits_to_f32
+
+    global _LUT_Q2
+    if _LUT_Q2 is None:
+        _LUT_Q2 = np.array([[(b >> (2 * i)) & 3 for i in range(4)] for b in range(256)], np.float32)
+    n = w.shape[0]
+    q = _LUT_Q2[np.ascontiguousarray(w).view(np.uint8)].reshape(n, -1, group)
+    out = q * bf16_bits_to_f32(scales_bits)[:, :, None]
+    out += bf16_bits_to_f32(biases_bits)[:, :, None]
+    return out.reshape(n, -1)[:, :k]
+
+
+def _deq_fp4_f32(packed, scales, block: int = 32):
+    """FP4 E2M1 [N, K/2] u8 + E8M0 [N, K/32] -> [N, K] float32 (one byte -> two values table)."""
+    import numpy as np
+
+    from oracle.fp4 import FP4_E2M1_TABLE
+
+    global _LUT_FP4
+    if _LUT_FP4 is None:
+        idx = np.arange(256)
+        _LUT_FP4 = np.stack([FP4_E2M1_TABLE[idx & 15], FP4_E2M1_TABLE[idx >> 4]], 1).astype(np.float32)
+    n = packed.shape[0]
+    q = _LUT_FP4[packed].reshape(n, -1, block)
+    e = np.ldexp(np.float32(1.0), np.asarray(scales, np.int32) - 127).astype(np.float32)
+    return (q * e[:, :, None]).reshape(n, -1)
+
+
+def _cpu_dense(t, kind, D, F):
+    if kind == "fp4":
+        return tuple(_deq_fp4_f32(t[f"{p}.weight"], t[f"{p}.scale"]) for p in ("w1", "w3", "w2"))
+    return tuple(_deq_q2_f32(t[f"{p}.weight"], t[f"{p}.scales"], t[f"{p}.biases"], k) for p, k in
+                 (("w1", D), ("w3", D), ("w2", F)))
+
+
+def _cpu_route(x, w_bits, bias, k=6):
+    """float32 router as a NumPy caller writes it: logits = x W^T, sigmoid, top-k of score + bias, normalise."""
+    import numpy as np
+
+    from oracle.bf16 import bf16_bits_to_f32
+
+    logits = x @ bf16_bits_to_f32(w_bits).T
+    scores = 1.0 / (1.0 + np.exp(-logits))
+    idx = np.argsort(scores + bias, axis=-1, kind="stable")[:, -k:]
+    w = np.take_along_axis(scores, idx, axis=-1)
+    return idx, (w / (w.sum(-1, keepdims=True) + 1e-20)).astype(np.float32)
+
+
+def cpu_baseline(seed: int, budget_s: float, log_fn, prefill_counts=None):
+    """The reference's CPU path restated in NumPy float32 (oracle/ dequant + BLAS), timed on the host on a
+    bounded sample of each workload: config 1 (the headline's unit), config 0, config 2 (B = 4) and config 3
+    (extrapolated from sampled experts).  Expert bytes are generated outside the timed regions ("resident")."""
+    import numpy as np
+
+    from cachalot_amd.storage.index import affine_format, fp4_format
+    from oracle import synth as osynth
+    from oracle.bf16 import bf16_bits_to_f32
+
+    from concurrent.futures import ThreadPoolExecutor
+
+    D, F, E, K = 4096, 2880, 384, 6
+    workers = min(16, os.cpu_count() or 1)
+    pool = ThreadPoolExecutor(max_workers=workers)     # experts in parallel (NumPy releases the GIL in its loops)
+    threads = max(workers, _blas_threads())
+    q2 = osynth.q2_tensor_specs(D, F)
+    f4 = osynth.fp4_tensor_specs(D, F)
+
+    def token_layers(kind, specs, budget, stream0):
+        done, t_total = 0, 0.0
+        while t_total < budget and done < 64:
+            layer = done % 16
+            w_bits, bias = osynth.router_tensors(seed, layer, E, D)
+            x = bf16_bits_to_f32(osynth.activations(seed, stream0 + done, 1, D))
+            idx, _ = _cpu_route(x, w_bits, bias)
+            tens = [osynth.expert_tensors(seed, layer, int(e), specs) for e in idx[0]]
+            t0 = time.perf_counter()
+            idx, wts = _cpu_route(x, w_bits, bias)
+            ys = list(pool.map(lambda j: _cpu_swiglu_f32(x, *_cpu_dense(tens[j], kind, D, F), wts[0, j:j + 1],
+                                                         kind == "affine")[0], range(K)))
+            out = np.float32(0.0) + ys[0]
+            for y in ys[1:]:
+                out = out + y
+            t_total += time.perf_counter() - t0
+            done += 1
+        return done, t_total
+
+    res = {}
+    n1, t1 = token_layers("affine", q2, budget_s * 0.4, 1000)
+    per1 = t1 / max(n1, 1)
+    fmt1 = affine_format(D, F)
+    log_fn(f"cpu config 1: {per1 * 1e3:.0f} ms per token-layer ({n1} sampled)")
+    n0, t0_ = token_layers("fp4", f4, budget_s * 0.2, 3000)
+    per0 = t0_ / max(n0, 1)
+    res["config0"] = {"ms_per_token_layer": round(per0 * 1e3, 1), "sample": f"{n0} token-layers",
+                      "expert_GBps": round(K * fp4_format(D, F).algorithmic_bytes / per0 / 1e9, 4)}
+    log_fn(f"cpu config 0: {per0 * 1e3:.0f} ms per token-layer ({n0} sampled)")
+    # config 2, B = 4: one step over the union of the four tokens' experts
+    B = 4
+    w_bits, bias = osynth.router_tensors(seed, 0, E, D)
+    x = bf16_bits_to_f32(osynth.activations(seed, 5000, B, D))
+    idx, wts = _cpu_route(x, w_bits, bias)
+    uni = sorted(set(idx.reshape(-1).tolist()))
+    tens = {e: osynth.expert_tensors(seed, 0, e, q2) for e in uni}
+    t0 = time.perf_counter()
+    idx, wts = _cpu_route(x, w_bits, bias)
+    y = np.zeros((B, K, D), np.float32)
+
+    def one(e):
+        rows = np.argwhere(idx == e)
+        y[rows[:, 0], rows[:, 1]] = _cpu_swiglu_f32(x[rows[:, 0]], *_cpu_dense(tens[e], "affine", D, F),
+                                                    wts[rows[:, 0], rows[:, 1]], True)
+
+    list(pool.map(one, uni))
+    out = np.float32(0.0) + y[:, 0]
+    for j in range(1, K):
+        out = out + y[:, j]
+    t2 = time.perf_counter() - t0
+    res["config2_B4"] = {"ms_per_step": round(t2 * 1e3, 1), "tok_per_s": round(B / t2, 2), "union_experts": len(uni),
+                         "sample": "one step"}
+    log_fn(f"cpu config 2 B=4: {t2 * 1e3:.0f} ms per step ({len(uni)} experts)")
+    # config 3: three experts of different loads timed with their rows; time per expert fitted as
+    # a + b * rows and summed over the GPU run's expert loads
+    if prefill_counts is not None:
+        counts = np.asarray(prefill_counts)
+        order = np.argsort(counts)
+        picks = [int(order[len(order) // 2]), int(order[-2]), int(order[-1])]
+        pts = []
+        for e in picks:
+            rows = int(counts[e])
+            t = osynth.expert_tensors(seed + 3, 0, e, f4)
+            xr = bf16_bits_to_f32(osynth.activations(seed, 7000 + e, rows, D))
+            wr = np.full(rows, 1.0 / K, np.float32)
+            t0 = time.perf_counter()
+            dense = _cpu_dense(t, "fp4", D, F)
+            _cpu_swiglu_f32(xr, *dense, wr, True)
+            pts.append((rows, time.perf_counter() - t0))
+        r_ = np.array([p[0] for p in pts], np.float64)
+        t_ = np.array([p[1] for p in pts], np.float64)
+        b_, a_ = np.polyfit(r_, t_, 1)
+        total = float(np.sum(a_ + b_ * counts[counts > 0]))
+        flops = 2.0 * 4096 * K * 3 * D * F
+        res["config3"] = {"ms_per_layer": round(total * 1e3, 1), "tflops": round(flops / total / 1e12, 4),
+                          "sample": f"experts with {r_.astype(int).tolist()} rows timed "
+                                    f"({', '.join(f'{v:.2f}' for v in t_)} s), extrapolated to all "
+                                    f"{int((counts > 0).sum())} touched experts as a + b * rows"}
+        log_fn(f"cpu config 3: {total * 1e3:.0f} ms per layer (extrapolated)")
+    pool.shutdown()
     return {
-        "value": round(1.0 / per, 4),
+        "value": round(1.0 / per1, 4),
         "unit": "tok/s (token-layers)",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{done} token-layers of config 1 (router + 6 experts dequant+matvec, NumPy float64, "
-                  f"oracle/), {t_total:.1f} s; host has {os.cpu_count()} CPUs",
-        "ms_per_token_layer": round(per * 1e3, 2),
-        "expert_GBps": round(6 * fmt.algorithmic_bytes / per / 1e9, 4),
+        "sample": f"{n1} token-layers of config 1 (router + 6 experts: float32 table dequant, float32 BLAS "
+                  f"products, bf16 rounding points; NumPy), {t1:.1f} s; the 6 experts on {workers} threads, BLAS "
+                  f"threads {_blas_threads()}; host has {os.cpu_count()} CPUs",
+        "ms_per_token_layer": round(per1 * 1e3, 2),
+        "expert_GBps": round(K * fmt1.algorithmic_bytes / per1 / 1e9, 4),
+        "other_configs": res,
     }
 
 
@@ -253,10 +402,19 @@ def prefill_config3(args, dev, log_fn):
     flops = 2.0 * T * K * 3 * D * F
     tflops = flops / (ms * 1e-3) / 1e12
     wbytes = touched * fmt.algorithmic_bytes
+    # HBM floor: every touched expert's weights once, x read once, out written once
+    floor_bytes = wbytes + 2 * T * D * 2
+    floor_ms = floor_bytes / (HBM_PEAK_GBPS * 1e9) * 1e3
     res = {"ms_per_layer": round(ms, 3), "tflops": round(tflops, 1),
            "frac_bf16_mfma_peak": round(tflops / 2500.0, 4), "frac_mxfp4_mfma_peak": round(tflops / 10100.0, 4),
            "experts_touched": touched, "max_rows_per_expert": int(counts.max()),
            "weight_GBps": round(wbytes / (ms * 1e-3) / 1e9, 1),
+           "roofline": {"bound": "hbm", "floor_bytes": int(floor_bytes), "floor_ms": round(floor_ms, 4),
+                        "frac_attainable": round(floor_ms / ms, 4), "achieved_TFLOPs": round(tflops, 1),
+                        "frac_mxfp4_peak": round(tflops / 10100.0, 4), "frac_bf16_peak": round(tflops / 2500.0, 4),
+                        "note": "1.739 TFLOP over >= the touched experts' FP4 bytes: 256 FLOP/B, below the MXFP4 "
+                                "ridge (1,250 FLOP/B), so the attainable bound is HBM"},
+           "_counts": counts.cpu().tolist(),
            "note": "exact bf16-MFMA path (FP4 dequantised to bf16 in registers), routing + permute + "
                    "grouped gate/up + down + combine, eager launches"}
     log_fn(f"config 3 prefill: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s, {touched} experts touched, "
@@ -426,6 +584,52 @@ def layer_with_shared(args, store, gates, log_fn):
     return out
 
 
+def stream_ceiling(dev) -> dict:
+    """Plain streaming reads (cachalot_stream_read) of 24, 60 and 288 MB, each from 8 rotating buffers
+    (the 256 MB MALL holds none of them between reads): the HBM read ceiling at the decode's sizes."""
+    import torch
+
+    from cachalot_amd import _lib
+
+    L = _lib.lib()
+    out = {}
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle(dev)
+    for mb in (24, 60, 288):
+        nbytes = mb * 1000 * 1000 // 16 * 16
+        bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(8 if mb < 288 else 2)]
+        best = None
+        for blocks in (1024, 2048, 4096, 8192):
+            for b in bufs:
+                _lib.check(L.cachalot_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), blocks, stream))
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                st = _lib.stream_handle(dev)
+                for _ in range(4):
+                    for b in bufs:
+                        _lib.check(L.cachalot_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), blocks, st))
+            g.replay()
+            torch.cuda.synchronize()
+            a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(4):
+                g.replay()
+            e.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(e) * 1e3 / (16 * len(bufs))
+            if best is None or us < best[0]:
+                best = (us, blocks)
+            del g
+        us, blocks = best
+        out[f"{mb}MB"] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "workgroups": blocks}
+        del bufs
+    torch.cuda.empty_cache()
+    out["note"] = ("stream_read_kernel: the best of 1024-8192 workgroups x 256 threads, 16-byte loads, back-to-back "
+                   "launches in a graph (launch gaps included, as in the decode), 8 (2 at 288 MB) rotating buffers")
+    return out
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -433,6 +637,10 @@ def main() -> int:
               "multi-GPU expert parallelism is a design note only.", file=sys.stderr)
         return 2
     import torch
+
+    if args.stream_ceiling:
+        print(json.dumps(stream_ceiling(torch.device("cuda:0"))), flush=True)
+        return 0
 
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0").fill_(1)
@@ -481,39 +689,56 @@ def main() -> int:
         log(f"{args.steps} eager steps done")
         return 0
 
-    # The chain is captured in a HIP graph of G steps (G a multiple of L) and
-    # replayed, so host launch overhead stays out of the GPU timeline.
-    G = L * max(1, 64 // L)
+    # The chain is captured in HIP graphs of G steps and replayed, so host launch
+    # overhead stays out of the GPU timeline; a second graph covers the remainder,
+    # so exactly --warmup and --steps steps run.  Step s of a graph visits layer
+    # s mod L: a layer's experts come back only after min(G, L) other layers'.
+    K_steps, W_steps = max(1, args.steps), max(0, args.warmup)
+    G = min(K_steps, 8 * L)
     xbuf = x0.clone()
     warm = xbuf
-    for s in range(G):                       # eager warm-up (and allocator priming)
+    for s in range(L):                       # allocator priming: one eager step per layer (untimed)
         warm = step(warm, s)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        xg = xbuf
-        for s in range(G):
-            xg = step(xg, s)
-        xbuf.copy_(xg)
-    replays_w = max(1, args.warmup // G)
-    replays = max(1, args.steps // G)
-    steps = replays * G
+    graphs = {}
+
+    def graph_of(n):
+        if n not in graphs:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                xg = xbuf
+                for s in range(n):
+                    xg = step(xg, s)
+                xbuf.copy_(xg)
+            graphs[n] = g
+        return graphs[n]
+
+    def run_steps(n):
+        for _ in range(n // G):
+            graph_of(G).replay()
+        if n % G:
+            graph_of(n % G).replay()
+
+    graph_of(G)
+    if K_steps % G:
+        graph_of(K_steps % G)
+    if W_steps % G:
+        graph_of(W_steps % G)
     xbuf.copy_(x0)
-    for _ in range(replays_w):
-        graph.replay()
+    run_steps(W_steps)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     xbuf.copy_(x0)
+    torch.cuda.synchronize()
     t_wall = time.perf_counter()
     start.record()
-    for _ in range(replays):
-        graph.replay()
+    run_steps(K_steps)
     end.record()
     torch.cuda.synchronize()
     t_wall = time.perf_counter() - t_wall
     ms = start.elapsed_time(end)
-    ms_per_step = ms / steps
-    log(f"chained steps: {ms_per_step * 1e3:.2f} us/step (wall {t_wall / steps * 1e6:.2f} us/step)")
+    ms_per_step = ms / K_steps
+    log(f"chained steps: {K_steps} timed, {ms_per_step * 1e3:.2f} us/step (wall {t_wall / K_steps * 1e6:.2f} us/step)")
     if not torch.isfinite(xbuf.float()).all():
         raise RuntimeError("non-finite activations after the chained run")
     # the graph replays must equal eager execution of the same chain
@@ -521,10 +746,31 @@ def main() -> int:
     for s in range(G):
         eager = step(eager, s)
     xbuf.copy_(x0)
-    graph.replay()
+    graph_of(G).replay()
     torch.cuda.synchronize()
     if not torch.equal(eager, xbuf):
         raise RuntimeError("graph replay differs from eager execution")
+
+    # ---- config 4: 512 tokens through the whole resident stack (512 x L chained layer-steps)
+    tokens4 = 512
+    G4 = 8 * L
+    xbuf.copy_(x0)
+    torch.cuda.synchronize()
+    s4, e4 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s4.record()
+    for _ in range(tokens4 * L // G4):
+        graph_of(G4).replay()
+    e4.record()
+    torch.cuda.synchronize()
+    ms4 = s4.elapsed_time(e4)
+    tok_bytes = L * (K * fmt.algorithmic_bytes + E * D * 2 + E * 4)
+    stack = {"tokens": tokens4, "layers": L, "layer_steps": tokens4 * L, "ms_total": round(ms4, 3),
+             "ms_per_token": round(ms4 / tokens4, 4), "tok_per_s": round(tokens4 / (ms4 * 1e-3), 1),
+             "us_per_layer_step": round(ms4 * 1e3 / (tokens4 * L), 3),
+             "hbm_frac": round(tok_bytes / (ms4 / tokens4 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+             "note": f"one token = {L} chained layer steps (router + 6 of 384 2-bit experts + residual add each); "
+                     f"{tokens4} tokens as {tokens4 * L // G4} replays of a {G4}-step graph"}
+    log(f"config 4: {tokens4} tokens x {L} layers in {ms4:.1f} ms = {stack['tok_per_s']} tok/s")
 
     # ---- expert GEMV kernel pair alone, over precomputed routes (distinct layers per launch)
     n_routes = 256
@@ -534,7 +780,7 @@ def main() -> int:
         w, b = gates[r % L]
         rt = route_topk_fused(xs[r], w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
         routes.append((xs[r], table[r % L], rt.indices, rt.weights))
-    reps = max(1, args.steps // n_routes)
+    reps = 8
     routed_buf = torch.empty(D, dtype=torch.float32, device=dev)
     ws_bytes = _lib.lib().cachalot_moe_decode_q2_workspace_bytes(D, F, K)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
@@ -569,6 +815,7 @@ def main() -> int:
     alg_bytes = K * fmt.algorithmic_bytes
     achieved = alg_bytes / (us_kernel * 1e-6) / 1e9
     log(f"expert kernel pair: {us_kernel:.2f} us/launch, {achieved:.0f} GB/s algorithmic")
+    ceiling = stream_ceiling(dev)
 
     router_bytes = E * D * 2 + E * 4
     step_bytes = alg_bytes + router_bytes
@@ -577,8 +824,8 @@ def main() -> int:
         "value": round(1e3 / ms_per_step, 1),
         "unit": "tok/s (token-layers, B=1)",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": args.warmup,
+        "steps": K_steps,
+        "warmup": W_steps,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -606,20 +853,21 @@ def main() -> int:
             "algorithmic_bytes_per_launch": alg_bytes,
         },
     }
-    result["stack40"] = {"layers": L, "us_per_layer_step": round(ms_per_step * 1e3, 2),
-                         "tok_per_s_full_stack": round(1e3 / (ms_per_step * L), 1),
-                         "note": "the chained decode above walks all resident layers in order: one token through "
-                                 f"the {L}-layer stack = {L} steps"}
+    result["config4_stack"] = stack
+    result["stream_ceiling"] = ceiling
+    result["roofline"]["frac_of_stream_ceiling"] = round(achieved / ceiling["60MB"]["GBps"], 4)
     if not args.no_extra:
         result["config0_fp4_decode"] = fp4_decode_config0(args, dev, log)
         result["config2_batched_decode"] = batched_decode(args, store, gates, log)
         result["config1_layer_with_shared_expert"] = layer_with_shared(args, store, gates, log)
         result["config3_prefill"] = prefill_config3(args, dev, log)
+        prefill_counts = result["config3_prefill"].pop("_counts")
         result["shared_fp8_expert"] = shared_expert_fp8(args, dev, log)
         result["requant_fp4_to_q2"] = requant_bank(args, dev, log)
     if not args.no_cpu:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_seconds, log,
+                                              None if args.no_extra else prefill_counts)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -95,6 +95,7 @@ _SIGNATURES = {
     "cachalot_shared_expert_fp8": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                            c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
     "cachalot_copy_records": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
+    "cachalot_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
     "cachalot_requant_fp4_to_q2": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
     "cachalot_dequant_fp4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "cachalot_dequant_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,

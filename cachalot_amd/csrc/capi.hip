@@ -55,3 +55,43 @@ extern "C" int cachalot_copy_records(uint8_t* pool, int64_t record_bytes, int64_
   if (e != hipSuccess) return fail(CACHALOT_EHIP, "copy_records: %s", hipGetErrorString(e));
   return CACHALOT_OK;
 }
+
+// Measurement aid: a plain streaming read of `bytes` (a multiple of 16) at `src`,
+// 16-byte loads, grid-stride, every lane's XOR of what it read folded into one
+// word per workgroup at sink[blockIdx.x] (so the loads cannot be dropped).  Its
+// time is the HBM read ceiling the expert kernels are judged against.
+namespace {
+__global__ void __launch_bounds__(256) stream_read_kernel(const uint4* __restrict__ src, size_t n16,
+                                                          uint32_t* __restrict__ sink) {
+  uint32_t acc = 0u;
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 a = src[i];
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t v = 0u;
+    for (int t = 0; t < 256; ++t) v ^= red[t];
+    sink[blockIdx.x] = v;
+  }
+}
+}  // namespace
+
+extern "C" int cachalot_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks,
+                                    cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(src && sink, "stream_read: null pointer");
+  CACHALOT_REQUIRE(bytes % 16 == 0 && blocks >= 1 && blocks <= 65536, "stream_read: bytes=%zu blocks=%d", bytes,
+                   blocks);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint4*>(src), bytes / 16, sink);
+  return check_launch("stream_read_kernel");
+}

@@ -253,6 +253,13 @@ int cachalot_shared_expert_fp8(const uint16_t* x, const uint8_t* w1, const uint8
 int cachalot_copy_records(uint8_t* pool, int64_t record_bytes, int64_t offset, int64_t first_slot,
                           const void* src, int64_t tensor_bytes, int64_t n, cachalot_stream_t stream);
 
+/* Measurement aid (no reference counterpart): a plain streaming read of `bytes`
+ * (a multiple of 16) at device address `src` by `blocks` workgroups of 256
+ * threads, 16-byte loads; sink [blocks] u32 receives one XOR per workgroup.
+ * bench.py times it to measure the HBM read ceiling the expert kernels are
+ * judged against. */
+int cachalot_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, cachalot_stream_t stream);
+
 /* FP4 -> 2-bit affine g128 requantization (the searched fit) of one weight
  * matrix: w_fp4 [N, K/2] packed E2M1 + s_fp4 [N, K/32] E8M0 -> q [N, Kp/16] u32
  * codes (16 per word, low field first), scales / biases [N, Kp/128] bf16,

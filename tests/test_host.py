@@ -146,3 +146,21 @@ def test_get_many_loads_a_repeated_key_once():
     budget = store.get_many([ExpertEntry(0, 1), ExpertEntry(0, 1), ExpertEntry(0, 3)], max_misses=1)
     assert budget[0] is not None and budget[1].slot is budget[0].slot
     assert budget[2] is None
+
+
+def test_bench_cpu_dequant_equals_oracle():
+    """The CPU baseline's table-driven dequant gives the oracle's values exactly."""
+    import bench
+    from cachalot_amd.storage.index import affine_format, fp4_format  # noqa: F401
+    from oracle import synth as osynth
+    from oracle.affine2 import dequantize_affine
+    from oracle.fp4 import dequantize_fp4_weight
+
+    t = osynth.expert_tensors(3, 0, 5, osynth.q2_tensor_specs(512, 320))
+    for p, k in (("w1", 512), ("w2", 320)):
+        got = bench._deq_q2_f32(t[f"{p}.weight"], t[f"{p}.scales"], t[f"{p}.biases"], k)
+        want = dequantize_affine(t[f"{p}.weight"], t[f"{p}.scales"], t[f"{p}.biases"], k=k, group=128)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), p
+    t = osynth.expert_tensors(3, 0, 5, osynth.fp4_tensor_specs(512, 320))
+    got = bench._deq_fp4_f32(t["w2.weight"], t["w2.scale"])
+    assert np.array_equal(got, dequantize_fp4_weight(t["w2.weight"], t["w2.scale"]))
