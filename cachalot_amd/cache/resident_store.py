@@ -64,6 +64,13 @@ class ResidentExpertStore:
         self._table = np.full((n_layers, n_experts), -1, np.int32)
         self._table_dev: torch.Tensor | None = None
         self.slot_table_version = 0
+        # opt-in partial-residency approximations read by moe_layer_forward
+        # (resident_store.py:272-276 of the reference; None = exact inference)
+        self.decode_miss_budget: int | None = None
+        self.decode_substitute_tau: float | None = None
+        self.decode_substitute_ranks = 4
+        self.substituted_experts = 0
+        self.skipped_experts = 0
 
     # ----------------------------------------------------------- slot table
     def track_slots(self, n_layers: int | None = None, n_experts: int | None = None) -> torch.Tensor:
@@ -151,6 +158,8 @@ class ResidentExpertStore:
             if priorities is not None:
                 misses.sort(key=lambda i: -priorities[i])
             budget = len(misses) if max_misses is None else max(0, int(max_misses))
+            unique_misses = len({keys[i] for i in misses})
+            self.skipped_experts += max(0, unique_misses - budget)
             protect = set(keys)
             loaded = 0
             for i in misses:

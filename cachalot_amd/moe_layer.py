@@ -11,7 +11,15 @@ resident in HBM and the store's (layer, expert) -> slot table lives on the
 device, so the router's ids go straight into the expert kernels: three
 launches (router scores; top-k + slot lookup + gate/up; down + route-order
 combine), no host synchronisation.  When a layer is not fully resident the host path is taken:
-one synchronisation, ``get_many`` (which loads misses), then the same kernels.
+one synchronisation, ``get_many`` (which loads misses), then the same kernels, with the
+store's opt-in approximations (``decode_substitute_tau`` router-share substitution and
+``decode_miss_budget`` drop-and-rescale, ``decode_substitution``).
+
+``fused`` is accepted for call-site compatibility and changes nothing: in the
+reference it picks between the two-launch FP4 kernel and a per-expert
+``fp4_gemv`` loop (``moe_layer_metal.py:165-166,348-376``), which share their
+rounding points (fp32 outputs throughout, ``fp4_gemv_metal.py:102-103``), and
+it is not consulted for affine banks; this build has the one device path.
 
 The FP8 shared expert (``shared_*``, ``moe_layer_metal.py:381-397``) runs
 first, on the same stream, and its bf16 output is added in the combine:
@@ -72,18 +80,45 @@ def moe_layer_forward(
     router = route_topk_fused if norm_topk_prob else route_topk
     route = router(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp, route_scale=route_scale,
                    norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order)
+    idx, weights = route.indices, route.weights
     if not expert_store.layer_fully_resident(layer_id):
         # host-addressed path: one sync for the ids, then load what is missing
-        ids = route.indices.tolist()
+        # (moe_layer_metal.py:220-310), with the store's opt-in approximations
+        ids = [int(e) for e in route.indices.tolist()]
+        wts = route.weights.tolist()
+        tau = getattr(expert_store, "decode_substitute_tau", None)
+        if tau is not None:
+            from .decode_substitution import plan_substitution, ranked_candidates
+
+            selection = route.scores.float().cpu().numpy() + gate_bias.float().cpu().numpy()
+            ids, replaced = plan_substitution(
+                ids, wts, ranked_candidates(selection, ids, getattr(expert_store, "decode_substitute_ranks", 4)),
+                lambda e: expert_store.is_cached((layer_id, e)), tau)
+            expert_store.substituted_experts += replaced
         entries = []
         for e in ids:
-            key = (layer_id, int(e))
+            key = (layer_id, e)
             entry = expert_index.get(key) if expert_index is not None else ExpertEntry(*key)
             if entry is None:
                 raise KeyError(f"Missing routed expert layer={layer_id}, expert={e}")
             entries.append(entry)
-        expert_store.get_many(entries, priorities=route.weights.tolist())
+        budget = getattr(expert_store, "decode_miss_budget", None)
+        got = expert_store.get_many(entries, max_misses=budget, priorities=wts)
+        if budget is not None and any(g is None for g in got):
+            # dropped experts; the kept weights carry the layer's routing mass
+            from .decode_substitution import rescale_kept
+
+            kept = [i for i, g in enumerate(got) if g is not None]
+            wts = rescale_kept(wts, kept)
+            ids = [ids[i] for i in kept]
+        if not ids:
+            out = torch.zeros_like(x, dtype=torch.float32)
+            if addend is not None:
+                out = out + addend.float()
+            return out.to(x.dtype), route
+        idx = torch.tensor(ids, dtype=torch.int32, device=x.device)
+        weights = torch.tensor(wts, dtype=torch.float32, device=x.device)
     table = expert_store.layer_table(layer_id)
-    _, out = decode_experts(x, pool, table, route.indices, route.weights, swiglu_limit=swiglu_limit,
-                            addend=addend, want_routed=False, want_out=True)
+    _, out = decode_experts(x, pool, table, idx, weights, swiglu_limit=swiglu_limit, addend=addend,
+                            want_routed=False, want_out=True)
     return out.to(x.dtype), route

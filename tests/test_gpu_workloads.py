@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (SEED, bf16_ulp_dist, fp4_dense, make_store, oracle_tensors, q2_mats, report, route_order_sum,
+from helpers import (SEED, bf16_ulp, bf16_ulp_dist, fp4_dense, make_store, oracle_tensors, q2_mats, report, route_order_sum,
                      term_flips)
 from oracle import dispatch as odispatch
 from oracle import experts as oexperts
@@ -294,3 +294,76 @@ def test_config3_prefill_workload(cuda):
     _grouped_check("config3 prefill fp4", fmt, 0, xf, oi, ow, _np(routed), _f32(out), yf, E, rows_of=rows_of)
     report("config3 prefill fp4", rows_per_heavy_expert=counts[heavy].tolist(), max_rows=int(counts.max()),
            experts_touched=int((counts > 0).sum()))
+
+
+# ------------------------------------------------------- partial residency ---
+def _partial_layer(cuda, resident_of):
+    """A 2-bit layer whose store holds only some experts (loader for misses), its router,
+    one token, and the router's own ids / weights / scores."""
+    from cachalot_amd import synth
+    from cachalot_amd.router import route_topk_fused
+    from cachalot_amd.storage.index import affine_format
+
+    fmt = affine_format(4096, 2880)
+    w, b = synth.router_weights(SEED, 0, 384, 4096, cuda)
+    x = synth.activations(SEED, 808, 1, 4096, cuda)[0]
+    r = route_topk_fused(x, w, b, topk=6, route_scale=1.0, score_fn="sigmoid")
+    ids, wts, scores = [int(e) for e in r.indices.tolist()], r.weights.tolist(), _np(r.scores)
+    keys = [(0, e) for e in resident_of(ids, scores + _np(b))]
+    store = make_store(fmt, n_layers=1, n_experts=384, keys=keys, n_slots=16, loader=True)
+    return fmt, store, x, w, b, ids, wts
+
+
+def _layer_out(x, w, b, store):
+    from cachalot_amd.moe_layer import moe_layer_forward
+
+    out, route = moe_layer_forward(x, layer_id=0, gate_weight=w, gate_bias=b, expert_index=None, expert_store=store,
+                                   topk=6, route_scale=1.0, score_fn="sigmoid")
+    return _f32(out), route
+
+
+def _oracle_out(fmt, x, ids, wts):
+    _, want_out, ys = oexperts.affine_decode(_f32(x), [q2_mats(fmt, oracle_tensors(fmt, 0, e)) for e in ids],
+                                             np.asarray(wts, np.float32), 10.0, terms=True)
+    return want_out, ys
+
+
+def test_decode_miss_budget_drops_and_rescales(cuda):
+    """decode_miss_budget = 2 with two of six routed experts resident: the two strongest
+    misses load, the other two are dropped and the kept weights rescaled to the
+    layer's routing mass (moe_layer_metal.py:286-310)."""
+    from cachalot_amd.decode_substitution import rescale_kept
+
+    fmt, store, x, w, b, ids, wts = _partial_layer(cuda, lambda ids, sel: ids[:2])
+    store.decode_miss_budget = 2
+    got, route = _layer_out(x, w, b, store)
+    assert [int(e) for e in route.indices.tolist()] == ids
+    miss = sorted(range(2, 6), key=lambda i: -wts[i])[:2]
+    kept = sorted([0, 1] + miss)
+    want, ys = _oracle_out(fmt, x, [ids[i] for i in kept], rescale_kept(wts, kept))
+    assert store.skipped_experts == 2 and store.stats.misses == 2
+    ulps = bf16_ulp_dist(got, want)
+    report("miss budget", kept=len(kept), out_ulps_max=int(ulps.max()), out_ulps_nonzero=int((ulps > 0).sum()))
+    assert np.all(np.abs(got - want) <= 2e-3 * np.abs(want).max() + np.sum(bf16_ulp(ys), 0) + bf16_ulp(want))
+
+
+def test_decode_substitution_replaces_weak_misses(cuda):
+    """decode_substitute_tau: weak non-resident routed experts are replaced by the best
+    resident experts ranked just below the top-6 (decode_substitution.py)."""
+    from cachalot_amd.decode_substitution import plan_substitution, ranked_candidates
+
+    def resident(ids, sel):
+        cand = ranked_candidates(sel, ids, 4)
+        return [ids[0], ids[3], cand[0], cand[2]]
+
+    fmt, store, x, w, b, ids, wts = _partial_layer(cuda, resident)
+    store.decode_substitute_tau = 0.5
+    sel = _np(__import__("cachalot_amd.router", fromlist=["x"]).route_topk_fused(
+        x, w, b, topk=6, route_scale=1.0, score_fn="sigmoid").scores) + _np(b)
+    want_ids, n = plan_substitution(ids, wts, ranked_candidates(sel, ids, 4),
+                                    lambda e: store.is_cached((0, e)), 0.5)
+    got, _ = _layer_out(x, w, b, store)
+    assert n >= 1 and store.substituted_experts == n
+    want, ys = _oracle_out(fmt, x, want_ids, wts)
+    report("substitution", replaced=n, ids=want_ids)
+    assert np.all(np.abs(got - want) <= 2e-3 * np.abs(want).max() + np.sum(bf16_ulp(ys), 0) + bf16_ulp(want))

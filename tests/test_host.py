@@ -164,3 +164,27 @@ def test_bench_cpu_dequant_equals_oracle():
     t = osynth.expert_tensors(3, 0, 5, osynth.fp4_tensor_specs(512, 320))
     got = bench._deq_fp4_f32(t["w2.weight"], t["w2.scale"])
     assert np.array_equal(got, dequantize_fp4_weight(t["w2.weight"], t["w2.scale"]))
+
+
+def test_substitution_plan_follows_the_reference_rule():
+    """Weakest non-resident experts under tau * total are replaced first, each by the best
+    unused resident candidate; strong or resident experts stay; weights stay aligned."""
+    from cachalot_amd.decode_substitution import plan_substitution, ranked_candidates, rescale_kept
+
+    sel = np.array([0.9, 0.1, 0.8, 0.7, 0.2, 0.6, 0.5, 0.3], np.float32)
+    assert ranked_candidates(sel, [0, 2, 3], 3) == [5, 6, 7]
+    assert ranked_candidates(sel, [0, 2, 3], 0) == []
+    tie = np.array([0.5, 0.5, 0.5, 0.1], np.float32)
+    assert ranked_candidates(tie, [1], 2) == [0, 2]               # ties: lower id first
+    resident = {0, 5, 7}
+    ids, n = plan_substitution([0, 2, 3], [0.6, 0.1, 0.3], [5, 6, 7], lambda e: e in resident, tau=0.35)
+    # expert 2 (share 0.1) is replaced by 5 (best resident); expert 3 (0.3 < 0.35) by 7; 0 is resident
+    assert ids == [0, 5, 7] and n == 2
+    ids, n = plan_substitution([0, 2, 3], [0.6, 0.1, 0.3], [5, 6, 7], lambda e: e in resident, tau=0.2)
+    assert ids == [0, 5, 3] and n == 1                           # 3 holds 0.3 of the mass >= 0.2
+    ids, n = plan_substitution([0, 2, 3], [0.6, 0.1, 0.3], [6], lambda e: e in resident, tau=0.5)
+    assert ids == [0, 2, 3] and n == 0                           # no resident candidate
+    ids, n = plan_substitution([1, 2], [0.0, 0.0], [5], lambda e: True, tau=0.5)
+    assert ids == [1, 2] and n == 0                              # no routing mass
+    w = rescale_kept([0.5, 0.25, 0.25], [0, 2])
+    assert np.isclose(sum(w), 1.0) and np.isclose(w[0], 2 / 3) and np.isclose(w[1], 1 / 3)
