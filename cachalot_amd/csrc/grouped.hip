@@ -41,6 +41,14 @@ int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const dec
                         int max_active, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
                         int F, int k, float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s);
 
+// FP4 prefill on the block-scaled matrix cores (prefill_mx.hip)
+size_t prefill_mx_ws_bytes(int T, int k, int D, int F);
+bool prefill_mx_supported(int D, int F, const decode::Layout& L);
+int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
+                      const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
+                      int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
+                      int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s);
+
 namespace {
 
 using namespace decode;
@@ -746,7 +754,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
 // hidden: rows x F bf16, or rows x ceil(F / 128) plane blocks (matrix-core batched decode);
 // x planes: T x D / 128 plane blocks (same).
 struct GroupedWs {
-  size_t tiles_n, tiles, hidden, xplanes, total;
+  size_t tiles_n, tiles, hidden, xplanes, mx, total;
   int max_tiles;
 };
 
@@ -760,7 +768,8 @@ inline GroupedWs grouped_ws(int T, int k, int E, int D, int F) {
   w.hidden = w.tiles + align256(std::max((size_t)w.max_tiles * sizeof(int2), (size_t)std::min(E, rows) * sizeof(int4)));
   const size_t hid = std::max((size_t)rows * F * sizeof(uint16_t), (size_t)rows * ((F + 127) / 128) * 320);
   w.xplanes = w.hidden + align256(hid);
-  w.total = w.xplanes + align256((size_t)T * ((D + 127) / 128) * 320);
+  w.mx = w.xplanes + align256((size_t)T * ((D + 127) / 128) * 320);
+  w.total = w.mx + (k > 0 && D > 0 ? prefill_mx_ws_bytes(T, k, D, F) : 0);
   return w;
 }
 
@@ -789,6 +798,13 @@ int launch_grouped_mt(const GroupedArgs& gu, const GroupedArgs& dn, int max_tile
 // tiles for FP4 prefill, bf16 MFMA for 2-bit batched decode.
 inline bool small_tiles_requested() {
   const char* env = getenv("CACHALOT_GROUPED_SMALL");
+  return env && env[0] == '1';
+}
+
+// FP4 prefill runs on the block-scaled matrix cores (prefill_mx.hip) unless
+// CACHALOT_PREFILL_BF16=1 selects the bf16-MFMA kernels (g2_fp4_kernel).
+inline bool prefill_bf16_requested() {
+  const char* env = getenv("CACHALOT_PREFILL_BF16");
   return env && env[0] == '1';
 }
 
@@ -832,6 +848,14 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
                                ws + wo.hidden, ws + wo.xplanes, y, s);
   }
   const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
+  if (KIND == KIND_FP4 && MT == 64 && prefill_mx_supported(D, F, L) && !small_tiles_requested() &&
+      !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
+    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, 64, tiles, tiles_n, zeros);
+    rc = check_launch("tile_list_kernel");
+    if (rc) return rc;
+    return launch_prefill_mx(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,
+                             row_w, D, F, k, limit, ws + wo.mx, y, s);
+  }
   const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested() &&
                      max_tiles <= (1 << 20);
   hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, large ? G2_MT : MT, tiles, tiles_n,

@@ -1,0 +1,477 @@
+// FP4 prefill (expert-major grouped GEMM) on the gfx950 block-scaled matrix cores.
+//
+// Reference: routed_expert_forward_sgmm / routed_expert_forward_batched
+// (src/cachalot/model/fp4_sgmm_metal.py:257-333, moe_prefill_batched.py:31-61),
+// called per expert from moe_prefill_grouped.py:420-467.  Rounding points:
+// g = bf16(x W1), u = bf16(x W3), h = bf16(silu(min(g, L)) * clip(u, +-L) * w),
+// y = bf16(h W2); the products accumulate in fp32.
+//
+// v_mfma_scale_f32_16x16x128_f8f6f4 multiplies A = fp8 (OCP E4M3) by B = fp4
+// (E2M1), each operand carrying one E8M0 scale per 32-element K block.  The
+// bank's FP4 weights are exactly that B operand: the packed codes go in as they
+// are stored and their E8M0 block scales are the B scales, so no weight is
+// converted.  The activations (x for gate/up, h for down) are bf16 and go in as
+// two fp8 planes per 32-element block: with S = 2^(E - 7), E the exponent of the
+// block's largest magnitude, hi = RNE_e4m3(v / S) and lo = RNE_e4m3(16 (v / S -
+// hi)), scales S and S / 16.  hi + lo / 16 == v / S for every element within
+// 2^13 of the block's largest magnitude (bf16 has 8 significant bits, each plane
+// 4); smaller elements carry an absolute error below 2^-21 of that magnitude.
+// Products of E4M3 and E2M1 values are exact; the instruction accumulates fp32.
+//
+// Layouts (workspace, written by these kernels):
+//   planes  [rows][K_pad / 128][256 B]: per 128-element chunk, hi bytes 0..127
+//           then lo bytes 128..255, element order;
+//   scales  [rows][sb B]: per 32-element block b, bytes 2b (hi) and 2b + 1 (lo),
+//           sb a multiple of 16.
+// x_planes_kernel writes x's planes per token; the gate/up kernel's epilogue
+// writes h's planes per permuted row (columns past F are zero, so K_pad = F
+// rounded up to 128 reads zeros there).
+//
+// Tiling: one 256-thread workgroup = a 64-row M tile of one expert (rows of the
+// expert-major permutation, tile list of grouped.hip) x 16 NF rows per wave of
+// each of NM matrices (gate/up: NM = 2, W1 and W3, NF = 2 -> 128 rows of each;
+// down: NM = 1, NF = 4 -> 256 rows of W2).  K runs in chunks of 128: the A planes
+// of the chunk through a three-stage LDS ring filled by direct-to-LDS loads
+// (16-byte slots XOR-swizzled by row, so the operand reads hit distinct banks),
+// the wave's codes and B scales two chunks ahead in registers.  The tile's A
+// scales sit in LDS for the whole K loop.  Two workgroups fit a CU.  Workgroups
+// go to the XCDs round-robin by launch index; the mapping gives every slice of
+// one tile to one XCD, so the tile's A rows are fetched into that XCD's L2 once.
+#include "decode_common.h"
+#include "mfma_tile.h"
+#include "mx_tile.h"
+
+namespace cachalot {
+namespace {
+
+using namespace decode;
+
+constexpr int P3_THREADS = 256;
+constexpr int P3_WAVES = 4;
+constexpr int P3_MT = 64;                     // token rows per tile
+constexpr int P3_TB = P3_MT / 16;             // token fragments
+constexpr int P3_STAGES = 3;
+constexpr int P3_ROWB = 256;                  // one row's chunk: hi 128 B | lo 128 B
+constexpr int P3_ABYTES = P3_MT * P3_ROWB;    // 16 KiB per stage
+constexpr int P3_ASLOTS = P3_ABYTES / 16 / P3_THREADS;   // 16-byte A slots per lane and chunk (4)
+
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+struct MxArgs {
+  const uint8_t* ap;          // A planes [source rows][kch][256]
+  const uint8_t* as;          // A scales [source rows][sb]
+  int sb;                     // A scale bytes per source row
+  int kch;                    // 128-element chunks along K (K_pad / 128)
+  const int32_t* a_gather;    // source row of a tile row (row_token) or null (the row itself)
+  const uint8_t* pool;
+  Layout L;
+  const int32_t* slot_table;
+  const int32_t* offsets;
+  const int2* tiles;
+  const int32_t* tiles_n;
+  const int32_t* row_token;
+  const int32_t* row_slot;
+  const float* row_w;
+  int K;                      // real K (D or F)
+  int N;                      // weight rows per matrix (F or D)
+  int k;
+  float limit;
+  uint8_t* hp;                // gate/up: h planes [rows][hkch][256]
+  uint8_t* hs;                // gate/up: h scales [rows][hsb]
+  int hsb, hkch;
+  uint16_t* y;                // down: [T, k, N]
+};
+
+__host__ __device__ inline int scale_row_bytes(int K) { return (K / 32 * 2 + 15) / 16 * 16; }
+
+// D += A (fp8 plane, row scales = byte OPSEL_A of sa) x B (fp4 codes, column scales = byte 0 of sb).
+// The destination must not share registers with A or B (see mx_tile.h).  The empty
+// asm pins the accumulator to the AGPRs, where the MFMA keeps it (A and B live in
+// VGPRs, so they cannot overlap it), and keeps A and B live until the result exists;
+// pinning it to VGPRs instead makes the compiler copy it out of and back into AGPRs
+// around every instruction.
+template <int OPSEL_A>
+__device__ __forceinline__ f32x4_t mfma_plane(const i32x8_t& a, const i32x8_t& b, f32x4_t c, uint32_t sa,
+                                              uint32_t sb) {
+  typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+  f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, OPSEL_A, (int)sa, 0, (int)sb);
+  const i32x4_t b4 = __builtin_shufflevector(b, b, 0, 1, 2, 3);
+  asm volatile("" : "+a"(d) : "v"(a), "v"(b4));
+  return d;
+}
+
+// Two fp8 planes of 8 values: hi = RNE(v * inv), lo = RNE(16 (v * inv - hi)).
+__device__ __forceinline__ void encode8(const float (&v)[8], float inv, uint2& hi, uint2& lo) {
+  float s[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s[j] = v[j] * inv;   // exact: inv is a power of two
+  uint32_t h0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(s[0], s[1], 0, false);
+  h0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(s[2], s[3], (int)h0, true);
+  uint32_t h1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(s[4], s[5], 0, false);
+  h1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(s[6], s[7], (int)h1, true);
+  float2_t p[4];
+  p[0] = __builtin_amdgcn_cvt_pk_f32_fp8((int)h0, false);
+  p[1] = __builtin_amdgcn_cvt_pk_f32_fp8((int)h0, true);
+  p[2] = __builtin_amdgcn_cvt_pk_f32_fp8((int)h1, false);
+  p[3] = __builtin_amdgcn_cvt_pk_f32_fp8((int)h1, true);
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    r[2 * j] = (s[2 * j] - p[j][0]) * 16.0f;       // exact
+    r[2 * j + 1] = (s[2 * j + 1] - p[j][1]) * 16.0f;
+  }
+  uint32_t l0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+  l0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], (int)l0, true);
+  uint32_t l1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[4], r[5], 0, false);
+  l1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[6], r[7], (int)l1, true);
+  hi = make_uint2(h0, h1);
+  lo = make_uint2(l0, l1);
+}
+
+// Plane scale exponent of a block whose largest magnitude is m: E = e(m) - 7,
+// clamped so that both E8M0 bytes (E + 127, E + 123) are finite scales.
+__device__ __forceinline__ int plane_exp(float m) {
+  const int e = (int)((__float_as_uint(m) >> 23) & 0xffu) - 127;   // zero / subnormal max: -127
+  const int E = e - 7;
+  return E < -123 ? -123 : (E > 120 ? 120 : E);
+}
+
+// x [T, D] bf16 -> planes and scales per token.  One thread = 8 values; the four
+// threads of an aligned lane quad hold one 32-element block.
+__global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __restrict__ x, int T, int D,
+                                                            uint8_t* __restrict__ xp, uint8_t* __restrict__ xs,
+                                                            int sb) {
+  const int64_t t8 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // index of an 8-value group
+  const int per_row = D / 8;
+  const bool live = t8 < (int64_t)T * per_row;
+  const int64_t tc = live ? t8 : 0;
+  const int t = (int)(tc / per_row), g8 = (int)(tc - (int64_t)t * per_row);
+  const uint4 raw = *reinterpret_cast<const uint4*>(x + (size_t)t * D + 8 * g8);
+  float v[8];
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(w[j] << 16);
+    v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+  m = fmaxf(m, __uint_as_float(xor1_u32(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(xor2_u32(__float_as_uint(m))));
+  const int E = plane_exp(m);
+  uint2 hi, lo;
+  encode8(v, __uint_as_float((uint32_t)(127 - E) << 23), hi, lo);
+  if (!live) return;
+  const int col = 8 * g8, ch = col >> 7, byte = col & 127;
+  uint8_t* dst = xp + ((size_t)t * (D / 128) + ch) * P3_ROWB + byte;
+  *reinterpret_cast<uint2*>(dst) = hi;
+  *reinterpret_cast<uint2*>(dst + 128) = lo;
+  if ((g8 & 3) == 0) {
+    const uint32_t sc = (uint32_t)(E + 127) | ((uint32_t)(E + 123) << 8);
+    *reinterpret_cast<uint16_t*>(xs + (size_t)t * sb + (col / 32) * 2) = (uint16_t)sc;
+  }
+}
+
+template <int NM, int NF>
+struct P3Chunk {
+  uint4 codes[NM][NF];
+};
+
+template <int NM, int NF>
+__device__ __forceinline__ void p3_issue(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS],
+                                         const uint8_t* (&wrow)[NM][NF], int c, int kg, int wave, int row_bytes,
+                                         P3Chunk<NM, NF>& out) {
+#pragma unroll
+  for (int q = 0; q < P3_ASLOTS; ++q)
+    tile::lds_load16_untracked(asrc[q] + (size_t)c * P3_ROWB, stage + (P3_ASLOTS * wave + q) * 1024);
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      out.codes[m][f] = *reinterpret_cast<const uint4*>(wrow[m][f] + min(c * 64 + kg * 16, row_bytes - 16));
+}
+
+// B scales of chunk c = 4 g + J from the group registers (lane (i, p) holds the 16
+// E8M0 bytes of group g -- chunks 4g .. 4g+3 -- of weight row i of pair p = (m, f)):
+// lane (i, kg) takes byte kg of word J from lane (i, p).  Blocks past K: 127.
+template <int NM, int NF>
+__device__ __forceinline__ void p3_scales(const uint4& grp, int J, int c, int i, int kg, int blocks,
+                                          uint32_t (&bs)[NM][NF]) {
+  const uint32_t w = J == 0 ? grp.x : J == 1 ? grp.y : J == 2 ? grp.z : grp.w;
+  const bool in_k = 4 * c + kg < blocks;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint32_t v = (uint32_t)__shfl((int)w, 16 * (m * NF + f) + i, 64);
+      bs[m][f] = in_k ? (v >> (8 * kg)) & 0xffu : 127u;
+    }
+}
+
+template <int NM, int NF>
+__device__ __forceinline__ void p3_compute(const uint8_t* ab, const uint8_t* sbuf, int sbs, const P3Chunk<NM, NF>& ch,
+                                           const uint32_t (&bs)[NM][NF], int c, int i, int kg, int ntb,
+                                           f32x4_t (&acc)[NM][NF][P3_TB]) {
+  i32x8_t b[NM][NF];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint4 w = ch.codes[m][f];
+      b[m][f] = i32x8_t{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+    }
+#pragma unroll
+  for (int tb = 0; tb < P3_TB; ++tb) {
+    if (tb >= ntb) break;
+    const int row = tb * 16 + i;
+    const uint8_t* ar = ab + row * P3_ROWB;
+    const uint4 h0 = mx::lds16(ar + ((kg ^ i) << 4));
+    const uint4 h1 = mx::lds16(ar + (((4 + kg) ^ i) << 4));
+    const uint4 l0 = mx::lds16(ar + (((8 + kg) ^ i) << 4));
+    const uint4 l1 = mx::lds16(ar + (((12 + kg) ^ i) << 4));
+    const uint32_t sa = *reinterpret_cast<const uint16_t*>(sbuf + row * sbs + (4 * c + kg) * 2);
+    const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+    const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) acc[m][f][tb] = mfma_plane<0>(ahi, b[m][f], acc[m][f][tb], sa, bs[m][f]);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) acc[m][f][tb] = mfma_plane<1>(alo, b[m][f], acc[m][f][tb], sa, bs[m][f]);
+  }
+}
+
+// grid = slices * tiles rounded up to 8; dynamic LDS = P3_STAGES * P3_ABYTES + P3_MT * (sb + 16).
+template <int NM, int NF>
+__global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
+  extern __shared__ __align__(16) uint8_t p3_lds[];
+  uint8_t* abuf = p3_lds;
+  uint8_t* sbuf = p3_lds + P3_STAGES * P3_ABYTES;
+  const int sbs = g.sb + 16;   // LDS row stride of the A scales (bank spread)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 15, kg = lane >> 4;
+  const int b8 = blockIdx.x >> 3;                         // sequence number on this XCD
+  const int slice = b8 % slices;
+  const int tile_id = (b8 / slices) * 8 + (int)(blockIdx.x & 7);
+  if (tile_id >= g.tiles_n[0]) return;
+  const int2 tl = g.tiles[tile_id];
+  const int e = tl.x, row0 = tl.y;
+  const int rows = min(P3_MT, g.offsets[e + 1] - row0);
+  const int ntb = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
+  const int slot = g.slot_table[e];
+  constexpr int WN = 16 * NF;                            // weight rows per wave and matrix
+  const int nw0 = slice * (P3_WAVES * WN) + WN * wave;   // the wave's first weight row
+  f32x4_t acc[NM][NF][P3_TB];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int tb = 0; tb < P3_TB; ++tb) acc[m][f][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (slot >= 0) {
+    const int row_bytes = g.K / 2, blocks = g.K / 32;
+    // the tile's A scales into LDS for the whole K loop (rows past the tile: its last row)
+    const int sq = g.sb / 16;
+    for (int it = threadIdx.x; it < P3_MT * sq; it += P3_THREADS) {
+      const int r = it / sq, q = it - r * sq;
+      const int rr = row0 + min(r, rows - 1);
+      const int src = g.a_gather ? g.a_gather[rr] : rr;
+      *reinterpret_cast<uint4*>(sbuf + r * sbs + q * 16) =
+          *reinterpret_cast<const uint4*>(g.as + (size_t)src * g.sb + q * 16);
+    }
+    // A plane sources of the lane's slots: slot S = 64 (P3_ASLOTS wave + q) + lane holds
+    // row S / 16, physical 16-byte column S % 16 = logical column ^ (row % 16)
+    const uint8_t* asrc[P3_ASLOTS];
+#pragma unroll
+    for (int q = 0; q < P3_ASLOTS; ++q) {
+      const int S = 64 * (P3_ASLOTS * wave + q) + lane;
+      const int r = S >> 4;
+      const int col = (S & 15) ^ (r & 15);
+      const int rr = row0 + min(r, rows - 1);
+      const int src = g.a_gather ? g.a_gather[rr] : rr;
+      asrc[q] = g.ap + (size_t)src * g.kch * P3_ROWB + col * 16;
+    }
+    const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
+    const int tq[2] = {NM == 2 ? 0 : 3, 6};   // w1, w3 (gate/up) or w2 (down)
+    const uint8_t* wrow[NM][NF];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const int n = min(nw0 + 16 * f + i, g.N - 1);   // rows past N: clamped (discarded)
+        wrow[m][f] = base + g.L.off[tq[m]] + (int64_t)n * row_bytes;
+      }
+    // B scales: lane (i, p), p = kg = (m, f) pair, loads 16 E8M0 bytes (4 chunks) of its
+    // pair's weight row i at a time (NM * NF == 4); p3_scales hands them out.  A group
+    // past the row's last block reads into what follows the tensor in the record (the
+    // host checks that something does); those bytes are never used.
+    static_assert(NM * NF == 4, "one (m, f) pair per lane group");
+    const int pm = kg / NF, pf = kg - pm * NF;
+    const uint8_t* sgp = base + g.L.off[tq[pm] + 1] + (int64_t)min(nw0 + 16 * pf + i, g.N - 1) * blocks;
+    const int ngrp = (blocks + 15) / 16;
+    const int nch = g.kch;
+    P3Chunk<NM, NF> ring[P3_STAGES];
+    uint4 sgrp[3];
+    // every issue is unconditional (a chunk past the end re-reads the last one into a
+    // stage nothing reads again), so each wait is for exactly the loads it needs
+    sgrp[0] = *reinterpret_cast<const uint4*>(sgp);
+    p3_issue<NM, NF>(abuf, asrc, wrow, 0, kg, wave, row_bytes, ring[0]);
+    p3_issue<NM, NF>(abuf + P3_ABYTES, asrc, wrow, min(1, nch - 1), kg, wave, row_bytes, ring[1]);
+    // twelve chunks per trip: A stage and code ring index u % 3, scale group buffer (u / 4) % 3
+    for (int c0 = 0; c0 < nch; c0 += 12) {
+#pragma unroll
+      for (int u = 0; u < 12; ++u) {
+        const int c = c0 + u;
+        // this wave's loads of chunk c have landed (its last code load is consumed
+        // here; its earlier direct-to-LDS loads complete first), then every wave's
+        asm volatile("" ::"v"(ring[u % 3].codes[NM - 1][NF - 1].w) : "memory");
+        lds_sync();
+        if ((u + 2) % 4 == 0)   // the scale group of chunk c + 2
+          sgrp[((u + 2) / 4) % 3] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 2) / 4, ngrp - 1));
+        p3_issue<NM, NF>(abuf + ((u + 2) % 3) * P3_ABYTES, asrc, wrow, min(c + 2, nch - 1), kg, wave, row_bytes,
+                         ring[(u + 2) % 3]);
+        if (c < nch) {
+          uint32_t bs[NM][NF];
+          p3_scales<NM, NF>(sgrp[(u / 4) % 3], u % 4, c, i, kg, blocks, bs);
+          p3_compute<NM, NF>(abuf + (u % 3) * P3_ABYTES, sbuf, sbs, ring[u % 3], bs, c, i, kg, ntb, acc);
+        }
+      }
+    }
+    // the re-reads issued past the end (direct-to-LDS among them) land before the
+    // workgroup's LDS is released
+    tile::wait_vmem();
+  }
+  // epilogue: lane holds rows tb*16 + 4kg + r (tile rows) x weight rows nw0 + 16f + i
+  if constexpr (NM == 2) {
+    // h = bf16(silu(min(g, L)) * clip(u) * w), written as the planes of its 32-element
+    // block (the wave's 32 weight rows are one block of h's columns)
+#pragma unroll
+    for (int tb = 0; tb < P3_TB; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tr = tb * 16 + 4 * kg + r;   // the same in the 16 lanes of a row group
+        if (tr >= rows) continue;
+        const int prow = row0 + tr;
+        const float wr = g.row_w[prow];
+        float hv[NF];
+        float m = 0.0f;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          float gv = round_bf16(acc[0][f][tb][r]);
+          float uv = round_bf16(acc[1][f][tb][r]);
+          if (g.limit > 0.0f) {
+            uv = fminf(fmaxf(uv, -g.limit), g.limit);
+            gv = fminf(gv, g.limit);
+          }
+          hv[f] = nw0 + 16 * f + i < g.N ? round_bf16((silu_f32(gv) * uv) * wr) : 0.0f;
+          m = fmaxf(m, fabsf(hv[f]));
+        }
+        m = mx::row16_max(m);
+        const int E = plane_exp(m);
+        const float inv = __uint_as_float((uint32_t)(127 - E) << 23);
+        uint8_t* dst = g.hp + (size_t)prow * g.hkch * P3_ROWB;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const float s = hv[f] * inv;
+          const uint32_t hi = mx::f32_to_e4m3(s);
+          const uint32_t lo = mx::f32_to_e4m3((s - mx::e4m3_to_f32(hi)) * 16.0f);
+          const int n = nw0 + 16 * f + i;
+          uint8_t* p = dst + (n >> 7) * P3_ROWB + (n & 127);
+          p[0] = (uint8_t)hi;
+          p[128] = (uint8_t)lo;
+        }
+        if (i == 0) {
+          const uint32_t sc = (uint32_t)(E + 127) | ((uint32_t)(E + 123) << 8);
+          *reinterpret_cast<uint16_t*>(g.hs + (size_t)prow * g.hsb + (nw0 / 32) * 2) = (uint16_t)sc;
+        }
+      }
+  } else {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int n = nw0 + 16 * f + i;
+      if (n >= g.N) continue;
+#pragma unroll
+      for (int tb = 0; tb < P3_TB; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tr = tb * 16 + 4 * kg + r;
+          if (tr >= rows) continue;
+          const int rr = row0 + tr;
+          g.y[((size_t)g.row_token[rr] * g.k + g.row_slot[rr]) * g.N + n] = f32_to_bf16(acc[0][f][tb][r]);
+        }
+    }
+  }
+}
+
+}  // namespace
+
+// Workspace of the block-scaled prefill beyond the tile list: x planes [T][D/128][256]
+// and scales [T][sb(D)], h planes [rows][F_pad/128][256] and scales [rows][sb(F_pad)].
+size_t prefill_mx_ws_bytes(int T, int k, int D, int F) {
+  const size_t rows = (size_t)T * k;
+  const int fch = (F + 127) / 128;
+  auto a256 = [](size_t v) { return (v + 255) & ~size_t(255); };
+  return a256((size_t)T * D * 2) + a256((size_t)T * scale_row_bytes(D)) + a256(rows * fch * P3_ROWB) +
+         a256(rows * scale_row_bytes(fch * 128));
+}
+
+// Shapes and slot layouts the kernels take.  Their B-scale loads read 16 bytes per
+// row at a time; when a scale row is not a whole number of 16-byte groups, the last
+// group of the tensor's last row reads up to 15 bytes past the tensor, which must
+// still lie inside the slot record.
+bool prefill_mx_supported(int D, int F, const decode::Layout& L) {
+  if (!(D % 128 == 0 && D >= 512 && D <= 8192 && F % 32 == 0 && F >= 512 && F <= 8192)) return false;
+  auto room = [&](int t, int64_t rows, int blocks) {
+    return blocks % 16 == 0 || L.off[t] + rows * blocks + 16 <= L.record_bytes;
+  };
+  return room(1, F, D / 32) && room(7, F, D / 32) && room(4, D, F / 32);
+}
+
+// tiles / tiles_n: the 64-row tile list (tile_list_kernel with MT = 64), max_tiles its bound.
+int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
+                      const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
+                      int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
+                      int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s) {
+  auto a256 = [](size_t v) { return (v + 255) & ~size_t(255); };
+  const size_t rows = (size_t)T * k;
+  const int fch = (F + 127) / 128;
+  const int sbx = scale_row_bytes(D), sbh = scale_row_bytes(fch * 128);
+  uint8_t* xp = ws;
+  uint8_t* xs = xp + a256((size_t)T * D * 2);
+  uint8_t* hp = xs + a256((size_t)T * sbx);
+  uint8_t* hs = hp + a256(rows * fch * P3_ROWB);
+  const int64_t groups = (int64_t)T * D / 8;
+  hipLaunchKernelGGL(x_planes_rows_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, x, T, D, xp, xs,
+                     sbx);
+  int rc = check_launch("x_planes_rows_kernel");
+  if (rc) return rc;
+  const int tiles8 = (max_tiles + 7) / 8 * 8;
+  MxArgs gu{xp, xs, sbx, D / 128, row_token, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot,
+            row_w, D, F, k, limit, hp, hs, sbh, fch, nullptr};
+  const int s_gu = (fch * 128) / (P3_WAVES * 32);   // h's padded columns, 128 per workgroup
+  const size_t lds_gu = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbx + 16);
+  auto kgu = p3_kernel<2, 2>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds_gu) != hipSuccess)
+    return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_gu);
+  hipLaunchKernelGGL(kgu, dim3(s_gu * tiles8), dim3(P3_THREADS), lds_gu, s, gu, s_gu);
+  rc = check_launch("p3_kernel<2,2>");
+  if (rc) return rc;
+  MxArgs dn{hp, hs, sbh, fch, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
+            F, D, k, limit, nullptr, nullptr, 0, 0, y};
+  const int s_dn = (D + P3_WAVES * 64 - 1) / (P3_WAVES * 64);
+  const size_t lds_dn = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbh + 16);
+  auto kdn = p3_kernel<1, 4>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kdn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds_dn) != hipSuccess)
+    return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_dn);
+  hipLaunchKernelGGL(kdn, dim3(s_dn * tiles8), dim3(P3_THREADS), lds_dn, s, dn, s_dn);
+  return check_launch("p3_kernel<1,4>");
+}
+
+}  // namespace cachalot

@@ -107,7 +107,7 @@ def test_permute_errors(cuda):
 
 
 @pytest.mark.parametrize("kind", ["affine", "fp4"])
-def test_grouped_experts_prefill_tiles(cuda, kind):
+def test_grouped_experts_prefill_tiles(cuda, kind, prefill_path):
     """64-row tiles (T*k >= 4E): an expert with more rows than one tile, ragged tails."""
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format, fp4_format
@@ -199,7 +199,7 @@ def test_grouped_is_deterministic(cuda):
 
 
 @pytest.mark.parametrize("kind", ["affine", "fp4"])
-def test_moe_prefill_grouped_end_to_end(cuda, kind):
+def test_moe_prefill_grouped_end_to_end(cuda, kind, prefill_path):
     """Router (bit-exact ids) -> permute -> grouped experts -> combine, small model shape."""
     from cachalot_amd.moe_prefill import moe_prefill_grouped
     from cachalot_amd.storage.index import affine_format, fp4_format

@@ -189,9 +189,11 @@ def _grouped_check(what, fmt, layer, xf, idx, w, routed, out, y, n_experts, rows
 
 
 @pytest.mark.parametrize("kind", ["fp4", "affine"])
-def test_grouped_experts_span_many_tiles(cuda, kind):
+def test_grouped_experts_span_many_tiles(cuda, kind, prefill_path):
     """One expert with 3 x 128 + 37 rows and several with more than 128 (ragged
     last tiles), T = 600, k = 2, E = 8, at the layer's shape."""
+    if kind == "affine" and prefill_path == "bf16":
+        pytest.skip("the prefill path choice concerns FP4 banks only")
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format, fp4_format
 
@@ -211,7 +213,7 @@ def test_grouped_experts_span_many_tiles(cuda, kind):
     routed, out, y = grouped_experts(_bf16(xb, cuda), torch.from_numpy(idx).to(cuda), torch.from_numpy(w).to(cuda),
                                      store.pool, store.layer_table(0), addend=_bf16(ab, cuda), want_routed=True,
                                      want_terms=True)
-    _grouped_check(f"grouped many tiles {kind}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed), _f32(out),
+    _grouped_check(f"grouped many tiles {kind} {prefill_path}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed), _f32(out),
                    _f32(y), E, addend=bf16_bits_to_f32(ab))
 
 
@@ -247,7 +249,7 @@ def test_grouped_out_of_range_ids_contribute_zero(cuda, t):
                        yf, E)
 
 
-def test_config3_prefill_workload(cuda):
+def test_config3_prefill_workload(cuda, prefill_path):
     """Config 3 itself: 4096 tokens, D 4096, F 2880, 384 FP4 experts, the Zipf
     router bias.  Router ids, weights and scores bit-exact for all 4096 tokens
     (the tiled router kernel at E = 384); the three heaviest experts' rows
@@ -291,8 +293,9 @@ def test_config3_prefill_workload(cuda):
         want = set(pairs)
         rows = np.argwhere(oi == e)
         rows_of[e] = np.asarray([i for i, (a, c) in enumerate(rows.tolist()) if (a, c) in want])
-    _grouped_check("config3 prefill fp4", fmt, 0, xf, oi, ow, _np(routed), _f32(out), yf, E, rows_of=rows_of)
-    report("config3 prefill fp4", rows_per_heavy_expert=counts[heavy].tolist(), max_rows=int(counts.max()),
+    _grouped_check(f"config3 prefill fp4 {prefill_path}", fmt, 0, xf, oi, ow, _np(routed), _f32(out), yf, E,
+                   rows_of=rows_of)
+    report(f"config3 prefill fp4 {prefill_path}", rows_per_heavy_expert=counts[heavy].tolist(), max_rows=int(counts.max()),
            experts_touched=int((counts > 0).sum()))
 
 
