@@ -254,20 +254,20 @@ __global__ void __launch_bounds__(THREADS) q2_decode_fused_kernel(FusedQ2 p) {
     // earlier scale copy too; no LDS read of the scales may move above this point
     asm volatile("" ::"v"(c3[m][1].w) : "memory");
     const uint8_t* blkA = s.planes + (4 * q + ro.kgR) * PB_BYTES;
-    f32x4_t a1 = mx::zero_acc(), a3 = mx::zero_acc();
+    f32x4_t a1 = mx::zero_acc<true>(), a3 = mx::zero_acc<true>();
     chain_load(CH, blkA, ro);
     const uint4& u1a = c1[m][0];
     const uint4& u1b = c1[m][1];
     const uint4& u3a = c3[m][0];
     const uint4& u3b = c3[m][1];
-    a1 = mx::mfma_fp8_fp4<0>(CH.a[0], mx::q2_spread(u1a.x, u1a.y), a1, CH.sa, mx::E8M0_TWO);
-    a3 = mx::mfma_fp8_fp4<0>(CH.a[0], mx::q2_spread(u3a.x, u3a.y), a3, CH.sa, mx::E8M0_TWO);
-    a1 = mx::mfma_fp8_fp4<1>(CH.a[1], mx::q2_spread(u1a.z, u1a.w), a1, CH.sa, mx::E8M0_TWO);
-    a3 = mx::mfma_fp8_fp4<1>(CH.a[1], mx::q2_spread(u3a.z, u3a.w), a3, CH.sa, mx::E8M0_TWO);
-    a1 = mx::mfma_fp8_fp4<2>(CH.a[2], mx::q2_spread(u1b.x, u1b.y), a1, CH.sa, mx::E8M0_TWO);
-    a3 = mx::mfma_fp8_fp4<2>(CH.a[2], mx::q2_spread(u3b.x, u3b.y), a3, CH.sa, mx::E8M0_TWO);
-    a1 = mx::mfma_fp8_fp4<3>(CH.a[3], mx::q2_spread(u1b.z, u1b.w), a1, CH.sa, mx::E8M0_TWO);
-    a3 = mx::mfma_fp8_fp4<3>(CH.a[3], mx::q2_spread(u3b.z, u3b.w), a3, CH.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<0, true>(CH.a[0], mx::q2_spread(u1a.x, u1a.y), a1, CH.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<0, true>(CH.a[0], mx::q2_spread(u3a.x, u3a.y), a3, CH.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<1, true>(CH.a[1], mx::q2_spread(u1a.z, u1a.w), a1, CH.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<1, true>(CH.a[1], mx::q2_spread(u3a.z, u3a.w), a3, CH.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<2, true>(CH.a[2], mx::q2_spread(u1b.x, u1b.y), a1, CH.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<2, true>(CH.a[2], mx::q2_spread(u3b.x, u3b.y), a3, CH.sa, mx::E8M0_TWO);
+    a1 = mx::mfma_fp8_fp4<3, true>(CH.a[3], mx::q2_spread(u1b.z, u1b.w), a1, CH.sa, mx::E8M0_TWO);
+    a3 = mx::mfma_fp8_fp4<3, true>(CH.a[3], mx::q2_spread(u3b.z, u3b.w), a3, CH.sa, mx::E8M0_TWO);
     const float sx = piece_sums(s.planes + (4 * q + kg) * PB_BYTES, mx::PIECES);
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(s.scl[wave][m]) + (j * 16 + gsb[m] + 2 * kg) / 2;
     const float v1 = bf16_to_f32(sc[0]) * dot4(a1) + bf16_to_f32(sc[128]) * sx;
@@ -410,12 +410,12 @@ __global__ void __launch_bounds__(THREADS) q2_decode_fused_kernel(FusedQ2 p) {
     const uint8_t* blkA = s.planes + (e * GK + min(4 * q2 + ro.kgR, GK - 1)) * PB_BYTES;
     const int g2 = 4 * q2 + kg;
     const float sh = g2 < GK ? piece_sums(s.planes + (e * GK + g2) * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
-    f32x4_t acc = mx::zero_acc();
+    f32x4_t acc = mx::zero_acc<true>();
     chain_load(CH, blkA, ro);
-    acc = mx::mfma_fp8_fp4<0>(CH.a[0], B2[m][0], acc, CH.sa, mx::E8M0_TWO);
-    acc = mx::mfma_fp8_fp4<1>(CH.a[1], B2[m][1], acc, CH.sa, mx::E8M0_TWO);
-    acc = mx::mfma_fp8_fp4<2>(CH.a[2], B2[m][2], acc, CH.sa, mx::E8M0_TWO);
-    acc = mx::mfma_fp8_fp4<3>(CH.a[3], B2[m][3], acc, CH.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<0, true>(CH.a[0], B2[m][0], acc, CH.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<1, true>(CH.a[1], B2[m][1], acc, CH.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<2, true>(CH.a[2], B2[m][2], acc, CH.sa, mx::E8M0_TWO);
+    acc = mx::mfma_fp8_fp4<3, true>(CH.a[3], B2[m][3], acc, CH.sa, mx::E8M0_TWO);
     float v = g2 < GK ? bf16_lo(dsc[m][0]) * dot4(acc) + bf16_lo(dsc[m][1]) * sh : 0.0f;
     v = tile::sum_lane_groups(v);
     if (lane < 16) s.red_dn[dn_tv[m]][e][q2][lane] = v;

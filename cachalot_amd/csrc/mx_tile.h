@@ -70,21 +70,30 @@ constexpr uint32_t E8M0_TWO = 128u;     // 2^1
 // 4-register MFMA destination to overlap its sources, and for this multi-pass
 // instruction that corrupted results (data-dependent wrong values and NaNs that
 // moved with register allocation).  The empty asm consumes A, B and the result,
-// so A and B are live when the result is defined and cannot be reused for it.
-template <int OPSEL_A = 0>
+// so A and B are live when the result is defined and cannot be reused for it,
+// and it keeps the result in AGPRs, a register file A and B are never in.
+template <int OPSEL_A = 0, bool ACC_VGPR = false>
 __device__ __forceinline__ f32x4_t mfma_fp8_fp4(const i32x8_t& a, const i32x8_t& b, f32x4_t c, uint32_t sa,
                                                 uint32_t sb) {
   typedef __attribute__((ext_vector_type(4))) int i32x4_t;
   f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, OPSEL_A, (int)sa, 0, (int)sb);
   const i32x4_t b4 = __builtin_shufflevector(b, b, 0, 1, 2, 3);   // an fp4 B operand is 4 registers
-  asm volatile("" : "+v"(d) : "v"(a), "v"(b4));
+  // the accumulator stays in the AGPRs the instruction writes (pinning it to VGPRs
+  // makes the compiler copy it out and back around every instruction); A and B sit
+  // in VGPRs, so they cannot overlap it
+  // (ACC_VGPR: a kernel whose register budget has no room for AGPR accumulators keeps
+  // them in VGPRs)
+  if constexpr (ACC_VGPR) asm volatile("" : "+v"(d) : "v"(a), "v"(b4));
+  else asm volatile("" : "+a"(d) : "v"(a), "v"(b4));
   return d;
 }
 
 // A zero accumulator held in registers (not folded into an inline-constant srcC).
+template <bool ACC_VGPR = false>
 __device__ __forceinline__ f32x4_t zero_acc() {
   f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
-  asm volatile("" : "+v"(z));
+  if constexpr (ACC_VGPR) asm volatile("" : "+v"(z));
+  else asm volatile("" : "+a"(z));
   return z;
 }
 
