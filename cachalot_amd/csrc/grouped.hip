@@ -44,6 +44,7 @@ int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const dec
 // FP4 prefill on the block-scaled matrix cores (prefill_mx.hip)
 size_t prefill_mx_ws_bytes(int T, int k, int D, int F);
 bool prefill_mx_supported(int D, int F, const decode::Layout& L);
+int prefill_mx_mt();
 int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
                       const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
                       int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
@@ -850,7 +851,7 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
   if (KIND == KIND_FP4 && MT == 64 && prefill_mx_supported(D, F, L) && !small_tiles_requested() &&
       !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
-    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, 64, tiles, tiles_n, zeros);
+    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, prefill_mx_mt(), tiles, tiles_n, zeros);
     rc = check_launch("tile_list_kernel");
     if (rc) return rc;
     return launch_prefill_mx(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,

@@ -424,6 +424,9 @@ size_t prefill_mx_ws_bytes(int T, int k, int D, int F) {
 // row at a time; when a scale row is not a whole number of 16-byte groups, the last
 // group of the tensor's last row reads up to 15 bytes past the tensor, which must
 // still lie inside the slot record.
+// Rows per tile of the tile list these kernels take.
+int prefill_mx_mt() { return P3_MT; }
+
 bool prefill_mx_supported(int D, int F, const decode::Layout& L) {
   if (!(D % 128 == 0 && D >= 512 && D <= 8192 && F % 32 == 0 && F >= 512 && F <= 8192)) return false;
   auto room = [&](int t, int64_t rows, int blocks) {
