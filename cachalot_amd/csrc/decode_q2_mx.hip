@@ -299,9 +299,11 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   const int row0 = blockIdx.x * 16;
   const int n_items = k * NQ2;
 
-  // ---- 0. the slots (KMAX entries are allocated) -> the wave's W2 codes into
-  //         registers, then the tile's scale / bias runs and the hidden plane
-  //         blocks into LDS; one wait for all of it
+  // ---- 0. the hidden plane blocks into LDS; the slots (KMAX entries are
+  //         allocated) -> the wave's W2 codes into registers, then the tile's
+  //         scale / bias runs into LDS; one wait for all of it
+  // the hidden plane blocks first: they do not wait for the slots
+  copy_to_lds_untracked(hid, s.planes, k * GK * PB_BYTES, wave, DN_WAVES, lane);
   int eslot[KMAX];
 #pragma unroll
   for (int e = 0; e < KMAX; ++e) eslot[e] = ws_slots[e];
@@ -340,7 +342,6 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
       }
     }
   }
-  copy_to_lds_untracked(hid, s.planes, k * GK * PB_BYTES, wave, DN_WAVES, lane);
   tile::wait_vmem();
   lds_sync();
 
