@@ -14,9 +14,9 @@
 //     with the router's scores it runs the top-k itself -- while the other
 //     three copy x's fp8 plane blocks (written once per token by the router
 //     kernel or x_planes_kernel) into LDS.  Items are (tile, quad of four
-//     128-code groups), quad q to wave q % 4; per item one direct-to-LDS copy of
-//     the four scale / bias chunks, then the codes, then four block-scaled MFMAs
-//     per matrix sharing the A operand.  Epilogue: bf16(g), bf16(u), clamp,
+//     128-code groups), quad q to wave q % 4.  Wave w copies the tile's run of
+//     scale / bias tensor w into LDS (16 rows, whole lines), then loads its items'
+//     codes; per item four block-scaled MFMAs per matrix sharing the A operand.  Epilogue: bf16(g), bf16(u), clamp,
 //     h = bf16(silu(g) * u * w_e), stored as one fp8 plane piece of the
 //     expert's hidden plane blocks (16 rows = one piece).
 //   q2mx_down_kernel  one 768-thread workgroup = one 16-row tile of W2 for all k
@@ -56,13 +56,12 @@ constexpr int MAX_GT = 40;                     // D <= 5120
 constexpr int MAX_NQ = MAX_GT / 4;
 constexpr int MAX_GK = 24;                     // F <= 3072
 constexpr int MAX_NQ2 = MAX_GK / 4;
-constexpr int GU_MAXM = (MAX_NQ + GU_WAVES - 1) / GU_WAVES;   // items per wave
 constexpr int DN_THREADS = 768;
 constexpr int DN_WAVES = DN_THREADS / 64;
 
 struct GuLds {
   uint8_t planes[MAX_GT * PB_BYTES];
-  uint8_t scl[GU_WAVES][GU_MAXM][1024];   // per wave and item: [s1, b1, s3, b3][16 rows] 16-byte chunks
+  uint16_t sc[4][1024];   // s1, b1, s3, b3 of the tile's 16 rows (one run of 32 GT bytes each; 2 KiB slots)
   float red[MAX_NQ][2][16];
   int top_i[KMAX], top_s[KMAX];
   float top_v[KMAX], top_w[KMAX];
@@ -115,10 +114,10 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
   // ---- 0. routing wave: the expert's slot; the others: x's plane blocks into LDS
   if (wave == rw) {
     const int slot = route_slot(src, ws_slots, e, s.top_i, s.top_v, s.top_s);
-    if (lane == 0) {
-      s.slot = slot;
-      if ((src.idx || src.scores) && tile == 0) ws_slots[e] = slot;   // read by the down kernel
-    }
+    if (lane == 0) s.slot = slot;
+    // (nothing is in flight here; the explicit wait tells the compiler so, and it then
+    // puts no wait between the loads below)
+    tile::wait_vmem();
   } else {
     copy_to_lds_untracked(xplanes, s.planes, GT * PB_BYTES, wave < rw ? wave : wave - 1, GU_WAVES - 1, lane);
     tile::wait_vmem();
@@ -134,19 +133,21 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
   Chain ch;
   chain_init(ch);
 
-  // ---- 1. loads: per item the scale / bias chunk copy (lane = tensor x row), then the codes
+  // ---- 1. loads: wave w copies the tile's run of scale / bias tensor w (whole
+  //         lines), then its items' codes; the runs are shared after a barrier
   uint4 c1[MAXM][2], c3[MAXM][2];
-  int gsb[MAXM];   // byte of the item's first group inside its scale chunks
   if (live) {
     const uint8_t* base = pool + (int64_t)slot * L.record_bytes;
-    const int t = lane >> 4, r = lane & 15;
-    const int64_t toff = t == 0 ? L.off[1] : t == 1 ? L.off[2] : t == 2 ? L.off[7] : L.off[8];
+    const int64_t toff = wave == 0 ? L.off[1] : wave == 1 ? L.off[2] : wave == 2 ? L.off[7] : L.off[8];
+    // 32 GT bytes (<= 1280): one 1 KiB load, a second one (clamped source) past 32
+    // columns; unpredicated, so that no wait lands between them and the codes
+    const uint8_t* run = base + toff + (int64_t)row0 * GT * 2;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(s.sc[wave]);
+    __builtin_amdgcn_global_load_lds(run + min(16 * lane, 32 * GT - 16), dst, 16, 0, 0);
+    if (GT > 32) __builtin_amdgcn_global_load_lds(run + min(1024 + 16 * lane, 32 * GT - 16), dst + 1024, 16, 0, 0);
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
       const int q = min(wave + GU_WAVES * m, NQ - 1);
-      const int o = ((row0 + r) * GT + 4 * q) * 2;
-      tile::lds_load16_untracked(base + toff + (o & ~15), s.scl[wave][m]);
-      gsb[m] = (8 * q) & 15;
       const int off = (row0 + j) * (D / 4) + (4 * q + kg) * 32;   // < 2^31: a 16-row tile of one tensor
       const uint4* r1 = reinterpret_cast<const uint4*>(base + L.off[0] + off);
       const uint4* r3 = reinterpret_cast<const uint4*>(base + L.off[6] + off);
@@ -155,16 +156,17 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
       c3[m][0] = r3[0];
       c3[m][1] = r3[1];
     }
+    // the run copy, issued before the 4 * MAXM code loads, has landed (loads
+    // complete in issue order); the codes stay in flight across the barrier
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * MAXM));
   }
+  lds_sync();
 
   // ---- 2. items
 #pragma unroll
   for (int m = 0; m < MAXM; ++m) {
     const int q = wave + GU_WAVES * m;
     if (!live || q >= NQ) break;
-    // the item's last code load has landed, hence (loads complete in issue order) its
-    // earlier scale copy too; no LDS read of the scales may move above this point
-    asm volatile("" ::"v"(c3[m][1].w) : "memory");
     f32x4_t a1 = mx::zero_acc(), a3 = mx::zero_acc();
     chain_load(ch, s.planes + (4 * q + ro.kgR) * PB_BYTES, ro);
     a1 = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c1[m][0].x, c1[m][0].y), a1, ch.sa, mx::E8M0_TWO);
@@ -176,9 +178,9 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
     a1 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c1[m][1].z, c1[m][1].w), a1, ch.sa, mx::E8M0_TWO);
     a3 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c3[m][1].z, c3[m][1].w), a3, ch.sa, mx::E8M0_TWO);
     const float sx = piece_sums(s.planes + (4 * q + kg) * PB_BYTES, mx::PIECES);
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(s.scl[wave][m]) + (j * 16 + gsb[m] + 2 * kg) / 2;
-    const float v1 = bf16_to_f32(sc[0]) * dot4(a1) + bf16_to_f32(sc[128]) * sx;
-    const float v3 = bf16_to_f32(sc[256]) * dot4(a3) + bf16_to_f32(sc[384]) * sx;
+    const int si = j * GT + 4 * q + kg;
+    const float v1 = bf16_to_f32(s.sc[0][si]) * dot4(a1) + bf16_to_f32(s.sc[1][si]) * sx;
+    const float v3 = bf16_to_f32(s.sc[2][si]) * dot4(a3) + bf16_to_f32(s.sc[3][si]) * sx;
     const float r1 = tile::sum_lane_groups(v1);
     const float r3 = tile::sum_lane_groups(v3);
     if (lane < 16) {
@@ -190,6 +192,9 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
 
   // ---- 3. epilogue (16 lanes of wave 0): h for the tile's rows as one plane piece
   if (tid < 16) {
+    // the expert's slot for the down kernel, stored here rather than before the loads:
+    // a store's data registers stay busy until it completes (one counter on gfx9)
+    if (tid == 0 && (src.idx || src.scores) && tile == 0) ws_slots[e] = slot;
     const float wexp = route_finish(src, ws_w, e, tile, s.top_v, s.top_w, s.top_i, blockIdx.x == 0);
     float hv = 0.0f;
     if (live) {
