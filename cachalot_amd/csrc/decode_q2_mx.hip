@@ -66,11 +66,13 @@ struct GuLds {
   int top_i[KMAX], top_s[KMAX];
   float top_v[KMAX], top_w[KMAX];
   int slot;
+  float wexp;
 };
 
 struct DnLds {
   uint8_t planes[KMAX * MAX_GK * PB_BYTES];
-  uint16_t sc[KMAX][2][16 * MAX_GK];      // per expert: s2, b2 runs of the tile's rows
+  uint16_t sc[KMAX][2][512];              // per expert: s2, b2 runs of the tile's rows (32 GK bytes in a
+                                          // 1 KiB slot: every lane of the copy writes its 16 bytes)
   float red[KMAX][MAX_NQ2][16];
   float y[KMAX][16];
 };
@@ -156,10 +158,16 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
       c3[m][0] = r3[0];
       c3[m][1] = r3[1];
     }
-    // the run copy, issued before the 4 * MAXM code loads, has landed (loads
-    // complete in issue order); the codes stay in flight across the barrier
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * MAXM));
   }
+  // with scores, the routing wave normalises the selected weights while the loads
+  // are in flight
+  if (src.scores != nullptr && wave == rw) {
+    const float w = route_weight(src, ws_w, e, s.top_v, s.top_w);
+    if (lane == 0) s.wexp = w;
+  }
+  // the run copy, issued before the 4 * MAXM code loads, has landed (loads
+  // complete in issue order); the codes stay in flight across the barrier
+  if (live) __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * MAXM));
   lds_sync();
 
   // ---- 2. items
@@ -195,7 +203,15 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
     // the expert's slot for the down kernel, stored here rather than before the loads:
     // a store's data registers stay busy until it completes (one counter on gfx9)
     if (tid == 0 && (src.idx || src.scores) && tile == 0) ws_slots[e] = slot;
-    const float wexp = route_finish(src, ws_w, e, tile, s.top_v, s.top_w, s.top_i, blockIdx.x == 0);
+    // given experts: the weight is loaded here (measured faster than with the slot)
+    const float wexp = src.scores != nullptr ? s.wexp : expert_weight(src, ws_w, e);
+    if (src.scores != nullptr) {   // the selection, for the down kernel and the caller
+      if (tile == 0 && tid == 0) ws_w[e] = wexp;
+      if (blockIdx.x == 0 && tid < src.k) {
+        if (src.idx_out) src.idx_out[tid] = s.top_i[tid];
+        if (src.w_out) src.w_out[tid] = s.top_w[tid];
+      }
+    }
     float hv = 0.0f;
     if (live) {
       float rg[MAX_NQ], ru[MAX_NQ];
@@ -305,13 +321,33 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   const int n_items = k * NQ2;
 
   // ---- 0. the hidden plane blocks into LDS; the slots (KMAX entries are
-  //         allocated) -> the wave's W2 codes into registers, then the tile's
-  //         scale / bias runs into LDS; one wait for all of it
+  //         allocated) -> the tile's scale / bias runs into LDS, then the wave's
+  //         W2 codes into registers
   // the hidden plane blocks first: they do not wait for the slots
   copy_to_lds_untracked(hid, s.planes, k * GK * PB_BYTES, wave, DN_WAVES, lane);
+  // the tile's addend, read now rather than in the epilogue (every lane loads, no
+  // branch: the wait for it then sits at its use)
+  const uint16_t add_bits = (addend != nullptr ? addend : reinterpret_cast<const uint16_t*>(hid))[row0 + (tid & 15)];
   int eslot[KMAX];
 #pragma unroll
   for (int e = 0; e < KMAX; ++e) eslot[e] = ws_slots[e];
+  {
+    // the tile's scale / bias runs (one per wave: 32 GK <= 1 KiB), before the codes
+    const int run = 32 * GK;   // 16 rows x GK bf16
+#pragma unroll
+    for (int r0 = 0; r0 < 2 * KMAX; r0 += DN_WAVES) {
+      const int r = r0 + wave;
+      if (r < 2 * k) {
+        int ps = eslot[0];
+#pragma unroll
+        for (int e = 1; e < KMAX; ++e) ps = e == (r >> 1) ? eslot[e] : ps;
+        ps = max(ps, 0);   // a missing expert's rows are never used
+        const uint8_t* src = pool + (int64_t)ps * L.record_bytes + ((r & 1) ? L.off[5] : L.off[4]) +
+                             (int64_t)row0 * GK * 2;
+        tile::lds_load16_untracked(src + min(16 * lane, run - 16), reinterpret_cast<uint8_t*>(s.sc[r >> 1][r & 1]));
+      }
+    }
+  }
   uint4 c2[MAXM][2];
   int it_e[MAXM], it_q[MAXM];
   bool on[MAXM];
@@ -331,23 +367,9 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
     c2[m][0] = r2[0];
     c2[m][1] = r2[1];
   }
-  {
-    const int run = 32 * GK;   // 16 rows x GK bf16
-#pragma unroll
-    for (int r0 = 0; r0 < 2 * KMAX; r0 += DN_WAVES) {
-      const int r = r0 + wave;
-      if (r < 2 * k) {
-        int ps = eslot[0];
-#pragma unroll
-        for (int e = 1; e < KMAX; ++e) ps = e == (r >> 1) ? eslot[e] : ps;
-        ps = max(ps, 0);   // a missing expert's rows are never used
-        copy_to_lds_untracked(pool + (int64_t)ps * L.record_bytes + ((r & 1) ? L.off[5] : L.off[4]) +
-                                  (int64_t)row0 * GK * 2,
-                              reinterpret_cast<uint8_t*>(s.sc[r >> 1][r & 1]), run, 0, 1, lane);
-      }
-    }
-  }
-  tile::wait_vmem();
+  // the copies, issued before the 2 MAXM code loads, have landed (loads complete in
+  // issue order); the codes stay in flight, each item waits for its own
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * MAXM));
   lds_sync();
 
   // ---- 1. items, in interleaved groups (every item's A operands, then each MFMA step
@@ -385,7 +407,7 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
     float total = 0.0f;
     for (int e = 0; e < k; ++e) total = total + s.y[e][tid];
     if (routed) routed[n] = total;
-    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(addend[n]) : total);
+    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(add_bits) : total);
   }
 }
 

@@ -5,9 +5,8 @@
 // tie to the larger index, rank order (argpartition(-sel)) to the lower one;
 // NaN never wins (it ranks as -inf) and -0 ties with +0, as float comparison
 // has it.  Each value becomes an order-preserving u32 key, so one round is a
-// u32 max over the lane's EPT keys, four DPP steps inside rows of 16 lanes and
-// four lane reads; the index rule is a second such max over the indices of the
-// holders of the maximum, and the winner's owner clears its key.
+// u32 max over the lane's EPT keys and over the wave (DPP), then the index rule
+// on the ballots of the maximum's holders, and the winner's owner clears its key.
 #pragma once
 
 #include "common.h"
@@ -23,12 +22,31 @@ __device__ __forceinline__ uint32_t topk_key(float s) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// u32 max over the wave, returned to every lane (uniform): the row maxima by four
+// DPP steps (every lane of a row of 16 ends with its row's maximum), then the
+// row broadcasts 15 and 31 carry rows 0-1 into rows 1-3, so lane 63 holds the
+// maximum of all four rows.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t m) {
+  m = max(m, xor1_u32(m));
+  m = max(m, xor2_u32(m));
+  m = max(m, mirror8_u32(m));
+  m = max(m, mirror16_u32(m));
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x142, 0xa, 0xf, false));   // row_bcast:15
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x143, 0xc, 0xf, false));   // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
+}
+
 // Writes top_i[pos] / top_v[pos] (winner index and its raw score), pos = k-1-r
 // (ascending order) or r (rank order) for round r, and, with a slot table,
 // top_s[pos] = slot_table[winner] (the table is read with the scores, so the
 // slot costs no dependent load).  COHERENT: the scores are read with agent-scope
 // loads (written by other workgroups of the running kernel).  Requires
 // E <= 64 * EPT and 1 <= k <= E.
+//
+// A round: the wave maximum of the keys, then one ballot per key register of the
+// holders of that maximum; the winner is found from the ballots with scalar bit
+// scans -- the highest index holding it (ascending order) or the lowest (rank
+// order) -- so ties cost nothing extra, and its owner clears its key.
 template <int EPT, bool COHERENT = false>
 __device__ __forceinline__ void wave_topk(const float* __restrict__ scores, const float* __restrict__ bias, int E,
                                           int k, int order, int* top_i, float* top_v,
@@ -52,33 +70,21 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ scores, cons
     uint32_t m = key[0];
 #pragma unroll
     for (int j = 1; j < EPT; ++j) m = max(m, key[j]);
-    m = max(m, xor1_u32(m));
-    m = max(m, xor2_u32(m));
-    m = max(m, mirror8_u32(m));
-    m = max(m, mirror16_u32(m));
-    const uint32_t mu = max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
-                            max((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
-    // winner among the holders of the maximum: ascending order takes the largest
-    // index, rank order the smallest -- a second u32 max, over (index rank + 1)
-    // of the lane's holders (0: none)
-    uint32_t cj[EPT];
+    const uint32_t mu = wave_max_u32(m);
+    uint64_t hold[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {   // independent selects, then a max tree (short dependency chain)
-      const uint32_t idx = (uint32_t)(lane + 64 * j);
-      cj[j] = key[j] == mu ? (asc ? idx + 1u : 65535u - idx) : 0u;
+    for (int j = 0; j < EPT; ++j) hold[j] = __ballot(key[j] == mu);
+    int win = -1;
+    if (asc) {
+#pragma unroll
+      for (int j = EPT - 1; j >= 0; --j)
+        if (win < 0 && hold[j] != 0) win = 64 * j + 63 - __clzll((long long)hold[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+        if (win < 0 && hold[j] != 0) win = 64 * j + __ffsll((long long)hold[j]) - 1;
     }
-#pragma unroll
-    for (int w = 1; w < EPT; w *= 2)
-#pragma unroll
-      for (int j = 0; j + w < EPT; j += 2 * w) cj[j] = max(cj[j], cj[j + w]);
-    uint32_t c = cj[0];
-    c = max(c, xor1_u32(c));
-    c = max(c, xor2_u32(c));
-    c = max(c, mirror8_u32(c));
-    c = max(c, mirror16_u32(c));
-    const uint32_t cu = max(max((uint32_t)__builtin_amdgcn_readlane((int)c, 0), (uint32_t)__builtin_amdgcn_readlane((int)c, 16)),
-                            max((uint32_t)__builtin_amdgcn_readlane((int)c, 32), (uint32_t)__builtin_amdgcn_readlane((int)c, 48)));
-    const int win = asc ? (int)cu - 1 : 65535 - (int)cu;
+    win = __builtin_amdgcn_readfirstlane(win);
     const int wl = win & 63, wj = win >> 6;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) key[j] = (j == wj && lane == wl) ? 0u : key[j];

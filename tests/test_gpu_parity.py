@@ -179,6 +179,13 @@ def test_router_ties_follow_order_rule(cuda):
     b.zero_()
     for order in ("ascending", "rank"):
         _check_router(cuda, x, w, b, k=7, score="sigmoid", order=order, temp=1.0, scale=1.0, norm=True)
+    # ties between experts e and e + 64 and e + 128 (held by one lane in different key registers)
+    x, w, b = _router_inputs(cuda, T, D, 384)
+    w[64:128] = w[0:64]
+    w[128:192] = w[0:64]
+    b.zero_()
+    for order in ("ascending", "rank"):
+        _check_router(cuda, x, w, b, k=9, score="sqrt_softplus", order=order, temp=1.0, scale=1.0, norm=True)
 
 
 def test_router_bias_vl_and_mask(cuda):
