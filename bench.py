@@ -27,7 +27,7 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per decode (gate/up + down kernels) at config 1, from two rocprofv3
 # counter passes (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
 # plain 1 GiB device copy (read x 2.0, write x 1.0); summary under profiles/.
-PAIR_TRAFFIC_BYTES = 61_416_756
+PAIR_TRAFFIC_BYTES = 61_412_659
 METRIC = "MoE-layer decode tok/s + expert-byte HBM GB/s (B=1); prefill grouped-GEMM TFLOPS"
 
 
@@ -49,6 +49,9 @@ def parse():
                     help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
+    ap.add_argument("--only", choices=("prefill", "batched"),
+                    help="profiling aid: run one secondary measurement alone (config 3 prefill, or config 2 "
+                         "batched decode over --layers resident layers), print its JSON and exit")
     return ap.parse_args()
 
 
@@ -415,8 +418,8 @@ def prefill_config3(args, dev, log_fn):
                         "note": "1.739 TFLOP over >= the touched experts' FP4 bytes: 256 FLOP/B, below the MXFP4 "
                                 "ridge (1,250 FLOP/B), so the attainable bound is HBM"},
            "_counts": counts.cpu().tolist(),
-           "note": "exact bf16-MFMA path (FP4 dequantised to bf16 in registers), routing + permute + "
-                   "grouped gate/up + down + combine, eager launches"}
+           "note": "block-scaled fp8 x fp4 matrix cores (x and h as two exact fp8 planes, FP4 codes and E8M0 "
+                   "scales as stored), routing + permute + grouped gate/up + down + combine, eager launches"}
     log_fn(f"config 3 prefill: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s, {touched} experts touched, "
            f"max {int(counts.max())} rows/expert")
     del store
@@ -658,6 +661,12 @@ def main() -> int:
     from cachalot_amd.storage.index import affine_format
 
     dev = torch.device("cuda:0")
+    if args.only == "prefill":
+        _lib.lib()
+        res = prefill_config3(args, dev, log)
+        res.pop("_counts")
+        print(json.dumps(res), flush=True)
+        return 0
     _lib.lib()
     D, F, E, K = 4096, 2880, 384, 6
     L = args.layers
@@ -672,6 +681,9 @@ def main() -> int:
     x0 = synth.activations(args.seed, 0, 1, D, dev)[0]
     torch.cuda.synchronize()
     log(f"bank ready in {time.time() - t0:.1f} s")
+    if args.only == "batched":
+        print(json.dumps(batched_decode(args, store, gates, log)), flush=True)
+        return 0
 
     pool = store.pool
 
