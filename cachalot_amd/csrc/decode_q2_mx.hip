@@ -517,9 +517,11 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
 
   // the first row's planes, then the tile's scale chunks and codes
   copy_to_lds_untracked(a.xplanes + (size_t)a.row_token[r0] * pbytes, s.planes[0], pbytes, wave, GU_WAVES, lane);
+  // (unconditional: a missing expert reads slot 0's bytes and discards them, so the
+  // code registers are defined on one path and the compiler copies none of them)
   uint4 c1[MAXM][2], c3[MAXM][2];
-  if (live) {
-    const uint8_t* base = a.pool + (int64_t)slot * a.L.record_bytes;
+  {
+    const uint8_t* base = a.pool + (int64_t)max(slot, 0) * a.L.record_bytes;
     // wave w: the 16 rows' run of scale / bias tensor w (whole lines)
     const int64_t toff = wave == 0 ? a.L.off[1] : wave == 1 ? a.L.off[2] : wave == 2 ? a.L.off[7] : a.L.off[8];
     copy_to_lds_untracked(base + toff + (int64_t)row0 * GT * 2, reinterpret_cast<uint8_t*>(s.sc[wave]), 32 * GT, 0,
@@ -536,7 +538,9 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
       c3[m][1] = w3[1];
     }
   }
-  tile::wait_vmem();
+  // the copies (issued first) have landed; the codes stay in flight, each item waits
+  // for its own
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * MAXM));
   lds_sync();
   const ARole ro = a_role(lane);
   Chain ch;
@@ -553,6 +557,12 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
     for (int m = 0; m < MAXM; ++m) {
       const int q = wave + GU_WAVES * m;
       if (!live || q >= NQ) break;
+      // items in order, each waiting only for its own codes (the asm pins the codes'
+      // first use here, so their conversion is not hoisted above the earlier items)
+      asm volatile("" : "+v"(c1[m][0].x), "+v"(c1[m][0].y), "+v"(c1[m][0].z), "+v"(c1[m][0].w),
+                   "+v"(c1[m][1].x), "+v"(c1[m][1].y), "+v"(c1[m][1].z), "+v"(c1[m][1].w)::"memory");
+      asm volatile("" : "+v"(c3[m][0].x), "+v"(c3[m][0].y), "+v"(c3[m][0].z), "+v"(c3[m][0].w),
+                   "+v"(c3[m][1].x), "+v"(c3[m][1].y), "+v"(c3[m][1].z), "+v"(c3[m][1].w)::"memory");
       f32x4_t a1 = mx::zero_acc(), a3 = mx::zero_acc();
       chain_load(ch, planes + (4 * q + ro.kgR) * PB_BYTES, ro);
       a1 = mx::mfma_fp8_fp4<0>(ch.a[0], mx::q2_spread(c1[m][0].x, c1[m][0].y), a1, ch.sa, mx::E8M0_TWO);
@@ -659,9 +669,11 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn4_kernel(BatchArgs a) {
   const int hbytes = GK * PB_BYTES;
 
   copy_to_lds_untracked(a.hid + (size_t)r0 * hbytes, s.planes[0], hbytes, wave, GU_WAVES, lane);
+  // (unconditional: a missing expert reads slot 0's bytes and discards them, so the
+  // code registers are defined on one path and the compiler copies none of them)
   uint4 c2[MAX_NQ2][2];
-  if (live) {
-    const uint8_t* base = a.pool + (int64_t)slot * a.L.record_bytes;
+  {
+    const uint8_t* base = a.pool + (int64_t)max(slot, 0) * a.L.record_bytes;
     const int run = 32 * GK;
     copy_to_lds_untracked(base + a.L.off[4] + (int64_t)n0 * GK * 2, reinterpret_cast<uint8_t*>(s.sc[wave][0]), run,
                           0, 1, lane);
@@ -675,7 +687,9 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn4_kernel(BatchArgs a) {
       c2[m][1] = w2[1];
     }
   }
-  tile::wait_vmem();
+  // the copies (issued first) have landed; the codes stay in flight, each item waits
+  // for its own
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * MAX_NQ2));
   lds_sync();
   const ARole ro = a_role(lane);
   Chain ch;
@@ -691,6 +705,10 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn4_kernel(BatchArgs a) {
 #pragma unroll
     for (int m = 0; m < MAX_NQ2; ++m) {
       if (!live || m >= NQ2) break;
+      // items in order, each waiting only for its own codes (the asm pins the codes'
+      // first use here, so their conversion is not hoisted above the earlier items)
+      asm volatile("" : "+v"(c2[m][0].x), "+v"(c2[m][0].y), "+v"(c2[m][0].z), "+v"(c2[m][0].w),
+                   "+v"(c2[m][1].x), "+v"(c2[m][1].y), "+v"(c2[m][1].z), "+v"(c2[m][1].w)::"memory");
       const int g2 = 4 * m + kg;
       f32x4_t acc = mx::zero_acc();
       chain_load(ch, planes + min(4 * m + ro.kgR, GK - 1) * PB_BYTES, ro);
