@@ -49,9 +49,10 @@ def parse():
                     help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=("prefill", "batched"),
-                    help="profiling aid: run one secondary measurement alone (config 3 prefill, or config 2 "
-                         "batched decode over --layers resident layers), print its JSON and exit")
+    ap.add_argument("--only", choices=("prefill", "batched", "fp4"),
+                    help="profiling aid: run one secondary measurement alone (config 3 prefill, config 2 "
+                         "batched decode over --layers resident layers, or config 0 FP4 decode), print its JSON "
+                         "and exit")
     return ap.parse_args()
 
 
@@ -666,6 +667,10 @@ def main() -> int:
         res = prefill_config3(args, dev, log)
         res.pop("_counts")
         print(json.dumps(res), flush=True)
+        return 0
+    if args.only == "fp4":
+        _lib.lib()
+        print(json.dumps(fp4_decode_config0(args, dev, log)), flush=True)
         return 0
     _lib.lib()
     D, F, E, K = 4096, 2880, 384, 6

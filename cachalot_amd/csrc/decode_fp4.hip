@@ -41,6 +41,18 @@ constexpr int ZERO_BYTES = 64;                   // 4 steps x 16 bytes
 constexpr int GU_ZERO = MAX_D * 2;
 constexpr int DN_ZERO = MAX_KF * 4;
 
+// Copy `bytes` (a multiple of 16) into LDS with untracked direct-to-LDS loads, 1 KiB
+// chunks c = part, part + parts, ... (tile::lds_load16_untracked); the caller waits.
+__device__ __forceinline__ void copy_untracked(const void* src, uint8_t* dst, int bytes, int part, int parts,
+                                               int lane) {
+  for (int c = __builtin_amdgcn_readfirstlane(part) * 1024; c < bytes; c += parts * 1024)
+    if (c + 16 * lane < bytes)
+      lds_load16_untracked(reinterpret_cast<const uint8_t*>(src) + c + 16 * lane, dst + c);
+}
+
+// s_waitcnt with vmcnt(n), expcnt and lgkmcnt unconstrained (gfx9 encoding, n < 64).
+#define VMCNT(n) (0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+
 template <int NB>
 __device__ __forceinline__ void lane_pieces(int first, int PW, int pieces, int kg, int (&pi)[NB], bool (&pv)[NB]) {
 #pragma unroll
@@ -62,7 +74,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   __shared__ __align__(16) uint8_t sc[2 * 16 * (MAX_D / PIECE)];   // s1, s3 of the tile's rows
   __shared__ float red[GU_WAVES][2][16];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int PT = D / PIECE;
   const int tiles = F / 16;
   const int e = blockIdx.x / tiles;
@@ -72,9 +84,12 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   __shared__ float top_v[GU_WAVES][KMAX], top_w[GU_WAVES][KMAX];
   __shared__ int top_s[GU_WAVES][KMAX];
   const int slot = route_slot(src, ws_slots, e, top_i[wave], top_v[wave], top_s[wave]);
-  if (src.scores && tile == 0 && threadIdx.x == 0) ws_slots[e] = slot;   // read by the down kernel
+  // the slot for the down kernel is stored at the end (a store's data registers stay
+  // busy until it completes, and the compiler would wait for it before the loads)
+  const bool store_slot = src.scores && tile == 0 && threadIdx.x == 0;
   uint16_t* hout = hidden + (size_t)e * F * 2;   // per expert: hi [F], lo [F] (bf16)
   if (slot < 0) {
+    if (store_slot) ws_slots[e] = slot;
     if (threadIdx.x < 16) {
       hout[row0 + threadIdx.x] = hout[F + row0 + threadIdx.x] = 0;
       route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0], blockIdx.x == 0);
@@ -89,6 +104,12 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   bool pv[NB];
   lane_pieces<NB>(wave * PW, PW, PT, kg, pi, pv);
 
+  // the tile's scales (two runs of 16 rows x PT bytes) and the activations into LDS
+  // first, then the codes; the barrier waits for the copies only, and each block of
+  // codes is consumed as it lands
+  copy_untracked(base + L.off[1] + (int64_t)row0 * PT, sc, 16 * PT, wave, GU_WAVES, lane);
+  copy_untracked(base + L.off[7] + (int64_t)row0 * PT, sc + 16 * PT, 16 * PT, (wave + 2) & 3, GU_WAVES, lane);
+  copy_untracked(x, xl, D * 2, wave, GU_WAVES, lane);
   uint4 wg[NB], wu[NB];
   {
     const uint4* r1 = reinterpret_cast<const uint4*>(base + L.off[0]) + (size_t)row * PT;
@@ -99,13 +120,9 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
       wu[b] = r3[pi[b]];
     }
   }
-  // the tile's scales (two runs of 16 rows x PT bytes) and the activations into LDS
-  dma_to_lds(base + L.off[1] + (int64_t)row0 * PT, sc, 16 * PT, wave, GU_WAVES, lane);
-  dma_to_lds(base + L.off[7] + (int64_t)row0 * PT, sc + 16 * PT, 16 * PT, (wave + 2) & 3, GU_WAVES, lane);
-  dma_to_lds(x, xl, D * 2, wave, GU_WAVES, lane);
   if (threadIdx.x < ZERO_BYTES / 16) reinterpret_cast<uint4*>(xl + GU_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
-  wait_vmem();
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(VMCNT(2 * NB));
+  lds_sync();
 
   f32x4_t cg = {0.0f, 0.0f, 0.0f, 0.0f}, cu = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -126,6 +143,7 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
   }
   __syncthreads();
   if (threadIdx.x < 16) {
+    if (store_slot) ws_slots[e] = slot;
     const float wexp = route_finish(src, ws_w, e, tile, top_v[0], top_w[0], top_i[0], blockIdx.x == 0);
     const int t = threadIdx.x;
     float g = 0.0f, u = 0.0f;
@@ -155,7 +173,7 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   __shared__ __align__(16) uint8_t sc[MAX_KF / 2];              // per expert: s2 of the tile's rows
   __shared__ float vals[KMAX][DN_HALVES][16];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
   const int PK = F / PIECE;
   const int e = wave / DN_HALVES;
@@ -168,23 +186,28 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   bool pv[NB];
   lane_pieces<NB>(half * PW, PW, PK, kg, pi, pv);
 
+  // hidden hi / lo parts and, per expert, the tile's scales (16 rows x PK bytes) into
+  // LDS first, then the codes (unconditional: a missing expert reads slot 0's bytes and
+  // discards them); the barrier waits for the copies only
+  // (wave r < k copies expert r's scales: 2k waves >= k; its slot is read with the wave's own)
+  const int ps = __builtin_amdgcn_readfirstlane(max(expert_slot(src, ws_slots, min(wave, k - 1)), 0));
+  // (both slots are in scalar registers before any copy is issued: a wait for them
+  // would otherwise wait for the copies too)
+  const int slot_s = __builtin_amdgcn_readfirstlane(slot);
+  copy_untracked(hidden, hl, k * F * 4, wave, nwaves, lane);
+  if (wave < k)
+    copy_untracked(pool + (int64_t)ps * L.record_bytes + L.off[4] + (int64_t)row0 * PK, sc + wave * 16 * PK, 16 * PK,
+                   0, 1, lane);
   uint4 wd[NB];
-  if (slot >= 0) {
-    const uint4* r2 =
-        reinterpret_cast<const uint4*>(pool + (int64_t)slot * L.record_bytes + L.off[3]) + (size_t)(row0 + j) * PK;
+  {
+    const uint4* r2 = reinterpret_cast<const uint4*>(pool + (int64_t)max(slot_s, 0) * L.record_bytes + L.off[3]) +
+                      (size_t)(row0 + j) * PK;
 #pragma unroll
     for (int b = 0; b < NB; ++b) wd[b] = r2[pi[b]];
   }
-  // hidden hi / lo parts and, per expert, the tile's scales (16 rows x PK bytes) into LDS
-  dma_to_lds(hidden, hl, k * F * 4, wave, nwaves, lane);
-  for (int r = wave; r < k; r += nwaves) {
-    const int ps = max(expert_slot(src, ws_slots, r), 0);   // a missing expert's rows are never used
-    dma_to_lds(pool + (int64_t)ps * L.record_bytes + L.off[4] + (int64_t)row0 * PK, sc + r * 16 * PK, 16 * PK, 0, 1,
-               lane);
-  }
   if (threadIdx.x < ZERO_BYTES / 16) reinterpret_cast<uint4*>(hl + DN_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
-  wait_vmem();
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(VMCNT(NB));
+  lds_sync();
 
   f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
   if (slot >= 0) {
