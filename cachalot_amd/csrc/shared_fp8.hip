@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs p) {
 constexpr int DEC_MT = 4;
 constexpr int DEC_MAX_K = 5120;
 #ifndef CACHALOT_DEC_WAVES
-#define CACHALOT_DEC_WAVES 8
+#define CACHALOT_DEC_WAVES 16
 #endif
 constexpr int DEC_WAVES = CACHALOT_DEC_WAVES;      // waves per workgroup (they split K)
 constexpr int DEC_PF = 32 / DEC_WAVES;             // chunks of weights in flight per wave
