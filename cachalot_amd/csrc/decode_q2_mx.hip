@@ -447,18 +447,37 @@ struct BGuLds {
   float red[GU_WAVES * MAXM][2][16];
 };
 
-// One launch before the batched kernels, grid 1 + T * ceil(D / 4096), 1024 threads:
+// One launch before the batched kernels, grid 2 + T * ceil(D / 4096), 1024 threads:
 //   workgroup 0: the record (expert, first row, end row, slot) of every expert with
 //     rows, experts ascending, and their count -- so a batched workgroup reads one
 //     record and issues its weight loads, with no dependent lookup in between;
+//   the last: zero y rows of the dropped routes (rows [offsets[E], n) of the
+//     permutation; entries outside [0, T) x [0, k) skipped), so the combine adds
+//     nothing for them -- the batched path's own copy of the grouped drop pass;
 //   the others: x (T tokens) as plane blocks, 1024 quads each.
 constexpr int PREP_THREADS = 1024;
 __global__ void __launch_bounds__(PREP_THREADS) batch_prep_kernel(const uint16_t* __restrict__ x, int T, int D,
                                                                   uint8_t* __restrict__ xplanes,
                                                                   const int32_t* __restrict__ offsets, int E,
                                                                   const int32_t* __restrict__ slot_table,
-                                                                  int4* __restrict__ recs, int32_t* __restrict__ n_recs) {
+                                                                  int4* __restrict__ recs, int32_t* __restrict__ n_recs,
+                                                                  int n, int k, const int32_t* __restrict__ row_token,
+                                                                  const int32_t* __restrict__ row_slot,
+                                                                  uint16_t* __restrict__ y) {
   const int tid = threadIdx.x;
+  if (blockIdx.x == gridDim.x - 1) {
+    const int first = offsets[E];
+    const int per_row = D / 8;   // 16-byte stores
+    const int total = max(n - first, 0) * per_row;
+    for (int i = tid; i < total; i += PREP_THREADS) {
+      const int r = first + i / per_row;
+      const int c = i - (r - first) * per_row;
+      const int t = row_token[r], sl = row_slot[r];
+      if (t < 0 || t >= T || sl < 0 || sl >= k) continue;
+      reinterpret_cast<uint4*>(y + ((size_t)t * k + sl) * D)[c] = uint4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
   if (blockIdx.x > 0) {
     const int per_row = (D + 4095) / 4096;
     const int t = (blockIdx.x - 1) / per_row;
@@ -782,8 +801,8 @@ int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const Lay
                         const int32_t* offsets, int E, int4* recs, int32_t* n_recs, int max_active,
                         const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k,
                         float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s) {
-  hipLaunchKernelGGL(batch_prep_kernel, dim3(1 + T * ((D + 4095) / 4096)), dim3(PREP_THREADS), 0, s, x, T, D, xplanes,
-                     offsets, E, slot_table, recs, n_recs);
+  hipLaunchKernelGGL(batch_prep_kernel, dim3(2 + T * ((D + 4095) / 4096)), dim3(PREP_THREADS), 0, s, x, T, D, xplanes,
+                     offsets, E, slot_table, recs, n_recs, T * k, k, row_token, row_slot, y);
   int rc = check_launch("batch_prep_kernel");
   if (rc) return rc;
   BatchArgs a{xplanes, pool, L, recs, n_recs, row_token, row_slot, row_w, D, F, k, limit, hid, y};

@@ -839,15 +839,16 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   // tiles of 64 rows when experts see many tokens, 16 for batched decode
   const int MT = T * k >= 4 * E ? 64 : 16;
   uint32_t* zeros = reinterpret_cast<uint32_t*>(ws + wo.tiles_n + 128);
-  hipLaunchKernelGGL(drop_zero_kernel, dim3(16), dim3(256), 0, s, offsets, E, T * k, T, k, D, row_token, row_slot, y);
-  rc = check_launch("drop_zero_kernel");
-  if (rc) return rc;
   if (KIND == KIND_Q2 && MT == 16 && q2mx_supported(D, F, k) && !small_tiles_requested()) {
     // few rows per expert: the matrix-core batched decode, one entry per active expert
+    // (its prep launch also clears the dropped routes' y rows)
     return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, E, reinterpret_cast<int4*>(ws + wo.tiles),
                                tiles_n, std::min(E, T * k), row_token, row_slot, row_w, D, F, k, limit,
                                ws + wo.hidden, ws + wo.xplanes, y, s);
   }
+  hipLaunchKernelGGL(drop_zero_kernel, dim3(16), dim3(256), 0, s, offsets, E, T * k, T, k, D, row_token, row_slot, y);
+  rc = check_launch("drop_zero_kernel");
+  if (rc) return rc;
   const int max_tiles = (T * k) / MT + std::min(E, T * k) + 1;
   if (KIND == KIND_FP4 && MT == 64 && prefill_mx_supported(D, F, L) && !small_tiles_requested() &&
       !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
