@@ -140,6 +140,67 @@ __global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __r
   }
 }
 
+// n <= 1024 routes (batched decode): the count, the scan and the scatter of the two
+// kernels above in one workgroup, thread i owning route i.  A route's place inside
+// its expert is the number of earlier routes with the same key (the expert, or E for
+// an id outside [0, E)), so rows stay in route order as the scatter kernel leaves them.
+__global__ void __launch_bounds__(PERMUTE_THREADS) permute_small_kernel(const int32_t* __restrict__ idx,
+                                                                        const float* __restrict__ w, int n, int k,
+                                                                        int E, int32_t* __restrict__ offsets,
+                                                                        int32_t* __restrict__ row_token,
+                                                                        int32_t* __restrict__ row_slot,
+                                                                        float* __restrict__ row_w) {
+  __shared__ int cnt[1024 + 1];
+  __shared__ int off[1024 + 1];
+  __shared__ __align__(16) int key[PERMUTE_THREADS];
+  __shared__ int wave_tot[PERMUTE_THREADS / 64];
+  const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
+  for (int e = i; e <= E; e += PERMUTE_THREADS) cnt[e] = 0;
+  int id = i < n ? idx[i] : 0;
+  const float wi = i < n ? w[i] : 0.0f;
+  const int my = id >= 0 && id < E ? id : E;
+  key[i] = i < n ? my : -1;
+  __syncthreads();
+  if (i < n && my < E) atomicAdd(&cnt[my], 1);
+  __syncthreads();
+  const int c = i < E ? cnt[i] : 0;
+  int v = c;
+#pragma unroll
+  for (int d = 1; d < 64; d *= 2) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) wave_tot[wave] = v;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int q = 0; q < PERMUTE_THREADS / 64; ++q) {
+    before += q < wave ? wave_tot[q] : 0;
+    total += wave_tot[q];
+  }
+  if (i < E) {
+    off[i] = before + v - c;
+    offsets[i] = before + v - c;
+  }
+  if (i == 0) {
+    off[E] = total;
+    offsets[E] = total;
+  }
+  __syncthreads();
+  if (i >= n) return;
+  int rank = 0;
+  const int4* k4 = reinterpret_cast<const int4*>(key);
+  for (int j = 0; j < (i >> 2); ++j) {
+    const int4 q = k4[j];
+    rank += (q.x == my) + (q.y == my) + (q.z == my) + (q.w == my);
+  }
+  for (int j = i & ~3; j < i; ++j) rank += key[j] == my;
+  const int pos = off[my] + rank;
+  row_token[pos] = i / k;
+  row_slot[pos] = i - (i / k) * k;
+  row_w[pos] = my == E ? 0.0f : wi;
+}
+
 // y rows of the dropped routes (rows [offsets[E], n) of the permutation) are
 // zero, so the combine adds nothing for them.  Runs before the expert kernels:
 // rows a caller's own permutation left undefined there are overwritten by the
@@ -894,6 +955,11 @@ extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k
   CACHALOT_REQUIRE(T >= 1 && k >= 1 && (int64_t)T * k <= (1 << 30), "permute: T=%d k=%d", T, k);
   CACHALOT_REQUIRE(E >= 1 && E <= 1024, "permute: E=%d outside 1..1024", E);
   hipStream_t s = (hipStream_t)stream;
+  if (T * k <= PERMUTE_THREADS) {
+    hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(PERMUTE_THREADS), 0, s, idx, w, T * k, k, E, offsets,
+                       row_token, row_slot, row_w);
+    return check_launch("permute_small_kernel");
+  }
   hipLaunchKernelGGL(permute_count_kernel, dim3(1), dim3(PERMUTE_THREADS), 0, s, idx, T * k, E, offsets);
   int rc = check_launch("permute_count_kernel");
   if (rc) return rc;

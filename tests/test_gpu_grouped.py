@@ -88,13 +88,21 @@ def test_permute_matches_oracle(cuda):
     from cachalot_amd.moe_prefill import permute
 
     rng = np.random.default_rng(3)
-    for t, k, e in [(1, 6, 384), (5, 1, 7), (300, 6, 384), (1000, 8, 64)]:
+    # one-workgroup permute up to 1024 routes, the two-kernel one past it; the last
+    # two cases carry ids outside [0, E) (dropped routes, weight 0, after every expert)
+    cases = [(1, 6, 384), (5, 1, 7), (170, 6, 384), (171, 6, 384), (128, 8, 1024), (300, 6, 384), (1000, 8, 64),
+             (32, 6, 384), (200, 6, 64)]
+    for n_case, (t, k, e) in enumerate(cases):
         idx, w = _zipf_routes(rng, t, k, np.arange(e))
+        if n_case >= len(cases) - 2:
+            idx = idx.copy()
+            idx[0, 1], idx[t // 2, 0], idx[t - 1, k - 1] = -3, e, 1 << 30
         offs, tok, slot, rw = permute(torch.from_numpy(idx).to(cuda), torch.from_numpy(w).to(cuda), e)
         p = odispatch.permute(idx, e)
         assert np.array_equal(_np(offs), p["offsets"])
         assert np.array_equal(_np(tok), p["token"]) and np.array_equal(_np(slot), p["slot"])
-        assert np.array_equal(_np(rw), w[p["token"], p["slot"]])
+        keep = (idx >= 0) & (idx < e)
+        assert np.array_equal(_np(rw), np.where(keep, w, 0)[p["token"], p["slot"]])
 
 
 def test_permute_errors(cuda):
