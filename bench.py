@@ -49,10 +49,10 @@ def parse():
                     help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=("prefill", "batched", "fp4"),
+    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared"),
                     help="profiling aid: run one secondary measurement alone (config 3 prefill, config 2 "
-                         "batched decode over --layers resident layers, or config 0 FP4 decode), print its JSON "
-                         "and exit")
+                         "batched decode over --layers resident layers, config 0 FP4 decode, or config 1's layer "
+                         "with the FP8 shared expert), print its JSON and exit")
     return ap.parse_args()
 
 
@@ -688,6 +688,9 @@ def main() -> int:
     log(f"bank ready in {time.time() - t0:.1f} s")
     if args.only == "batched":
         print(json.dumps(batched_decode(args, store, gates, log)), flush=True)
+        return 0
+    if args.only == "shared":
+        print(json.dumps(layer_with_shared(args, store, gates, log)), flush=True)
         return 0
 
     pool = store.pool

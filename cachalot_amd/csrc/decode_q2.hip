@@ -27,6 +27,7 @@
 #include <mutex>
 
 #include "decode_common.h"
+#include "fp8_common.h"
 #include "mfma_tile.h"
 #include "router_launch.h"
 
@@ -348,10 +349,26 @@ size_t q2_workspace_bytes(int D, int F, int k) {
 // With `router` the experts come from the router tail, else from src.idx / src.w.
 
 bool q2mx_supported(int D, int F, int k);
+bool q2mx_shared_supported(int D, int F_sh);
 int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, const uint8_t* pool,
                        const Layout& L, const ExpertSource& src, int32_t* ws_slots, float* ws_w, int D, int F,
                        int k, float limit, const uint16_t* addend, float* routed, uint16_t* out, uint8_t* hid,
-                       hipStream_t s);
+                       hipStream_t s, const fp8::DecodeArgs* sh_gu, const fp8::DecodeArgs* sh_dn);
+namespace fp8 {
+int launch_decode(const uint16_t* x, const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, const uint8_t* s3,
+                  const uint8_t* w2, const uint8_t* s2, int M, int D, int F, float limit, uint16_t* h, uint16_t* y,
+                  hipStream_t s);
+}
+
+// The FP8 shared expert of a decode layer (E4M3 weights, E8M0 block-32 scales):
+// w1, w3 [F, D] with scales [F / 32, D / 32], w2 [D, F] with [D / 32, F / 32].
+struct SharedFp8 {
+  const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;
+  int F;
+};
+// After the routed workspace: h_sh [F] bf16, then y_sh [D] bf16 (used when the
+// shared expert runs in launches of its own).
+static size_t shared_region_bytes(int D, int F_sh) { return align256((size_t)F_sh * 2) + align256((size_t)D * 2); }
 
 // The bf16 kernels stay selectable (CACHALOT_DECODE_BF16=1) for comparison.
 static bool bf16_requested() {
@@ -362,7 +379,7 @@ static bool bf16_requested() {
 int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
                      ExpertSource src, const RouterCall* router, int D, int F, int k, int group, float swiglu_limit,
                      const uint16_t* addend, float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
-                     hipStream_t s) {
+                     hipStream_t s, const SharedFp8* shared = nullptr) {
   CACHALOT_REQUIRE(pool && layout && src.slot_table && x, "moe_decode_q2: null pointer");
   CACHALOT_REQUIRE(routed || out, "moe_decode_q2: no output requested");
   CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_q2: k=%d outside 1..%d", k, KMAX);
@@ -373,7 +390,7 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   CACHALOT_REQUIRE(F % 16 == 0 && F >= 64 && F <= GROUP * MAX_F_GROUPS,
                    "moe_decode_q2: F=%d must be a multiple of 16 in 64..4096", F);
   const WsOffsets wo = ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t));
-  const size_t need = q2_workspace_bytes(D, F, k);
+  const size_t need = q2_workspace_bytes(D, F, k) + (shared ? shared_region_bytes(D, shared->F) : 0);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(CACHALOT_ESPACE, "moe_decode_q2: workspace %zu < %zu bytes", workspace_bytes, need);
   Layout L;
@@ -403,9 +420,26 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
     src.idx = nullptr;
     src.w = nullptr;
   }
+  if (shared) {
+    uint16_t* h_sh = reinterpret_cast<uint16_t*>(ws + q2_workspace_bytes(D, F, k));
+    uint16_t* y_sh = h_sh + align256((size_t)shared->F * 2) / 2;
+    if (mx && q2mx_shared_supported(D, shared->F)) {   // carried by the routed launches
+      const fp8::DecodeArgs gu{x, D, {shared->w1, shared->w3}, {shared->s1, shared->s3}, 1, shared->F, D,
+                               swiglu_limit, h_sh, shared->F};
+      const fp8::DecodeArgs dn{h_sh, shared->F, {shared->w2, shared->w2}, {shared->s2, shared->s2}, 1, D,
+                               shared->F, swiglu_limit, y_sh, D};
+      return launch_q2mx_decode(x, router != nullptr, xplanes, pool, L, src, ws_slots, ws_w, D, F, k,
+                                swiglu_limit, nullptr, routed, out, ws + wo.total, s, &gu, &dn);
+    }
+    // its own two launches ahead of the experts, y_sh as the addend
+    rc = fp8::launch_decode(x, shared->w1, shared->s1, shared->w3, shared->s3, shared->w2, shared->s2, 1, D,
+                            shared->F, swiglu_limit, h_sh, y_sh, s);
+    if (rc) return rc;
+    addend = y_sh;
+  }
   if (mx)
     return launch_q2mx_decode(x, router != nullptr, xplanes, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit,
-                              addend, routed, out, ws + wo.total, s);
+                              addend, routed, out, ws + wo.total, s, nullptr, nullptr);
   if (G > 0)
     return launch_q2_decode_fused(G, x, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit, addend, routed, out,
                                   ws + wo.sync, ws + wo.total, s);
@@ -487,6 +521,47 @@ extern "C" int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* g
                               route_scale};
   return launch_q2_decode(x, pool, layout, src, &rt, D, F, k, group, swiglu_limit, addend, routed, out, workspace,
                           workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" size_t cachalot_moe_layer_decode_q2_shared_workspace_bytes(int D, int F, int k, int shared_F) {
+  if (D <= 0 || F <= 0 || k <= 0 || k > cachalot::decode::KMAX || shared_F <= 0) return 0;
+  return cachalot::q2_workspace_bytes(D, F, k) + cachalot::shared_region_bytes(D, shared_F);
+}
+
+extern "C" int cachalot_moe_layer_decode_q2_shared(
+    const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias, int E, int k, int score_fn,
+    float gate_temp, float route_scale, int norm, int order, const uint8_t* pool,
+    const cachalot_expert_layout* layout, const int32_t* slot_table, int D, int F, int group, float swiglu_limit,
+    const uint8_t* shared_w1, const uint8_t* shared_w1_scales, const uint8_t* shared_w3,
+    const uint8_t* shared_w3_scales, const uint8_t* shared_w2, const uint8_t* shared_w2_scales, int shared_F,
+    int32_t* idx_out, float* w_out, float* scores, float* routed, uint16_t* out, void* workspace,
+    size_t workspace_bytes, cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(gate_weight && gate_bias && scores, "moe_layer_decode_q2_shared: null router pointer");
+  CACHALOT_REQUIRE(shared_w1 && shared_w1_scales && shared_w3 && shared_w3_scales && shared_w2 && shared_w2_scales,
+                   "moe_layer_decode_q2_shared: null shared expert pointer");
+  CACHALOT_REQUIRE(out, "moe_layer_decode_q2_shared: out is required (it carries the shared expert)");
+  CACHALOT_REQUIRE(D % 128 == 0, "moe_layer_decode_q2_shared: D=%d must be a multiple of 128", D);
+  CACHALOT_REQUIRE(shared_F > 0 && shared_F % 32 == 0 && shared_F <= fp8::DEC_MAX_K && D <= fp8::DEC_MAX_K,
+                   "moe_layer_decode_q2_shared: shared F=%d (a multiple of 32) and D=%d must be at most %d", shared_F,
+                   D, fp8::DEC_MAX_K);
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  CACHALOT_REQUIRE(a16(x) && a16(shared_w1) && a16(shared_w3) && a16(shared_w2),
+                   "moe_layer_decode_q2_shared: x and the shared weights must be 16-byte aligned");
+  CACHALOT_REQUIRE(score_fn == CACHALOT_SCORE_SQRT_SOFTPLUS || score_fn == CACHALOT_SCORE_SIGMOID,
+                   "moe_layer_decode_q2_shared: unknown score function %d", score_fn);
+  CACHALOT_REQUIRE(order == CACHALOT_ORDER_ASCENDING || order == CACHALOT_ORDER_RANK,
+                   "moe_layer_decode_q2_shared: unknown order %d", order);
+  CACHALOT_REQUIRE(gate_temp != 0.0f, "moe_layer_decode_q2_shared: gate_temp must be non-zero");
+  CACHALOT_REQUIRE(k >= 1 && k <= E && E <= 1024, "moe_layer_decode_q2_shared: invalid topk=%d for %d experts", k,
+                   E);
+  decode::ExpertSource src{slot_table, nullptr, nullptr, E};
+  RouterCall rt{gate_weight, score_fn, gate_temp, scores, {}};
+  rt.tail = decode::RouteTail{gate_bias, slot_table, idx_out, w_out, nullptr, nullptr, nullptr, E, k, order, norm,
+                              route_scale};
+  const SharedFp8 sh{shared_w1, shared_w1_scales, shared_w3, shared_w3_scales, shared_w2, shared_w2_scales, shared_F};
+  return launch_q2_decode(x, pool, layout, src, &rt, D, F, k, group, swiglu_limit, nullptr, routed, out, workspace,
+                          workspace_bytes, (hipStream_t)stream, &sh);
 }
 
 // ------------------------------------------------- decode with no allocation ---

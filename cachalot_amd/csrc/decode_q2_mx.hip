@@ -29,6 +29,7 @@
 // (piece, plane) partial sums of a group, then the four groups of a quad
 // (lane-group butterfly), then the quads in order.
 #include "decode_common.h"
+#include "fp8_common.h"
 #include "mfma_tile.h"
 #include "mx_tile.h"
 
@@ -93,25 +94,23 @@ __global__ void __launch_bounds__(256) x_planes_kernel(const uint16_t* __restric
   if (4 * t4 < D) mx::encode_x_quad(xplanes, t4, reinterpret_cast<const uint2*>(x)[t4]);   // whole quads
 }
 
-// grid.x = k * F / 16.  MAXM = ceil(D / 512 / 4) items per wave.
+// Workgroup bid of the gate/up grid (k * F / 16).  MAXM = ceil(D / 512 / 4) items per wave.
 template <int MAXM>
-__global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t* __restrict__ xplanes,
-                                                                  const uint8_t* __restrict__ pool, Layout L,
-                                                                  ExpertSource src, int D, int F, float limit,
-                                                                  uint8_t* __restrict__ hid,
-                                                                  int32_t* __restrict__ ws_slots,
-                                                                  float* __restrict__ ws_w) {
-  __shared__ __align__(16) GuLds s;
+__device__ __forceinline__ void q2mx_gate_up_body(GuLds& s, const int bid, const uint8_t* __restrict__ xplanes,
+                                                  const uint8_t* __restrict__ pool, const Layout& L,
+                                                  const ExpertSource& src, int D, int F, float limit,
+                                                  uint8_t* __restrict__ hid, int32_t* __restrict__ ws_slots,
+                                                  float* __restrict__ ws_w) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
   const int GT = D / 128, NQ = GT / 4;
   const int GK = (F + 127) / 128, FT = F / 16;
-  const int e = blockIdx.x / FT;
-  const int tile = blockIdx.x - e * FT;
+  const int e = bid / FT;
+  const int tile = bid - e * FT;
   const int row0 = tile * 16;
-  const int rw = blockIdx.x & (GU_WAVES - 1);   // the routing wave
+  const int rw = bid & (GU_WAVES - 1);   // the routing wave
 
   // ---- 0. routing wave: the expert's slot; the others: x's plane blocks into LDS
   if (wave == rw) {
@@ -207,7 +206,7 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
     const float wexp = src.scores != nullptr ? s.wexp : expert_weight(src, ws_w, e);
     if (src.scores != nullptr) {   // the selection, for the down kernel and the caller
       if (tile == 0 && tid == 0) ws_w[e] = wexp;
-      if (blockIdx.x == 0 && tid < src.k) {
+      if (bid == 0 && tid < src.k) {
         if (src.idx_out) src.idx_out[tid] = s.top_i[tid];
         if (src.w_out) src.w_out[tid] = s.top_w[tid];
       }
@@ -260,6 +259,65 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
   }
 }
 
+template <int MAXM>
+__global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t* __restrict__ xplanes,
+                                                                  const uint8_t* __restrict__ pool, Layout L,
+                                                                  ExpertSource src, int D, int F, float limit,
+                                                                  uint8_t* __restrict__ hid,
+                                                                  int32_t* __restrict__ ws_slots,
+                                                                  float* __restrict__ ws_w) {
+  __shared__ __align__(16) GuLds s;
+  q2mx_gate_up_body<MAXM>(s, blockIdx.x, xplanes, pool, L, src, D, F, limit, hid, ws_slots, ws_w);
+}
+
+// ---- the FP8 shared expert carried by the routed launches (one token)
+// Its K (D in gate/up, its own F in down) runs as 16 virtual waves of at most two
+// chunks each (fp8_common.h), so the outputs equal the shared expert's own launches
+// bit for bit.
+constexpr int SH_MAX_K = fp8::DEC_VW * 2 * fp8::CHUNK;   // 4096
+constexpr int SH_CPV = 2;
+
+// One shared gate/up tile (8 rows of w1 and of w3) per workgroup: h [F_sh] bf16.
+__device__ __forceinline__ void shared_gu_tile(const fp8::DecodeArgs& p, int bx, uint8_t* lds) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  fp8::DecAct<1, GU_THREADS> xa;
+  fp8::dec_act_load<1, GU_THREADS>(p, 0, 1, tid, xa);
+  __builtin_amdgcn_sched_barrier(0);   // the activation loads ahead of the weight loads
+  fp8::DecW<fp8::DEC_VW / GU_WAVES, SH_CPV> w;
+  fp8::dec_w_load<true, GU_WAVES, fp8::DEC_VW / GU_WAVES, SH_CPV>(p, bx, wave, lane, w);
+  fp8::dec_act_quant<1, GU_THREADS>(p, 1, tid, xa, lds);
+  lds_sync();
+  fp8::dec_mfma<1, GU_WAVES, fp8::DEC_VW / GU_WAVES, SH_CPV>(p, 1, wave, lane, w, lds);
+  lds_sync();
+  if (tid < 8) {
+    const float g = round_bf16(fp8::dec_total(lds, 1, p.K, tid, 0));
+    const float u = round_bf16(fp8::dec_total(lds, 1, p.K, tid + 8, 0));
+    p.out[bx * 8 + tid] = f32_to_bf16(fp8::swiglu_h(g, u, p.limit));
+  }
+}
+
+// grid.x = n_sh + k * F / 16: the shared expert's gate/up tiles first (they need no
+// routing, so their weight stream starts while the routed workgroups select), then
+// the routed workgroups.
+template <int MAXM>
+__global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_shared_kernel(const uint8_t* __restrict__ xplanes,
+                                                                         const uint8_t* __restrict__ pool, Layout L,
+                                                                         ExpertSource src, int D, int F, float limit,
+                                                                         uint8_t* __restrict__ hid,
+                                                                         int32_t* __restrict__ ws_slots,
+                                                                         float* __restrict__ ws_w,
+                                                                         fp8::DecodeArgs sh, int n_sh) {
+  constexpr int SH_LDS = fp8::dec_tile_lds(1, SH_MAX_K);
+  __shared__ __align__(16) uint8_t buf[sizeof(GuLds) > SH_LDS ? sizeof(GuLds) : SH_LDS];
+  if ((int)blockIdx.x < n_sh) {
+    shared_gu_tile(sh, blockIdx.x, buf);
+    return;
+  }
+  q2mx_gate_up_body<MAXM>(*reinterpret_cast<GuLds*>(buf), blockIdx.x - n_sh, xplanes, pool, L, src, D, F, limit,
+                          hid, ws_slots, ws_w);
+}
+
 // Down items m0 .. m0 + NI - 1 of a wave, interleaved.
 template <int NI, int MAXM>
 __device__ __forceinline__ void down_items(DnLds& s, const uint4 (&c2)[MAXM][2], const int (&it_e)[MAXM],
@@ -303,15 +361,25 @@ __device__ __forceinline__ void down_items(DnLds& s, const uint4 (&c2)[MAXM][2],
   }
 }
 
-// grid.x = D / 16.  MAXM = ceil(k * ceil(GK / 4) / 12) items per wave.
-template <int MAXM>
+// grid.x = D / 16.  MAXM = ceil(k * ceil(GK / 4) / 12) items per wave.  SH: the
+// workgroup also runs the shared expert's down tile of the same 16 rows (w2 over
+// act_quant(h_sh), sh.a = h_sh), whose bf16 y is the addend.
+template <int MAXM, bool SH>
 __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __restrict__ pool, Layout L,
                                                                const int32_t* __restrict__ ws_slots, int D, int F,
                                                                int k, const uint8_t* __restrict__ hid,
                                                                const uint16_t* __restrict__ addend,
                                                                float* __restrict__ routed,
-                                                               uint16_t* __restrict__ out) {
+                                                               uint16_t* __restrict__ out, fp8::DecodeArgs sh) {
   __shared__ __align__(16) DnLds s;
+  // shared expert: act_quant(h_sh) and the partial tiles, its 16 w2 rows (16 K bytes),
+  // h_sh as copied (bf16) and the tile's scale row
+  constexpr int SH_TILE = fp8::dec_tile_lds(1, SH_MAX_K);
+  __shared__ __align__(16) uint8_t sh_lds[SH ? SH_TILE + 18 * SH_MAX_K + SH_MAX_K / 32 : 16];
+  constexpr int SH_NPV = (fp8::DEC_VW + DN_WAVES - 1) / DN_WAVES;   // virtual waves per wave (2)
+  uint8_t* sh_w = sh_lds + SH_TILE;
+  uint8_t* sh_h = sh_w + 16 * SH_MAX_K;
+  uint8_t* sh_sc = sh_h + 2 * SH_MAX_K;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -323,8 +391,16 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   // ---- 0. the hidden plane blocks into LDS; the slots (KMAX entries are
   //         allocated) -> the tile's scale / bias runs into LDS, then the wave's
   //         W2 codes into registers
+  // (the shared expert's scale row first: one byte per thread, into LDS at the barrier)
+  uint32_t sh_sb = 0;
+  if constexpr (SH) sh_sb = sh.ws[0][(size_t)(row0 / 32) * (sh.K / 32) + min(tid, sh.K / 32 - 1)];
   // the hidden plane blocks first: they do not wait for the slots
   copy_to_lds_untracked(hid, s.planes, k * GK * PB_BYTES, wave, DN_WAVES, lane);
+  // the shared expert's h (bf16) and 16 w2 rows (contiguous)
+  if constexpr (SH) {
+    copy_to_lds_untracked(reinterpret_cast<const uint8_t*>(sh.a), sh_h, 2 * sh.K, wave, DN_WAVES, lane);
+    copy_to_lds_untracked(sh.w[0] + (size_t)row0 * sh.K, sh_w, 16 * sh.K, wave, DN_WAVES, lane);
+  }
   // the tile's addend, read now rather than in the epilogue (every lane loads, no
   // branch: the wait for it then sits at its use)
   const uint16_t add_bits = (addend != nullptr ? addend : reinterpret_cast<const uint16_t*>(hid))[row0 + (tid & 15)];
@@ -370,7 +446,15 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   // the copies, issued before the 2 MAXM code loads, have landed (loads complete in
   // issue order); the codes stay in flight, each item waits for its own
   __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * MAXM));
+  if (SH && tid < sh.K / 32) sh_sc[tid] = (uint8_t)sh_sb;
   lds_sync();
+  if constexpr (SH) {   // act_quant(h_sh) into LDS, read after the items' barrier
+    fp8::DecAct<1, DN_THREADS> xa;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(xa.v) / sizeof(xa.v[0])); ++i)
+      xa.v[i] = *reinterpret_cast<const uint4*>(sh_h + 16 * min(tid + DN_THREADS * i, sh.K / 8 - 1));
+    fp8::dec_act_quant<1, DN_THREADS>(sh, 1, tid, xa, sh_lds);
+  }
 
   // ---- 1. items, in interleaved groups (every item's A operands, then each MFMA step
   //         for all items of the group: independent accumulators keep the matrix
@@ -384,6 +468,11 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
     down_items<MAXM - 2>(s, c2, it_e, it_q, on, 2, ro, GK, FT, j, kg, lane);
   }
   lds_sync();
+  if constexpr (SH) {   // the shared tile's partial tiles (read after the next barrier)
+    uint32_t bs[SH_NPV][SH_CPV];
+    fp8::dec_wscale<DN_WAVES, SH_NPV, SH_CPV>(sh_sc, sh.K, wave, lane, bs);
+    fp8::dec_mfma_wlds<1, DN_WAVES, SH_NPV, SH_CPV>(sh, 1, wave, lane, sh_w, bs, sh_lds);
+  }
 
   // ---- 2. per expert (16 lanes each): the row values rounded to bf16; then the
   //         route-order sum of the tile's rows
@@ -407,7 +496,11 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
     float total = 0.0f;
     for (int e = 0; e < k; ++e) total = total + s.y[e][tid];
     if (routed) routed[n] = total;
-    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(add_bits) : total);
+    if constexpr (SH) {
+      if (out) out[n] = f32_to_bf16(total + round_bf16(fp8::dec_total(sh_lds, 1, sh.K, tid, 0)));
+    } else {
+      if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(add_bits) : total);
+    }
   }
 }
 
@@ -760,23 +853,35 @@ bool q2mx_supported(int D, int F, int k) {
   return D % 1024 == 0 && D <= 128 * MAX_GT && F % 16 == 0 && F <= 128 * MAX_GK && k >= 1 && k <= KMAX;
 }
 
+// The shapes the routed launches carry the shared expert for (else it runs in its
+// own launches before them): one token, K <= SH_MAX_K on both sides.
+bool q2mx_shared_supported(int D, int F_sh) { return D <= SH_MAX_K && F_sh <= SH_MAX_K; }
+
 // hid: k * ceil(F / 128) plane blocks; xplanes: D / 128 plane blocks, written by
-// the router kernel when planes_ready, else here.
+// the router kernel when planes_ready, else here.  sh_gu / sh_dn (both or neither):
+// the shared expert's gate/up (out = h_sh [F_sh]) and down (a = h_sh) tiles, carried
+// by the two routed launches; out then gets bf16(routed + y_sh) and addend is null.
 int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, const uint8_t* pool,
                        const Layout& L, const ExpertSource& src, int32_t* ws_slots, float* ws_w, int D, int F,
                        int k, float limit, const uint16_t* addend, float* routed, uint16_t* out, uint8_t* hid,
-                       hipStream_t s) {
+                       hipStream_t s, const fp8::DecodeArgs* sh_gu, const fp8::DecodeArgs* sh_dn) {
   if (!planes_ready) {
     hipLaunchKernelGGL(x_planes_kernel, dim3((D / 4 + 255) / 256), dim3(256), 0, s, x, D, xplanes);
     const int rc = check_launch("x_planes_kernel");
     if (rc) return rc;
   }
+  const bool sh = sh_gu != nullptr;
   const int NQ = D / 512;
   const int mg = (NQ + GU_WAVES - 1) / GU_WAVES;
-  const dim3 grid_gu(k * (F / 16));
-#define CACHALOT_GU(MV)                                                                                           \
-  hipLaunchKernelGGL((q2mx_gate_up_kernel<MV>), grid_gu, dim3(GU_THREADS), 0, s, xplanes, pool, L, src, D, F, limit, \
-                     hid, ws_slots, ws_w)
+  const int n_sh = sh ? sh_gu->N / 8 : 0;
+  const dim3 grid_gu(n_sh + k * (F / 16));
+#define CACHALOT_GU(MV)                                                                                            \
+  if (sh)                                                                                                          \
+    hipLaunchKernelGGL((q2mx_gate_up_shared_kernel<MV>), grid_gu, dim3(GU_THREADS), 0, s, xplanes, pool, L, src, D, \
+                       F, limit, hid, ws_slots, ws_w, *sh_gu, n_sh);                                               \
+  else                                                                                                             \
+    hipLaunchKernelGGL((q2mx_gate_up_kernel<MV>), grid_gu, dim3(GU_THREADS), 0, s, xplanes, pool, L, src, D, F,     \
+                       limit, hid, ws_slots, ws_w)
   if (mg <= 2) CACHALOT_GU(2);
   else CACHALOT_GU(3);
 #undef CACHALOT_GU
@@ -784,11 +889,17 @@ int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, c
   if (rc) return rc;
   const int NQ2 = ((F + 127) / 128 + 3) / 4;
   const int md = (k * NQ2 + DN_WAVES - 1) / DN_WAVES;
-#define CACHALOT_DN(MV)                                                                                          \
-  hipLaunchKernelGGL((q2mx_down_kernel<MV>), dim3(D / 16), dim3(DN_THREADS), 0, s, pool, L, ws_slots, D, F, k, hid, \
-                     addend, routed, out)
-  if (md <= 3) CACHALOT_DN(3);
-  else CACHALOT_DN(4);
+  const fp8::DecodeArgs none{};
+#define CACHALOT_DN(MV, SHV)                                                                                     \
+  hipLaunchKernelGGL((q2mx_down_kernel<MV, SHV>), dim3(D / 16), dim3(DN_THREADS), 0, s, pool, L, ws_slots, D, F, k, \
+                     hid, addend, routed, out, sh ? *sh_dn : none)
+  if (md <= 3) {
+    if (sh) CACHALOT_DN(3, true);
+    else CACHALOT_DN(3, false);
+  } else {
+    if (sh) CACHALOT_DN(4, true);
+    else CACHALOT_DN(4, false);
+  }
 #undef CACHALOT_DN
   return check_launch("q2mx_down_kernel");
 }

@@ -20,72 +20,10 @@
 // register i % 4.
 //
 // Launches: quant(x) -> linear(w1 | w3) -> swiglu+quant(h) -> linear(w2).
-#include "common.h"
-#include "decode_common.h"
+#include "fp8_common.h"
 
 namespace cachalot {
 namespace fp8 {
-
-typedef __attribute__((ext_vector_type(4))) float f32x4_t;
-
-constexpr int BLOCK = 32;
-constexpr int CHUNK = 128;
-constexpr float FP8_MAX = 448.0f;
-constexpr float MIN_AMAX = 1e-4f;
-constexpr uint32_t E8M0_ONE = 127u;
-
-// ------------------------------------------------------------ act_quant ---
-// Block exponent e = ceil(log2(r)) of r = fl32(amax / 448) >= 2^-23 (a normal
-// float): the unbiased exponent, plus one unless the significand is exactly 1.
-__device__ __forceinline__ int block_exponent(float amax) {
-  const uint32_t bits = __float_as_uint(amax / FP8_MAX);
-  return (int)((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0u ? 1 : 0);
-}
-
-// 2^-e as a float (e in [-23, 126]).
-__device__ __forceinline__ float pow2_neg(int e) { return __uint_as_float((uint32_t)(127 - e) << 23); }
-
-__device__ __forceinline__ float clip448(float v) { return fminf(fmaxf(v, -FP8_MAX), FP8_MAX); }
-
-// One quarter (8 consecutive values) of a 32-element block whose four quarters
-// sit in an aligned group of 4 lanes (quarter q in lane 4 g + q): the block's
-// exponent (amax over the 4 lanes by two quad swaps) and this quarter's E4M3
-// codes, element i in byte i % 4 of word i / 4, converted by the hardware
-// round-to-nearest-even fp32 -> E4M3 converter after the exact power-of-two
-// scaling and the clip.  Every lane of the wave must execute it.
-__device__ __forceinline__ uint2 quant_quarter(const float (&v)[8], int& e) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __uint_as_float(xor1_u32(__float_as_uint(amax))));
-  amax = fmaxf(amax, __uint_as_float(xor2_u32(__float_as_uint(amax))));
-  e = block_exponent(fmaxf(amax, MIN_AMAX));
-  const float inv = pow2_neg(e);
-  uint2 w;
-  int t = __builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[0] * inv), clip448(v[1] * inv), 0, false);
-  w.x = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[2] * inv), clip448(v[3] * inv), t, true);
-  t = __builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[4] * inv), clip448(v[5] * inv), 0, false);
-  w.y = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clip448(v[6] * inv), clip448(v[7] * inv), t, true);
-  return w;
-}
-
-__device__ __forceinline__ void unpack_bf16x8(const uint4& w, float (&v)[8]) {
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __uint_as_float(ws[i] << 16);
-    v[2 * i + 1] = __uint_as_float(ws[i] & 0xffff0000u);
-  }
-}
-
-// h = bf16(silu(min(g, L)) * clip(u, -L, L)) from bf16 g and u (L <= 0: no clamp).
-__device__ __forceinline__ float swiglu_h(float g, float u, float limit) {
-  if (limit > 0.0f) {
-    u = fminf(fmaxf(u, -limit), limit);
-    g = fminf(g, limit);
-  }
-  return round_bf16(decode::silu_f32(g) * u);
-}
 
 struct QuantArgs {
   const uint16_t* x;      // act_quant: x [M, K] bf16 (row stride ldx); swiglu: gu [M, 2K] bf16 (g | u)
@@ -136,64 +74,6 @@ struct LinearArgs {
   int ldo;
 };
 
-// A lane's share of one 128-element chunk of a row: K [128 c + 32 kg, +32) of
-// an E4M3 row (zeros past K or for an invalid row) and the E8M0 scale of that
-// 32-element block (1.0 past K).
-struct Operand {
-  uint4 lo, hi;
-  uint32_t s;
-};
-
-// Branch-free: out-of-range lanes load from the row start and are zeroed after,
-// so every load is issued unconditionally and the compiler can wait for exactly
-// the loads a use needs (loads under a branch make it wait for all of them).
-__device__ __forceinline__ Operand load_operand(const uint8_t* base, const uint8_t* scales, int K, int c, int kg,
-                                                bool row_ok) {
-  Operand o;
-  const int k0 = c * CHUNK + BLOCK * kg;
-  const bool ok = row_ok && k0 < K;
-  const int kk = ok ? k0 : 0, blk = ok ? 4 * c + kg : 0;
-  const uint4 lo = *reinterpret_cast<const uint4*>(base + kk);
-  const uint4 hi = *reinterpret_cast<const uint4*>(base + kk + 16);
-  const uint32_t sc = scales[blk];
-  const uint4 z = make_uint4(0, 0, 0, 0);
-  o.lo = ok ? lo : z;
-  o.hi = ok ? hi : z;
-  o.s = ok ? sc : E8M0_ONE;
-  return o;
-}
-
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
-
-// Eight E4M3 values (two words) times their block scale, as bf16 (exact: 4
-// significant bits and a power-of-two factor), by the gfx950 scaled converter.
-__device__ __forceinline__ bf16x8_t to_bf16x8(uint32_t w0, uint32_t w1, float scale) {
-  uint4 r;
-  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, false));
-  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, scale, true));
-  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, false));
-  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, scale, true));
-  return __builtin_bit_cast(bf16x8_t, r);
-}
-
-// The eight values of step j (0..3) of an operand: bytes [8 j, 8 j + 8) of its 32.
-__device__ __forceinline__ bf16x8_t step_values(const Operand& o, int j, float scale) {
-  const uint32_t w[8] = {o.lo.x, o.lo.y, o.lo.z, o.lo.w, o.hi.x, o.hi.y, o.hi.z, o.hi.w};
-  return to_bf16x8(w[2 * j], w[2 * j + 1], scale);
-}
-
-// Products of scaled E4M3 values are exact in fp32 and the bf16 matrix cores
-// accumulate them in fp32, the reference's arithmetic.  (The fp8 matrix-core
-// instructions were measured to align products to the largest one and drop
-// bits about 2^-19 below it, far from fp32 accumulation on wide-range data.)
-__device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t& a, const bf16x8_t& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Workgroup = 4 waves = 16 MT tokens x 16 RT rows of one matrix; the waves split
-// the K chunks (wave w: chunks w, w + 4, ..), loading PF chunks at a time, and
-// their partial tiles are summed in LDS in wave order.  A chunk is four
-// 16x16x32 steps; in step j lane (c, kg) carries K 128 chunk + 32 kg + 8 j + [0, 8)
 // of its token row (A) and weight row (B).
 template <int MT, int RT, int PF>
 __global__ __launch_bounds__(256) void linear_kernel(LinearArgs p) {
@@ -286,151 +166,42 @@ __global__ __launch_bounds__(256) void linear_kernel(LinearArgs p) {
 }
 
 // ---------------------------------------------------------- decode GEMV ---
-// Few tokens (M <= DEC_MT per workgroup tile): the activation rows are
-// quantized by the workgroup itself into LDS (E4M3 codes + E8M0 exponents, the
-// act_quant above), so a decode call is two launches:
-//   gate/up (PAIRED): a 16-column tile = 8 rows of w1 and the same 8 rows of w3;
-//     the epilogue forms h = bf16(silu(min(g, L)) * clip(u, -L, L)) from the
-//     bf16-rounded g and u of each row and writes h [M, F] bf16;
+// Few tokens (M <= DEC_MT per workgroup tile), two launches of the decode tile
+// (fp8_common.h), 16 waves each, one virtual wave per wave:
+//   gate/up (PAIRED): 8 rows of w1 and the same 8 rows of w3; the epilogue forms
+//     h = bf16(silu(min(g, L)) * clip(u, -L, L)) from the bf16-rounded g and u of
+//     each row and writes h [M, F] bf16;
 //   down: 16 rows of w2 over act_quant(h), y [M, D] bf16.
-// The waves split the K chunks; a wave's first PF chunks of weights are
-// requested before the activation rows are quantized, so the HBM stream starts
-// at once (the activation loads are issued first, so waiting for them leaves
-// the weight loads in flight).
-constexpr int DEC_MT = 4;
-constexpr int DEC_MAX_K = 5120;
-#ifndef CACHALOT_DEC_WAVES
-#define CACHALOT_DEC_WAVES 16
-#endif
-constexpr int DEC_WAVES = CACHALOT_DEC_WAVES;      // waves per workgroup (they split K)
-constexpr int DEC_PF = 32 / DEC_WAVES;             // chunks of weights in flight per wave
+// The activation loads are issued first and the weight loads right after, so
+// waiting for the activations leaves the weight stream in flight while the
+// rows are quantized.
+constexpr int DEC_CPV = 3;   // chunks per virtual wave: K <= 16 * 3 * 128 = DEC_MAX_K (and beyond)
+static_assert(DEC_VW * DEC_CPV * CHUNK >= DEC_MAX_K, "chunks per virtual wave");
 
-struct DecodeArgs {
-  const uint16_t* a;         // bf16 activation rows [M, K], row stride lda
-  int lda;
-  const uint8_t* w[2];       // w1, w3 (PAIRED) or w2
-  const uint8_t* ws[2];
-  int M, N, K;               // N = rows per matrix
-  float limit;
-  uint16_t* out;             // PAIRED: h [M, N]; else y [M, N]; row stride ldo
-  int ldo;
-};
-
-__host__ __device__ inline int dec_stride(int K) { return K + 16; }
-__host__ __device__ inline int dec_lds_bytes(int K, int waves) {
-  const int codes = DEC_MT * dec_stride(K), scales = DEC_MT * (K / BLOCK);
-  return ((codes + scales + 15) & ~15) + waves * 64 * 4 * 4;
-}
-
-template <bool PAIRED, int WAVES, int PF>
-__global__ __launch_bounds__(WAVES * 64) void decode_kernel(DecodeArgs p) {
-  constexpr int NT = WAVES * 64;
-  constexpr int XP = (DEC_MT * DEC_MAX_K / 8 + NT - 1) / NT;   // activation quarters per thread
+template <bool PAIRED, int CPV>
+__global__ __launch_bounds__(DEC_VW * 64) void decode_kernel(DecodeArgs p) {
+  constexpr int NT = DEC_VW * 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c16 = lane & 15, kg = lane >> 4;
-  const int K = p.K, nkb = K / BLOCK, nch = (K + CHUNK - 1) / CHUNK, stride = dec_stride(K);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = blockIdx.y * DEC_MT, mt = min(DEC_MT, p.M - t0);
-  uint8_t* codes = lds;
-  uint8_t* scl = lds + DEC_MT * stride;
-  float* red = reinterpret_cast<float*>(lds + ((DEC_MT * stride + DEC_MT * nkb + 15) & ~15));
-
-  // 1. the activation quarters this thread quantizes (loads first in program order)
-  const int nq = K / 8, total = mt * nq;
-  uint4 xv[XP];
-#pragma unroll
-  for (int i = 0; i < XP; ++i) {
-    const int q = min(threadIdx.x + NT * i, total - 1);     // unconditional load; extra lanes are unused
-    const int r = q / nq, k8 = (q - r * nq) * 8;
-    xv[i] = *reinterpret_cast<const uint4*>(p.a + (size_t)(t0 + r) * p.lda + k8);
-  }
+  DecAct<DEC_MT, NT> xa;
+  dec_act_load<DEC_MT, NT>(p, t0, mt, tid, xa);
   __builtin_amdgcn_sched_barrier(0);   // keep the activation loads ahead of the weight loads
-
-  // 2. this wave's first PF chunks of weights
-  int mat, n;
-  if constexpr (PAIRED) {
-    mat = c16 >> 3;
-    n = blockIdx.x * 8 + (c16 & 7);
-  } else {
-    mat = 0;
-    n = blockIdx.x * 16 + c16;
-  }
-  // (select, not index: a lane-dependent index into the argument block would be a
-  // vector memory load, ordered behind the activation loads above)
-  const uint8_t* brow = (mat ? p.w[1] : p.w[0]) + (size_t)n * K;
-  const uint8_t* bsc = (mat ? p.ws[1] : p.ws[0]) + (size_t)(n / 32) * nkb;
-  Operand B[PF];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) {
-    const int c = wave + WAVES * i;
-    B[i] = load_operand(brow, bsc, c < nch ? K : 0, c, kg, true);
-  }
-
-  // 3. quantize the activation rows into LDS
-#pragma unroll
-  for (int i = 0; i < XP; ++i) {
-    if (NT * i >= total) break;                        // uniform
-    const int q = threadIdx.x + NT * i;
-    float v[8];
-    unpack_bf16x8(q < total ? xv[i] : make_uint4(0, 0, 0, 0), v);
-    int e;
-    const uint2 w = quant_quarter(v, e);
-    if (q < total) {
-      const int r = q / nq, k8 = (q - r * nq) * 8;
-      *reinterpret_cast<uint2*>(codes + r * stride + k8) = w;
-      if ((k8 & 31) == 0) scl[r * nkb + k8 / BLOCK] = (uint8_t)(e + 127);
-    }
-  }
+  DecW<1, CPV> w;
+  dec_w_load<PAIRED, DEC_VW, 1, CPV>(p, blockIdx.x, wave, lane, w);
+  dec_act_quant<DEC_MT, NT>(p, mt, tid, xa, lds);
   lds_sync();
-
-  // 4. chunks: A from LDS (rows >= mt are zero), B from registers
-  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = wave;; c0 += WAVES * PF) {
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int c = c0 + WAVES * i;
-      if (c >= nch) break;
-      const int k0 = c * CHUNK + BLOCK * kg;
-      Operand A;
-      A.lo = make_uint4(0, 0, 0, 0);
-      A.hi = make_uint4(0, 0, 0, 0);
-      A.s = E8M0_ONE;
-      if (c16 < mt && k0 < K) {
-        A.lo = *reinterpret_cast<const uint4*>(codes + c16 * stride + k0);
-        A.hi = *reinterpret_cast<const uint4*>(codes + c16 * stride + k0 + 16);
-        A.s = scl[c16 * nkb + 4 * c + kg];
-      }
-      const float sa = e8m0_to_f32(A.s), sb = e8m0_to_f32(B[i].s);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma_bf16(step_values(A, j, sa), step_values(B[i], j, sb), acc);
-    }
-    if (c0 + WAVES * PF >= nch) break;
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int c = c0 + WAVES * PF + WAVES * i;
-      B[i] = load_operand(brow, bsc, c < nch ? K : 0, c, kg, true);
-    }
-  }
-
-  // 5. sum the waves' tiles in wave order; D[i][j] is lane j + 16 (i / 4), register i % 4
-#pragma unroll
-  for (int j = 0; j < 4; ++j) red[(wave * 64 + lane) * 4 + j] = acc[j];
+  dec_mfma<DEC_MT, DEC_VW, 1, CPV>(p, mt, wave, lane, w, lds);
   __syncthreads();
-  const int j = threadIdx.x & 15, i = threadIdx.x >> 4;
+  const int j = tid & 15, i = tid >> 4;
   if (i >= mt) return;
-  auto total_of = [&](int col) {
-    const int idx = ((col + 16 * (i >> 2)) * 4) + (i & 3);
-    float t = red[idx];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) t += red[256 * w + idx];
-    return t;
-  };
   if constexpr (PAIRED) {
     if (j >= 8) return;
-    const float g = round_bf16(total_of(j)), u = round_bf16(total_of(j + 8));
+    const float g = round_bf16(dec_total(lds, DEC_MT, p.K, j, i)), u = round_bf16(dec_total(lds, DEC_MT, p.K, j + 8, i));
     p.out[(size_t)(t0 + i) * p.ldo + blockIdx.x * 8 + j] = f32_to_bf16(swiglu_h(g, u, p.limit));
   } else {
-    p.out[(size_t)(t0 + i) * p.ldo + blockIdx.x * 16 + j] = f32_to_bf16(total_of(j));
+    p.out[(size_t)(t0 + i) * p.ldo + blockIdx.x * 16 + j] = f32_to_bf16(dec_total(lds, DEC_MT, p.K, j, i));
   }
 }
 
@@ -484,19 +255,25 @@ int launch_linear(const LinearArgs& a, int nmat, hipStream_t s) {
 }
 
 // Decode (M <= DEC_MT): gate/up + SwiGLU -> h [M, F] bf16 (in the gu region), down -> y.
+template <int CPV>
+int launch_decode_cpv(const DecodeArgs& gu, const DecodeArgs& dn, hipStream_t s) {
+  const dim3 grid_gu((unsigned)(gu.N / 8), (unsigned)((gu.M + DEC_MT - 1) / DEC_MT));
+  hipLaunchKernelGGL((decode_kernel<true, CPV>), grid_gu, dim3(64 * DEC_VW), dec_tile_lds(DEC_MT, gu.K), s, gu);
+  if (int rc = check_launch("fp8 decode gate/up")) return rc;
+  const dim3 grid_dn((unsigned)(dn.N / 16), (unsigned)((dn.M + DEC_MT - 1) / DEC_MT));
+  hipLaunchKernelGGL((decode_kernel<false, CPV>), grid_dn, dim3(64 * DEC_VW), dec_tile_lds(DEC_MT, dn.K), s, dn);
+  return check_launch("fp8 decode down");
+}
+
 int launch_decode(const uint16_t* x, const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, const uint8_t* s3,
                   const uint8_t* w2, const uint8_t* s2, int M, int D, int F, float limit, uint16_t* h, uint16_t* y,
                   hipStream_t s) {
-  DecodeArgs gu{x, D, {w1, w3}, {s1, s3}, M, F, D, limit, h, F};
-  const dim3 grid_gu((unsigned)(F / 8), (unsigned)((M + DEC_MT - 1) / DEC_MT));
-  hipLaunchKernelGGL((decode_kernel<true, DEC_WAVES, DEC_PF>), grid_gu, dim3(64 * DEC_WAVES), dec_lds_bytes(D, DEC_WAVES),
-                     s, gu);
-  if (int rc = check_launch("fp8 decode gate/up")) return rc;
-  DecodeArgs dn{h, F, {w2, w2}, {s2, s2}, M, D, F, limit, y, D};
-  const dim3 grid_dn((unsigned)(D / 16), (unsigned)((M + DEC_MT - 1) / DEC_MT));
-  hipLaunchKernelGGL((decode_kernel<false, DEC_WAVES, DEC_PF>), grid_dn, dim3(64 * DEC_WAVES),
-                     dec_lds_bytes(F, DEC_WAVES), s, dn);
-  return check_launch("fp8 decode down");
+  const DecodeArgs gu{x, D, {w1, w3}, {s1, s3}, M, F, D, limit, h, F};
+  const DecodeArgs dn{h, F, {w2, w2}, {s2, s2}, M, D, F, limit, y, D};
+  const int nch = (std::max(D, F) + CHUNK - 1) / CHUNK;   // chunks of the longer K
+  if (nch <= DEC_VW) return launch_decode_cpv<1>(gu, dn, s);
+  if (nch <= 2 * DEC_VW) return launch_decode_cpv<2>(gu, dn, s);
+  return launch_decode_cpv<3>(gu, dn, s);
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

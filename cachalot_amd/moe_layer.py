@@ -21,9 +21,11 @@ reference it picks between the two-launch FP4 kernel and a per-expert
 rounding points (fp32 outputs throughout, ``fp4_gemv_metal.py:102-103``), and
 it is not consulted for affine banks; this build has the one device path.
 
-The FP8 shared expert (``shared_*``, ``moe_layer_metal.py:381-397``) runs
-first, on the same stream, and its bf16 output is added in the combine:
-``out = bf16(routed + shared)``.  ``addend`` (bf16 [D]) is the same hook for a
+The FP8 shared expert (``shared_*``, ``moe_layer_metal.py:381-397``) is added
+in the combine: ``out = bf16(routed + shared)``.  On the device path over a
+2-bit bank its tiles run inside the routed gate/up and down launches (one weight
+stream); otherwise it runs first, on the same stream, and its bf16 output is the
+combine's addend.  Both give the same bits.  ``addend`` (bf16 [D]) is the same hook for a
 caller that computes the shared branch itself; it cannot be combined with
 ``shared_*``.
 """
@@ -65,17 +67,20 @@ def moe_layer_forward(
     if x.ndim != 1:
         raise ValueError(f"x must be 1D for decode, got {tuple(x.shape)}")
     shared = shared_args(shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3, shared_w3_scales)
-    if shared is not None:
-        if addend is not None:
-            raise ValueError("pass either the shared expert weights or addend, not both")
-        addend = shared_expert_forward(x.to(torch.bfloat16), **shared, swiglu_limit=swiglu_limit)
+    if shared is not None and addend is not None:
+        raise ValueError("pass either the shared expert weights or addend, not both")
     pool = expert_store.pool
-    if expert_store.layer_fully_resident(layer_id) and x.dtype == torch.bfloat16 and topk <= 8:
-        # routing, slot lookup and experts on the device, no host round trip
+    device_path = expert_store.layer_fully_resident(layer_id) and x.dtype == torch.bfloat16 and topk <= 8
+    if shared is not None and not (device_path and pool.format.kind == "affine"):
+        addend = shared_expert_forward(x.to(torch.bfloat16), **shared, swiglu_limit=swiglu_limit)
+        shared = None
+    if device_path:
+        # routing, slot lookup and experts on the device, no host round trip (a 2-bit
+        # bank's decode launches also carry the shared expert)
         _, out, route = moe_layer_decode(x, gate_weight, gate_bias, pool, expert_store.layer_table(layer_id),
                                          topk=topk, gate_temp=gate_temp, route_scale=route_scale,
                                          norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order,
-                                         swiglu_limit=swiglu_limit, addend=addend)
+                                         swiglu_limit=swiglu_limit, addend=addend, shared=shared)
         return out, route
     router = route_topk_fused if norm_topk_prob else route_topk
     route = router(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp, route_scale=route_scale,

@@ -163,6 +163,18 @@ def shared_expert_forward_batched(x: torch.Tensor, *, w1, w1_scales, w2, w2_scal
     return _shared(x, w1, w1_scales, w2, w2_scales, w3, w3_scales, swiglu_limit)
 
 
+def shared_weights(shared: dict, d_model: int) -> tuple:
+    """The bundle's tensors checked for a layer of width d_model: (w1, s1, w3, s3, w2, s2, F)."""
+    w1, s1 = _check_weight(shared["w1"], shared["w1_scales"], "w1")
+    w3, s3 = _check_weight(shared["w3"], shared["w3_scales"], "w3")
+    w2, s2 = _check_weight(shared["w2"], shared["w2_scales"], "w2")
+    f, d = w1.shape
+    if d != d_model or tuple(w3.shape) != (f, d) or tuple(w2.shape) != (d, f):
+        raise ValueError(f"w1 {tuple(w1.shape)}, w3 {tuple(w3.shape)}, w2 {tuple(w2.shape)} do not form an expert "
+                         f"of width {d_model}")
+    return w1, s1, w3, s3, w2, s2, f
+
+
 def shared_args(shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3, shared_w3_scales):
     """The six shared_* call-site arguments as one bundle (None when all are None)."""
     parts = (shared_w1, shared_w1_scales, shared_w2, shared_w2_scales, shared_w3, shared_w3_scales)

@@ -135,6 +135,29 @@ int cachalot_moe_layer_decode_q2(const uint16_t* x, const uint16_t* gate_weight,
                                  const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
                                  float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
                                  cachalot_stream_t stream);
+/* cachalot_moe_layer_decode_q2_shared: cachalot_moe_layer_decode_q2 with the
+ * layer's FP8 shared expert (the arguments of cachalot_shared_expert_fp8 for one
+ * token: shared_w1 / shared_w3 [shared_F, D], shared_w2 [D, shared_F] E4M3 with
+ * their E8M0 block-32 scales) in place of `addend`: out = bf16(routed + y_sh),
+ * y_sh the shared expert's bf16 output, bit for bit what the two calls give.
+ * Where the shapes allow (D, shared_F <= 4096 on the matrix-core decode), the
+ * shared expert's tiles run inside the routed gate/up and down launches, so its
+ * weights stream together with the experts' (three launches in all).  out is
+ * required; shared_F a multiple of 32, D and shared_F <= 5120.  Workspace from
+ * cachalot_moe_layer_decode_q2_shared_workspace_bytes.  Replaces the shared and
+ * routed halves of moe_layer_forward (src/cachalot/model/moe_layer_metal.py:
+ * 133-405, the shared expert at :381-397, shared_expert_metal.py:44-188). */
+size_t cachalot_moe_layer_decode_q2_shared_workspace_bytes(int D, int F, int k, int shared_F);
+int cachalot_moe_layer_decode_q2_shared(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                        int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                        int order, const uint8_t* pool,
+                                        const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                        int D, int F, int group, float swiglu_limit, const uint8_t* shared_w1,
+                                        const uint8_t* shared_w1_scales, const uint8_t* shared_w3,
+                                        const uint8_t* shared_w3_scales, const uint8_t* shared_w2,
+                                        const uint8_t* shared_w2_scales, int shared_F, int32_t* idx_out,
+                                        float* w_out, float* scores, float* routed, uint16_t* out, void* workspace,
+                                        size_t workspace_bytes, cachalot_stream_t stream);
 /* cachalot_moe_layer_decode_q2_static: cachalot_moe_layer_decode_q2 with the
  * same arguments minus the workspace, which allocates nothing.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory (code

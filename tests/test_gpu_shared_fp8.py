@@ -180,3 +180,48 @@ def test_shared_expert_argument_errors_and_no_limit(cuda):
         shared_expert_forward(_to_dev_bf16(x, cuda)[None], **dev)                       # decode takes 1-D x
     with pytest.raises(ValueError):
         shared_expert_forward(_to_dev_bf16(x, cuda), **{**dev, "w2": dev["w1"]})       # w2 shape
+
+
+@pytest.mark.parametrize("d,f_sh,k,limit", [(4096, 2880, 6, 10.0), (4096, 2880, 8, 0.25), (2048, 4096, 6, 0.0),
+                                            (1024, 640, 3, 10.0), (5120, 2880, 6, 10.0), (4096, 4608, 6, 10.0)])
+def test_layer_decode_carries_the_shared_expert(cuda, d, f_sh, k, limit):
+    """cachalot_moe_layer_decode_q2_shared equals, bit for bit, the shared expert's own
+    call followed by the layer decode with its output as addend -- where the routed
+    launches carry the shared tiles (D, F_sh <= 4096) and where the shared expert
+    runs first (D = 5120, F_sh = 4608); routing and the fp32 routed sum unchanged."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_decode import moe_layer_decode
+    from cachalot_amd.shared_expert import shared_expert_forward
+    from cachalot_amd.storage.index import affine_format
+
+    f, e = 2880, 24
+    store = make_store(affine_format(d, f), n_layers=1, n_experts=e)
+    w, b = synth.router_weights(SEED, 3, e, d, cuda)
+    rng = np.random.default_rng(SEED + d + f_sh + k)
+    (w1, s1), (w3, s3), (w2, s2) = _expert(rng, d, f_sh)
+    plain = dict(w1=_dev(w1, cuda), w1_scales=_dev(s1, cuda), w2=_dev(w2, cuda), w2_scales=_dev(s2, cuda),
+                 w3=_dev(w3, cuda), w3_scales=_dev(s3, cuda))
+    kw = dict(topk=k, route_scale=1.0, score_fn="sigmoid", swiglu_limit=limit, want_routed=True)
+    xs = synth.activations(SEED, 91, 3, d, cuda)
+    for t in range(3):
+        args = (xs[t], w, b, store.pool, store.layer_table(0))
+        r1, o1, rt1 = moe_layer_decode(*args, **kw, shared=plain)
+        r2, o2, rt2 = moe_layer_decode(*args, **kw, addend=shared_expert_forward(xs[t], **plain, swiglu_limit=limit))
+        assert torch.equal(rt1.indices, rt2.indices) and torch.equal(rt1.weights, rt2.weights), (d, f_sh, k, t)
+        assert torch.equal(r1, r2), (d, f_sh, k, t)
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), (d, f_sh, k, t)
+    # a captured step replays to the eager result (the workspace exists from the eager calls)
+    x = xs[0].clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _, og, _ = moe_layer_decode(x, w, b, store.pool, store.layer_table(0), **kw, shared=plain)
+    _, want, _ = moe_layer_decode(xs[0], w, b, store.pool, store.layer_table(0), **kw, shared=plain)
+    for t in (1, 0, 2, 0):
+        x.copy_(xs[t])
+        g.replay()
+        torch.cuda.synchronize()
+        _, eager, _ = moe_layer_decode(xs[t], w, b, store.pool, store.layer_table(0), **kw, shared=plain)
+        assert torch.equal(og.view(torch.int16), eager.view(torch.int16)), t
+    with pytest.raises(ValueError):
+        moe_layer_decode(xs[0], w, b, store.pool, store.layer_table(0), **kw, shared=plain, addend=xs[1])
