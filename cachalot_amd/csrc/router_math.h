@@ -3,7 +3,8 @@
 // reproducible bit for bit; reference: src/cachalot/model/router_mlx.py:29-37,
 // minimax/language.py:280-292):
 //   * D is cut into 64 contiguous chunks of D/64; lane l owns chunk l and adds
-//     its bf16*bf16 products (exact in fp32) sequentially in fp32;
+//     its bf16*bf16 products (exact in fp32) sequentially in fp32 (an fma rounds
+//     the same exact sum once, so it is the same operation);
 //   * the 64 partials are combined by the xor butterfly 1, 2, 4, 8, 16, 32;
 //   * logit = sum / gate_temp (fp32);
 //   * score functions use only IEEE basic operations (Cody-Waite exp with a
@@ -93,8 +94,8 @@ __device__ __forceinline__ void router_row(const uint16_t* __restrict__ x, const
         const uint32_t xx[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          acc[j] = acc[j] + __uint_as_float(xx[q] << 16) * __uint_as_float(ww[q] << 16);
-          acc[j] = acc[j] + __uint_as_float(xx[q] & 0xffff0000u) * __uint_as_float(ww[q] & 0xffff0000u);
+          acc[j] = __builtin_fmaf(__uint_as_float(xx[q] << 16), __uint_as_float(ww[q] << 16), acc[j]);
+          acc[j] = __builtin_fmaf(__uint_as_float(xx[q] & 0xffff0000u), __uint_as_float(ww[q] & 0xffff0000u), acc[j]);
         }
       }
     }
@@ -105,8 +106,8 @@ __device__ __forceinline__ void router_row(const uint16_t* __restrict__ x, const
 #pragma unroll
       for (int j = 0; j < TT; ++j) {
         const uint32_t xx = reinterpret_cast<const uint32_t*>(xrow[j])[v];
-        acc[j] = acc[j] + __uint_as_float(xx << 16) * __uint_as_float(ww << 16);
-        acc[j] = acc[j] + __uint_as_float(xx & 0xffff0000u) * __uint_as_float(ww & 0xffff0000u);
+        acc[j] = __builtin_fmaf(__uint_as_float(xx << 16), __uint_as_float(ww << 16), acc[j]);
+        acc[j] = __builtin_fmaf(__uint_as_float(xx & 0xffff0000u), __uint_as_float(ww & 0xffff0000u), acc[j]);
       }
     }
   }
