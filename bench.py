@@ -49,10 +49,10 @@ def parse():
                     help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared"),
+    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared", "sharedfp8"),
                     help="profiling aid: run one secondary measurement alone (config 3 prefill, config 2 "
-                         "batched decode over --layers resident layers, config 0 FP4 decode, or config 1's layer "
-                         "with the FP8 shared expert), print its JSON and exit")
+                         "batched decode over --layers resident layers, config 0 FP4 decode, config 1's layer "
+                         "with the FP8 shared expert, or the shared expert alone), print its JSON and exit")
     return ap.parse_args()
 
 
@@ -430,7 +430,7 @@ def prefill_config3(args, dev, log_fn):
 
 def shared_expert_fp8(args, dev, log_fn):
     """The FP8 shared expert (E4M3 weights, E8M0 block-32 scales) at the layer's shape (D 4096, F 2880):
-    one token (two launches), a B=32 batch and a 4096-token prefill chunk; 16 weight sets rotated so that
+    one token (two launches), B=16 and B=32 batches and a 4096-token prefill chunk; 16 weight sets rotated so that
     the decode figures stream from HBM."""
     import torch
 
@@ -452,7 +452,7 @@ def shared_expert_fp8(args, dev, log_fn):
         sets.append(dict(w1=w1, w1_scales=s1, w3=w3, w3_scales=s3, w2=w2, w2_scales=s2))
     wbytes = 3 * D * F + 3 * (D // 32) * (F // 32)          # E4M3 weights + E8M0 scales
     out = {}
-    for M in (1, 32, 4096):
+    for M in (1, 16, 32, 4096):
         x = torch.randn(M, D, device=dev, generator=g).to(torch.bfloat16)
         n = S if M < 1024 else 2
         for i in range(n):
@@ -671,6 +671,10 @@ def main() -> int:
     if args.only == "fp4":
         _lib.lib()
         print(json.dumps(fp4_decode_config0(args, dev, log)), flush=True)
+        return 0
+    if args.only == "sharedfp8":
+        _lib.lib()
+        print(json.dumps(shared_expert_fp8(args, dev, log)), flush=True)
         return 0
     _lib.lib()
     D, F, E, K = 4096, 2880, 384, 6
