@@ -31,10 +31,12 @@
 // expert-major permutation, tile list of grouped.hip) x 16 NF rows per wave of
 // each of NM matrices (gate/up: NM = 2, W1 and W3, NF = 2 -> 128 rows of each;
 // down: NM = 1, NF = 4 -> 256 rows of W2).  K runs in chunks of 128: the A planes
-// of the chunk through a three-stage LDS ring filled by direct-to-LDS loads
+// of the chunk through a two-stage LDS ring filled by direct-to-LDS loads
 // (16-byte slots XOR-swizzled by row, so the operand reads hit distinct banks),
-// the wave's codes and B scales two chunks ahead in registers.  The tile's A
-// scales sit in LDS for the whole K loop.  Two workgroups fit a CU.  Workgroups
+// the wave's codes and B scales one chunk ahead in registers.  The tile's A
+// scales sit in LDS for the whole K loop.  Three workgroups fit a CU (49 KiB of
+// LDS, 96 VGPRs + 64 AGPRs each): measured 3.51 ms per config-3 layer against
+// 3.64 with a three-stage ring (two chunks ahead), which left room for two.  Workgroups
 // go to the XCDs round-robin by launch index; the mapping gives every slice of
 // one tile to one XCD, so the tile's A rows are fetched into that XCD's L2 once.
 #include "decode_common.h"
@@ -50,7 +52,7 @@ constexpr int P3_THREADS = 256;
 constexpr int P3_WAVES = 4;
 constexpr int P3_MT = 64;                     // token rows per tile
 constexpr int P3_TB = P3_MT / 16;             // token fragments
-constexpr int P3_STAGES = 3;
+constexpr int P3_STAGES = 2;
 constexpr int P3_ROWB = 256;                  // one row's chunk: hi 128 B | lo 128 B
 constexpr int P3_ABYTES = P3_MT * P3_ROWB;    // 16 KiB per stage
 constexpr int P3_ASLOTS = P3_ABYTES / 16 / P3_THREADS;   // 16-byte A slots per lane and chunk (4)
@@ -316,29 +318,28 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
     const int ngrp = (blocks + 15) / 16;
     const int nch = g.kch;
     P3Chunk<NM, NF> ring[P3_STAGES];
-    uint4 sgrp[3];
+    uint4 sgrp[2];
     // every issue is unconditional (a chunk past the end re-reads the last one into a
     // stage nothing reads again), so each wait is for exactly the loads it needs
     sgrp[0] = *reinterpret_cast<const uint4*>(sgp);
     p3_issue<NM, NF>(abuf, asrc, wrow, 0, kg, wave, row_bytes, ring[0]);
-    p3_issue<NM, NF>(abuf + P3_ABYTES, asrc, wrow, min(1, nch - 1), kg, wave, row_bytes, ring[1]);
-    // twelve chunks per trip: A stage and code ring index u % 3, scale group buffer (u / 4) % 3
-    for (int c0 = 0; c0 < nch; c0 += 12) {
+    // eight chunks per trip: A stage and code ring index u % 2, scale group buffer (u / 4) % 2
+    for (int c0 = 0; c0 < nch; c0 += 8) {
 #pragma unroll
-      for (int u = 0; u < 12; ++u) {
+      for (int u = 0; u < 8; ++u) {
         const int c = c0 + u;
         // this wave's loads of chunk c have landed (its last code load is consumed
         // here; its earlier direct-to-LDS loads complete first), then every wave's
-        asm volatile("" ::"v"(ring[u % 3].codes[NM - 1][NF - 1].w) : "memory");
+        asm volatile("" ::"v"(ring[u % 2].codes[NM - 1][NF - 1].w) : "memory");
         lds_sync();
-        if ((u + 2) % 4 == 0)   // the scale group of chunk c + 2
-          sgrp[((u + 2) / 4) % 3] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 2) / 4, ngrp - 1));
-        p3_issue<NM, NF>(abuf + ((u + 2) % 3) * P3_ABYTES, asrc, wrow, min(c + 2, nch - 1), kg, wave, row_bytes,
-                         ring[(u + 2) % 3]);
+        if ((u + 1) % 4 == 0)   // the scale group of chunk c + 1
+          sgrp[((u + 1) / 4) % 2] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 1) / 4, ngrp - 1));
+        p3_issue<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, wrow, min(c + 1, nch - 1), kg, wave, row_bytes,
+                         ring[(u + 1) % 2]);
         if (c < nch) {
           uint32_t bs[NM][NF];
-          p3_scales<NM, NF>(sgrp[(u / 4) % 3], u % 4, c, i, kg, blocks, bs);
-          p3_compute<NM, NF>(abuf + (u % 3) * P3_ABYTES, sbuf, sbs, ring[u % 3], bs, c, i, kg, ntb, acc);
+          p3_scales<NM, NF>(sgrp[(u / 4) % 2], u % 4, c, i, kg, blocks, bs);
+          p3_compute<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, ring[u % 2], bs, c, i, kg, ntb, acc);
         }
       }
     }
