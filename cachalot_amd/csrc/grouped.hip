@@ -26,7 +26,8 @@
 //   grouped_down_kernel<KIND, MT>
 //       same tiling over W2 with A = h rows; y = bf16(h W2) goes straight to
 //       its (token, route slot) place: y [T, k, D] bf16.
-//   combine_kernel     out[t] = bf16(0 + y[t,0] + ... + y[t,k-1] (+ addend)).
+//   combine_kernel     out[t] = bf16(0 + y[t,0] + ... + y[t,k-1] (+ addend));
+//                      combine8_kernel the same with 16-byte accesses.
 #include "decode_common.h"
 #include "mfma_tile.h"
 
@@ -812,6 +813,56 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
   }
 }
 
+// The same, 8 columns per thread with 16-byte loads and stores (D a multiple of 8,
+// 16-byte aligned arrays): the k slot loads of a thread are all in flight together,
+// and each column is summed in the same order as above.
+__global__ void __launch_bounds__(256) combine8_kernel(const uint16_t* __restrict__ y,
+                                                       const uint16_t* __restrict__ addend, int T, int k, int D,
+                                                       float* __restrict__ routed, uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // one group of 8 columns
+  const int64_t groups = (int64_t)T * D / 8;
+  if (i >= groups) return;
+  const int64_t t = (8 * i) / D;
+  const int d = (int)(8 * i - t * D);
+  uint4 v[KMAX];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s)
+    if (s < k) v[s] = *reinterpret_cast<const uint4*>(y + ((size_t)t * k + s) * D + d);
+  float a[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) a[c] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    if (s >= k) break;
+    const uint32_t w[4] = {v[s].x, v[s].y, v[s].z, v[s].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a[2 * q] = a[2 * q] + bf16_to_f32((uint16_t)(w[q] & 0xffff));
+      a[2 * q + 1] = a[2 * q + 1] + bf16_to_f32((uint16_t)(w[q] >> 16));
+    }
+  }
+  if (routed) {
+    float4* r = reinterpret_cast<float4*>(routed + t * D + d);
+    r[0] = make_float4(a[0], a[1], a[2], a[3]);
+    r[1] = make_float4(a[4], a[5], a[6], a[7]);
+  }
+  if (out) {
+    if (addend) {
+      const uint4 av = *reinterpret_cast<const uint4*>(addend + t * D + d);
+      const uint32_t w[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[2 * q] = a[2 * q] + bf16_to_f32((uint16_t)(w[q] & 0xffff));
+        a[2 * q + 1] = a[2 * q + 1] + bf16_to_f32((uint16_t)(w[q] >> 16));
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = (uint32_t)f32_to_bf16(a[2 * q]) | ((uint32_t)f32_to_bf16(a[2 * q + 1]) << 16);
+    *reinterpret_cast<uint4*>(out + t * D + d) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // Workspace of a grouped call: [tiles_n][tiles][hidden][x planes], 256-byte aligned regions.
 // hidden: rows x F bf16, or rows x ceil(F / 128) plane blocks (matrix-core batched decode);
 // x planes: T x D / 128 plane blocks (same).
@@ -1005,6 +1056,13 @@ extern "C" int cachalot_unpermute_combine(const uint16_t* y, const uint16_t* add
   CACHALOT_REQUIRE(y, "unpermute_combine: null pointer");
   CACHALOT_REQUIRE(routed || out, "unpermute_combine: no output requested");
   CACHALOT_REQUIRE(T >= 1 && k >= 1 && D >= 2 && D % 2 == 0, "unpermute_combine: T=%d k=%d D=%d", T, k, D);
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  if (D % 8 == 0 && k <= decode::KMAX && a16(y) && a16(addend) && a16(routed) && a16(out)) {
+    const int64_t groups = (int64_t)T * D / 8;
+    hipLaunchKernelGGL(combine8_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, (hipStream_t)stream, y,
+                       addend, T, k, D, routed, out);
+    return check_launch("combine8_kernel");
+  }
   const int64_t pairs = (int64_t)T * D / 2;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, (hipStream_t)stream, y,
                      addend, T, k, D, routed, out);

@@ -18,7 +18,7 @@ from oracle import dispatch as odispatch
 from oracle import experts as oexperts
 from oracle import router as orouter
 from oracle import synth as osynth
-from oracle.bf16 import bf16_bits_to_f32
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -226,3 +226,31 @@ def test_moe_prefill_grouped_end_to_end(cuda, kind, prefill_path):
     want, ys = _oracle_grouped(fmt, 1, x, idx, w)
     got = bf16_bits_to_f32(_bits(out))
     assert np.all(np.abs(got - want) <= TOL * np.abs(want).max() + np.sum(bf16_ulp(ys), axis=1) + bf16_ulp(want))
+
+
+@pytest.mark.parametrize("t,k,d,with_addend,offset", [(37, 6, 4096, True, 0), (5, 8, 4096, False, 0),
+                                                      (3, 1, 1024, True, 0), (7, 6, 6, True, 0),
+                                                      (9, 6, 4096, True, 2)])
+def test_unpermute_combine_bit_exact(cuda, t, k, d, with_addend, offset):
+    """cachalot_unpermute_combine against the oracle's route-order sum (moe_prefill_grouped.py:
+    526-545): routed fp32 and out bf16 bit for bit -- the 16-byte kernel (D % 8 == 0, aligned)
+    and the pair kernel (D = 6; y 4 bytes past a 16-byte boundary)."""
+    from cachalot_amd import _lib
+
+    rng = np.random.default_rng(SEED + t * d + k)
+    yv = round_bf16(rng.standard_normal((t, k, d)).astype(np.float32) * np.exp2(rng.integers(-8, 8, (t, k, 1))))
+    av = round_bf16(rng.standard_normal((t, d)).astype(np.float32)) if with_addend else None
+    buf = torch.zeros(t * k * d + offset + 8, dtype=torch.int16, device=cuda)
+    y = buf[offset:offset + t * k * d].view(t, k, d)
+    y.copy_(torch.from_numpy(f32_to_bf16_bits(yv).view(np.int16)).to(cuda))
+    add = torch.from_numpy(f32_to_bf16_bits(av).view(np.int16)).to(cuda) if with_addend else None
+    routed = torch.empty((t, d), dtype=torch.float32, device=cuda)
+    out = torch.empty((t, d), dtype=torch.int16, device=cuda)
+    L = _lib.lib()
+    rc = L.cachalot_unpermute_combine(y.data_ptr(), _lib.ptr(add), t, k, d, routed.data_ptr(), out.data_ptr(),
+                                      _lib.stream_handle(cuda))
+    _lib.check(rc, "unpermute_combine")
+    pos = np.arange(t * k, dtype=np.int32).reshape(t, k)
+    want_r, want_o = odispatch.combine(yv.reshape(t * k, d), pos, av)
+    assert np.array_equal(_np(routed).view(np.uint32), want_r.astype(np.float32).view(np.uint32))
+    assert np.array_equal(_np(out).view(np.uint16), f32_to_bf16_bits(want_o))
