@@ -100,44 +100,71 @@ __global__ void __launch_bounds__(PERMUTE_THREADS) permute_count_kernel(const in
   if (e == 0) offsets[E] = total;
 }
 
-// One workgroup per expert e: walk the routes in order, keep those that chose e.
-// Workgroup E collects the routes whose id lies outside [0, E) into rows
-// [offsets[E], n), in route order, with weight 0: the dropped routes, whose y
-// rows drop_zero_kernel clears.
-__global__ void __launch_bounds__(256) permute_scatter_kernel(const int32_t* __restrict__ idx,
-                                                              const float* __restrict__ w, int n, int k, int E,
-                                                              const int32_t* __restrict__ offsets,
-                                                              int32_t* __restrict__ row_token,
-                                                              int32_t* __restrict__ row_slot,
-                                                              float* __restrict__ row_w) {
-  __shared__ int wave_count[4];
+// One 1024-thread workgroup per expert e, keeping the routes that chose e in route
+// order.  Workgroup E collects the routes whose id lies outside [0, E) into rows
+// [offsets[E], n), in route order, with weight 0: the dropped routes, whose y rows
+// drop_zero_kernel clears.  Wave w owns the w-th of 16 contiguous segments of the
+// routes: it counts its hits (ballots, no barrier), one barrier gives each segment
+// the hits of the segments before it, and the wave walks its segment again writing
+// rows.  (Config 3, 24,576 routes: 64.5 us with one 256-thread workgroup stepping
+// through all routes, 29.9 us so; 512- and 256-thread workgroups 35.8 / 50.3 us.)
+constexpr int SCATTER_THREADS = 1024;
+__global__ void __launch_bounds__(SCATTER_THREADS) permute_scatter_kernel(const int32_t* __restrict__ idx,
+                                                                          const float* __restrict__ w, int n, int k,
+                                                                          int E, const int32_t* __restrict__ offsets,
+                                                                          int32_t* __restrict__ row_token,
+                                                                          int32_t* __restrict__ row_slot,
+                                                                          float* __restrict__ row_w) {
+  constexpr int WAVES = SCATTER_THREADS / 64;
+  __shared__ int seg_count[WAVES];
   const int e = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const bool dropped = e == E;
-  int base = offsets[e];
+  const int base = offsets[e];
   if ((dropped ? n : offsets[e + 1]) == base) return;
-  for (int i0 = 0; i0 < n; i0 += 256) {
-    const int i = i0 + threadIdx.x;
-    int id = i < n ? idx[i] : 0;
-    const bool hit = i < n && (dropped ? (id < 0 || id >= E) : id == e);
-    const uint64_t mask = __ballot(hit);
-    if (lane == 0) wave_count[wave] = __popcll(mask);
-    __syncthreads();
-    int before = 0, total = 0;
+  const int seg = ((n + WAVES - 1) / WAVES + 63) & ~63;
+  const int s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
+  const uint64_t below = (1ull << lane) - 1ull;
+  // a block is NB ids per lane, all loaded before any is used; a segment of one block
+  // (n <= 16 * 64 * NB) keeps its ids in registers for the second pass
+  constexpr int NB = 32;
+  int id[NB];
+  auto load_block = [&](int b0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      before += q < wave ? wave_count[q] : 0;
-      total += wave_count[q];
+    for (int j = 0; j < NB; ++j) id[j] = idx[min(b0 + 64 * j + lane, n - 1)];   // unconditional, clamped
+  };
+  auto hit_of = [&](int b0, int j) {
+    const int i = b0 + 64 * j + lane;
+    const int v = id[j];
+    return i < s1 && (dropped ? (v < 0 || v >= E) : v == e);
+  };
+  int count = 0;
+  for (int b0 = s0; b0 < s1; b0 += 64 * NB) {
+    load_block(b0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) count += __popcll(__ballot(hit_of(b0, j)));
+  }
+  if (lane == 0) seg_count[wave] = count;
+  __syncthreads();
+  int pos = base;
+  for (int q = 0; q < wave; ++q) pos += seg_count[q];
+  const bool one_block = s1 - s0 <= 64 * NB;
+  for (int b0 = s0; b0 < s1; b0 += 64 * NB) {
+    if (!one_block) load_block(b0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int i = b0 + 64 * j + lane;
+      const bool hit = hit_of(b0, j);
+      const uint64_t mask = __ballot(hit);
+      if (hit) {
+        const int p = pos + __popcll(mask & below);
+        row_token[p] = i / k;
+        row_slot[p] = i - (i / k) * k;
+        row_w[p] = dropped ? 0.0f : w[i];
+      }
+      pos += __popcll(mask);
     }
-    if (hit) {
-      const int pos = base + before + __popcll(mask & ((1ull << lane) - 1ull));
-      row_token[pos] = i / k;
-      row_slot[pos] = i - (i / k) * k;
-      row_w[pos] = dropped ? 0.0f : w[i];
-    }
-    base += total;
-    __syncthreads();
   }
 }
 
@@ -1014,8 +1041,8 @@ extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k
   hipLaunchKernelGGL(permute_count_kernel, dim3(1), dim3(PERMUTE_THREADS), 0, s, idx, T * k, E, offsets);
   int rc = check_launch("permute_count_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(permute_scatter_kernel, dim3(E + 1), dim3(256), 0, s, idx, w, T * k, k, E, offsets, row_token,
-                     row_slot, row_w);
+  hipLaunchKernelGGL(permute_scatter_kernel, dim3(E + 1), dim3(SCATTER_THREADS), 0, s, idx, w, T * k, k, E, offsets,
+                     row_token, row_slot, row_w);
   return check_launch("permute_scatter_kernel");
 }
 
