@@ -242,70 +242,76 @@ int launch_quant(const uint16_t* x, int ldx, int M, int K, bool swiglu, float li
 }
 
 // ------------------------------------------------------------ many-token GEMM ---
-// One 256-thread workgroup = a 128-token x 128-row tile of one matrix; wave (wm, wn)
-// owns rows [64 wm, +64) x columns [64 wn, +64) as 4 x 4 tiles of 16 x 16.  K runs in
-// stages of 64: each thread loads 32 E4M3 bytes of one A row and 32 of one B row (one
-// 32-element block each, so one E8M0 scale each), converts them to bf16 with the scale
-// folded in (exact) and stores them to LDS; the waves read their fragments back as
-// 8 bf16 values per lane (ds_read_b128; rows 144 bytes apart, so the 16 rows of a
-// fragment fall on distinct banks) into v_mfma_f32_16x16x32_bf16.  Two LDS buffers:
-// the next stage's bytes are loaded into registers while the current one is
-// multiplied.  Rows past M and N read row 0 (masked at the store); K a multiple of 32
-// (a half stage past K is zero).
-constexpr int GM_TILE = 128;
-constexpr int GM_KS = 64;                       // K per stage
-constexpr int GM_ROWB = GM_KS * 2 + 16;         // bytes per LDS row (bf16 + padding)
-constexpr int GM_STAGE = 2 * GM_TILE * GM_ROWB;  // A then B, one buffer
+// One 512-thread workgroup = a 128-token x 256-row tile of one matrix; wave (wm, wn),
+// wm < 2, wn < 4, owns tokens [64 wm, +64) x rows [64 wn, +64) as 4 x 4 tiles of
+// 16 x 16.  K runs in stages of one 32-element block (one E8M0 scale per row and
+// stage).  The tiles stay E4M3 bytes in LDS (rows 40 bytes apart, so the 16 rows of a
+// fragment fall on distinct banks) with their scale bytes beside them; a wave converts
+// each fragment as it reads it (8 values per lane, scale folded in: exact) for
+// v_mfma_f32_16x16x32_bf16.  Two LDS buffers, GM_RING blocks of bytes in registers
+// (the loads run that many blocks ahead); 123 VGPRs, four waves per SIMD.  Rows past
+// M and N read row 0 (masked at the store).
+// Measured at M = 4096 (the whole expert, ~450 us against 620 us for 64 x 64 tiles
+// read straight from global memory): bf16 tiles in LDS, 64 x 128 wave tiles, two
+// waves per SIMD and one to three blocks of prefetch all landed within 450-467 us,
+// with the matrix cores ~28 % busy.
+constexpr int GM_TM = 128;                      // tokens per tile
+constexpr int GM_TN = 256;                      // weight rows per tile
+constexpr int GM_ROWB = BLOCK + 8;              // bytes per LDS row: 32 E4M3 + padding
+constexpr int GM_STAGE = (GM_TM + GM_TN) * GM_ROWB + GM_TM + GM_TN;   // rows, then one scale byte per row
 
-__global__ __launch_bounds__(256) void gemm_kernel(LinearArgs p) {
+constexpr int GM_THREADS = 512;
+#ifndef CACHALOT_GM_RING
+#define CACHALOT_GM_RING 2
+#endif
+constexpr int GM_RING = CACHALOT_GM_RING;       // blocks of bytes in registers
+__global__ __launch_bounds__(GM_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void gemm_kernel(LinearArgs p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t glds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int nt = (p.N + GM_TILE - 1) / GM_TILE;
-  const int mat = blockIdx.x / nt, n0 = (blockIdx.x - mat * nt) * GM_TILE;
-  const int t0 = blockIdx.y * GM_TILE;
-  const int K = p.K, nkb = K / BLOCK, nst = (K + GM_KS - 1) / GM_KS;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int nt = (p.N + GM_TN - 1) / GM_TN;
+  const int mat = blockIdx.x / nt, n0 = (blockIdx.x - mat * nt) * GM_TN;
+  const int t0 = blockIdx.y * GM_TM;
+  const int K = p.K, nkb = K / BLOCK;
   const uint8_t* w = mat ? p.w[1] : p.w[0];
   const uint8_t* ws = mat ? p.ws[1] : p.ws[0];
 
-  // this thread's staged row (A row lr, B row lr) and half stage (32 bytes at k 32 lh)
-  const int lr = tid >> 1, lh = tid & 1;
-  const int at = t0 + lr, bn = n0 + lr;
-  const uint8_t* arow = p.a + (size_t)(at < p.M ? at : 0) * K;
+  // staged by this thread: 8 bytes of A row (tid / 4) at byte 8 (tid % 4) of the
+  // block, and 16 bytes of B row (tid / 2) at byte 16 (tid % 2)
+  const int ar = tid >> 2, ah = tid & 3, br = tid >> 1, bh = tid & 1;
+  const int at = t0 + ar, bn = n0 + br;
+  const uint8_t* arow = p.a + (size_t)(at < p.M ? at : 0) * K + 8 * ah;
   const uint8_t* asc = p.ae + (size_t)(at < p.M ? at : 0) * nkb;
-  const uint8_t* brow = w + (size_t)(bn < p.N ? bn : 0) * K;
+  const uint8_t* brow = w + (size_t)(bn < p.N ? bn : 0) * K + 16 * bh;
   const uint8_t* bsc = ws + (size_t)((bn < p.N ? bn : 0) / 32) * nkb;
-  uint4 ra[2], rb[2];
-  uint32_t sa, sb;
-  auto load = [&](int st) {
-    const int k0 = st * GM_KS + 32 * lh;
-    const bool ok = k0 < K;
-    const int kk = ok ? k0 : 0;
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    const uint4 a0 = *reinterpret_cast<const uint4*>(arow + kk), a1 = *reinterpret_cast<const uint4*>(arow + kk + 16);
-    const uint4 b0 = *reinterpret_cast<const uint4*>(brow + kk), b1 = *reinterpret_cast<const uint4*>(brow + kk + 16);
-    const uint32_t xa = asc[kk / BLOCK], xb = bsc[kk / BLOCK];
-    ra[0] = ok ? a0 : z;   // the block past K: zeros
-    ra[1] = ok ? a1 : z;
-    rb[0] = ok ? b0 : z;
-    rb[1] = ok ? b1 : z;
-    sa = ok ? xa : E8M0_ONE;
-    sb = ok ? xb : E8M0_ONE;
+  struct Raw {
+    uint2 a;
+    uint4 b;
+    uint32_t sa, sb;
   };
-  auto store = [&](uint8_t* buf) {
-    const float fa = e8m0_to_f32(sa), fb = e8m0_to_f32(sb);
-    uint8_t* da = buf + lr * GM_ROWB + 64 * lh;
-    uint8_t* db = buf + (GM_TILE + lr) * GM_ROWB + 64 * lh;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const bf16x8_t a0 = to_bf16x8(ra[h].x, ra[h].y, fa), a1 = to_bf16x8(ra[h].z, ra[h].w, fa);
-      const bf16x8_t b0 = to_bf16x8(rb[h].x, rb[h].y, fb), b1 = to_bf16x8(rb[h].z, rb[h].w, fb);
-      *reinterpret_cast<bf16x8_t*>(da + 32 * h) = a0;
-      *reinterpret_cast<bf16x8_t*>(da + 32 * h + 16) = a1;
-      *reinterpret_cast<bf16x8_t*>(db + 32 * h) = b0;
-      *reinterpret_cast<bf16x8_t*>(db + 32 * h + 16) = b1;
-    }
+  // blocks past K re-read the last one (unconditional loads; never stored)
+  auto load = [&](int kb, Raw& r) {
+    const int k = BLOCK * min(kb, nkb - 1);
+    r.a = *reinterpret_cast<const uint2*>(arow + k);
+    r.b = *reinterpret_cast<const uint4*>(brow + k);
+    r.sa = asc[k / BLOCK];
+    r.sb = bsc[k / BLOCK];
+  };
+  auto store = [&](const Raw& r, uint8_t* buf) {
+    *reinterpret_cast<uint2*>(buf + ar * GM_ROWB + 8 * ah) = r.a;
+    uint2* db = reinterpret_cast<uint2*>(buf + (GM_TM + br) * GM_ROWB + 16 * bh);
+    db[0] = make_uint2(r.b.x, r.b.y);
+    db[1] = make_uint2(r.b.z, r.b.w);
+    uint8_t* sc = buf + (GM_TM + GM_TN) * GM_ROWB;
+    if (ah == 0) sc[ar] = (uint8_t)r.sa;
+    if (bh == 0) sc[GM_TM + br] = (uint8_t)r.sb;
+  };
+  // the 8 values of lane (fr, fg) of a fragment whose 16 rows start at LDS row `row0`
+  auto frag = [&](const uint8_t* buf, int row, int fg) {
+    const uint2 v = *reinterpret_cast<const uint2*>(buf + row * GM_ROWB + 8 * fg);
+    const uint32_t sc = buf[(GM_TM + GM_TN) * GM_ROWB + row];
+    return to_bf16x8(v.x, v.y, e8m0_to_f32(sc));
   };
 
   f32x4_t acc[4][4];
@@ -314,54 +320,58 @@ __global__ __launch_bounds__(256) void gemm_kernel(LinearArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const int fr = lane & 15, fg = lane >> 4;   // fragment row / column and k group
-  load(0);
-  store(glds);
+  // a ring of GM_RING blocks in registers, two in LDS; GM_RING blocks per trip so the
+  // ring index is a constant
+  Raw ring[GM_RING];
+#pragma unroll
+  for (int r = 0; r < GM_RING; ++r) load(r, ring[r]);
+  store(ring[0], glds);
   __syncthreads();
-  for (int st = 0; st < nst; ++st) {
-    const uint8_t* buf = glds + (st & 1) * GM_STAGE;
-    if (st + 1 < nst) load(st + 1);
+  for (int kb0 = 0; kb0 < nkb; kb0 += GM_RING) {
 #pragma unroll
-    for (int ks = 0; ks < GM_KS / 32; ++ks) {
-      bf16x8_t af[4], bfr[4];
+    for (int u = 0; u < GM_RING; ++u) {
+      const int kb = kb0 + u;
+      if (kb < nkb) {
+        const uint8_t* buf = glds + (kb & 1) * GM_STAGE;
+        load(kb + GM_RING, ring[u]);   // the slot of block kb, already in LDS
+        bf16x8_t af[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const bf16x8_t*>(buf + (64 * wm + 16 * i + fr) * GM_ROWB + 64 * ks + 16 * fg);
+        for (int i = 0; i < 4; ++i) af[i] = frag(buf, 64 * wm + 16 * i + fr, fg);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_t*>(buf + (GM_TILE + 64 * wn + 16 * j + fr) * GM_ROWB + 64 * ks +
-                                                     16 * fg);
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8_t bfr = frag(buf, GM_TM + 64 * wn + 16 * j + fr, fg);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
+          for (int i = 0; i < 4; ++i) acc[i][j] = mfma_bf16(af[i], bfr, acc[i][j]);
+        }
+        if (kb + 1 < nkb) store(ring[(u + 1) % GM_RING], glds + ((kb + 1) & 1) * GM_STAGE);
+        __syncthreads();
+      }
     }
-    if (st + 1 < nst) store(glds + ((st + 1) & 1) * GM_STAGE);
-    __syncthreads();
   }
   // D[r][c] of a 16 x 16 tile: lane c + 16 (r / 4), register r % 4
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 64 * wn + 16 * j + fr;
+    if (n >= p.N) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 64 * wn + 16 * j + fr;
-      if (n >= p.N) continue;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int t = t0 + 64 * wm + 16 * i + 4 * fg + v;
         if (t < p.M) p.out[(size_t)t * p.ldo + mat * p.N + n] = f32_to_bf16(acc[i][j][v]);
       }
-    }
+  }
 }
 
 // Tile choice: token-tiled GEMV (one 16-token tile per workgroup, 8 chunks of
 // every wave in flight) for decode-sized M; 128 x 128 LDS tiles for many tokens.
 int launch_linear(const LinearArgs& a, int nmat, hipStream_t s) {
   if (a.M > 64) {
-    const dim3 grid((unsigned)(nmat * ((a.N + GM_TILE - 1) / GM_TILE)), (unsigned)((a.M + GM_TILE - 1) / GM_TILE));
+    const dim3 grid((unsigned)(nmat * ((a.N + GM_TN - 1) / GM_TN)), (unsigned)((a.M + GM_TM - 1) / GM_TM));
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             2 * GM_STAGE) != hipSuccess)
       return fail(CACHALOT_EHIP, "fp8 linear: cannot grant %d bytes of LDS", 2 * GM_STAGE);
-    hipLaunchKernelGGL(gemm_kernel, grid, dim3(256), 2 * GM_STAGE, s, a);
+    hipLaunchKernelGGL(gemm_kernel, grid, dim3(GM_THREADS), 2 * GM_STAGE, s, a);
   } else {
     const dim3 grid((unsigned)(nmat * a.N / 16), (unsigned)((a.M + 15) / 16));
     hipLaunchKernelGGL((linear_kernel<1, 1, 8>), grid, dim3(256), 0, s, a);
