@@ -8,7 +8,7 @@
 // fp32, then the dtype cast).  Rounding points of every path: g = bf16(x W1),
 // u = bf16(x W3), h = bf16(silu(min(g, L)) * clip(u, +-L) * w), y = bf16(h W2).
 //
-//   permute_count_kernel / permute_scatter_kernel
+//   permute_scatter_kernel (or permute_small_kernel up to 1024 routes)
 //       rows grouped by expert (ascending), tokens ascending inside an expert:
 //       offsets [E+1], row_token, row_slot, row_w.  The scatter runs one
 //       workgroup per expert over all T*k routes with ballot compaction, so
@@ -66,63 +66,28 @@ constexpr int PERMUTE_THREADS = 1024;
 constexpr int ZERO_WORDS = 16;         // 64 zero bytes at offset 128 of the workspace
 
 // ------------------------------------------------------------------ permute ---
-// offsets[e] = rows before expert e (E+1 entries).
-__global__ void __launch_bounds__(PERMUTE_THREADS) permute_count_kernel(const int32_t* __restrict__ idx, int n, int E,
-                                                                        int32_t* __restrict__ offsets) {
-  __shared__ int cnt[1024 + 1];
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int e = idx[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-  }
-  __syncthreads();
-  // exclusive scan over the E <= 1024 counts, one per thread: inclusive within each
-  // wave by shifted adds, then the wave totals
-  __shared__ int wave_tot[PERMUTE_THREADS / 64];
-  const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
-  const int c = e < E ? cnt[e] : 0;
-  int v = c;
-#pragma unroll
-  for (int d = 1; d < 64; d *= 2) {
-    const int o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  if (lane == 63) wave_tot[wave] = v;
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < PERMUTE_THREADS / 64; ++w) {
-    before += w < wave ? wave_tot[w] : 0;
-    total += wave_tot[w];
-  }
-  if (e < E) offsets[e] = before + v - c;
-  if (e == 0) offsets[E] = total;
-}
-
 // One 1024-thread workgroup per expert e, keeping the routes that chose e in route
 // order.  Workgroup E collects the routes whose id lies outside [0, E) into rows
 // [offsets[E], n), in route order, with weight 0: the dropped routes, whose y rows
 // drop_zero_kernel clears.  Wave w owns the w-th of 16 contiguous segments of the
-// routes: it counts its hits (ballots, no barrier), one barrier gives each segment
-// the hits of the segments before it, and the wave walks its segment again writing
-// rows.  (Config 3, 24,576 routes: 64.5 us with one 256-thread workgroup stepping
+// routes: it counts its hits and the routes of lower experts (ballots, no barrier);
+// one barrier gives the expert's first row -- offsets[e], which the workgroup writes
+// (workgroup E: offsets[E], the valid routes) -- and each segment the hits of the
+// segments before it, and the wave walks its segment again writing rows.  (Config 3, 24,576 routes: 64.5 us with one 256-thread workgroup stepping
 // through all routes, 29.9 us so; 512- and 256-thread workgroups 35.8 / 50.3 us.)
 constexpr int SCATTER_THREADS = 1024;
 __global__ void __launch_bounds__(SCATTER_THREADS) permute_scatter_kernel(const int32_t* __restrict__ idx,
                                                                           const float* __restrict__ w, int n, int k,
-                                                                          int E, const int32_t* __restrict__ offsets,
+                                                                          int E, int32_t* __restrict__ offsets,
                                                                           int32_t* __restrict__ row_token,
                                                                           int32_t* __restrict__ row_slot,
                                                                           float* __restrict__ row_w) {
   constexpr int WAVES = SCATTER_THREADS / 64;
-  __shared__ int seg_count[WAVES];
+  __shared__ int seg_count[WAVES], seg_below[WAVES];
   const int e = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const bool dropped = e == E;
-  const int base = offsets[e];
-  if ((dropped ? n : offsets[e + 1]) == base) return;
   const int seg = ((n + WAVES - 1) / WAVES + 63) & ~63;
   const int s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
   const uint64_t below = (1ull << lane) - 1ull;
@@ -139,14 +104,26 @@ __global__ void __launch_bounds__(SCATTER_THREADS) permute_scatter_kernel(const 
     const int v = id[j];
     return i < s1 && (dropped ? (v < 0 || v >= E) : v == e);
   };
-  int count = 0;
+  // below: routes of experts < e (all valid routes for the dropped workgroup)
+  int count = 0, below_e = 0;
   for (int b0 = s0; b0 < s1; b0 += 64 * NB) {
     load_block(b0);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) count += __popcll(__ballot(hit_of(b0, j)));
+    for (int j = 0; j < NB; ++j) {
+      const int i = b0 + 64 * j + lane;
+      const int v = id[j];
+      count += __popcll(__ballot(hit_of(b0, j)));
+      below_e += __popcll(__ballot(i < s1 && v >= 0 && v < e));
+    }
   }
-  if (lane == 0) seg_count[wave] = count;
+  if (lane == 0) {
+    seg_count[wave] = count;
+    seg_below[wave] = below_e;
+  }
   __syncthreads();
+  int base = 0;
+  for (int q = 0; q < WAVES; ++q) base += seg_below[q];
+  if (threadIdx.x == 0) offsets[e] = base;
   int pos = base;
   for (int q = 0; q < wave; ++q) pos += seg_count[q];
   const bool one_block = s1 - s0 <= 64 * NB;
@@ -168,8 +145,8 @@ __global__ void __launch_bounds__(SCATTER_THREADS) permute_scatter_kernel(const 
   }
 }
 
-// n <= 1024 routes (batched decode): the count, the scan and the scatter of the two
-// kernels above in one workgroup, thread i owning route i.  A route's place inside
+// n <= 1024 routes (batched decode): the counts, their scan and the scatter in one
+// workgroup, thread i owning route i.  A route's place inside
 // its expert is the number of earlier routes with the same key (the expert, or E for
 // an id outside [0, E)), so rows stay in route order as the scatter kernel leaves them.
 __global__ void __launch_bounds__(PERMUTE_THREADS) permute_small_kernel(const int32_t* __restrict__ idx,
@@ -1038,9 +1015,6 @@ extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k
                        row_token, row_slot, row_w);
     return check_launch("permute_small_kernel");
   }
-  hipLaunchKernelGGL(permute_count_kernel, dim3(1), dim3(PERMUTE_THREADS), 0, s, idx, T * k, E, offsets);
-  int rc = check_launch("permute_count_kernel");
-  if (rc) return rc;
   hipLaunchKernelGGL(permute_scatter_kernel, dim3(E + 1), dim3(SCATTER_THREADS), 0, s, idx, w, T * k, k, E, offsets,
                      row_token, row_slot, row_w);
   return check_launch("permute_scatter_kernel");
