@@ -361,6 +361,8 @@ def fp4_decode_config0(args, dev, log_fn):
            "note": "chained layer steps (router + FP4 gate/up + down), graph replays; FP4 decode computes in fp32 "
                    "(bf16 hi/lo MFMA), the reference's FP4 rounding points"}
     log_fn(f"config 0 FP4 decode: {us:.2f} us/step, {res['expert_GBps']:.0f} GB/s expert bytes")
+    # the same FP4 layers with the FP8 shared expert (moe_layer_forward, independent steps)
+    res["layer_with_shared"] = layer_with_shared(args, store, gates, log_fn)
     del store
     torch.cuda.empty_cache()
     return res
@@ -526,9 +528,10 @@ def requant_bank(args, dev, log_fn):
 
 
 def layer_with_shared(args, store, gates, log_fn):
-    """Config 1's layer as the reference's call site runs it: routed experts + the FP8 shared expert
-    (moe_layer_forward with shared_*), against the routed experts alone.  Steps rotate through the
-    resident layers and 8 shared weight sets (283 MB, beyond the MALL)."""
+    """A layer as the reference's call site runs it: routed experts + the FP8 shared expert
+    (moe_layer_forward with shared_*), against the routed experts alone, over `store` (config 1's
+    2-bit bank, or config 0's FP4 one).  Steps rotate through the resident layers and 8 shared
+    weight sets (283 MB, beyond the MALL)."""
     import torch
 
     from cachalot_amd.moe_layer import moe_layer_forward

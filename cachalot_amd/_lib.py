@@ -76,6 +76,12 @@ _SIGNATURES = {
                                                     c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                                                     c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
                                                     c_void_p]),
+    "cachalot_moe_layer_decode_fp4_shared_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "cachalot_moe_layer_decode_fp4_shared": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float,
+                                                     c_float, c_int, c_int, c_void_p, ctypes.POINTER(ExpertLayout),
+                                                     c_void_p, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p,
+                                                     c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                                     c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "cachalot_moe_layer_decode_q2_static_max_bytes": (c_size_t, []),
     "cachalot_moe_layer_decode_q2_static": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float,
                                                     c_float, c_int, c_int, c_void_p, ctypes.POINTER(ExpertLayout),

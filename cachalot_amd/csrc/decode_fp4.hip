@@ -23,6 +23,7 @@
 //                       h = hi + lo to 16 significant bits); expert row values
 //                       are summed in fp32 in route order.
 #include "decode_common.h"
+#include "fp8_common.h"
 #include "mfma_tile.h"
 #include "router_launch.h"
 
@@ -64,15 +65,25 @@ __device__ __forceinline__ void lane_pieces(int first, int PW, int pieces, int k
   }
 }
 
-// grid.x = k * F / 16.  NB = ceil(ceil(D/32 / 4) / 4); XI = ceil(D / 4096).
-template <int NB, int XI>
+// grid.x = k * F / 16 + n_sh: the routed tiles, then n_sh tiles of the FP8 shared
+// expert's gate/up (fp8::shared_gu_tile, h_sh to sh.out; they need no routing, so they
+// go last, into the slots the first routed workgroups leave).
+// NB = ceil(ceil(D/32 / 4) / 4); XI = ceil(D / 4096).
+template <int NB, int XI, bool SH>
 __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ pool, Layout L, ExpertSource src, int D, int F,
     float limit, uint16_t* __restrict__ hidden, int32_t* __restrict__ ws_slots,
-    float* __restrict__ ws_w) {
+    float* __restrict__ ws_w, fp8::DecodeArgs sh, int n_sh) {
   __shared__ __align__(16) uint8_t xl[GU_ZERO + ZERO_BYTES];
   __shared__ __align__(16) uint8_t sc[2 * 16 * (MAX_D / PIECE)];   // s1, s3 of the tile's rows
   __shared__ float red[GU_WAVES][2][16];
+  static_assert(GU_ZERO + ZERO_BYTES >= fp8::dec_tile_lds(1, fp8::SH_MAX_K), "shared tile LDS");
+  if constexpr (SH) {
+    if ((int)blockIdx.x >= (int)gridDim.x - n_sh) {
+      fp8::shared_gu_tile<64 * GU_WAVES>(sh, blockIdx.x - (gridDim.x - n_sh), xl);
+      return;
+    }
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int PT = D / PIECE;
@@ -164,14 +175,31 @@ __global__ void __launch_bounds__(64 * GU_WAVES) fp4_gate_up_kernel(
 }
 
 // grid.x = D / 16; block = 64 * k * DN_HALVES.  NB = ceil(ceil(F/32 / 2) / 4).
-template <int NB>
-__global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
+// SH: the workgroup also runs the FP8 shared expert's down tile of the same 16 rows
+// (w2 over act_quant(h_sh), sh.a = h_sh; its 16 w2 rows, h_sh and the scale row in LDS,
+// the 2k waves running the 16 virtual waves), whose bf16 y is the addend.  SH holds
+// k F <= SH_KF hidden values and a shared F <= SH_F in LDS.
+constexpr int SH_KF = 6 * 2880;
+constexpr int SH_F = 3072;
+template <bool SH>
+struct DnShape {
+  static constexpr int KF = SH ? SH_KF : MAX_KF;
+  static constexpr int THREADS = SH ? 64 * 6 * DN_HALVES : 64 * KMAX * DN_HALVES;
+};
+template <int NB, bool SH>
+__global__ void __launch_bounds__(DnShape<SH>::THREADS) fp4_down_kernel(
     const uint8_t* __restrict__ pool, Layout L, ExpertSource src, const int32_t* __restrict__ ws_slots, int D, int F,
     int k, const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ addend, float* __restrict__ routed,
-    uint16_t* __restrict__ out) {
-  __shared__ __align__(16) uint8_t hl[DN_ZERO + ZERO_BYTES];   // per expert: hi [F] bf16, lo [F] bf16
-  __shared__ __align__(16) uint8_t sc[MAX_KF / 2];              // per expert: s2 of the tile's rows
+    uint16_t* __restrict__ out, fp8::DecodeArgs sh) {
+  constexpr int KF = DnShape<SH>::KF;
+  __shared__ __align__(16) uint8_t hl[KF * 4 + ZERO_BYTES];     // per expert: hi [F] bf16, lo [F] bf16
+  __shared__ __align__(16) uint8_t sc[KF / 2];                  // per expert: s2 of the tile's rows
   __shared__ float vals[KMAX][DN_HALVES][16];
+  constexpr int SH_TILE = fp8::dec_tile_lds(1, SH_F);
+  __shared__ __align__(16) uint8_t sh_lds[SH ? SH_TILE + 18 * SH_F + SH_F / 32 : 16];
+  uint8_t* sh_w = sh_lds + SH_TILE;   // the 16 w2 rows (16 K bytes)
+  uint8_t* sh_h = sh_w + 16 * SH_F;   // h_sh as copied (bf16)
+  uint8_t* sh_sc = sh_h + 2 * SH_F;   // the tile's scale row
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
@@ -180,6 +208,10 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   const int half = wave - e * DN_HALVES;
   const int row0 = blockIdx.x * 16;
   const int j = lane & 15, kg = lane >> 4;
+  const int DNZ = KF * 4;   // the zero bytes after the staged hidden values
+  // (shared expert: its scale-row byte first, into LDS at the barrier)
+  uint32_t sh_sb = 0;
+  if constexpr (SH) sh_sb = sh.ws[0][(size_t)(row0 / 32) * (sh.K / 32) + min((int)threadIdx.x, sh.K / 32 - 1)];
   const int slot = expert_slot(src, ws_slots, e);
   const int PW = (PK + DN_HALVES - 1) / DN_HALVES;
   int pi[NB];
@@ -195,6 +227,7 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   // would otherwise wait for the copies too)
   const int slot_s = __builtin_amdgcn_readfirstlane(slot);
   copy_untracked(hidden, hl, k * F * 4, wave, nwaves, lane);
+  if constexpr (SH) copy_untracked(sh.a, sh_h, 2 * sh.K, wave, nwaves, lane);
   if (wave < k)
     copy_untracked(pool + (int64_t)ps * L.record_bytes + L.off[4] + (int64_t)row0 * PK, sc + wave * 16 * PK, 16 * PK,
                    0, 1, lane);
@@ -205,9 +238,22 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
 #pragma unroll
     for (int b = 0; b < NB; ++b) wd[b] = r2[pi[b]];
   }
-  if (threadIdx.x < ZERO_BYTES / 16) reinterpret_cast<uint4*>(hl + DN_ZERO)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+  if (threadIdx.x < ZERO_BYTES / 16) reinterpret_cast<uint4*>(hl + DNZ)[threadIdx.x] = make_uint4(0, 0, 0, 0);
   __builtin_amdgcn_s_waitcnt(VMCNT(NB));
+  if constexpr (SH) {
+    if ((int)threadIdx.x < sh.K / 32) sh_sc[threadIdx.x] = (uint8_t)sh_sb;
+    // the shared expert's 16 w2 rows (contiguous), in flight during the items
+    copy_untracked(sh.w[0] + (size_t)row0 * sh.K, sh_w, 16 * sh.K, wave, nwaves, lane);
+  }
   lds_sync();
+  if constexpr (SH) {   // act_quant(h_sh) into LDS, read after the items' barrier
+    fp8::DecAct<1, DnShape<SH>::THREADS> xa;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(xa.v) / sizeof(xa.v[0])); ++i)
+      xa.v[i] = *reinterpret_cast<const uint4*>(sh_h + 16 * min((int)threadIdx.x + DnShape<SH>::THREADS * i,
+                                                                 sh.K / 8 - 1));
+    fp8::dec_act_quant<1, DnShape<SH>::THREADS>(sh, 1, threadIdx.x, xa, sh_lds);
+  }
 
   f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
   if (slot >= 0) {
@@ -216,7 +262,7 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const uint32_t aoff =
-          (pv[b] && j < 2) ? (uint32_t)e * F * 4 + part + (uint32_t)pi[b] * (PIECE * 2) : (uint32_t)DN_ZERO;
+          (pv[b] && j < 2) ? (uint32_t)e * F * 4 + part + (uint32_t)pi[b] * (PIECE * 2) : (uint32_t)DNZ;
       const float sd = e8m0_to_f32(scale_rows[j * PK + pi[b]]);
 #pragma unroll
       for (int s = 0; s < 4; ++s) c = mfma(lds_a(hl, aoff + 16 * s), fp4_codes_to_b(word_of(wd[b], s), sd), c);
@@ -224,6 +270,14 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
   }
   // D[0][j] (hi) and D[1][j] (lo) sit in lane j, registers 0 and 1
   if (lane < 16) vals[e][half][lane] = c[0] + c[1];
+  if constexpr (SH) {   // the shared tile's partial tiles, after every wave's copies and quantization
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // this wave's w2 row copies
+    __syncthreads();
+    constexpr int NPV = 8;                // 16 virtual waves over 2k >= 2 waves
+    uint32_t bs[NPV][fp8::SH_CPV];
+    fp8::dec_wscale<NPV, fp8::SH_CPV>(sh_sc, sh.K, wave, nwaves, lane, bs);
+    fp8::dec_mfma_wlds<1, NPV, fp8::SH_CPV>(sh, 1, wave, nwaves, lane, sh_w, bs, sh_lds);
+  }
   __syncthreads();
   if (threadIdx.x < 16) {
     const int t = threadIdx.x;
@@ -236,7 +290,11 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) fp4_down_kernel(
       total = total + y;
     }
     if (routed) routed[n] = total;
-    if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(addend[n]) : total);
+    if constexpr (SH) {
+      if (out) out[n] = f32_to_bf16(total + round_bf16(fp8::dec_total(sh_lds, 1, sh.K, t, 0)));
+    } else {
+      if (out) out[n] = f32_to_bf16(addend ? total + bf16_to_f32(addend[n]) : total);
+    }
   }
 }
 
@@ -247,10 +305,22 @@ size_t fp4_workspace_bytes(int D, int F, int k) {
   return ws_offsets((size_t)k * F * sizeof(float)).total;
 }
 
+// After the routed workspace: h_sh [F_sh] bf16, then y_sh [D] bf16 (used when the
+// shared expert runs in launches of its own).
+size_t fp4_shared_region_bytes(int D, int F_sh) {
+  return align256((size_t)F_sh * 2) + align256((size_t)D * 2);
+}
+
+// The shapes the FP4 launches carry the shared expert for (else it runs first, in
+// launches of its own, and its output is the addend).
+bool fp4_shared_fused(int D, int F, int k, int F_sh) {
+  return D <= fp8::SH_MAX_K && F_sh <= SH_F && k >= 3 && k <= 6 && k * F <= SH_KF;
+}
+
 int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
                       ExpertSource src, const RouterCall* router, int D, int F, int k, float swiglu_limit,
                       const uint16_t* addend, float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
-                      hipStream_t s) {
+                      hipStream_t s, const fp8::SharedWeights* shared = nullptr) {
   CACHALOT_REQUIRE(pool && layout && src.slot_table && x, "moe_decode_fp4: null pointer");
   CACHALOT_REQUIRE(routed || out, "moe_decode_fp4: no output requested");
   CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_fp4: k=%d outside 1..%d", k, KMAX);
@@ -262,8 +332,9 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   CACHALOT_REQUIRE(k * F <= MAX_KF, "moe_decode_fp4: k*F=%d exceeds the %d hidden values staged per workgroup",
                    k * F, MAX_KF);
   const WsOffsets wo = ws_offsets((size_t)k * F * sizeof(float));
-  if (workspace == nullptr || workspace_bytes < wo.total)
-    return fail(CACHALOT_ESPACE, "moe_decode_fp4: workspace %zu < %zu bytes", workspace_bytes, wo.total);
+  const size_t need = wo.total + (shared ? fp4_shared_region_bytes(D, shared->F) : 0);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(CACHALOT_ESPACE, "moe_decode_fp4: workspace %zu < %zu bytes", workspace_bytes, need);
   Layout L;
   static const int used[6] = {0, 1, 3, 4, 6, 7};
   int rc = make_layout(layout, 6, used, L, "moe_decode_fp4");
@@ -278,13 +349,36 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
     if (rc) return rc;
     src = route_source(src, *router);
   }
+  // the shared expert: carried by the two launches below, or run first with its
+  // output as the addend
+  const bool sh = shared && fp4_shared_fused(D, F, k, shared->F);
+  fp8::DecodeArgs sh_gu{}, sh_dn{};
+  if (shared) {
+    uint16_t* h_sh = reinterpret_cast<uint16_t*>(ws + wo.total);
+    uint16_t* y_sh = h_sh + align256((size_t)shared->F * 2) / 2;
+    sh_gu = fp8::DecodeArgs{x, D, {shared->w1, shared->w3}, {shared->s1, shared->s3}, 1, shared->F, D,
+                            swiglu_limit, h_sh, shared->F};
+    sh_dn = fp8::DecodeArgs{h_sh, shared->F, {shared->w2, shared->w2}, {shared->s2, shared->s2}, 1, D, shared->F,
+                            swiglu_limit, y_sh, D};
+    if (!sh) {
+      rc = fp8::launch_decode(x, shared->w1, shared->s1, shared->w3, shared->s3, shared->w2, shared->s2, 1, D,
+                              shared->F, swiglu_limit, h_sh, y_sh, s);
+      if (rc) return rc;
+      addend = y_sh;
+    }
+  }
   const int PT = D / PIECE;
   const int nb_gu = ((PT + GU_WAVES - 1) / GU_WAVES + 3) / 4;
   const int xi = (D / 16 + 255) / 256;
-  const dim3 grid_gu(k * (F / 16)), block_gu(64 * GU_WAVES);
-#define CACHALOT_GU(NBV, XIV)                                                                                   \
-  hipLaunchKernelGGL((fp4_gate_up_kernel<NBV, XIV>), grid_gu, block_gu, 0, s, x, pool, L, src, D, F, swiglu_limit, \
-                     hidden, ws_slots, ws_w)
+  const int n_sh = sh ? shared->F / 8 : 0;
+  const dim3 grid_gu(k * (F / 16) + n_sh), block_gu(64 * GU_WAVES);
+#define CACHALOT_GU(NBV, XIV)                                                                                \
+  if (sh)                                                                                                      \
+    hipLaunchKernelGGL((fp4_gate_up_kernel<NBV, XIV, true>), grid_gu, block_gu, 0, s, x, pool, L, src, D, F,   \
+                       swiglu_limit, hidden, ws_slots, ws_w, sh_gu, n_sh);                                     \
+  else                                                                                                         \
+    hipLaunchKernelGGL((fp4_gate_up_kernel<NBV, XIV, false>), grid_gu, block_gu, 0, s, x, pool, L, src, D, F,  \
+                       swiglu_limit, hidden, ws_slots, ws_w, sh_gu, n_sh)
   // the smallest instantiated NB >= nb_gu (extra blocks are masked)
   if (xi == 1) {
     if (nb_gu <= 1) CACHALOT_GU(1, 1);
@@ -302,9 +396,13 @@ int launch_fp4_decode(const uint16_t* x, const uint8_t* pool, const cachalot_exp
   const int PK = F / PIECE;
   const int nb_dn = ((PK + DN_HALVES - 1) / DN_HALVES + 3) / 4;
   const dim3 grid_dn(D / 16), block_dn(64 * k * DN_HALVES);
-#define CACHALOT_DN(NBV)                                                                                    \
-  hipLaunchKernelGGL((fp4_down_kernel<NBV>), grid_dn, block_dn, 0, s, pool, L, src, ws_slots, D, F, k, hidden, addend, \
-                     routed, out)
+#define CACHALOT_DN(NBV)                                                                                        \
+  if (sh)                                                                                                         \
+    hipLaunchKernelGGL((fp4_down_kernel<NBV, true>), grid_dn, block_dn, 0, s, pool, L, src, ws_slots, D, F, k,    \
+                       hidden, nullptr, routed, out, sh_dn);                                                      \
+  else                                                                                                            \
+    hipLaunchKernelGGL((fp4_down_kernel<NBV, false>), grid_dn, block_dn, 0, s, pool, L, src, ws_slots, D, F, k,   \
+                       hidden, addend, routed, out, sh_dn)
   if (nb_dn <= 4) CACHALOT_DN(4);
   else if (nb_dn <= 8) CACHALOT_DN(8);
   else if (nb_dn <= 12) CACHALOT_DN(12);
@@ -354,4 +452,46 @@ extern "C" int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* 
                               route_scale};
   return launch_fp4_decode(x, pool, layout, src, &rt, D, F, k, swiglu_limit, addend, routed, out, workspace,
                            workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" size_t cachalot_moe_layer_decode_fp4_shared_workspace_bytes(int D, int F, int k, int shared_F) {
+  if (D <= 0 || F <= 0 || k <= 0 || k > cachalot::decode::KMAX || shared_F <= 0) return 0;
+  return cachalot::fp4_workspace_bytes(D, F, k) + cachalot::fp4_shared_region_bytes(D, shared_F);
+}
+
+extern "C" int cachalot_moe_layer_decode_fp4_shared(
+    const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias, int E, int k, int score_fn,
+    float gate_temp, float route_scale, int norm, int order, const uint8_t* pool,
+    const cachalot_expert_layout* layout, const int32_t* slot_table, int D, int F, float swiglu_limit,
+    const uint8_t* shared_w1, const uint8_t* shared_w1_scales, const uint8_t* shared_w3,
+    const uint8_t* shared_w3_scales, const uint8_t* shared_w2, const uint8_t* shared_w2_scales, int shared_F,
+    int32_t* idx_out, float* w_out, float* scores, float* routed, uint16_t* out, void* workspace,
+    size_t workspace_bytes, cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(gate_weight && gate_bias && scores, "moe_layer_decode_fp4_shared: null router pointer");
+  CACHALOT_REQUIRE(shared_w1 && shared_w1_scales && shared_w3 && shared_w3_scales && shared_w2 && shared_w2_scales,
+                   "moe_layer_decode_fp4_shared: null shared expert pointer");
+  CACHALOT_REQUIRE(out, "moe_layer_decode_fp4_shared: out is required (it carries the shared expert)");
+  CACHALOT_REQUIRE(D % 128 == 0, "moe_layer_decode_fp4_shared: D=%d must be a multiple of 128", D);
+  CACHALOT_REQUIRE(shared_F > 0 && shared_F % 32 == 0 && shared_F <= fp8::DEC_MAX_K && D <= fp8::DEC_MAX_K,
+                   "moe_layer_decode_fp4_shared: shared F=%d (a multiple of 32) and D=%d must be at most %d",
+                   shared_F, D, fp8::DEC_MAX_K);
+  auto a16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  CACHALOT_REQUIRE(a16(x) && a16(shared_w1) && a16(shared_w3) && a16(shared_w2),
+                   "moe_layer_decode_fp4_shared: x and the shared weights must be 16-byte aligned");
+  CACHALOT_REQUIRE(score_fn == CACHALOT_SCORE_SQRT_SOFTPLUS || score_fn == CACHALOT_SCORE_SIGMOID,
+                   "moe_layer_decode_fp4_shared: unknown score function %d", score_fn);
+  CACHALOT_REQUIRE(order == CACHALOT_ORDER_ASCENDING || order == CACHALOT_ORDER_RANK,
+                   "moe_layer_decode_fp4_shared: unknown order %d", order);
+  CACHALOT_REQUIRE(gate_temp != 0.0f, "moe_layer_decode_fp4_shared: gate_temp must be non-zero");
+  CACHALOT_REQUIRE(k >= 1 && k <= E && E <= 1024, "moe_layer_decode_fp4_shared: invalid topk=%d for %d experts", k,
+                   E);
+  decode::ExpertSource src{slot_table, nullptr, nullptr, E};
+  RouterCall rt{gate_weight, score_fn, gate_temp, scores, {}};
+  rt.tail = decode::RouteTail{gate_bias, slot_table, idx_out, w_out, nullptr, nullptr, nullptr, E, k, order, norm,
+                              route_scale};
+  const fp8::SharedWeights sh{shared_w1, shared_w1_scales, shared_w3, shared_w3_scales, shared_w2, shared_w2_scales,
+                              shared_F};
+  return launch_fp4_decode(x, pool, layout, src, &rt, D, F, k, swiglu_limit, nullptr, routed, out, workspace,
+                           workspace_bytes, (hipStream_t)stream, &sh);
 }

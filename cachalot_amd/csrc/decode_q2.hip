@@ -354,18 +354,7 @@ int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, c
                        const Layout& L, const ExpertSource& src, int32_t* ws_slots, float* ws_w, int D, int F,
                        int k, float limit, const uint16_t* addend, float* routed, uint16_t* out, uint8_t* hid,
                        hipStream_t s, const fp8::DecodeArgs* sh_gu, const fp8::DecodeArgs* sh_dn);
-namespace fp8 {
-int launch_decode(const uint16_t* x, const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, const uint8_t* s3,
-                  const uint8_t* w2, const uint8_t* s2, int M, int D, int F, float limit, uint16_t* h, uint16_t* y,
-                  hipStream_t s);
-}
-
-// The FP8 shared expert of a decode layer (E4M3 weights, E8M0 block-32 scales):
-// w1, w3 [F, D] with scales [F / 32, D / 32], w2 [D, F] with [D / 32, F / 32].
-struct SharedFp8 {
-  const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;
-  int F;
-};
+using SharedFp8 = fp8::SharedWeights;
 // After the routed workspace: h_sh [F] bf16, then y_sh [D] bf16 (used when the
 // shared expert runs in launches of its own).
 static size_t shared_region_bytes(int D, int F_sh) { return align256((size_t)F_sh * 2) + align256((size_t)D * 2); }

@@ -270,32 +270,8 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_kernel(const uint8_t*
   q2mx_gate_up_body<MAXM>(s, blockIdx.x, xplanes, pool, L, src, D, F, limit, hid, ws_slots, ws_w);
 }
 
-// ---- the FP8 shared expert carried by the routed launches (one token)
-// Its K (D in gate/up, its own F in down) runs as 16 virtual waves of at most two
-// chunks each (fp8_common.h), so the outputs equal the shared expert's own launches
-// bit for bit.
-constexpr int SH_MAX_K = fp8::DEC_VW * 2 * fp8::CHUNK;   // 4096
-constexpr int SH_CPV = 2;
-
-// One shared gate/up tile (8 rows of w1 and of w3) per workgroup: h [F_sh] bf16.
-__device__ __forceinline__ void shared_gu_tile(const fp8::DecodeArgs& p, int bx, uint8_t* lds) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  fp8::DecAct<1, GU_THREADS> xa;
-  fp8::dec_act_load<1, GU_THREADS>(p, 0, 1, tid, xa);
-  __builtin_amdgcn_sched_barrier(0);   // the activation loads ahead of the weight loads
-  fp8::DecW<fp8::DEC_VW / GU_WAVES, SH_CPV> w;
-  fp8::dec_w_load<true, GU_WAVES, fp8::DEC_VW / GU_WAVES, SH_CPV>(p, bx, wave, lane, w);
-  fp8::dec_act_quant<1, GU_THREADS>(p, 1, tid, xa, lds);
-  lds_sync();
-  fp8::dec_mfma<1, GU_WAVES, fp8::DEC_VW / GU_WAVES, SH_CPV>(p, 1, wave, lane, w, lds);
-  lds_sync();
-  if (tid < 8) {
-    const float g = round_bf16(fp8::dec_total(lds, 1, p.K, tid, 0));
-    const float u = round_bf16(fp8::dec_total(lds, 1, p.K, tid + 8, 0));
-    p.out[bx * 8 + tid] = f32_to_bf16(fp8::swiglu_h(g, u, p.limit));
-  }
-}
+using fp8::SH_CPV;
+using fp8::SH_MAX_K;
 
 // grid.x = k * F / 16 + n_sh: the routed workgroups, then the shared expert's gate/up
 // tiles.  (Workgroups are dispatched in order and not all of them fit the chip at
@@ -313,7 +289,7 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_shared_kernel(const u
   constexpr int SH_LDS = fp8::dec_tile_lds(1, SH_MAX_K);
   __shared__ __align__(16) uint8_t buf[sizeof(GuLds) > SH_LDS ? sizeof(GuLds) : SH_LDS];
   if ((int)blockIdx.x >= (int)gridDim.x - n_sh) {
-    shared_gu_tile(sh, blockIdx.x - (gridDim.x - n_sh), buf);
+    fp8::shared_gu_tile<GU_THREADS>(sh, blockIdx.x - (gridDim.x - n_sh), buf);
     return;
   }
   q2mx_gate_up_body<MAXM>(*reinterpret_cast<GuLds*>(buf), blockIdx.x, xplanes, pool, L, src, D, F, limit,
@@ -474,8 +450,8 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   lds_sync();
   if constexpr (SH) {   // the shared tile's partial tiles (read after the next barrier)
     uint32_t bs[SH_NPV][SH_CPV];
-    fp8::dec_wscale<DN_WAVES, SH_NPV, SH_CPV>(sh_sc, sh.K, wave, lane, bs);
-    fp8::dec_mfma_wlds<1, DN_WAVES, SH_NPV, SH_CPV>(sh, 1, wave, lane, sh_w, bs, sh_lds);
+    fp8::dec_wscale<SH_NPV, SH_CPV>(sh_sc, sh.K, wave, DN_WAVES, lane, bs);
+    fp8::dec_mfma_wlds<1, SH_NPV, SH_CPV>(sh, 1, wave, DN_WAVES, lane, sh_w, bs, sh_lds);
   }
 
   // ---- 2. per expert (16 lanes each): the row values rounded to bf16; then the

@@ -282,8 +282,9 @@ __device__ __forceinline__ void dec_mfma(const DecodeArgs& p, int mt, int wave, 
 //    [16 bx, 16 bx + 16) x K bytes): the E8M0 scales of the wave's chunks (bsc =
 //    the tile's scale row, K / 32 bytes), then the partial tiles as dec_mfma forms
 //    them -- the same operands, so the same bits.
-template <int RW, int NPV, int CPV>
-__device__ __forceinline__ void dec_wscale(const uint8_t* bsc, int K, int wave, int lane, uint32_t (&bs)[NPV][CPV]) {
+template <int NPV, int CPV>
+__device__ __forceinline__ void dec_wscale(const uint8_t* bsc, int K, int wave, int RW, int lane,
+                                           uint32_t (&bs)[NPV][CPV]) {
   const int kg = lane >> 4;
   const int nch = (K + CHUNK - 1) / CHUNK;
 #pragma unroll
@@ -297,9 +298,9 @@ __device__ __forceinline__ void dec_wscale(const uint8_t* bsc, int K, int wave, 
     }
 }
 
-template <int MT, int RW, int NPV, int CPV>
-__device__ __forceinline__ void dec_mfma_wlds(const DecodeArgs& p, int mt, int wave, int lane, const uint8_t* wl,
-                                              const uint32_t (&bs)[NPV][CPV], uint8_t* lds) {
+template <int MT, int NPV, int CPV>
+__device__ __forceinline__ void dec_mfma_wlds(const DecodeArgs& p, int mt, int wave, int RW, int lane,
+                                              const uint8_t* wl, const uint32_t (&bs)[NPV][CPV], uint8_t* lds) {
   const int c16 = lane & 15, kg = lane >> 4;
   const int K = p.K, nkb = K / BLOCK, nch = (K + CHUNK - 1) / CHUNK, stride = dec_stride(K);
   const uint8_t* codes = lds;
@@ -347,6 +348,49 @@ __device__ __forceinline__ float dec_total(const uint8_t* lds, int MT, int K, in
   for (int v = 1; v < DEC_VW; ++v) s += red[(v * 16 + col) * 4 + t];
   return s;
 }
+
+
+// ---- the shared expert carried by routed decode launches (one token)
+// K (D in gate/up, the shared F in down) runs as the 16 virtual waves above, at most
+// two chunks each, so the outputs equal the shared expert's own launches bit for bit.
+constexpr int SH_MAX_K = DEC_VW * 2 * CHUNK;   // 4096
+constexpr int SH_CPV = 2;
+
+// One shared gate/up tile (8 rows of w1 and of w3) per workgroup of THREADS threads
+// (4 or more waves): h [F_sh] bf16 to p.out.  lds: dec_tile_lds(1, K) bytes.
+template <int THREADS>
+__device__ __forceinline__ void shared_gu_tile(const DecodeArgs& p, int bx, uint8_t* lds) {
+  constexpr int RW = THREADS / 64;
+  constexpr int NPV = (DEC_VW + RW - 1) / RW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  DecAct<1, THREADS> xa;
+  dec_act_load<1, THREADS>(p, 0, 1, tid, xa);
+  __builtin_amdgcn_sched_barrier(0);   // the activation loads ahead of the weight loads
+  DecW<NPV, SH_CPV> w;
+  dec_w_load<true, RW, NPV, SH_CPV>(p, bx, wave, lane, w);
+  dec_act_quant<1, THREADS>(p, 1, tid, xa, lds);
+  lds_sync();
+  dec_mfma<1, RW, NPV, SH_CPV>(p, 1, wave, lane, w, lds);
+  lds_sync();
+  if (tid < 8) {
+    const float g = round_bf16(dec_total(lds, 1, p.K, tid, 0));
+    const float u = round_bf16(dec_total(lds, 1, p.K, tid + 8, 0));
+    p.out[bx * 8 + tid] = f32_to_bf16(swiglu_h(g, u, p.limit));
+  }
+}
+
+// The FP8 shared expert of a decode layer (E4M3 weights, E8M0 block-32 scales):
+// w1, w3 [F, D] with scales [F / 32, D / 32], w2 [D, F] with [D / 32, F / 32].
+struct SharedWeights {
+  const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;
+  int F;
+};
+
+// Standalone one-token decode of the shared expert (shared_fp8.hip): h [F], y [D] bf16.
+int launch_decode(const uint16_t* x, const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, const uint8_t* s3,
+                  const uint8_t* w2, const uint8_t* s2, int M, int D, int F, float limit, uint16_t* h, uint16_t* y,
+                  hipStream_t s);
 
 }  // namespace fp8
 }  // namespace cachalot

@@ -99,9 +99,9 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
                      want_out: bool = True, shared: dict | None = None):
     """One token through one MoE layer with routing on the device (three launches).
 
-    ``shared`` (2-bit banks): the layer's FP8 shared expert as ``shared_args``
-    bundles it; out = bf16(routed + shared expert), the shared expert's tiles
-    carried by the routed launches (``moe_layer_metal.py:381-397``).
+    ``shared``: the layer's FP8 shared expert as ``shared_args`` bundles it;
+    out = bf16(routed + shared expert), the shared expert's tiles carried by the
+    routed launches where the shapes allow (``moe_layer_metal.py:381-397``).
 
     Returns (routed fp32 [D] or None, out bf16 [D] or None, RouterResult)."""
     fmt: ExpertFormat = pool.format
@@ -140,8 +140,8 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
     tail = (_lib.ptr(addend), idx.data_ptr(), w.data_ptr(), scores.data_ptr(), _lib.ptr(routed), _lib.ptr(out))
     stream = _lib.stream_handle(dev)
     if shared is not None:
-        if fmt.kind != "affine":
-            raise ValueError("the shared expert rides the 2-bit decode only; pass its output as addend")
+        if fmt.kind not in ("affine", "fp4"):
+            raise ValueError(f"unknown expert format {fmt.kind!r}")
         if addend is not None:
             raise ValueError("pass either the shared expert weights or addend, not both")
         if not want_out:
@@ -150,11 +150,17 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
 
         sw = shared_weights(shared, d)
         _lib.require_cuda(*sw[:6])
-        nbytes = L.cachalot_moe_layer_decode_q2_shared_workspace_bytes(d, f, topk, sw[6])
-        ws = workspace(dev, nbytes)
-        rc = L.cachalot_moe_layer_decode_q2_shared(*args_route, fmt.group_size, float(swiglu_limit),
-                                                   *(t.data_ptr() for t in sw[:6]), sw[6], *tail[1:],
-                                                   ws.data_ptr(), nbytes, stream)
+        ptrs = tuple(t.data_ptr() for t in sw[:6])
+        if fmt.kind == "affine":
+            nbytes = L.cachalot_moe_layer_decode_q2_shared_workspace_bytes(d, f, topk, sw[6])
+            ws = workspace(dev, nbytes)
+            rc = L.cachalot_moe_layer_decode_q2_shared(*args_route, fmt.group_size, float(swiglu_limit), *ptrs, sw[6],
+                                                       *tail[1:], ws.data_ptr(), nbytes, stream)
+        else:
+            nbytes = L.cachalot_moe_layer_decode_fp4_shared_workspace_bytes(d, f, topk, sw[6])
+            ws = workspace(dev, nbytes)
+            rc = L.cachalot_moe_layer_decode_fp4_shared(*args_route, float(swiglu_limit), *ptrs, sw[6], *tail[1:],
+                                                        ws.data_ptr(), nbytes, stream)
     elif fmt.kind == "affine":
         nbytes = L.cachalot_moe_decode_q2_workspace_bytes(d, f, topk)
         ws = workspace(dev, nbytes)

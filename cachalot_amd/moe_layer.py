@@ -22,10 +22,10 @@ rounding points (fp32 outputs throughout, ``fp4_gemv_metal.py:102-103``), and
 it is not consulted for affine banks; this build has the one device path.
 
 The FP8 shared expert (``shared_*``, ``moe_layer_metal.py:381-397``) is added
-in the combine: ``out = bf16(routed + shared)``.  On the device path over a
-2-bit bank its tiles run inside the routed gate/up and down launches (one weight
-stream); otherwise it runs first, on the same stream, and its bf16 output is the
-combine's addend.  Both give the same bits.  ``addend`` (bf16 [D]) is the same hook for a
+in the combine: ``out = bf16(routed + shared)``.  On the device path its tiles
+run inside the routed gate/up and down launches (one weight stream); otherwise it
+runs first, on the same stream, and its bf16 output is the combine's addend.
+Both give the same bits.  ``addend`` (bf16 [D]) is the same hook for a
 caller that computes the shared branch itself; it cannot be combined with
 ``shared_*``.
 """
@@ -71,12 +71,12 @@ def moe_layer_forward(
         raise ValueError("pass either the shared expert weights or addend, not both")
     pool = expert_store.pool
     device_path = expert_store.layer_fully_resident(layer_id) and x.dtype == torch.bfloat16 and topk <= 8
-    if shared is not None and not (device_path and pool.format.kind == "affine"):
+    if shared is not None and not device_path:
         addend = shared_expert_forward(x.to(torch.bfloat16), **shared, swiglu_limit=swiglu_limit)
         shared = None
     if device_path:
-        # routing, slot lookup and experts on the device, no host round trip (a 2-bit
-        # bank's decode launches also carry the shared expert)
+        # routing, slot lookup and experts on the device, no host round trip (the
+        # decode launches also carry the shared expert)
         _, out, route = moe_layer_decode(x, gate_weight, gate_bias, pool, expert_store.layer_table(layer_id),
                                          topk=topk, gate_temp=gate_temp, route_scale=route_scale,
                                          norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order,

@@ -182,6 +182,25 @@ int cachalot_moe_layer_decode_fp4(const uint16_t* x, const uint16_t* gate_weight
                                   const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
                                   float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
                                   cachalot_stream_t stream);
+/* cachalot_moe_layer_decode_fp4_shared: cachalot_moe_layer_decode_fp4 with the
+ * layer's FP8 shared expert in place of `addend`, as cachalot_moe_layer_decode_q2_shared
+ * (same shared arguments, out required, bit for bit the two-call form).  The FP4
+ * launches carry the shared tiles for D <= 4096, shared_F <= 3072, 3 <= k <= 6 and
+ * k * F <= 17280; other shapes run the shared expert first.  Workspace from
+ * cachalot_moe_layer_decode_fp4_shared_workspace_bytes.  Replaces moe_layer_forward
+ * over an FP4 bank with shared_* (src/cachalot/model/moe_layer_metal.py:133-405,
+ * :381-397; shared_expert_metal.py:44-188). */
+size_t cachalot_moe_layer_decode_fp4_shared_workspace_bytes(int D, int F, int k, int shared_F);
+int cachalot_moe_layer_decode_fp4_shared(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                         int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                         int order, const uint8_t* pool,
+                                         const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                         int D, int F, float swiglu_limit, const uint8_t* shared_w1,
+                                         const uint8_t* shared_w1_scales, const uint8_t* shared_w3,
+                                         const uint8_t* shared_w3_scales, const uint8_t* shared_w2,
+                                         const uint8_t* shared_w2_scales, int shared_F, int32_t* idx_out,
+                                         float* w_out, float* scores, float* routed, uint16_t* out, void* workspace,
+                                         size_t workspace_bytes, cachalot_stream_t stream);
 
 /* Many tokens (prefill chunk, batched decode), expert-major.
  *

@@ -234,20 +234,25 @@ def test_shared_expert_argument_errors_and_no_limit(cuda):
         shared_expert_forward(_to_dev_bf16(x, cuda), **{**dev, "w2": dev["w1"]})       # w2 shape
 
 
-@pytest.mark.parametrize("d,f_sh,k,limit", [(4096, 2880, 6, 10.0), (4096, 2880, 8, 0.25), (2048, 4096, 6, 0.0),
-                                            (1024, 640, 3, 10.0), (5120, 2880, 6, 10.0), (4096, 4608, 6, 10.0)])
-def test_layer_decode_carries_the_shared_expert(cuda, d, f_sh, k, limit):
-    """cachalot_moe_layer_decode_q2_shared equals, bit for bit, the shared expert's own
-    call followed by the layer decode with its output as addend -- where the routed
-    launches carry the shared tiles (D, F_sh <= 4096) and where the shared expert
-    runs first (D = 5120, F_sh = 4608); routing and the fp32 routed sum unchanged."""
+@pytest.mark.parametrize("kind,d,f_sh,k,limit", [
+    ("affine", 4096, 2880, 6, 10.0), ("affine", 4096, 2880, 8, 0.25), ("affine", 2048, 4096, 6, 0.0),
+    ("affine", 1024, 640, 3, 10.0), ("affine", 5120, 2880, 6, 10.0), ("affine", 4096, 4608, 6, 10.0),
+    ("fp4", 4096, 2880, 6, 10.0), ("fp4", 2048, 3072, 3, 0.25), ("fp4", 4096, 2880, 8, 10.0),
+    ("fp4", 1024, 640, 2, 0.0)])
+def test_layer_decode_carries_the_shared_expert(cuda, kind, d, f_sh, k, limit):
+    """cachalot_moe_layer_decode_{q2,fp4}_shared equal, bit for bit, the shared expert's
+    own call followed by the layer decode with its output as addend -- where the routed
+    launches carry the shared tiles (2-bit: D, F_sh <= 4096; FP4: also 3 <= k <= 6) and
+    where the shared expert runs first (D = 5120, F_sh = 4608, FP4 at k = 8 and 2);
+    routing and the fp32 routed sum unchanged."""
     from cachalot_amd import synth
     from cachalot_amd.moe_decode import moe_layer_decode
     from cachalot_amd.shared_expert import shared_expert_forward
-    from cachalot_amd.storage.index import affine_format
+    from cachalot_amd.storage.index import affine_format, fp4_format
 
     f, e = 2880, 24
-    store = make_store(affine_format(d, f), n_layers=1, n_experts=e)
+    fmt = affine_format(d, f) if kind == "affine" else fp4_format(d, f)
+    store = make_store(fmt, n_layers=1, n_experts=e)
     w, b = synth.router_weights(SEED, 3, e, d, cuda)
     rng = np.random.default_rng(SEED + d + f_sh + k)
     (w1, s1), (w3, s3), (w2, s2) = _expert(rng, d, f_sh)
@@ -259,9 +264,9 @@ def test_layer_decode_carries_the_shared_expert(cuda, d, f_sh, k, limit):
         args = (xs[t], w, b, store.pool, store.layer_table(0))
         r1, o1, rt1 = moe_layer_decode(*args, **kw, shared=plain)
         r2, o2, rt2 = moe_layer_decode(*args, **kw, addend=shared_expert_forward(xs[t], **plain, swiglu_limit=limit))
-        assert torch.equal(rt1.indices, rt2.indices) and torch.equal(rt1.weights, rt2.weights), (d, f_sh, k, t)
-        assert torch.equal(r1, r2), (d, f_sh, k, t)
-        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), (d, f_sh, k, t)
+        assert torch.equal(rt1.indices, rt2.indices) and torch.equal(rt1.weights, rt2.weights), (kind, d, f_sh, k, t)
+        assert torch.equal(r1, r2), (kind, d, f_sh, k, t)
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), (kind, d, f_sh, k, t)
     # a captured step replays to the eager result (the workspace exists from the eager calls)
     x = xs[0].clone()
     torch.cuda.synchronize()
