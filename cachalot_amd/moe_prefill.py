@@ -64,14 +64,18 @@ def permute(indices: torch.Tensor, weights: torch.Tensor, n_experts: int):
 
 def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tensor, pool: HBMSlotPool,
                     slot_table: torch.Tensor, *, swiglu_limit: float = 10.0, addend: torch.Tensor | None = None,
-                    want_routed: bool = False, want_out: bool = True, want_terms: bool = False):
+                    want_routed: bool = False, want_out: bool = True, want_terms: bool = False,
+                    addend_ready: torch.cuda.Event | None = None):
     """x [T, D] bf16, routes [T, k] -> (routed fp32 [T, D] or None, out bf16 [T, D] or None).
 
     routed[t] = sum over route slots s (in order) of expert idx[t, s] applied to x[t]
     with router weight w[t, s]; out = bf16(routed + addend).  A route whose expert
     id lies outside [0, E), or whose expert has no slot, contributes zero.  With
     ``want_terms`` the per-route expert outputs y [T, k, D] bf16 (each one the
-    reference's bf16 cast of its expert's output) come back as a third value."""
+    reference's bf16 cast of its expert's output) come back as a third value.
+    ``addend_ready``, when given, is an event recorded after the work that
+    writes ``addend`` on another stream: the combine waits for it, the grouped
+    GEMMs before it do not."""
     fmt = pool.format
     d, f = fmt.d_model, fmt.d_ff
     if x.ndim != 2 or x.shape[1] != d:
@@ -108,9 +112,45 @@ def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tenso
     _lib.check(rc, "grouped_experts")
     routed = torch.empty((t, d), dtype=torch.float32, device=dev) if want_routed else None
     out = torch.empty((t, d), dtype=torch.bfloat16, device=dev) if want_out else None
+    if addend_ready is not None:
+        torch.cuda.current_stream(dev).wait_event(addend_ready)
     rc = L.cachalot_unpermute_combine(y.data_ptr(), _lib.ptr(addend), t, k, d, _lib.ptr(routed), _lib.ptr(out), stream)
     _lib.check(rc, "unpermute_combine")
     return (routed, out, y) if want_terms else (routed, out)
+
+
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+# From this many tokens on the shared expert's GEMMs run beside the router and
+# the routed grouped GEMMs; below it the launches are too short to gain.
+SIDE_STREAM_MIN_TOKENS = 256
+
+
+def _shared_on_side_stream(x: torch.Tensor, shared: dict, swiglu_limit: float):
+    """Shared expert of x -> (bf16 [T, D], event or None).
+
+    Many-token calls outside graph capture run it on a second stream (default
+    priority) forked from the current one; the returned event marks its end."""
+    xb = x.to(torch.bfloat16)
+    if x.shape[0] < SIDE_STREAM_MIN_TOKENS or torch.cuda.is_current_stream_capturing():
+        return shared_expert_forward_batched(xb, **shared, swiglu_limit=swiglu_limit), None
+    dev = x.device
+    main = torch.cuda.current_stream(dev)
+    side = _SIDE_STREAMS.get(dev.index)
+    if side is None:
+        side = torch.cuda.Stream(device=dev)
+        _SIDE_STREAMS[dev.index] = side
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        addend = shared_expert_forward_batched(xb, **shared, swiglu_limit=swiglu_limit)
+        done = torch.cuda.Event()
+        done.record(side)
+    # tensors made or read on the side stream stay allocated until it is done
+    xb.record_stream(side)
+    addend.record_stream(main)
+    for v in shared.values():
+        if isinstance(v, torch.Tensor):
+            v.record_stream(side)
+    return addend, done
 
 
 def moe_prefill_grouped(
@@ -152,7 +192,9 @@ def moe_prefill_grouped(
     if shared is not None:
         if addend is not None:
             raise ValueError("pass either the shared expert weights or addend, not both")
-        addend = shared_expert_forward_batched(x.to(torch.bfloat16), **shared, swiglu_limit=swiglu_limit)
+        addend, addend_ready = _shared_on_side_stream(x, shared, swiglu_limit)
+    else:
+        addend_ready = None
     if batched:
         indices, weights, scores = route_topk_rows(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp,
                                                    route_scale=route_scale, norm_topk_prob=norm_topk_prob,
@@ -176,5 +218,5 @@ def moe_prefill_grouped(
         expert_store.get_many(entries)
     table = expert_store.layer_table(layer_id)
     _, out = grouped_experts(x.to(torch.bfloat16), route.indices, route.weights, expert_store.pool, table,
-                             swiglu_limit=swiglu_limit, addend=addend)
+                             swiglu_limit=swiglu_limit, addend=addend, addend_ready=addend_ready)
     return out.to(x.dtype), route

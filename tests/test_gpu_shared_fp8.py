@@ -206,6 +206,12 @@ def test_layer_entries_add_the_shared_expert(cuda):
     outp, _ = moe_prefill_grouped(x, **kw, **shared)
     refp, _ = moe_prefill_grouped(x, **kw, addend=shared_expert_forward_batched(x, **plain))
     assert torch.equal(outp.view(torch.int16), refp.view(torch.int16))
+    # from SIDE_STREAM_MIN_TOKENS tokens on the shared expert runs on a second stream
+    xl = synth.activations(SEED, 91, 300, d, cuda)
+    refl, _ = moe_prefill_grouped(xl, **kw, addend=shared_expert_forward_batched(xl, **plain))
+    for _ in range(3):
+        outl, _ = moe_prefill_grouped(xl, **kw, **shared)
+        assert torch.equal(outl.view(torch.int16), refl.view(torch.int16))
     with pytest.raises(ValueError):
         moe_layer_forward(x[0], **kw, **shared, addend=refp[0])
 
