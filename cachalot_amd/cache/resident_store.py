@@ -21,6 +21,7 @@ expressed on one HIP stream.
 """
 from __future__ import annotations
 
+import os
 from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Callable
@@ -31,6 +32,13 @@ import torch
 from ..storage.index import ExpertEntry, ExpertFormat
 from .resident import ResidentExpert
 from .slots import ExpertSlot, HBMSlotPool
+
+
+# Free slots a prediction leaves for the demand path (resident_store.py:52 of the reference).
+PREDICT_SLOT_RESERVE = 16
+# At most this many non-resident predicted experts per layer and call, in the
+# caller's (ranked) order; 0 = no limit (resident_store.py:58).
+DECODE_PREFETCH_LIMIT = int(os.environ.get("CACHALOT_DECODE_PREFETCH_LIMIT", "0"))
 
 
 @dataclass
@@ -71,6 +79,20 @@ class ResidentExpertStore:
         self.decode_substitute_ranks = 4
         self.substituted_experts = 0
         self.skipped_experts = 0
+        # one-layer-early routing prediction (resident_store.py:230-262 of the
+        # reference): layer -> (gate weight, gate bias), set by the runtime; a
+        # predicted expert is loaded into a free slot ahead of its layer and becomes
+        # resident only when that layer requests it
+        self.decode_gates: dict[int, tuple] = {}
+        self.predict_slot_reserve = PREDICT_SLOT_RESERVE
+        self.predicted_loads = 0
+        self.predicted_used = 0
+        self.predicted_expired = 0
+        self.predicted_wasted_bytes = 0
+        self._inflight: dict[tuple[int, int], tuple[ExpertSlot, ExpertEntry]] = {}
+        self._inflight_deadline: dict[tuple[int, int], tuple[int, int]] = {}
+        self._decode_pass = 0
+        self._decode_layer = -1
 
     # ----------------------------------------------------------- slot table
     def track_slots(self, n_layers: int | None = None, n_experts: int | None = None) -> torch.Tensor:
@@ -125,7 +147,68 @@ class ResidentExpertStore:
                 self._set_table(key, -1)
                 self.stats.evictions += 1
                 return slot
+        for key in list(self._inflight):  # then a prediction nobody has asked for yet
+            if key not in protect:
+                return self._drop_prediction(key)
         raise TimeoutError("every slot holds an expert of the current request")
+
+    # ------------------------------------------------------ routing prediction
+    def prefetch_decode(self, entries: list[ExpertEntry], limit: int | None = None) -> int:
+        """Load experts predicted for an upcoming decode layer into free slots,
+        never evicting a resident and leaving ``predict_slot_reserve`` slots free
+        (``resident_store.py:291-320`` of the reference).  Entries are taken in
+        the caller's order, at most ``limit`` (default DECODE_PREFETCH_LIMIT, 0 =
+        no limit) per layer.  Returns how many loads were started."""
+        if self.loader is None:
+            return 0
+        cap = DECODE_PREFETCH_LIMIT if limit is None else limit
+        per_layer: dict[int, int] = {}
+        submitted = 0
+        for entry in entries:
+            if cap and per_layer.get(entry.layer, 0) >= cap:
+                continue
+            key = (entry.layer, entry.expert)
+            if key in self._items or key in self._inflight:
+                continue
+            if self.pool.free_count() <= self.predict_slot_reserve:
+                break
+            slot = self.pool.try_acquire()
+            if slot is None:
+                break
+            self.loader(entry, slot)
+            self._inflight[key] = (slot, entry)
+            self._inflight_deadline[key] = (self._decode_pass, entry.layer)
+            self.predicted_loads += 1
+            submitted += 1
+            per_layer[entry.layer] = per_layer.get(entry.layer, 0) + 1
+        return submitted
+
+    def _advance_decode_pass(self, layer: int) -> None:
+        """Decode requests layers in ascending order, once per token: a layer that
+        does not advance starts a new walk (``resident_store.py:420-430``)."""
+        if layer <= self._decode_layer:
+            self._decode_pass += 1
+        self._decode_layer = layer
+
+    def _drop_prediction(self, key) -> ExpertSlot:
+        slot, _ = self._inflight.pop(key)
+        self._inflight_deadline.pop(key, None)
+        self.predicted_expired += 1
+        self.predicted_wasted_bytes += self.expert_bytes
+        self.stats.bytes_loaded += self.expert_bytes
+        return slot
+
+    def _sweep_inflight(self, keep) -> None:
+        """Give back the slots of predictions whose walk is over or whose target
+        layer has already been requested (``resident_store.py:432-476``); a
+        prediction for a layer this walk has not reached yet is kept."""
+        for key in list(self._inflight):
+            if key in keep:
+                continue
+            pass_id, target = self._inflight_deadline.get(key, (self._decode_pass, self._decode_layer))
+            if pass_id == self._decode_pass and target > self._decode_layer:
+                continue
+            self.pool.release(self._drop_prediction(key))
 
     def _wrap(self, key, slot) -> ResidentExpert:
         return ResidentExpert(layer=key[0], expert=key[1], slot=slot)
@@ -140,12 +223,37 @@ class ResidentExpertStore:
         """Resident experts for `entries`, in order; misses are loaded (strongest
         priority first) up to `max_misses`, the rest returned as None.  Without a
         loader a miss raises KeyError, as ``moe_layer_forward`` does for a missing
-        expert (``moe_layer_metal.py:279-283``)."""
+        expert (``moe_layer_metal.py:279-283``).
+
+        An entry predicted earlier (``prefetch_decode``) is admitted from its slot
+        without a load.  ``prefetch`` (a list, or a callable returning one) names
+        experts predicted for a later layer; they are loaded into free slots after
+        this layer's misses (``resident_store.py:789-943``), ``prefetch_limit``
+        capping them per layer.  Loads here are enqueued on the stream as they are
+        issued, so ``prefetch_after`` (the reference's choice between issuing the
+        prediction beside or after the demand reads) changes nothing and is only
+        accepted."""
         keys = [(e.layer, e.expert) for e in entries]
         out: list[ResidentExpert | None] = [None] * len(keys)
+        if keys:
+            # decode asks for one layer at a time, so the first entry names it
+            self._advance_decode_pass(keys[0][0])
+        self._sweep_inflight(keep=set(keys))
         misses = []
         for i, key in enumerate(keys):
             slot = self._items.get(key)
+            if slot is None and key in self._inflight:
+                # predicted earlier: its data already sits in a slot, so it becomes
+                # resident without a load (counted as the miss it was)
+                slot, _ = self._inflight.pop(key)
+                self._inflight_deadline.pop(key, None)
+                self._items[key] = slot
+                self._set_table(key, slot.index)
+                self.predicted_used += 1
+                self.stats.misses += 1
+                self.stats.bytes_loaded += self.expert_bytes
+                out[i] = self._wrap(key, slot)
+                continue
             if slot is not None:
                 self._items.move_to_end(key)
                 self.stats.hits += 1
@@ -179,6 +287,12 @@ class ResidentExpertStore:
                 self.stats.misses += 1
                 self.stats.bytes_loaded += self.expert_bytes
                 out[i] = self._wrap(keys[i], slot)
+        if prefetch:
+            # predicted experts of a later layer, after this layer's own loads have
+            # their slots (a callable is evaluated only here)
+            ents = prefetch() if callable(prefetch) else prefetch
+            if ents:
+                self.prefetch_decode(list(ents), prefetch_limit)
         return out
 
 

@@ -370,3 +370,45 @@ def test_decode_substitution_replaces_weak_misses(cuda):
     want, ys = _oracle_out(fmt, x, want_ids, wts)
     report("substitution", replaced=n, ids=want_ids)
     assert np.all(np.abs(got - want) <= 2e-3 * np.abs(want).max() + np.sum(bf16_ulp(ys), 0) + bf16_ulp(want))
+
+
+def test_routing_prediction_loads_the_next_layer_ahead(cuda):
+    """With the next layer's gate in decode_gates, a partially resident layer also
+    routes its input through that gate (top-6, moe_layer_metal.py:186-244) and loads
+    those experts ahead; the next layer then admits them without a load.  The outputs
+    equal those of the same calls without prediction, bit for bit."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_layer import moe_layer_forward
+    from cachalot_amd.router import route_topk_fused
+    from cachalot_amd.storage.index import affine_format
+
+    fmt = affine_format(4096, 2880)
+    gates = {la: synth.router_weights(SEED, la, 384, 4096, cuda) for la in range(2)}
+    x = synth.activations(SEED, 809, 1, 4096, cuda)[0]
+    outs = []
+    for predict in (False, True):
+        store = make_store(fmt, n_layers=2, n_experts=384, keys=[], n_slots=32, loader=True)
+        store.predict_slot_reserve = 0
+        loads = []
+        inner = store.loader
+        store.loader = lambda entry, slot: (loads.append((entry.layer, entry.expert)), inner(entry, slot))
+        if predict:
+            store.decode_gates = {1: gates[1]}
+        got = []
+        for la in range(2):
+            w, b = gates[la]
+            out, route = moe_layer_forward(x, layer_id=la, gate_weight=w, gate_bias=b, expert_index=None,
+                                           expert_store=store, topk=6, route_scale=1.0, score_fn="sigmoid")
+            got.append((out.clone(), [int(e) for e in route.indices.tolist()]))
+        outs.append(got)
+        if predict:
+            pred = [int(e) for e in route_topk_fused(x, *gates[1], topk=6, route_scale=1.0,
+                                                      score_fn="sigmoid").indices.tolist()]
+            assert got[1][1] == pred                      # layer 1 routes the same input through the same gate
+            assert store.predicted_loads == 6 and store.predicted_used == 6 and store.predicted_expired == 0
+            assert loads[6:12] == [(1, e) for e in reversed(pred)]   # strongest first, ascending order
+            assert len(loads) == 12                       # layer 1 loaded nothing itself
+        else:
+            assert len(loads) == 12 and store.predicted_loads == 0
+    for (a, ia), (b, ib) in zip(outs[0], outs[1]):
+        assert ia == ib and torch.equal(a.view(torch.int16), b.view(torch.int16))

@@ -148,6 +148,42 @@ def test_get_many_loads_a_repeated_key_once():
     assert budget[2] is None
 
 
+def test_predicted_experts_load_ahead_and_expire():
+    """prefetch_decode loads predicted experts into free slots without making them
+    resident; the layer that asks for one admits it without a load, and the rest expire
+    once their layer has been requested or a new walk begins
+    (resident_store.py:291-320,432-476,871-940 of the reference)."""
+    from cachalot_amd.cache.resident_store import ResidentExpertStore
+    from cachalot_amd.storage.index import ExpertEntry, affine_format
+
+    loads = []
+    store = ResidentExpertStore(fmt=affine_format(256, 128), n_slots=8, n_layers=3, n_experts=8, device="cpu",
+                                loader=lambda entry, slot: loads.append((entry.layer, entry.expert)))
+    store.predict_slot_reserve = 0
+    assert store.prefetch_decode([ExpertEntry(1, 3), ExpertEntry(1, 4), ExpertEntry(1, 3)]) == 2
+    assert loads == [(1, 3), (1, 4)] and not store.is_resident((1, 3)) and store.layer_table(1)[3] == -1
+    store.get_many([ExpertEntry(0, 1)])                       # layer 0: layer-1 predictions are kept
+    assert store.predicted_expired == 0 and len(loads) == 3
+    got = store.get_many([ExpertEntry(1, 3), ExpertEntry(1, 5)])
+    assert [g.expert for g in got] == [3, 5] and loads[3:] == [(1, 5)]   # (1, 3) admitted without a load
+    assert store.is_resident((1, 3)) and store.layer_table(1)[3] == got[0].slot.index
+    assert store.predicted_used == 1 and store.predicted_expired == 1   # (1, 4): its layer came and went
+    assert store.predicted_wasted_bytes == store.expert_bytes and store.stats.misses == 3
+    # a layer that does not advance begins a new walk: older predictions expire
+    store.prefetch_decode([ExpertEntry(2, 0), ExpertEntry(2, 1), ExpertEntry(2, 2)], limit=2)
+    assert loads[-2:] == [(2, 0), (2, 1)] and store.predicted_loads == 4
+    store.get_many([ExpertEntry(0, 1)])
+    assert store.predicted_expired == 3
+    # the prediction is issued after the demand loads, a callable only then
+    order = []
+    store.loader = lambda entry, slot: order.append((entry.layer, entry.expert))
+    store.get_many([ExpertEntry(1, 6)], prefetch=lambda: [ExpertEntry(2, 7)])
+    assert order == [(1, 6), (2, 7)]
+    # the reserve: no prediction takes the last free slots
+    store.predict_slot_reserve = store.pool.free_count()
+    assert store.prefetch_decode([ExpertEntry(2, 5)]) == 0
+
+
 def test_bench_cpu_dequant_equals_oracle():
     """The CPU baseline's table-driven dequant gives the oracle's values exactly."""
     import bench
