@@ -425,9 +425,56 @@ def prefill_config3(args, dev, log_fn):
                    "scales as stored), routing + permute + grouped gate/up + down + combine, eager launches"}
     log_fn(f"config 3 prefill: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s, {touched} experts touched, "
            f"max {int(counts.max())} rows/expert")
+    res["layer_with_shared_fp8"] = prefill_layer_with_shared(x, w, b, store, dev, args.seed + 3)
     del store
     torch.cuda.empty_cache()
     return res
+
+
+def prefill_layer_with_shared(x, w, b, store, dev, seed):
+    """The whole config-3 layer as the reference's call site runs it (moe_prefill_grouped with the
+    FP8 shared expert, D 4096 x F 2880, random E4M3 weights and E8M0 scales): the shared expert on a
+    second stream beside the routed experts, and sequential for comparison."""
+    import torch
+
+    from cachalot_amd import moe_prefill
+
+    D, F = x.shape[1], 2880
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def wt(n, k):
+        q = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev, generator=g)
+        q[(q & 0x7F) == 0x7F] = 0x3F
+        return q, torch.randint(120, 131, ((n + 31) // 32, k // 32), dtype=torch.uint8, device=dev, generator=g)
+
+    (w1, s1), (w3, s3), (w2, s2) = wt(F, D), wt(F, D), wt(D, F)
+    kw = dict(layer_id=0, gate_weight=w, gate_bias=b, expert_index=None, expert_store=store, topk=6,
+              route_scale=1.0, score_fn="sigmoid", shared_w1=w1, shared_w1_scales=s1, shared_w2=w2,
+              shared_w2_scales=s2, shared_w3=w3, shared_w3_scales=s3)
+    keep = moe_prefill.SIDE_STREAM_MIN_TOKENS
+    forms = (("side_stream", keep), ("sequential", 1 << 30))
+    times = {name: [] for name, _ in forms}
+    try:
+        for rnd in range(3):              # round 0 warms both forms; rounds 1-2 alternate and are timed
+            for name, limit in forms:
+                moe_prefill.SIDE_STREAM_MIN_TOKENS = limit
+                moe_prefill.moe_prefill_grouped(x, **kw)
+                torch.cuda.synchronize()
+                a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(5):
+                    moe_prefill.moe_prefill_grouped(x, **kw)
+                e.record()
+                torch.cuda.synchronize()
+                if rnd:
+                    times[name].append(a.elapsed_time(e) / 5)
+    finally:
+        moe_prefill.SIDE_STREAM_MIN_TOKENS = keep
+    out = {name: {"ms_per_layer": round(sum(t) / len(t), 3)} for name, t in times.items()}
+    out["note"] = ("moe_prefill_grouped with shared_* (router, permute, grouped FP4 experts, FP8 shared expert, "
+                   "combine), eager calls; the default runs the shared expert on a second stream")
+    return out
 
 
 def shared_expert_fp8(args, dev, log_fn):
