@@ -6,7 +6,9 @@ mirror the reference's call sites:
 
 * routing: ``route_topk``, ``route_topk_fused``, ``route_topk_batch``, ``route_topk_rows``
 * decode:  ``moe_layer_forward``, ``fused_routed_experts``, ``affine_routed_experts``
-* prefill / batched decode: ``moe_prefill_grouped``, ``grouped_experts``
+* prefill / batched decode: ``moe_prefill_grouped``, ``grouped_experts``; one expert over
+  many rows: ``routed_expert_forward_batched``, ``routed_expert_forward_sgmm``,
+  ``affine_expert_forward_batched``
 * shared FP8 expert: ``shared_expert_forward``, ``shared_expert_forward_fused``,
   ``shared_expert_forward_batched``, ``fp8_linear``, ``quantize_fp8_activation``
 * store:   ``ResidentExpertStore`` over an ``HBMSlotPool``; formats in ``storage.index``
@@ -18,6 +20,7 @@ __version__ = "0.1.0"
 __all__ = [
     "RouterResult", "route_topk", "route_topk_fused", "route_topk_batch", "route_topk_rows",
     "moe_layer_forward", "moe_prefill_grouped", "grouped_experts", "fused_routed_experts", "affine_routed_experts", "affine_expert_forward",
+    "routed_expert_forward_batched", "routed_expert_forward_sgmm", "affine_expert_forward_batched",
     "shared_expert_forward", "shared_expert_forward_fused", "shared_expert_forward_batched", "fp8_linear",
     "fp8_linear_quantized", "quantize_fp8_activation",
     "ResidentExpertStore", "HBMSlotPool", "ExpertFormat", "FP4_FORMAT", "affine_format", "fp4_format",
@@ -31,6 +34,9 @@ def __getattr__(name):  # lazy: importing the package does not load torch or the
     if name in ("fused_routed_experts", "affine_routed_experts", "affine_expert_forward"):
         from . import moe_decode
         return getattr(moe_decode, name)
+    if name in ("routed_expert_forward_batched", "routed_expert_forward_sgmm", "affine_expert_forward_batched"):
+        from . import expert_rows
+        return getattr(expert_rows, name)
     if name in ("moe_prefill_grouped", "grouped_experts"):
         from . import moe_prefill
         return getattr(moe_prefill, name)

@@ -254,3 +254,42 @@ def test_unpermute_combine_bit_exact(cuda, t, k, d, with_addend, offset):
     want_r, want_o = odispatch.combine(yv.reshape(t * k, d), pos, av)
     assert np.array_equal(_np(routed).view(np.uint32), want_r.astype(np.float32).view(np.uint32))
     assert np.array_equal(_np(out).view(np.uint16), f32_to_bf16_bits(want_o))
+
+
+@pytest.mark.parametrize("kind", ["affine", "fp4"])
+def test_one_expert_over_rows(cuda, kind):
+    """routed_expert_forward_batched / routed_expert_forward_sgmm (FP4; a resident
+    expert in place, and the reference's keyword tensors copied into a scratch slot:
+    bit-identical) and affine_expert_forward_batched (2-bit): 150 rows of one expert
+    (three 64-row tiles, the last ragged) against oracle swiglu_rows, the rounding
+    points of moe_prefill_batched.py:31-61 / expert_affine.py:84-99."""
+    from cachalot_amd.expert_rows import (affine_expert_forward_batched, routed_expert_forward_batched,
+                                          routed_expert_forward_sgmm)
+    from cachalot_amd.storage.index import ExpertEntry, affine_format, fp4_format
+
+    fmt = affine_format(1024, 640) if kind == "affine" else fp4_format(1024, 640)
+    store = make_store(fmt, n_layers=1, n_experts=4)
+    ex = store.get(ExpertEntry(0, 2))
+    rng = np.random.default_rng(19)
+    m = 150
+    x = round_bf16(rng.standard_normal((m, fmt.d_model)).astype(np.float32))
+    w = rng.uniform(0.05, 1.0, m).astype(np.float32)
+    xd = _bf16(f32_to_bf16_bits(x), cuda)
+    wd = torch.from_numpy(w).to(cuda)
+    if kind == "affine":
+        got = affine_expert_forward_batched(xd, ex, fmt, wd)
+    else:
+        got = routed_expert_forward_batched(xd, expert=ex, weights=wd)
+        arrays = {n: t.clone() for n, t in ex.as_model_dict().items()}
+        copied = routed_expert_forward_sgmm(xd, w1_packed=arrays["w1.weight"], w1_scales=arrays["w1.scale"],
+                                            w2_packed=arrays["w2.weight"], w2_scales=arrays["w2.scale"],
+                                            w3_packed=arrays["w3.weight"], w3_scales=arrays["w3.scale"], weights=wd)
+        assert torch.equal(got, copied)
+        with pytest.raises(ValueError):
+            routed_expert_forward_batched(xd, w1_packed=arrays["w1.weight"], weights=wd)
+    assert got.dtype == torch.float32 and tuple(got.shape) == (m, fmt.d_model)
+    mm1, mm3, mm2 = _mats(fmt, 0, 2)
+    want = oexperts.swiglu_rows(x, mm1, mm3, mm2, w, 10.0)
+    g = _np(got)
+    assert np.array_equal(round_bf16(g), g)                 # each value a bf16 cast, as in the reference
+    _check_rows(g, want, want[:, None, :], f"one expert, {kind}")
