@@ -22,6 +22,8 @@ Weights are device tensors: ``w`` uint8 ``[N, K]`` (E4M3 bytes, or a
 """
 from __future__ import annotations
 
+import os
+
 from dataclasses import dataclass
 
 import torch
@@ -109,6 +111,59 @@ def fp8_linear_quantized(x: QuantizedActivation, weight: torch.Tensor, weight_sc
 
 def fp8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scales: torch.Tensor) -> torch.Tensor:
     return fp8_linear_quantized(quantize_fp8_activation(x), weight, weight_scales)
+
+
+# moe_prefill_batched.py:28: CACHALOT_PREFILL_BF16_GEMM picks the operand dtype of the
+# reference's dense FP8 row GEMMs; the kernels here take the E4M3 bytes directly.
+PREFILL_BF16_GEMM = os.environ.get("CACHALOT_PREFILL_BF16_GEMM", "1") != "0"
+
+
+def gemm_dtype() -> torch.dtype:
+    """The dtype the reference dequantizes FP8 operands to for its row GEMMs (``moe_prefill_batched.py:88-89``)."""
+    return torch.bfloat16 if PREFILL_BF16_GEMM else torch.float32
+
+
+def _e8m0_values(s: torch.Tensor) -> torch.Tensor:
+    """E8M0 bytes -> float32 2^(s - 127), built from the bits (exact; 0 -> 2^-127, 255 -> NaN)."""
+    b = s.to(torch.int32)
+    bits = torch.where(b == 0, torch.full_like(b, 0x00400000), b << 23)
+    bits = torch.where(b == 255, torch.full_like(b, 0x7FC00000), bits)
+    return bits.view(torch.float32)
+
+
+def quantize_activation_fp8_rows(x: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """x [M, K] bf16 -> act_quant per 32-element block, returned dequantized in ``dtype``
+    (E4M3 value x its power-of-two scale, exact in bf16 and fp32;
+    ``moe_prefill_batched.py:62-73``).  The codes come from the act_quant kernel."""
+    if x.ndim != 2:
+        raise ValueError(f"x must be [rows, K], got {tuple(x.shape)}")
+    qa = quantize_fp8_activation(x)
+    m, k = x.shape
+    vals = qa.values.view(torch.float8_e4m3fn).to(torch.float32).reshape(m, k // BLOCK, BLOCK)
+    return (vals * _e8m0_values(qa.scales)[..., None]).reshape(m, k).to(dtype)
+
+
+def dequantize_fp8_weight(weight: torch.Tensor, weight_scales: torch.Tensor,
+                          dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """E4M3 weight [N, K] (uint8 or float8_e4m3fn) and E8M0 scales [ceil(N/32), K/32] -> [N, K]
+    in ``dtype`` (exact; ``moe_prefill_batched.py:76-84``): row block n // 32, column block k // 32."""
+    w = _bytes(weight, "weight")
+    n, k = w.shape
+    if k % BLOCK or tuple(weight_scales.shape) != ((n + BLOCK - 1) // BLOCK, k // BLOCK):
+        raise ValueError(f"scales {tuple(weight_scales.shape)} do not match weight {(n, k)}")
+    vals = w.contiguous().view(torch.float8_e4m3fn).to(torch.float32)
+    sc = _e8m0_values(weight_scales.to(w.device))
+    sc = sc.repeat_interleave(BLOCK, dim=0)[:n].repeat_interleave(BLOCK, dim=1)
+    return (vals * sc).to(dtype)
+
+
+def fp8_linear_rows(x: torch.Tensor, weight: torch.Tensor, weight_scales: torch.Tensor) -> torch.Tensor:
+    """x [T, K] bf16 -> bf16 [T, N], the FP8 GEMM of the reference's prefill rows
+    (``moe_prefill_batched.py:92-96``): act_quant rows times E4M3 weights, exact products
+    accumulated in fp32, one bf16 cast."""
+    if x.ndim != 2:
+        raise ValueError(f"x must be [rows, K], got {tuple(x.shape)}")
+    return fp8_linear(x, weight, weight_scales)
 
 
 def _shared(x: torch.Tensor, w1, s1, w2, s2, w3, s3, swiglu_limit: float) -> torch.Tensor:

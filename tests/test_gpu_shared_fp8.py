@@ -288,3 +288,47 @@ def test_layer_decode_carries_the_shared_expert(cuda, kind, d, f_sh, k, limit):
         assert torch.equal(og.view(torch.int16), eager.view(torch.int16)), t
     with pytest.raises(ValueError):
         moe_layer_decode(xs[0], w, b, store.pool, store.layer_table(0), **kw, shared=plain, addend=xs[1])
+
+
+def test_fp8_row_helpers_match_oracle(cuda):
+    """quantize_activation_fp8_rows / dequantize_fp8_weight (moe_prefill_batched.py:62-84):
+    exact dequantized values, bit for bit against oracle.fp8 (act_quant codes times 2^e,
+    E4M3 times E8M0 with N not a multiple of 32 and edge scale bytes); fp8_linear_rows
+    is fp8_linear on rows."""
+    from cachalot_amd.shared_expert import (dequantize_fp8_weight, fp8_linear, fp8_linear_rows, gemm_dtype,
+                                            quantize_activation_fp8_rows)
+
+    rng = np.random.default_rng(SEED + 31)
+    x = rng.standard_normal((7, 256)).astype(np.float32) * np.float32(3.0)
+    x[1, :32] = 0.0                                  # an all-zero block (the amax floor)
+    x[2, 32:64] *= np.float32(1e-6)                  # a tiny block
+    x = round_bf16(x)
+    xd = _to_dev_bf16(x, cuda)
+    q, e = ofp8.act_quant(x)
+    want = (ofp8.e4m3_decode(q).reshape(7, 8, 32) * np.exp2(e.astype(np.float64))[..., None]).reshape(7, 256)
+    got = _np(quantize_activation_fp8_rows(xd))
+    assert got.dtype == np.float32 and np.array_equal(got, want.astype(np.float32))
+    got_bf = quantize_activation_fp8_rows(xd, torch.bfloat16)
+    assert got_bf.dtype == torch.bfloat16 and np.array_equal(_np(got_bf.float()), want.astype(np.float32))
+
+    w = rng.integers(0, 256, size=(80, 256), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0x3F
+    s = rng.integers(100, 140, size=(3, 8), dtype=np.uint8)
+    s[0, 0], s[2, 7] = 10, 240                       # the smallest products stay normal; 2^113
+    rows = np.arange(80) // 32
+    want_w = ofp8.e4m3_decode(w).astype(np.float64) * np.exp2(s.astype(np.float64) - 127.0)[rows][:, np.arange(256) // 32]
+    got_w = _np(dequantize_fp8_weight(_dev(w, cuda), _dev(s, cuda)))
+    assert np.array_equal(got_w, want_w.astype(np.float32))
+    with pytest.raises(ValueError):
+        dequantize_fp8_weight(_dev(w, cuda), _dev(s[:2], cuda))
+
+    wd, sd = _dev(w[:64], cuda), _dev(s[:2], cuda)
+    assert torch.equal(fp8_linear_rows(xd, wd, sd).view(torch.int16), fp8_linear(xd, wd, sd).view(torch.int16))
+    with pytest.raises(ValueError):
+        fp8_linear_rows(xd[0], wd, sd)
+    assert gemm_dtype() in (torch.bfloat16, torch.float32)
+    from cachalot_amd.shared_expert import _e8m0_values
+
+    sv = _np(_e8m0_values(torch.tensor([0, 1, 127, 254, 255], dtype=torch.uint8, device=cuda)))
+    assert sv[0] == np.float32(2.0 ** -127) and sv[1] == np.float32(2.0 ** -126)
+    assert sv[2] == 1.0 and sv[3] == np.float32(2.0 ** 127) and np.isnan(sv[4])
