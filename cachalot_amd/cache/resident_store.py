@@ -94,6 +94,15 @@ class ResidentExpertStore:
         self._decode_pass = 0
         self._decode_layer = -1
 
+    # the reference's counters (resident_store.py:270-271), over this store's stats
+    @property
+    def cache_hits(self) -> int:
+        return self.stats.hits
+
+    @property
+    def cache_misses(self) -> int:
+        return self.stats.misses
+
     # ----------------------------------------------------------- slot table
     def track_slots(self, n_layers: int | None = None, n_experts: int | None = None) -> torch.Tensor:
         """Device int32 [layers, experts] table, -1 for a non-resident expert."""

@@ -168,7 +168,7 @@ def test_predicted_experts_load_ahead_and_expire():
     assert [g.expert for g in got] == [3, 5] and loads[3:] == [(1, 5)]   # (1, 3) admitted without a load
     assert store.is_resident((1, 3)) and store.layer_table(1)[3] == got[0].slot.index
     assert store.predicted_used == 1 and store.predicted_expired == 1   # (1, 4): its layer came and went
-    assert store.predicted_wasted_bytes == store.expert_bytes and store.stats.misses == 3
+    assert store.predicted_wasted_bytes == store.expert_bytes and store.stats.misses == 3 == store.cache_misses
     # a layer that does not advance begins a new walk: older predictions expire
     store.prefetch_decode([ExpertEntry(2, 0), ExpertEntry(2, 1), ExpertEntry(2, 2)], limit=2)
     assert loads[-2:] == [(2, 0), (2, 1)] and store.predicted_loads == 4
