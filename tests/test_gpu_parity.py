@@ -128,6 +128,9 @@ ROUTER_CASES = [
     (37, 4096, 384, 6, "sigmoid", "rank", 1.0, 2.5, True),
     (64, 4096, 384, 8, "sqrt_softplus", "ascending", 0.7, 1.5, False),
     (5, 128, 100, 1, "sigmoid", "ascending", 1.0, 1.0, True),
+    # 4 <= T < 8: two tokens per wave (the batched decode at B = 4)
+    (4, 4096, 384, 6, "sigmoid", "ascending", 1.0, 1.0, True),
+    (7, 4096, 384, 6, "sqrt_softplus", "rank", 1.0, 1.5, True),
     (3, 256, 64, 64, "sqrt_softplus", "rank", 1.0, 1.0, True),
     (9, 5120, 384, 6, "sqrt_softplus", "ascending", 1.0, 1.5, True),
     (40, 5120, 384, 6, "sigmoid", "ascending", 1.0, 1.0, True),
