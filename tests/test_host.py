@@ -224,3 +224,21 @@ def test_substitution_plan_follows_the_reference_rule():
     assert ids == [1, 2] and n == 0                              # no routing mass
     w = rescale_kept([0.5, 0.25, 0.25], [0, 2])
     assert np.isclose(sum(w), 1.0) and np.isclose(w[0], 2 / 3) and np.isclose(w[1], 1 / 3)
+
+
+def test_prediction_entries_strongest_first():
+    """moe_layer_metal.py:236-244: predicted ids go to the store strongest first (route_topk's
+    ascending order lists them weakest first; rank order strongest first), each layer's in turn,
+    and an id the expert index does not hold is skipped."""
+    import torch
+
+    from cachalot_amd.moe_layer import prediction_entries
+    from cachalot_amd.storage.index import ExpertEntry
+
+    pred = [(3, torch.tensor([5, 9, 2])), (4, torch.tensor([7, 1, 8]))]
+    got = prediction_entries(pred, None, "ascending")
+    assert [(e.layer, e.expert) for e in got] == [(3, 2), (3, 9), (3, 5), (4, 8), (4, 1), (4, 7)]
+    got = prediction_entries(pred, None, "rank")
+    assert [(e.layer, e.expert) for e in got] == [(3, 5), (3, 9), (3, 2), (4, 7), (4, 1), (4, 8)]
+    index = {(3, 5): ExpertEntry(3, 5), (3, 2): ExpertEntry(3, 2)}
+    assert [(e.layer, e.expert) for e in prediction_entries(pred[:1], index, "ascending")] == [(3, 2), (3, 5)]
