@@ -97,6 +97,10 @@ _SIGNATURES = {
     "cachalot_grouped_experts_q2": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                             c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_grouped_experts_q2_routes": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p,
+                                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                   c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p,
+                                                   c_void_p, c_size_t, c_void_p]),
     "cachalot_grouped_experts_fp4": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
                                              c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                              c_float, c_void_p, c_void_p, c_size_t, c_void_p]),

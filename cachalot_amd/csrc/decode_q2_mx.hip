@@ -32,6 +32,7 @@
 #include "fp8_common.h"
 #include "mfma_tile.h"
 #include "mx_tile.h"
+#include "permute_small.h"
 
 namespace cachalot {
 namespace {
@@ -529,26 +530,40 @@ struct BGuLds {
 //     nothing for them -- the batched path's own copy of the grouped drop pass;
 //   the others: x (T tokens) as plane blocks, 1024 quads each.
 constexpr int PREP_THREADS = 1024;
+// The dropped routes' y rows (rows [offsets[E], n) of the permutation) cleared by
+// one workgroup.
+__device__ __forceinline__ void clear_dropped_rows(const int32_t* offsets, int E, int n, int T, int k, int D,
+                                                   const int32_t* row_token, const int32_t* row_slot, uint16_t* y) {
+  const int first = offsets[E];
+  const int per_row = D / 8;   // 16-byte stores
+  const int total = max(n - first, 0) * per_row;
+  for (int i = threadIdx.x; i < total; i += PREP_THREADS) {
+    const int r = first + i / per_row;
+    const int c = i - (r - first) * per_row;
+    const int t = row_token[r], sl = row_slot[r];
+    if (t < 0 || t >= T || sl < 0 || sl >= k) continue;
+    reinterpret_cast<uint4*>(y + ((size_t)t * k + sl) * D)[c] = uint4{0u, 0u, 0u, 0u};
+  }
+}
+
+// ridx / rw (the routes [n], or null when the caller permuted them): workgroup 0
+// first runs the permutation itself (permute_small_body, n <= PREP_THREADS) and, after
+// the records, clears the dropped routes' rows; without routes the last workgroup
+// of the grid clears them.
 __global__ void __launch_bounds__(PREP_THREADS) batch_prep_kernel(const uint16_t* __restrict__ x, int T, int D,
                                                                   uint8_t* __restrict__ xplanes,
-                                                                  const int32_t* __restrict__ offsets, int E,
+                                                                  int32_t* __restrict__ offsets, int E,
                                                                   const int32_t* __restrict__ slot_table,
                                                                   int4* __restrict__ recs, int32_t* __restrict__ n_recs,
-                                                                  int n, int k, const int32_t* __restrict__ row_token,
-                                                                  const int32_t* __restrict__ row_slot,
-                                                                  uint16_t* __restrict__ y) {
+                                                                  int n, int k, int32_t* __restrict__ row_token,
+                                                                  int32_t* __restrict__ row_slot,
+                                                                  uint16_t* __restrict__ y,
+                                                                  const int32_t* __restrict__ ridx,
+                                                                  const float* __restrict__ rw,
+                                                                  float* __restrict__ row_w) {
   const int tid = threadIdx.x;
-  if (blockIdx.x == gridDim.x - 1) {
-    const int first = offsets[E];
-    const int per_row = D / 8;   // 16-byte stores
-    const int total = max(n - first, 0) * per_row;
-    for (int i = tid; i < total; i += PREP_THREADS) {
-      const int r = first + i / per_row;
-      const int c = i - (r - first) * per_row;
-      const int t = row_token[r], sl = row_slot[r];
-      if (t < 0 || t >= T || sl < 0 || sl >= k) continue;
-      reinterpret_cast<uint4*>(y + ((size_t)t * k + sl) * D)[c] = uint4{0u, 0u, 0u, 0u};
-    }
+  if (ridx == nullptr && blockIdx.x == gridDim.x - 1) {
+    clear_dropped_rows(offsets, E, n, T, k, D, row_token, row_slot, y);
     return;
   }
   if (blockIdx.x > 0) {
@@ -559,6 +574,10 @@ __global__ void __launch_bounds__(PREP_THREADS) batch_prep_kernel(const uint16_t
       mx::encode_x_quad(xplanes + (size_t)t * (D / 128) * PB_BYTES, t4,
                         reinterpret_cast<const uint2*>(x + (size_t)t * D)[t4]);   // whole quads
     return;
+  }
+  if (ridx != nullptr) {
+    permute_small_body<PREP_THREADS>(ridx, rw, n, k, E, offsets, row_token, row_slot, row_w);
+    __syncthreads();   // the offsets and rows are this workgroup's own global stores
   }
   __shared__ int wave_n[PREP_THREADS / 64];
   const int lane = tid & 63, wave = tid >> 6;
@@ -584,6 +603,7 @@ __global__ void __launch_bounds__(PREP_THREADS) batch_prep_kernel(const uint16_t
     __syncthreads();
   }
   if (tid == 0) n_recs[0] = base;
+  if (ridx != nullptr) clear_dropped_rows(offsets, E, n, T, k, D, row_token, row_slot, y);
 }
 
 template <int MAXM>
@@ -891,9 +911,14 @@ int launch_q2mx_decode(const uint16_t* x, bool planes_ready, uint8_t* xplanes, c
 int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const Layout& L, const int32_t* slot_table,
                         const int32_t* offsets, int E, int4* recs, int32_t* n_recs, int max_active,
                         const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k,
-                        float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s) {
-  hipLaunchKernelGGL(batch_prep_kernel, dim3(2 + T * ((D + 4095) / 4096)), dim3(PREP_THREADS), 0, s, x, T, D, xplanes,
-                     offsets, E, slot_table, recs, n_recs, T * k, k, row_token, row_slot, y);
+                        float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s,
+                        const int32_t* ridx, const float* rw) {
+  // with routes (T k <= PREP_THREADS) the prep launch permutes them itself into offsets / row_*
+  if (ridx != nullptr && T * k > PREP_THREADS) return fail(CACHALOT_EINVAL, "batched decode: %d routes", T * k);
+  hipLaunchKernelGGL(batch_prep_kernel, dim3((ridx ? 1 : 2) + T * ((D + 4095) / 4096)), dim3(PREP_THREADS), 0, s, x,
+                     T, D, xplanes, const_cast<int32_t*>(offsets), E, slot_table, recs, n_recs, T * k, k,
+                     const_cast<int32_t*>(row_token), const_cast<int32_t*>(row_slot), y, ridx, rw,
+                     const_cast<float*>(row_w));
   int rc = check_launch("batch_prep_kernel");
   if (rc) return rc;
   BatchArgs a{xplanes, pool, L, recs, n_recs, row_token, row_slot, row_w, D, F, k, limit, hid, y};

@@ -30,9 +30,15 @@
 //                      combine8_kernel the same with 16-byte accesses.
 #include "decode_common.h"
 #include "mfma_tile.h"
+#include "permute_small.h"
 
 #include <algorithm>
 
+namespace cachalot {
+
+}  // namespace cachalot
+extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k, int E, int32_t* offsets,
+                                int32_t* row_token, int32_t* row_slot, float* row_w, cachalot_stream_t stream);
 namespace cachalot {
 
 // matrix-core batched decode (decode_q2_mx.hip)
@@ -40,7 +46,8 @@ bool q2mx_supported(int D, int F, int k);
 int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
                         const int32_t* slot_table, const int32_t* offsets, int E, int4* recs, int32_t* n_recs,
                         int max_active, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
-                        int F, int k, float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s);
+                        int F, int k, float limit, uint8_t* hid, uint8_t* xplanes, uint16_t* y, hipStream_t s,
+                        const int32_t* ridx, const float* rw);
 
 // FP4 prefill on the block-scaled matrix cores (prefill_mx.hip)
 size_t prefill_mx_ws_bytes(int T, int k, int D, int F);
@@ -145,65 +152,15 @@ __global__ void __launch_bounds__(SCATTER_THREADS) permute_scatter_kernel(const 
   }
 }
 
-// n <= 1024 routes (batched decode): the counts, their scan and the scatter in one
-// workgroup, thread i owning route i.  A route's place inside
-// its expert is the number of earlier routes with the same key (the expert, or E for
-// an id outside [0, E)), so rows stay in route order as the scatter kernel leaves them.
+// n <= 1024 routes (batched decode) in one workgroup: permute_small_body
+// (permute_small.h), which the batched decode's prep launch also runs.
 __global__ void __launch_bounds__(PERMUTE_THREADS) permute_small_kernel(const int32_t* __restrict__ idx,
                                                                         const float* __restrict__ w, int n, int k,
                                                                         int E, int32_t* __restrict__ offsets,
                                                                         int32_t* __restrict__ row_token,
                                                                         int32_t* __restrict__ row_slot,
                                                                         float* __restrict__ row_w) {
-  __shared__ int cnt[1024 + 1];
-  __shared__ int off[1024 + 1];
-  __shared__ __align__(16) int key[PERMUTE_THREADS];
-  __shared__ int wave_tot[PERMUTE_THREADS / 64];
-  const int i = threadIdx.x, lane = i & 63, wave = i >> 6;
-  for (int e = i; e <= E; e += PERMUTE_THREADS) cnt[e] = 0;
-  int id = i < n ? idx[i] : 0;
-  const float wi = i < n ? w[i] : 0.0f;
-  const int my = id >= 0 && id < E ? id : E;
-  key[i] = i < n ? my : -1;
-  __syncthreads();
-  if (i < n && my < E) atomicAdd(&cnt[my], 1);
-  __syncthreads();
-  const int c = i < E ? cnt[i] : 0;
-  int v = c;
-#pragma unroll
-  for (int d = 1; d < 64; d *= 2) {
-    const int o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  if (lane == 63) wave_tot[wave] = v;
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int q = 0; q < PERMUTE_THREADS / 64; ++q) {
-    before += q < wave ? wave_tot[q] : 0;
-    total += wave_tot[q];
-  }
-  if (i < E) {
-    off[i] = before + v - c;
-    offsets[i] = before + v - c;
-  }
-  if (i == 0) {
-    off[E] = total;
-    offsets[E] = total;
-  }
-  __syncthreads();
-  if (i >= n) return;
-  int rank = 0;
-  const int4* k4 = reinterpret_cast<const int4*>(key);
-  for (int j = 0; j < (i >> 2); ++j) {
-    const int4 q = k4[j];
-    rank += (q.x == my) + (q.y == my) + (q.z == my) + (q.w == my);
-  }
-  for (int j = i & ~3; j < i; ++j) rank += key[j] == my;
-  const int pos = off[my] + rank;
-  row_token[pos] = i / k;
-  row_slot[pos] = i - (i / k) * k;
-  row_w[pos] = my == E ? 0.0f : wi;
+  permute_small_body<PERMUTE_THREADS>(idx, w, n, k, E, offsets, row_token, row_slot, row_w);
 }
 
 // y rows of the dropped routes (rows [offsets[E], n) of the permutation) are
@@ -929,9 +886,12 @@ template <int KIND>
 int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,
                    const int32_t* slot_table, const int32_t* offsets, const int32_t* row_token,
                    const int32_t* row_slot, const float* row_w, int T, int D, int F, int E, int k, float limit,
-                   uint16_t* y, void* workspace, size_t workspace_bytes, hipStream_t s, const char* who) {
+                   uint16_t* y, void* workspace, size_t workspace_bytes, hipStream_t s, const char* who,
+                   const int32_t* ridx = nullptr, const float* rw = nullptr) {
+  // ridx / rw: the routes [T, k], permuted here into offsets / row_* (outputs then)
   CACHALOT_REQUIRE(x && pool && layout && slot_table && offsets && row_token && row_slot && row_w && y,
                    "%s: null pointer", who);
+  CACHALOT_REQUIRE((ridx == nullptr) == (rw == nullptr), "%s: routes need both ids and weights", who);
   CACHALOT_REQUIRE(T >= 1, "%s: x must contain at least one token (T=%d)", who, T);
   CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "%s: k=%d outside 1..%d", who, k, KMAX);
   CACHALOT_REQUIRE(E >= 1 && E <= 1024, "%s: E=%d outside 1..1024", who, E);
@@ -955,12 +915,20 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
   // tiles of 64 rows when experts see many tokens, 16 for batched decode
   const int MT = T * k >= 4 * E ? 64 : 16;
   uint32_t* zeros = reinterpret_cast<uint32_t*>(ws + wo.tiles_n + 128);
-  if (KIND == KIND_Q2 && MT == 16 && q2mx_supported(D, F, k) && !small_tiles_requested()) {
+  const bool batched = KIND == KIND_Q2 && MT == 16 && q2mx_supported(D, F, k) && !small_tiles_requested();
+  // routes given: permuted by the batched prep launch when one workgroup holds them, else here
+  const bool fused = ridx != nullptr && batched && T * k <= PERMUTE_THREADS;
+  if (ridx != nullptr && !fused) {
+    rc = cachalot_permute(ridx, rw, T, k, E, const_cast<int32_t*>(offsets), const_cast<int32_t*>(row_token),
+                          const_cast<int32_t*>(row_slot), const_cast<float*>(row_w), s);
+    if (rc) return rc;
+  }
+  if (batched) {
     // few rows per expert: the matrix-core batched decode, one entry per active expert
     // (its prep launch also clears the dropped routes' y rows)
     return launch_q2mx_batched(x, T, pool, L, slot_table, offsets, E, reinterpret_cast<int4*>(ws + wo.tiles),
                                tiles_n, std::min(E, T * k), row_token, row_slot, row_w, D, F, k, limit,
-                               ws + wo.hidden, ws + wo.xplanes, y, s);
+                               ws + wo.hidden, ws + wo.xplanes, y, s, fused ? ridx : nullptr, fused ? rw : nullptr);
   }
   hipLaunchKernelGGL(drop_zero_kernel, dim3(16), dim3(256), 0, s, offsets, E, T * k, T, k, D, row_token, row_slot, y);
   rc = check_launch("drop_zero_kernel");
@@ -1024,6 +992,23 @@ extern "C" size_t cachalot_grouped_experts_workspace_bytes(int T, int k, int E, 
   (void)D;
   if (T <= 0 || k <= 0 || E <= 0 || F <= 0) return 0;
   return cachalot::grouped_ws(T, k, E, D, F).total;
+}
+
+// cachalot_permute followed by cachalot_grouped_experts_q2, with offsets / row_* as outputs;
+// a batched decode of up to 1,024 routes permutes them inside its prep launch.
+extern "C" int cachalot_grouped_experts_q2_routes(const uint16_t* x, const uint8_t* pool,
+                                                  const cachalot_expert_layout* layout, const int32_t* slot_table,
+                                                  const int32_t* idx, const float* w, int32_t* offsets,
+                                                  int32_t* row_token, int32_t* row_slot, float* row_w, int T, int D,
+                                                  int F, int E, int k, int group, float swiglu_limit, uint16_t* y,
+                                                  void* workspace, size_t workspace_bytes, cachalot_stream_t stream) {
+  using namespace cachalot;
+  CACHALOT_REQUIRE(group == KC, "grouped_experts_q2: group_size %d (the bank format uses 128)", group);
+  CACHALOT_REQUIRE(idx && w, "grouped_experts_q2: null routes");
+  CACHALOT_REQUIRE((int64_t)T * k <= (1 << 30), "grouped_experts_q2: T=%d k=%d", T, k);
+  return launch_grouped<KIND_Q2>(x, pool, layout, slot_table, offsets, row_token, row_slot, row_w, T, D, F, E, k,
+                                 swiglu_limit, y, workspace, workspace_bytes, (hipStream_t)stream,
+                                 "grouped_experts_q2", idx, w);
 }
 
 extern "C" int cachalot_grouped_experts_q2(const uint16_t* x, const uint8_t* pool,

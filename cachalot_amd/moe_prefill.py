@@ -94,18 +94,31 @@ def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tenso
     dev = x.device
     x = x.contiguous()
     slot_table = slot_table.to(torch.int32).contiguous()
-    offsets, row_token, row_slot, row_w = permute(indices, weights, n_experts)
     L = _lib.lib()
     stream = _lib.stream_handle(dev)
     y = torch.empty((t, k, d), dtype=torch.bfloat16, device=dev)
     nbytes = L.cachalot_grouped_experts_workspace_bytes(t, k, n_experts, d, f)
     ws = _workspace(dev, nbytes)
-    common = (x.data_ptr(), pool.storage.data_ptr(), pool.layout(), slot_table.data_ptr(), offsets.data_ptr(),
-              row_token.data_ptr(), row_slot.data_ptr(), row_w.data_ptr(), t, d, f, n_experts, k)
     if fmt.kind == "affine":
-        rc = L.cachalot_grouped_experts_q2(*common, fmt.group_size, float(swiglu_limit), y.data_ptr(), ws.data_ptr(),
-                                           nbytes, stream)
+        # the routes go in as they are: a batched decode permutes them inside its prep launch
+        if indices.ndim != 2 or tuple(weights.shape) != tuple(indices.shape):
+            raise ValueError(f"indices {tuple(indices.shape)} / weights {tuple(weights.shape)} must be [T, k]")
+        _lib.require_cuda(indices, weights)
+        ids = indices.to(torch.int32).contiguous()
+        wts = weights.to(torch.float32).contiguous()
+        offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+        row_token = torch.empty(t * k, dtype=torch.int32, device=dev)
+        row_slot = torch.empty(t * k, dtype=torch.int32, device=dev)
+        row_w = torch.empty(t * k, dtype=torch.float32, device=dev)
+        rc = L.cachalot_grouped_experts_q2_routes(x.data_ptr(), pool.storage.data_ptr(), pool.layout(),
+                                                  slot_table.data_ptr(), ids.data_ptr(), wts.data_ptr(),
+                                                  offsets.data_ptr(), row_token.data_ptr(), row_slot.data_ptr(),
+                                                  row_w.data_ptr(), t, d, f, n_experts, k, fmt.group_size,
+                                                  float(swiglu_limit), y.data_ptr(), ws.data_ptr(), nbytes, stream)
     elif fmt.kind == "fp4":
+        offsets, row_token, row_slot, row_w = permute(indices, weights, n_experts)
+        common = (x.data_ptr(), pool.storage.data_ptr(), pool.layout(), slot_table.data_ptr(), offsets.data_ptr(),
+                  row_token.data_ptr(), row_slot.data_ptr(), row_w.data_ptr(), t, d, f, n_experts, k)
         rc = L.cachalot_grouped_experts_fp4(*common, float(swiglu_limit), y.data_ptr(), ws.data_ptr(), nbytes, stream)
     else:
         raise ValueError(f"unknown expert format {fmt.kind!r}")

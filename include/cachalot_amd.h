@@ -238,6 +238,17 @@ int cachalot_grouped_experts_q2(const uint16_t* x, const uint8_t* pool,
                                 const float* row_w, int T, int D, int F, int E, int k, int group,
                                 float swiglu_limit, uint16_t* y, void* workspace, size_t workspace_bytes,
                                 cachalot_stream_t stream);
+/* cachalot_grouped_experts_q2_routes: cachalot_permute(idx, w, ...) followed by
+ * cachalot_grouped_experts_q2 (the same routes, rows and y), with offsets / row_*
+ * as outputs.  A batched decode of up to 1,024 routes permutes them inside its prep
+ * launch, one launch fewer.  Replaces the assignment + per-expert loop of
+ * moe_prefill_grouped.py:199-225,420-467 for 2-bit banks. */
+int cachalot_grouped_experts_q2_routes(const uint16_t* x, const uint8_t* pool,
+                                       const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                       const int32_t* idx, const float* w, int32_t* offsets, int32_t* row_token,
+                                       int32_t* row_slot, float* row_w, int T, int D, int F, int E, int k, int group,
+                                       float swiglu_limit, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                       cachalot_stream_t stream);
 int cachalot_grouped_experts_fp4(const uint16_t* x, const uint8_t* pool,
                                  const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
                                  const int32_t* offsets, const int32_t* row_token, const int32_t* row_slot,

@@ -164,6 +164,28 @@ def test_grouped_experts_batched_decode(cuda, kind):
                   + bf16_ulp(want + a))
 
 
+@pytest.mark.parametrize("t", [1, 4, 7])
+def test_grouped_batched_routes_outside_range(cuda, t):
+    """The batched 2-bit decode permutes its routes inside the prep launch: ids outside
+    [0, E) are dropped (zero y rows, after every expert) and the rest match the oracle."""
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.storage.index import affine_format
+
+    fmt = affine_format(4096, 2880)
+    rng = np.random.default_rng(40 + t)
+    k = 6
+    experts = [3, 17, 100, 101, 250, 383, 7]
+    idx, w = _zipf_routes(rng, t, k, experts)
+    idx[0, 1] = -3
+    idx[t - 1, k - 1] = 384
+    store = make_store(fmt, n_layers=1, n_experts=384, keys=[(0, e) for e in experts], n_slots=len(experts))
+    xb = osynth.activations(SEED, 410 + t, t, 4096)
+    routed, _ = grouped_experts(_bf16(xb, cuda), torch.from_numpy(idx).to(cuda), torch.from_numpy(w).to(cuda),
+                                store.pool, store.layer_table(0), want_routed=True)
+    want, ys = _oracle_grouped(fmt, 0, bf16_bits_to_f32(xb), idx, w, drop=(-3, 384))
+    _check_rows(_np(routed), want, ys, f"routes outside [0, E), T={t}")
+
+
 @pytest.mark.parametrize("path", ["matrix_core", "bf16"])
 @pytest.mark.parametrize("shape", [(4096, 2880), (5120, 2304)])
 def test_grouped_batched_decode_many_rows(cuda, path, shape, monkeypatch):
