@@ -32,20 +32,28 @@ def _mm(m, group):
     return lambda x: qmv64(x, w, s, b, k=k, group=group)
 
 
-def _torch_expert(x, mats, weight, limit, group):
-    """Same expert in torch float64 with torch's bf16 casts."""
+def _torch_rows(x, mats, weights, limit, group):
+    """The SwiGLU expert over rows in torch float64 with torch's own bf16 casts
+    (fp64 -> fp32 -> bf16, as an fp32 accumulator cast to bf16), at the points of
+    expert_affine.py:65-81 (g, u, h, y each cast to bf16; clamp skipped for limit 0)."""
     def dense(m):
         w, s, b, k = m
         return torch.from_numpy(dequantize_affine64(w, s, b, k=k, group=group))
     w1, w3, w2 = (dense(m) for m in mats)
-    xt = torch.from_numpy(x.astype(np.float64))
+    xt = torch.from_numpy(np.atleast_2d(x).astype(np.float64))
     bf = lambda t: t.float().to(torch.bfloat16).double()  # noqa: E731
-    g = bf(w1 @ xt)
-    u = bf(w3 @ xt)
-    u = u.clamp(-limit, limit)
-    g = g.clamp(max=limit)
-    h = bf(torch.nn.functional.silu(g) * u * float(np.float32(weight)))
-    return bf(w2 @ h).float().numpy()
+    g = bf(xt @ w1.T)
+    u = bf(xt @ w3.T)
+    if limit > 0:
+        u = u.clamp(-limit, limit)
+        g = g.clamp(max=limit)
+    wt = torch.from_numpy(np.asarray(weights, np.float32).astype(np.float64))[:, None]
+    h = bf(torch.nn.functional.silu(g) * u * wt)
+    return bf(h @ w2.T).float().numpy()
+
+
+def _torch_expert(x, mats, weight, limit, group):
+    return _torch_rows(x, mats, [weight], limit, group)[0]
 
 
 def test_affine_decode_matches_torch_reference():
@@ -59,9 +67,72 @@ def test_affine_decode_matches_torch_reference():
     want = np.zeros(d, np.float32)
     for e, w in zip(ex, weights):
         want = want + _torch_expert(x, e, w, 10.0, group)
-    assert np.allclose(routed, want, rtol=0, atol=4e-3 * np.abs(want).max())
+    # bit-equal: the route-order fp32 sum of bf16-exact terms, each at the same casts
+    assert np.array_equal(routed, want)
     tb = torch.from_numpy(routed + addend).to(torch.bfloat16).float().numpy()
     assert np.array_equal(out, tb)
+
+
+def _rows_case(seed, limit):
+    rng = np.random.default_rng(seed)
+    d, f, group = 80, 56, 16        # D = 5 groups, F = 3.5 groups: a partial last group in W2
+    m = 7
+    # scaled so that some g and u exceed the clamp limit
+    x = round_bf16((rng.normal(size=(m, d)) * 6).astype(np.float32))
+    e = _affine_expert(rng, d, f, group)
+    weights = rng.uniform(0.05, 1.5, size=m).astype(np.float32)
+    return x, e, weights, group
+
+
+def _oracle_rows(x, e, weights, limit, group):
+    return experts.swiglu_rows(x, *[_mm(mm, group) for mm in e], weights, limit=limit)
+
+
+def test_swiglu_rows_bit_equal_torch():
+    for seed, limit in [(21, 10.0), (22, 1.0), (23, 0.0)]:
+        x, e, weights, group = _rows_case(seed, limit)
+        got = _oracle_rows(x, e, weights, limit, group)
+        want = _torch_rows(x, e, weights, limit, group)
+        assert np.array_equal(got, want), (seed, limit)
+
+
+def test_swiglu_rows_clamp_engaged():
+    """The limit-1 case clamps some g and u (else the clamp would go unpinned)."""
+    x, e, weights, group = _rows_case(22, 1.0)
+    a = _oracle_rows(x, e, weights, 1.0, group)
+    b = _oracle_rows(x, e, weights, 0.0, group)
+    assert not np.array_equal(a, b)
+
+
+def test_swiglu_rows_pin_catches_each_dropped_cast(monkeypatch):
+    """Mutation check: skipping any one of the g, u, h, y casts breaks bit-equality
+    with torch, for the rows pin and for the decode pin."""
+    real = experts.round_bf16
+    for skip in range(4):
+        calls = {"n": 0}
+
+        def mutated(v, _skip=skip, _calls=calls):
+            i = _calls["n"] % 4
+            _calls["n"] += 1
+            return np.asarray(v, np.float32) if i == _skip else real(v)
+
+        monkeypatch.setattr(experts, "round_bf16", mutated)
+        x, e, weights, group = _rows_case(21, 10.0)
+        got = _oracle_rows(x, e, weights, 10.0, group)
+        want = _torch_rows(x, e, weights, 10.0, group)
+        assert not np.array_equal(got, want), f"dropping cast {skip} went unnoticed (rows)"
+        calls["n"] = 0
+        rng = np.random.default_rng(7)
+        d, f, g16 = 64, 40, 16
+        xd = round_bf16(rng.normal(size=d).astype(np.float32))
+        ex = [_affine_expert(rng, d, f, g16) for _ in range(3)]
+        wts = np.array([0.5, 0.3, 0.2], np.float32)
+        routed, _ = experts.affine_decode(xd, [tuple(_mm(m, g16) for m in q) for q in ex], wts, 10.0)
+        want_d = np.zeros(d, np.float32)
+        for q, w in zip(ex, wts):
+            want_d = want_d + _torch_expert(xd, q, w, 10.0, g16)
+        assert not np.array_equal(routed, want_d), f"dropping cast {skip} went unnoticed (decode)"
+        monkeypatch.setattr(experts, "round_bf16", real)
 
 
 def test_swiglu_limit_zero_disables_clamp():
