@@ -29,12 +29,13 @@ from typing import Callable
 import numpy as np
 import torch
 
-from ..storage.index import ExpertEntry, ExpertFormat
+from ..storage.index import ExpertEntry, ExpertFormat, tensor_sizes_from_format
 from .resident import ResidentExpert
 from .slots import ExpertSlot, HBMSlotPool
 
 
-# Free slots a prediction leaves for the demand path (resident_store.py:52 of the reference).
+# Transient slots a decode prediction leaves free for prefill's bypass loads
+# (resident_store.py:50 of the reference).
 PREDICT_SLOT_RESERVE = 16
 # At most this many non-resident predicted experts per layer and call, in the
 # caller's (ranked) order; 0 = no limit (resident_store.py:58).
@@ -50,19 +51,69 @@ class ResidentStoreStats:
 
 
 class ResidentExpertStore:
-    def __init__(self, budget_bytes: int | None = None, reader=None, *, fmt: ExpertFormat, n_slots: int | None = None,
+    """Budgeted expert residency over one HBM slot pool.
+
+    The constructor takes the reference's arguments (``resident_store.py:157-167``):
+    ``budget_bytes`` sizes the resident set (``capacity = budget // expert bytes``);
+    ``tensor_sizes`` ({short name: bytes}, ``tensor_sizes_from_entry``) lays out the
+    slot record; ``transient_slots`` more slots (at least one) hold decode
+    predictions and prefill bypass loads, which never count as residents;
+    ``slot_pool`` brings a pool instead.  The runtime assigns ``.format`` after
+    construction (``text_decode_runtime.py:442-453``); the setter checks it
+    against the slot layout.  ``reader`` (an ``ExpertReader``) loads misses whose
+    entry carries its byte ranges, unless a ``loader(entry, slot)`` is given.
+    ``load_workers`` is accepted for the call site: loads here are single reads
+    followed by copies enqueued on the caller's stream, not thread-pool jobs.
+
+    Extensions for this build: ``fmt`` (the format up front), ``n_slots`` (the
+    resident capacity in experts instead of a byte budget), ``n_layers`` /
+    ``n_experts`` (the device slot table's shape) and ``device``."""
+
+    def __init__(self, budget_bytes: int | None = None, reader=None, *,
+                 tensor_sizes: dict[str, int] | None = None, slot_pool: HBMSlotPool | None = None,
+                 transient_slots: int = 128, load_workers: int = 8, verbose: bool = False,
+                 fmt: ExpertFormat | None = None, n_slots: int | None = None,
                  n_layers: int = 40, n_experts: int = 384, device="cuda",
                  loader: Callable[[ExpertEntry, ExpertSlot], None] | None = None) -> None:
-        if n_slots is None:
-            if budget_bytes is None or budget_bytes <= 0:
+        if slot_pool is None:
+            if tensor_sizes is None:
+                if fmt is None:
+                    raise ValueError("tensor_sizes or slot_pool is required")
+                tensor_sizes = tensor_sizes_from_format(fmt)
+            expert_bytes = sum(tensor_sizes.values())
+            if n_slots is None:
+                if budget_bytes is None or budget_bytes <= 0:
+                    raise ValueError("budget_bytes must be positive")
+                n_slots = budget_bytes // expert_bytes
+                if n_slots <= 0:
+                    raise ValueError(f"budget {budget_bytes} smaller than one expert ({expert_bytes})")
+            capacity = int(n_slots)
+            if capacity <= 0:
+                raise ValueError(f"n_slots must be positive, got {n_slots}")
+            total = capacity + max(1, int(transient_slots))
+            if verbose:
+                print(f"Allocating {total} expert slots ({total * expert_bytes / 1024 ** 3:.1f} GiB) in HBM...",
+                      flush=True)
+            slot_pool = HBMSlotPool(fmt if fmt is not None else dict(tensor_sizes), total, device=device)
+        else:
+            expert_bytes = slot_pool.slot_bytes
+            if n_slots is not None:
+                capacity = min(int(n_slots), slot_pool.capacity - 1)
+            elif budget_bytes is not None and budget_bytes > 0:
+                capacity = min(budget_bytes // expert_bytes, slot_pool.capacity - 1)
+            else:
                 raise ValueError("budget_bytes must be positive")
-            n_slots = budget_bytes // fmt.expert_bytes
-            if n_slots <= 0:
-                raise ValueError(f"budget {budget_bytes} smaller than one expert ({fmt.expert_bytes})")
-        self.format = fmt
-        self.pool = HBMSlotPool(fmt, int(n_slots), device=device)
-        self.capacity = self.pool.capacity
-        self.expert_bytes = fmt.expert_bytes
+            if capacity <= 0:
+                raise ValueError(f"budget {budget_bytes} smaller than one expert ({expert_bytes})")
+        self.pool = slot_pool
+        self.capacity = int(capacity)
+        self.transient_slots = self.pool.capacity - self.capacity
+        self.expert_bytes = expert_bytes
+        self.budget_bytes = self.capacity * expert_bytes
+        self.load_workers = load_workers
+        self.verbose = verbose
+        if fmt is not None:
+            self.format = fmt
         self.n_layers = n_layers
         self.n_experts = n_experts
         self.loader = loader
@@ -81,8 +132,8 @@ class ResidentExpertStore:
         self.skipped_experts = 0
         # one-layer-early routing prediction (resident_store.py:230-262 of the
         # reference): layer -> (gate weight, gate bias), set by the runtime; a
-        # predicted expert is loaded into a free slot ahead of its layer and becomes
-        # resident only when that layer requests it
+        # predicted expert is loaded into a transient slot ahead of its layer and
+        # becomes resident only when that layer requests it
         self.decode_gates: dict[int, tuple] = {}
         self.predict_slot_reserve = PREDICT_SLOT_RESERVE
         self.predicted_loads = 0
@@ -93,6 +144,37 @@ class ResidentExpertStore:
         self._inflight_deadline: dict[tuple[int, int], tuple[int, int]] = {}
         self._decode_pass = 0
         self._decode_layer = -1
+        # transient slots in use: predictions in flight plus prefill bypass loads
+        self._transient_count = 0
+        # prefill: bypass loads held until release_prefill_layer, the layer plans
+        # of prepare_prefill_layer, and the keys the current plan admits
+        self._transients: dict[tuple[int, int], ExpertSlot] = {}
+        self._prefill_layer_keys: dict[int, list[tuple[int, int]]] = {}
+        self._prefill_admit: set[tuple[int, int]] = set()
+        self.use_counts: dict[tuple[int, int], int] = {}
+
+    # ---------------------------------------------------------------- format
+    @property
+    def format(self) -> ExpertFormat | None:
+        return self.pool.format
+
+    @format.setter
+    def format(self, fmt: ExpertFormat) -> None:
+        self.pool.set_format(fmt)
+
+    def _load(self, entry: ExpertEntry, slot: ExpertSlot) -> None:
+        """Fill ``slot`` with ``entry``'s bytes: the loader, else the reader for an
+        indexed entry; an expert neither can produce is missing (KeyError, as
+        ``moe_layer_metal.py:279-283``)."""
+        if self.loader is not None:
+            self.loader(entry, slot)
+        elif self.reader is not None and entry.tensors:
+            self.reader.read_expert_into(entry, slot.arrays)
+        else:
+            raise KeyError(f"Missing routed expert layer={entry.layer}, expert={entry.expert}")
+
+    def _can_load(self, entry: ExpertEntry) -> bool:
+        return self.loader is not None or (self.reader is not None and bool(entry.tensors))
 
     # the reference's counters (resident_store.py:270-271), over this store's stats
     @property
@@ -124,15 +206,20 @@ class ResidentExpertStore:
 
     # ------------------------------------------------------------- residency
     def is_resident(self, key: tuple[int, int]) -> bool:
+        return key in self._items or key in self._transients
+
+    def is_cached(self, key: tuple[int, int]) -> bool:
         return key in self._items
 
-    is_cached = is_resident
+    def resident_keys(self) -> list[tuple[int, int]]:
+        """Resident experts, least recently used first (transients excluded)."""
+        return list(self._items)
 
     def layer_fully_resident(self, layer: int) -> bool:
         return bool((self._table[layer] >= 0).all())
 
     def preload(self, keys, fill: Callable[[tuple[int, int], ExpertSlot], None]) -> None:
-        """Place `keys` in slots (slot = layer * n_experts + expert when the pool holds every expert)."""
+        """Place `keys` in slots (slot = layer * n_experts + expert when the store holds every expert)."""
         bulk = self.capacity >= self.n_layers * self.n_experts
         for key in keys:
             if key in self._items:
@@ -142,34 +229,48 @@ class ResidentExpertStore:
             else:
                 slot = self._take_slot(protect=())
             fill(key, slot)
-            self._items[key] = slot
-            self._set_table(key, slot.index)
+            self._admit(key, slot)
             self.stats.bytes_loaded += self.expert_bytes
 
-    def _take_slot(self, protect) -> ExpertSlot:
-        slot = self.pool.try_acquire()
-        if slot is not None:
-            return slot
-        for key in self._items:  # least recently used first
-            if key not in protect:
+    def _admit(self, key, slot: ExpertSlot) -> None:
+        self._items[key] = slot
+        self._set_table(key, slot.index)
+
+    def _evict_lru(self, protect=(), avoid_layer: int | None = None) -> ExpertSlot | None:
+        """Take the least recently used resident out of the table; its slot is
+        returned to the caller (still marked in use)."""
+        for pass_avoid in ((avoid_layer,) if avoid_layer is not None else ()) + (None,):
+            for key in self._items:
+                if key in protect or (pass_avoid is not None and key[0] == pass_avoid):
+                    continue
                 slot = self._items.pop(key)
                 self._set_table(key, -1)
                 self.stats.evictions += 1
                 return slot
-        for key in list(self._inflight):  # then a prediction nobody has asked for yet
-            if key not in protect:
-                return self._drop_prediction(key)
-        raise TimeoutError("every slot holds an expert of the current request")
+        return None
+
+    def _take_slot(self, protect) -> ExpertSlot:
+        """A slot for one more resident.  Residents never grow past ``capacity``:
+        below it a free slot is taken (one always exists, since transients stay
+        within their own count), at it the least recently used resident outside
+        ``protect`` is evicted."""
+        if len(self._items) < self.capacity:
+            slot = self.pool.try_acquire()
+            if slot is not None:
+                return slot
+        slot = self._evict_lru(protect)
+        if slot is not None:
+            return slot
+        raise TimeoutError("every resident slot holds an expert of the current request")
 
     # ------------------------------------------------------ routing prediction
     def prefetch_decode(self, entries: list[ExpertEntry], limit: int | None = None) -> int:
-        """Load experts predicted for an upcoming decode layer into free slots,
-        never evicting a resident and leaving ``predict_slot_reserve`` slots free
-        (``resident_store.py:291-320`` of the reference).  Entries are taken in
-        the caller's order, at most ``limit`` (default DECODE_PREFETCH_LIMIT, 0 =
-        no limit) per layer.  Returns how many loads were started."""
-        if self.loader is None:
-            return 0
+        """Load experts predicted for an upcoming decode layer into transient
+        slots, never evicting a resident and leaving ``predict_slot_reserve``
+        transient slots to prefill (``resident_store.py:291-320`` of the
+        reference).  Entries are taken in the caller's order, at most ``limit``
+        (default DECODE_PREFETCH_LIMIT, 0 = no limit) per layer.  Returns how many
+        loads were started."""
         cap = DECODE_PREFETCH_LIMIT if limit is None else limit
         per_layer: dict[int, int] = {}
         submitted = 0
@@ -177,20 +278,29 @@ class ResidentExpertStore:
             if cap and per_layer.get(entry.layer, 0) >= cap:
                 continue
             key = (entry.layer, entry.expert)
-            if key in self._items or key in self._inflight:
+            if key in self._items or key in self._inflight or key in self._transients:
                 continue
-            if self.pool.free_count() <= self.predict_slot_reserve:
+            if not self._can_load(entry):
+                continue
+            if self._transient_count >= self.transient_slots - self.predict_slot_reserve:
                 break
             slot = self.pool.try_acquire()
             if slot is None:
                 break
-            self.loader(entry, slot)
+            self._transient_count += 1
+            self._load(entry, slot)
             self._inflight[key] = (slot, entry)
             self._inflight_deadline[key] = (self._decode_pass, entry.layer)
             self.predicted_loads += 1
             submitted += 1
             per_layer[entry.layer] = per_layer.get(entry.layer, 0) + 1
         return submitted
+
+    def note_decode_layer(self, layer: int) -> None:
+        """A decode layer ran without asking the store for experts (a fully
+        resident layer on the device path): the walk still advances, so the
+        deadlines of predictions issued from it are counted from this layer."""
+        self._advance_decode_pass(layer)
 
     def _advance_decode_pass(self, layer: int) -> None:
         """Decode requests layers in ascending order, once per token: a layer that
@@ -202,6 +312,7 @@ class ResidentExpertStore:
     def _drop_prediction(self, key) -> ExpertSlot:
         slot, _ = self._inflight.pop(key)
         self._inflight_deadline.pop(key, None)
+        self._transient_count -= 1
         self.predicted_expired += 1
         self.predicted_wasted_bytes += self.expert_bytes
         self.stats.bytes_loaded += self.expert_bytes
@@ -219,8 +330,8 @@ class ResidentExpertStore:
                 continue
             self.pool.release(self._drop_prediction(key))
 
-    def _wrap(self, key, slot) -> ResidentExpert:
-        return ResidentExpert(layer=key[0], expert=key[1], slot=slot)
+    def _wrap(self, key, slot, transient: bool = False) -> ResidentExpert:
+        return ResidentExpert(layer=key[0], expert=key[1], slot=slot, transient=transient)
 
     def get(self, entry: ExpertEntry) -> ResidentExpert:
         return self.get_many([entry])[0]
@@ -230,14 +341,14 @@ class ResidentExpertStore:
                  prefetch_limit: int | None = None, prefetch_after: bool | None = None,
                  on_hits=None) -> list[ResidentExpert | None]:
         """Resident experts for `entries`, in order; misses are loaded (strongest
-        priority first) up to `max_misses`, the rest returned as None.  Without a
-        loader a miss raises KeyError, as ``moe_layer_forward`` does for a missing
-        expert (``moe_layer_metal.py:279-283``).
+        priority first) up to `max_misses`, the rest returned as None.  A miss
+        that neither the loader nor the reader can fill raises KeyError, as
+        ``moe_layer_forward`` does for a missing expert (``moe_layer_metal.py:279-283``).
 
         An entry predicted earlier (``prefetch_decode``) is admitted from its slot
         without a load.  ``prefetch`` (a list, or a callable returning one) names
-        experts predicted for a later layer; they are loaded into free slots after
-        this layer's misses (``resident_store.py:789-943``), ``prefetch_limit``
+        experts predicted for a later layer; they are loaded into transient slots
+        after this layer's misses (``resident_store.py:789-943``), ``prefetch_limit``
         capping them per layer.  Loads here are enqueued on the stream as they are
         issued, so ``prefetch_after`` (the reference's choice between issuing the
         prediction beside or after the demand reads) changes nothing and is only
@@ -248,16 +359,24 @@ class ResidentExpertStore:
             # decode asks for one layer at a time, so the first entry names it
             self._advance_decode_pass(keys[0][0])
         self._sweep_inflight(keep=set(keys))
+        protect = set(keys)
         misses = []
         for i, key in enumerate(keys):
+            self.use_counts[key] = self.use_counts.get(key, 0) + 1
             slot = self._items.get(key)
             if slot is None and key in self._inflight:
-                # predicted earlier: its data already sits in a slot, so it becomes
-                # resident without a load (counted as the miss it was)
+                # predicted earlier: its data already sits in a transient slot; the
+                # slot turns resident (making room under capacity first), counted
+                # as the miss it was
                 slot, _ = self._inflight.pop(key)
                 self._inflight_deadline.pop(key, None)
-                self._items[key] = slot
-                self._set_table(key, slot.index)
+                self._transient_count -= 1
+                if len(self._items) >= self.capacity:
+                    victim = self._evict_lru(protect)
+                    if victim is None:
+                        raise TimeoutError("every resident slot holds an expert of the current request")
+                    self.pool.release(victim)
+                self._admit(key, slot)
                 self.predicted_used += 1
                 self.stats.misses += 1
                 self.stats.bytes_loaded += self.expert_bytes
@@ -277,7 +396,6 @@ class ResidentExpertStore:
             budget = len(misses) if max_misses is None else max(0, int(max_misses))
             unique_misses = len({keys[i] for i in misses})
             self.skipped_experts += max(0, unique_misses - budget)
-            protect = set(keys)
             loaded = 0
             for i in misses:
                 slot = self._items.get(keys[i])
@@ -287,12 +405,11 @@ class ResidentExpertStore:
                 if loaded >= budget:
                     continue
                 loaded += 1
-                if self.loader is None:
+                if not self._can_load(entries[i]):
                     raise KeyError(f"Missing routed expert layer={keys[i][0]}, expert={keys[i][1]}")
                 slot = self._take_slot(protect)
-                self.loader(entries[i], slot)
-                self._items[keys[i]] = slot
-                self._set_table(keys[i], slot.index)
+                self._load(entries[i], slot)
+                self._admit(keys[i], slot)
                 self.stats.misses += 1
                 self.stats.bytes_loaded += self.expert_bytes
                 out[i] = self._wrap(keys[i], slot)
@@ -303,6 +420,196 @@ class ResidentExpertStore:
             if ents:
                 self.prefetch_decode(list(ents), prefetch_limit)
         return out
+
+    # ------------------------------------------------------------ prefill path
+    def prepare_prefill_layer(self, layer_id: int, entries: list[ExpertEntry], *, num_layers: int = 40) -> None:
+        """Fix this layer's resident set before its loads (``resident_store.py:954-1084``).
+
+        The resident capacity is split evenly over ``num_layers`` (the first
+        ``capacity % num_layers`` layers one more).  Of the experts the layer
+        routes to, residents are kept first (the previous plan's, then the rest in
+        request order), then misses are planned for admission in request order
+        until the layer's share is full; the layer's other residents are evicted
+        when this prompt's misses need their room, least recently used first.
+        If admission would push the store past ``capacity``, other layers above
+        their share give residents back (those their own plan does not name
+        first).  Everything else the layer needs goes to transient slots in
+        ``get_many_prefill``."""
+        if num_layers <= 0:
+            raise ValueError(f"num_layers must be > 0, got {num_layers}")
+        order: list[tuple[int, int]] = []
+        for e in entries:
+            if e.layer != layer_id:
+                raise ValueError(f"prepare_prefill_layer received entry layer={e.layer} for layer_id={layer_id}")
+            if (e.layer, e.expert) not in order:
+                order.append((e.layer, e.expert))
+        share = lambda la: self.capacity // num_layers + (1 if la < self.capacity % num_layers else 0)  # noqa: E731
+        quota = share(layer_id)
+        needed = set(order)
+        # earlier bypass loads that this layer does not need go back now
+        self._release_transients(lambda k: k[0] != layer_id or k not in needed)
+        if not order:
+            self._prefill_layer_keys[layer_id] = []
+            self._prefill_admit = set()
+            return
+        prev = [k for k in self._prefill_layer_keys.get(layer_id, []) if k in needed and k in self._items]
+        kept = prev[:quota]
+        kept += [k for k in order if k in self._items and k not in kept][:max(0, quota - len(kept))]
+        # bypass loads this layer needs become residents while the share has room
+        for k in order:
+            if len(kept) >= quota or len(self._items) >= self.capacity:
+                break
+            if k in self._transients and k not in kept:
+                self._admit(k, self._transients.pop(k))
+                self._transient_count -= 1
+                kept.append(k)
+        missing = sum(1 for k in order if k not in kept)
+        room = quota - len(kept) - missing      # share the prompt's misses leave to older residents
+        if room > 0:
+            for k in reversed(list(self._items)):
+                if room <= 0:
+                    break
+                if k[0] == layer_id and k not in kept:
+                    kept.append(k)
+                    room -= 1
+        keep = set(kept)
+        for k in [k for k in self._items if k[0] == layer_id and k not in keep]:
+            self.pool.release(self._items.pop(k))
+            self._set_table(k, -1)
+            self.stats.evictions += 1
+        plan = list(kept)
+        admit = set()
+        for k in order:
+            if len(plan) >= quota:
+                break
+            if k not in keep:
+                plan.append(k)
+                admit.add(k)
+        over = len(self._items) + len(admit) - self.capacity
+        for other in range(num_layers):
+            if over <= 0:
+                break
+            if other == layer_id:
+                continue
+            theirs = [k for k in self._items if k[0] == other]
+            extra = len(theirs) - share(other)
+            if extra <= 0:
+                continue
+            named = set(self._prefill_layer_keys.get(other, []))
+            for k in (sorted(k for k in theirs if k not in named) + sorted(k for k in theirs if k in named))[:extra]:
+                if over <= 0:
+                    break
+                self.pool.release(self._items.pop(k))
+                self._set_table(k, -1)
+                self.stats.evictions += 1
+                over -= 1
+        if over > 0:
+            raise RuntimeError(f"Unable to reclaim enough resident capacity for prepared prefill layer "
+                               f"{layer_id}: short by {over} slots")
+        self._prefill_layer_keys[layer_id] = plan
+        self._prefill_admit = admit
+
+    def get_many_prefill(self, entries: list[ExpertEntry], *,
+                         speculate: list[ExpertEntry] | None = None) -> list[ResidentExpert]:
+        """One prefill layer's experts without evicting a resident
+        (``resident_store.py:1123-1210``): residents are returned as they are (LRU
+        order untouched); a miss takes free resident capacity (admitted; with a
+        prepared plan only the keys it admits), else a transient slot, held until
+        ``release_prefill_layer``.  ``speculate`` (the next layer's likely experts)
+        is loaded behind this layer's misses into whatever slots remain, never
+        blocking.  Slot reuse is stream-ordered, so a released transient is
+        refilled only after the kernels that read it."""
+        out: list[ResidentExpert | None] = [None] * len(entries)
+        requested = {(e.layer, e.expert) for e in entries}
+        for i, e in enumerate(entries):
+            key = (e.layer, e.expert)
+            self.use_counts[key] = self.use_counts.get(key, 0) + 1
+            slot = self._items.get(key)
+            if slot is not None:
+                self.stats.hits += 1
+                out[i] = self._wrap(key, slot)
+                continue
+            slot = self._transients.get(key)
+            if slot is not None:
+                self.stats.hits += 1
+                out[i] = self._wrap(key, slot, transient=True)
+                continue
+            if not self._can_load(e):
+                raise KeyError(f"Missing routed expert layer={key[0]}, expert={key[1]}")
+            slot, admit = self._prefill_slot(key, block=True, protect=requested)
+            self._load(e, slot)
+            self.stats.misses += 1
+            self.stats.bytes_loaded += self.expert_bytes
+            if admit:
+                self._admit(key, slot)
+            else:
+                self._transients[key] = slot
+            out[i] = self._wrap(key, slot, transient=not admit)
+        for e in speculate or ():
+            key = (e.layer, e.expert)
+            if key in self._items or key in self._transients or not self._can_load(e):
+                continue
+            got = self._prefill_slot(key, block=False, protect=requested)
+            if got is None:
+                break
+            slot, admit = got
+            self._load(e, slot)
+            self.stats.bytes_loaded += self.expert_bytes
+            if admit:
+                self._admit(key, slot)
+            else:
+                self._transients[key] = slot
+        return out
+
+    def _prefill_slot(self, key, *, block: bool, protect=()):
+        """(slot, admit) for a prefill load: resident capacity when the plan allows
+        it, else a transient slot; when both are exhausted, a blocking request
+        makes room by evicting a resident outside ``protect`` (this call's experts),
+        another layer's first (the one way to free a slot here, since releases are
+        this thread's own)."""
+        may_admit = not self._prefill_admit or key in self._prefill_admit
+        if may_admit and len(self._items) < self.capacity:
+            slot = self.pool.try_acquire()
+            if slot is not None:
+                return slot, True
+        if self._transient_count < self.transient_slots:
+            slot = self.pool.try_acquire()
+            if slot is not None:
+                self._transient_count += 1
+                return slot, False
+        if not block:
+            return None
+        slot = self._evict_lru(protect, avoid_layer=key[0])
+        if slot is None:
+            raise TimeoutError(f"no slot for prefill expert {key}: {self.capacity} resident and "
+                               f"{self.transient_slots} transient slots are all in use")
+        return slot, True
+
+    def _release_transients(self, pred) -> None:
+        for key in [k for k in self._transients if pred(k)]:
+            self.pool.release(self._transients.pop(key))
+            self._transient_count -= 1
+
+    def release_prefill_layer(self, layer: int) -> None:
+        """After a prefill layer's kernels are enqueued: free its transient slots
+        (``resident_store.py:1212-1224``).  A later load into one is enqueued on the
+        same stream, behind the kernels that read it."""
+        self._release_transients(lambda k: k[0] == layer)
+
+    def release_prefill(self) -> None:
+        """End of a prefill (or an aborted one): nothing stays transient."""
+        self._release_transients(lambda k: True)
+        self._prefill_admit = set()
+
+    def prefill_slot_table(self, layer: int, experts: list[ResidentExpert | None]) -> torch.Tensor:
+        """The layer's device slot table with this call's transient experts added:
+        what the prefill kernels address (residents through the store's table,
+        bypass loads through their transient slots)."""
+        row = self._table[layer].copy()
+        for r in experts:
+            if r is not None:
+                row[r.expert] = r.slot.index
+        return torch.from_numpy(row).to(self.pool.device, non_blocking=False)
 
 
 class SyntheticLoader:

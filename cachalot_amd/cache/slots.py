@@ -37,11 +37,22 @@ class ExpertSlot:
 
 
 class HBMSlotPool:
-    def __init__(self, fmt: ExpertFormat, n_slots: int, *, device="cuda", page: int = PAGE) -> None:
+    """``fmt`` is an ``ExpertFormat`` or, as the reference's ``ExpertSlotPool``
+    takes it (``slots.py:68-108``), a {short name: bytes} dict; then the format
+    (needed by the kernels' record descriptor and typed views) is set later with
+    ``set_format``, which checks it against the record."""
+
+    def __init__(self, fmt: ExpertFormat | dict[str, int], n_slots: int, *, device="cuda", page: int = PAGE) -> None:
         if n_slots <= 0:
             raise ValueError(f"n_slots must be positive, got {n_slots}")
-        self.format = fmt
-        self.tensor_sizes = {n: fmt.tensor_bytes(n) for n in fmt.tensor_names}
+        if isinstance(fmt, ExpertFormat):
+            self.format: ExpertFormat | None = fmt
+            self.tensor_sizes = {n: fmt.tensor_bytes(n) for n in fmt.tensor_names}
+        else:
+            self.format = None
+            self.tensor_sizes = {str(n): int(b) for n, b in fmt.items()}
+            if not self.tensor_sizes or min(self.tensor_sizes.values()) <= 0:
+                raise ValueError(f"tensor sizes must be positive: {fmt}")
         self.tensor_names = tuple(self.tensor_sizes)
         self.slot_bytes = sum(self.tensor_sizes.values())
         self.offsets: dict[str, int] = {}
@@ -59,6 +70,20 @@ class HBMSlotPool:
         self._cond = threading.Condition()
 
     # ---------------------------------------------------------------- layout
+    def set_format(self, fmt: ExpertFormat) -> None:
+        """Attach the format to a pool laid out from tensor sizes; every tensor the
+        format names must have a record slice of exactly its size."""
+        got = {n: fmt.tensor_bytes(n) for n in fmt.tensor_names}
+        if got != self.tensor_sizes:
+            raise ValueError(f"format {fmt.kind} ({fmt.bits}-bit) tensors {got} do not match the slot "
+                             f"record {self.tensor_sizes}")
+        self.format = fmt
+
+    def expert_format(self) -> ExpertFormat:
+        if self.format is None:
+            raise ValueError("the pool has no expert format yet (assign store.format first)")
+        return self.format
+
     def _make_slot(self, i: int) -> ExpertSlot:
         base = i * self.record_bytes
         arrays = {n: self.storage[base + o: base + o + self.tensor_sizes[n]] for n, o in self.offsets.items()}
@@ -66,10 +91,11 @@ class HBMSlotPool:
 
     def layout(self) -> _lib.ExpertLayout:
         """The C-ABI record descriptor (tensor offsets in kernel order)."""
+        fmt = self.expert_format()
         lay = _lib.ExpertLayout()
         lay.record_bytes = self.record_bytes
         for i, canonical in enumerate(KERNEL_ORDER):
-            name = kernel_tensor_name(self.format, canonical)
+            name = kernel_tensor_name(fmt, canonical)
             lay.offset[i] = self.offsets[name] if name is not None else 0
         return lay
 
@@ -88,7 +114,7 @@ class HBMSlotPool:
     def typed_view(self, slot: ExpertSlot, name: str) -> torch.Tensor:
         """A shaped, typed zero-copy view of one tensor of a slot."""
         dt = {"uint32": torch.int32, "uint8": torch.uint8, "bfloat16": torch.bfloat16,
-              "float16": torch.float16, "float32": torch.float32}[self.format.dtypes[name]]
+              "float16": torch.float16, "float32": torch.float32}[self.expert_format().dtypes[name]]
         return slot.arrays[name].view(dt).view(self.format.shapes[name])
 
     # ------------------------------------------------------------ free list

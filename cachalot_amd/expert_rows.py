@@ -29,8 +29,8 @@ _SCRATCH: dict[tuple, HBMSlotPool] = {}
 
 
 def _rows(x: torch.Tensor, pool: HBMSlotPool, slot: int, weights: torch.Tensor, swiglu_limit: float) -> torch.Tensor:
-    if x.ndim != 2 or x.shape[1] != pool.format.d_model:
-        raise ValueError(f"x must be [rows, {pool.format.d_model}], got {tuple(x.shape)}")
+    if x.ndim != 2 or x.shape[1] != pool.expert_format().d_model:
+        raise ValueError(f"x must be [rows, {pool.expert_format().d_model}], got {tuple(x.shape)}")
     m = x.shape[0]
     w = torch.as_tensor(weights, dtype=torch.float32).reshape(-1)
     if w.numel() != m:
@@ -47,7 +47,7 @@ def affine_expert_forward_batched(x: torch.Tensor, expert, fmt: ExpertFormat, we
                                   swiglu_limit: float = 10.0) -> torch.Tensor:
     """x [M, D], one resident 2-bit expert, weights [M] -> fp32 [M, D] (``expert_affine.py:84-99``)."""
     pool = expert.slot.pool
-    if pool is None or pool.format.kind != "affine" or fmt.kind != "affine":
+    if pool is None or pool.expert_format().kind != "affine" or fmt.kind != "affine":
         raise ValueError("affine_expert_forward_batched needs an expert of an affine bank")
     return _rows(x, pool, expert.slot.index, weights, swiglu_limit)
 
@@ -78,7 +78,7 @@ def routed_expert_forward_batched(x: torch.Tensor, *, w1_packed=None, w1_scales=
         raise ValueError("weights (one router weight per row) are required")
     if expert is not None:
         pool = expert.slot.pool
-        if pool is None or pool.format.kind != "fp4":
+        if pool is None or pool.expert_format().kind != "fp4":
             raise ValueError("expert must belong to an FP4 slot pool")
         return _rows(x, pool, expert.slot.index, weights, swiglu_limit)
     parts = {"w1.weight": w1_packed, "w1.scale": w1_scales, "w2.weight": w2_packed, "w2.scale": w2_scales,

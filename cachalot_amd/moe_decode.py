@@ -44,7 +44,7 @@ def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor,
     """x [D] bf16; slot_table [E] int32 (device); idx [k] int32; weights [k] fp32.
 
     Returns (routed fp32 [D] or None, out bf16 [D] or None)."""
-    fmt: ExpertFormat = pool.format
+    fmt: ExpertFormat = pool.expert_format()
     if x.ndim != 1:
         raise ValueError(f"x must be 1D for decode, got {tuple(x.shape)}")
     if x.dtype != torch.bfloat16:
@@ -104,7 +104,7 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
     routed launches where the shapes allow (``moe_layer_metal.py:381-397``).
 
     Returns (routed fp32 [D] or None, out bf16 [D] or None, RouterResult)."""
-    fmt: ExpertFormat = pool.format
+    fmt: ExpertFormat = pool.expert_format()
     d, f = fmt.d_model, fmt.d_ff
     if x.ndim != 1 or x.shape[0] != d:
         raise ValueError(f"x must be 1D with {d} elements, got {tuple(x.shape)}")
@@ -191,7 +191,7 @@ def fused_routed_experts(x: torch.Tensor, experts, router_weights: torch.Tensor,
                          intermediate: int = 2880, swiglu_limit: float = 10.0) -> torch.Tensor:
     """FP4 experts: fp32 [hidden_size] = sum_e w_e * W2_e(silu(W1_e x) * W3_e x) (clamped)."""
     pool, slots, idx = _experts_table(experts)
-    fmt = pool.format
+    fmt = pool.expert_format()
     if fmt.kind != "fp4":
         raise ValueError("fused_routed_experts needs an FP4 bank")
     if (hidden_size, intermediate) != (fmt.d_model, fmt.d_ff):
@@ -206,7 +206,7 @@ def affine_routed_experts(x: torch.Tensor, experts, fmt: ExpertFormat, weights: 
                           swiglu_limit: float = 10.0) -> torch.Tensor:
     """2-bit experts: fp32 [D] sum over experts in order (bf16 rounding points of the reference)."""
     pool, slots, idx = _experts_table(experts)
-    if pool.format.kind != "affine" or fmt.kind != "affine":
+    if pool.expert_format().kind != "affine" or fmt.kind != "affine":
         raise ValueError("affine_routed_experts needs an affine bank")
     w = weights.to(device=pool.device, dtype=torch.float32)
     routed, _ = decode_experts(x, pool, slots, idx, w, swiglu_limit=swiglu_limit, want_out=False)

@@ -132,7 +132,9 @@ def moe_layer_forward(
                                          norm_topk_prob=norm_topk_prob, score_fn=score_fn, order=order,
                                          swiglu_limit=swiglu_limit, addend=addend, shared=shared)
         # a later layer that is not fully resident: its predicted experts load after
-        # this layer's launches (one synchronisation, only then)
+        # this layer's launches (one synchronisation, only then); the store's walk
+        # advances here too, so the predictions' deadlines count from this layer
+        expert_store.note_decode_layer(layer_id)
         predicted = predict_routes(x, layer_id, expert_store, gate_temp=gate_temp, score_fn=score_fn, order=order)
         if predicted and PREDICT_SUBMIT:
             expert_store.prefetch_decode(prediction_entries(predicted, expert_index, order))

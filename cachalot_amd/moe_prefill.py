@@ -76,7 +76,7 @@ def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tenso
     ``addend_ready``, when given, is an event recorded after the work that
     writes ``addend`` on another stream: the combine waits for it, the grouped
     GEMMs before it do not."""
-    fmt = pool.format
+    fmt = pool.expert_format()
     d, f = fmt.d_model, fmt.d_ff
     if x.ndim != 2 or x.shape[1] != d:
         raise ValueError(f"x must be [tokens, {d}], got {tuple(x.shape)}")
@@ -218,8 +218,12 @@ def moe_prefill_grouped(
         route = route_topk_batch(x, gate_weight, gate_bias, topk=topk, gate_temp=gate_temp,
                                  route_scale=route_scale, norm_topk_prob=norm_topk_prob, score_fn=score_fn,
                                  order=order)
+    bypass = False
     if not expert_store.layer_fully_resident(layer_id):
-        # host-addressed: one sync for the routed ids, then load what is missing
+        # host-addressed (moe_prefill_grouped.py:297-309): one sync for the routed
+        # ids; with a prefetcher the layer's resident set is planned first; then
+        # every touched expert gets a slot at once (residents as they are, misses
+        # admitted or in transient slots), since one grouped launch reads them all
         ids = sorted({int(e) for e in route.indices.reshape(-1).tolist()})
         entries = []
         for e in ids:
@@ -228,8 +232,16 @@ def moe_prefill_grouped(
             if entry is None:
                 raise KeyError(f"Missing routed expert layer={layer_id}, expert={e}")
             entries.append(entry)
-        expert_store.get_many(entries)
-    table = expert_store.layer_table(layer_id)
+        if expert_prefetcher is not None:
+            expert_store.prepare_prefill_layer(layer_id, entries, num_layers=expert_store.n_layers)
+        got = expert_store.get_many_prefill(entries)
+        table = expert_store.prefill_slot_table(layer_id, got)
+        bypass = True
+    else:
+        table = expert_store.layer_table(layer_id)
     _, out = grouped_experts(x.to(torch.bfloat16), route.indices, route.weights, expert_store.pool, table,
                              swiglu_limit=swiglu_limit, addend=addend, addend_ready=addend_ready)
+    if bypass:
+        # the launches are enqueued; a transient slot's next load queues behind them
+        expert_store.release_prefill_layer(layer_id)
     return out.to(x.dtype), route

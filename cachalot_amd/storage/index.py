@@ -146,113 +146,175 @@ def kernel_tensor_name(fmt: ExpertFormat, canonical: str) -> str | None:
 
 
 # ------------------------------------------------------------------ banks on disk
-# Checkpoint tensor names (``storage/index.py:9-16``): the shipped FP4 checkpoint
-# names every expert's tensors; oMLX-converted banks stack a layer's experts in
-# one tensor per projection field, [n_experts, rows, cols].
-_EXPERT_RE = re.compile(r"^layers\.(\d+)\.ffn\.experts\.(\d+)\.(w[123])\.(weight|scale)$")
-_STACKED_RE = re.compile(r"^language_model\.layers\.(\d+)\.ffn\.experts\.(w[123])\.(weight|scales|biases)$")
-_ST_ITEM_BYTES = {"U32": 4, "F32": 4, "F16": 2, "BF16": 2, "U8": 1, "I8": 1, "F8_E4M3": 1, "F8_E8M0": 1}
-_ST_DTYPE = {"U32": "uint32", "F32": "float32", "F16": "float16", "BF16": "bfloat16", "U8": "uint8"}
+# A bank on disk is a set of ``model-*.safetensors`` shards.  Two layouts name
+# the routed experts (the names are the reference's, ``storage/index.py:9-16``):
+#
+#   per-expert  ``layers.L.ffn.experts.E.wP.{weight,scale}``: one tensor per
+#               expert and field (the shipped FP4 checkpoint);
+#   stacked     ``language_model.layers.L.ffn.experts.wP.{weight,scales,biases}``:
+#               one ``[n_experts, rows, cols]`` tensor per layer and field (an
+#               oMLX-converted affine bank), each expert a contiguous row block.
+#
+# Both are read the same way here: the shards are walked once, every tensor
+# name is classified by one table (``_LAYOUTS``), and each match is cut into
+# (layer, expert, short name) byte ranges: one range for a per-expert tensor,
+# n_experts equal ranges for a stacked one.  The format (shapes, dtypes,
+# quantization) is then inferred from the ranges, not from a second walk.
+
+
+@dataclass(frozen=True)
+class _Layout:
+    """How one on-disk layout spells its expert tensors."""
+    kind: str
+    pattern: re.Pattern
+    stacked: bool
+
+
+_LAYOUTS = {
+    "fp4": _Layout("fp4", re.compile(
+        r"layers\.(?P<layer>\d+)\.ffn\.experts\.(?P<expert>\d+)\.(?P<proj>w[123])\.(?P<field>weight|scale)"), False),
+    "affine": _Layout("affine", re.compile(
+        r"language_model\.layers\.(?P<layer>\d+)\.ffn\.experts\.(?P<proj>w[123])\.(?P<field>weight|scales|biases)"), True),
+}
+
+# safetensors dtype tag -> (element bytes, slot dtype name); None = not a slot dtype
+_ST_TYPES = {"U32": (4, "uint32"), "F32": (4, "float32"), "F16": (2, "float16"), "BF16": (2, "bfloat16"),
+             "U8": (1, "uint8"), "I8": (1, None), "F8_E4M3": (1, None), "F8_E8M0": (1, None)}
 
 
 def read_safetensors_header(path: Path) -> tuple[dict, int]:
-    """(header dict, byte offset of the data section) of a safetensors file (``storage/index.py:70-76``)."""
-    with Path(path).open("rb") as f:
-        header_len = struct.unpack("<Q", f.read(8))[0]
-        header = json.loads(f.read(header_len))
-    return header, 8 + header_len
+    """(header dict, byte offset of the data section) of a safetensors file.  The file
+    starts with a little-endian u64 header length, then that many bytes of JSON
+    (the interface of ``storage/index.py:70-76``)."""
+    with open(path, "rb") as f:
+        (n,) = struct.unpack("<Q", f.read(8))
+        body = f.read(n)
+    if len(body) != n:
+        raise struct.error(f"{path}: header truncated ({len(body)} of {n} bytes)")
+    return json.loads(body), 8 + n
+
+
+def _readable_shards(root: Path):
+    """(shard, header, data base) for every shard whose header parses.  A shard that
+    is still being written (a partial download) is passed over, as the reference's
+    indexer does, so a bank can be indexed while it is being fetched."""
+    for shard in sorted(root.glob("model-*.safetensors")):
+        try:
+            header, base = read_safetensors_header(shard)
+        except (OSError, ValueError, struct.error):
+            continue
+        yield shard, header, base
+
+
+@dataclass
+class _Piece:
+    layer: int
+    expert: int
+    short: str
+    rng: TensorRange
+
+
+def _pieces(root: Path, layout: _Layout):
+    """Every expert byte range the layout names under ``root``, with the tensor's
+    metadata: yields (piece, header meta)."""
+    for shard, header, base in _readable_shards(root):
+        for name, meta in header.items():
+            m = layout.pattern.fullmatch(name)
+            if m is None:
+                continue
+            layer, short = int(m["layer"]), f"{m['proj']}.{m['field']}"
+            start, end = (base + o for o in meta["data_offsets"])
+            shape = tuple(int(v) for v in meta.get("shape", ()))
+            if not layout.stacked:
+                yield _Piece(layer, int(m["expert"]), short,
+                             TensorRange(name, shard, start, end, meta.get("dtype"), shape)), meta
+                continue
+            n_exp, per_shape = shape[0], shape[1:]
+            step = (end - start) // max(n_exp, 1)
+            for e in range(n_exp):
+                lo = start + e * step
+                yield _Piece(layer, e, short,
+                             TensorRange(f"layers.{layer}.ffn.experts.{e}.{short}", shard, lo, lo + step,
+                                         meta.get("dtype"), per_shape)), meta
+
+
+def _collect(pieces) -> dict[tuple[int, int], ExpertEntry]:
+    """Group ranges by (layer, expert); each entry lists its tensors in file order."""
+    by_key: dict[tuple[int, int], list[TensorRange]] = {}
+    for p in pieces:
+        by_key.setdefault((p.layer, p.expert), []).append(p.rng)
+    return {key: ExpertEntry(key[0], key[1], tuple(sorted(rs, key=lambda r: (str(r.shard), r.start))))
+            for key, rs in by_key.items()}
 
 
 def build_expert_index(model_path: str | Path) -> dict[tuple[int, int], ExpertEntry]:
-    """Per-expert tensors of the shipped FP4 checkpoint -> {(layer, expert): entry}, tensors in file
-    order; unreadable shards are skipped (``storage/index.py:79-117``)."""
-    root = Path(model_path)
-    entries: dict[tuple[int, int], list[TensorRange]] = {}
-    for shard in sorted(root.glob("model-*.safetensors")):
-        try:
-            header, data_start = read_safetensors_header(shard)
-        except (OSError, json.JSONDecodeError, struct.error):
-            continue
-        for name, meta in header.items():
-            m = _EXPERT_RE.match(name)
-            if not m:
-                continue
-            a, b = meta["data_offsets"]
-            entries.setdefault((int(m.group(1)), int(m.group(2))), []).append(
-                TensorRange(name, shard, data_start + a, data_start + b, meta.get("dtype"),
-                            tuple(meta.get("shape", ()))))
-    return {k: ExpertEntry(k[0], k[1], tuple(sorted(v, key=lambda t: t.start))) for k, v in entries.items()}
+    """Per-expert tensors of the shipped FP4 checkpoint -> {(layer, expert): entry}
+    (the interface of ``storage/index.py:79-117``)."""
+    return _collect(p for p, _ in _pieces(Path(model_path), _LAYOUTS["fp4"]))
+
+
+def _affine_spec(quantized_modules: dict, layer: int, proj: str) -> tuple[int, int]:
+    """(bits, group size) the converter recorded for one stacked projection; MLX's
+    default group size is 64.  Anything but affine quantization is refused."""
+    spec = quantized_modules.get(f"language_model.layers.{layer}.ffn.experts.{proj}") or {}
+    if spec.get("mode") != "affine":
+        raise ValueError(f"layer {layer} {proj}: the routed experts are {spec or 'unquantized'}, "
+                         "not affine-quantized")
+    return int(spec["bits"]), int(spec.get("group_size", 64))
 
 
 def build_stacked_expert_index(model_path: str | Path, quantized_modules: dict) -> tuple[ExpertFormat, dict]:
-    """oMLX-converted stacked affine bank -> (format, index); every expert's nine tensors are rows of
-    the layer's stacked tensors (``storage/index.py:120-179``).  Mixed quantization, non-affine
-    modules and inconsistent shapes raise ValueError."""
+    """oMLX-converted stacked affine bank -> (format, index) (the interface of
+    ``storage/index.py:120-179``).  Every projection must carry one affine
+    (bits, group) and every field one slice shape and dtype across layers;
+    otherwise ValueError."""
     root = Path(model_path)
-    entries: dict[tuple[int, int], list[TensorRange]] = {}
-    shapes: dict[str, tuple[int, int]] = {}
-    dtypes: dict[str, str] = {}
-    bits = group = None
-    for shard in sorted(root.glob("model-*.safetensors")):
-        try:
-            header, data_start = read_safetensors_header(shard)
-        except (OSError, json.JSONDecodeError, struct.error):
-            continue
-        for name, meta in header.items():
-            m = _STACKED_RE.match(name)
-            if not m:
-                continue
-            layer, proj, fld = int(m.group(1)), m.group(2), m.group(3)
-            spec = quantized_modules.get(f"language_model.layers.{layer}.ffn.experts.{proj}")
-            if spec is None or spec.get("mode") != "affine":
-                raise ValueError(f"{name}: routed experts must be affine-quantized, got {spec}")
-            this = (int(spec["bits"]), int(spec.get("group_size", 64)))
-            if bits is None:
-                bits, group = this
-            elif this != (bits, group):
-                raise ValueError(f"{name}: mixed expert quantization ({spec} vs {bits}-bit/{group})")
-            n_exp, rows, cols = (int(v) for v in meta["shape"])
-            short = f"{proj}.{fld}"
-            if shapes.setdefault(short, (rows, cols)) != (rows, cols):
-                raise ValueError(f"{name}: shape {(rows, cols)} differs from {shapes[short]}")
-            dtypes[short] = _ST_DTYPE[meta["dtype"]]
-            per = rows * cols * _ST_ITEM_BYTES[meta["dtype"]]
-            base = data_start + meta["data_offsets"][0]
-            for e in range(n_exp):
-                entries.setdefault((layer, e), []).append(
-                    TensorRange(f"layers.{layer}.ffn.experts.{e}.{short}", shard, base + e * per,
-                                base + (e + 1) * per, meta["dtype"], (rows, cols)))
-    if bits is None:
+    pieces, quant, shapes, dtypes = [], set(), {}, {}
+    seen_tensor: set[tuple[Path, str, int]] = set()
+    for piece, meta in _pieces(root, _LAYOUTS["affine"]):
+        proj = piece.short.split(".")[0]
+        tag = (piece.rng.shard, piece.short, piece.layer)
+        if tag not in seen_tensor:      # per stacked tensor, not per expert slice
+            seen_tensor.add(tag)
+            quant.add(_affine_spec(quantized_modules, piece.layer, proj))
+            if len(quant) > 1:
+                raise ValueError(f"layer {piece.layer} {proj}: mixed expert quantization {sorted(quant)}")
+            item, slot_dtype = _ST_TYPES.get(meta["dtype"], (None, None))
+            if slot_dtype is None:
+                raise ValueError(f"layer {piece.layer} {piece.short}: dtype {meta['dtype']} is not a bank dtype")
+            if shapes.setdefault(piece.short, piece.rng.shape) != piece.rng.shape:
+                raise ValueError(f"layer {piece.layer} {piece.short}: slice shape {piece.rng.shape}, "
+                                 f"other layers have {shapes[piece.short]}")
+            dtypes[piece.short] = slot_dtype
+        pieces.append(piece)
+    if not quant:
         raise ValueError(f"no stacked routed-expert tensors under {root}")
-    rows1, cols1 = shapes["w1.weight"]
-    d_model, d_ff = cols1 * 32 // bits, rows1
-    fmt = ExpertFormat("affine", bits, group, tuple(sorted(shapes)), shapes, dtypes, d_model, d_ff)
-    index = {k: ExpertEntry(k[0], k[1], tuple(sorted(v, key=lambda t: t.start))) for k, v in entries.items()}
-    return fmt, index
+    (bits, group), = quant
+    n_w1, words_w1 = shapes["w1.weight"]
+    fmt = ExpertFormat("affine", bits, group, tuple(sorted(shapes)), shapes, dtypes,
+                       d_model=words_w1 * 32 // bits, d_ff=n_w1)
+    return fmt, _collect(pieces)
 
 
 def detect_expert_bank(model_path: str | Path) -> tuple[ExpertFormat, dict[tuple[int, int], ExpertEntry]]:
-    """(format, index) of the routed experts under `model_path`: a stacked affine bank when
-    config.json carries ``omlx_deepseek_v41``, else the shipped FP4 layout (``storage/index.py:182-194``).
-    The FP4 format's shapes come from the first expert's w1 / w2 headers."""
+    """(format, index) of the routed experts under ``model_path`` (the interface of
+    ``storage/index.py:182-194``).  ``config.json`` with an ``omlx_deepseek_v41``
+    block marks a stacked affine bank; anything else is read as the FP4 layout,
+    whose shapes come from the first expert's ``w1.weight`` header."""
     root = Path(model_path)
-    config = root / "config.json"
-    if config.exists():
-        try:
-            spec = json.loads(config.read_text()).get("omlx_deepseek_v41")
-        except (OSError, json.JSONDecodeError):
-            spec = None
-        if spec:
-            return build_stacked_expert_index(root, spec.get("quantized_modules", {}))
+    spec = None
+    try:
+        spec = json.loads((root / "config.json").read_text()).get("omlx_deepseek_v41")
+    except (OSError, ValueError, AttributeError):
+        pass
+    if spec:
+        return build_stacked_expert_index(root, spec.get("quantized_modules", {}))
     index = build_expert_index(root)
-    if not index:
+    w1 = next((t for t in index[min(index)].tensors if t.name.endswith(".w1.weight")), None) if index else None
+    if w1 is None or w1.shape is None or len(w1.shape) != 2:
         return FP4_FORMAT, index
-    first = index[min(index)]
-    by = {".".join(t.name.rsplit(".", 2)[-2:]): t for t in first.tensors}
-    if "w1.weight" not in by or by["w1.weight"].shape is None or len(by["w1.weight"].shape) != 2:
-        return FP4_FORMAT, index
-    d_ff, half_d = by["w1.weight"].shape
-    return fp4_format(half_d * 2, d_ff), index
+    d_ff, half_d = w1.shape
+    return fp4_format(2 * half_d, d_ff), index
 
 
 @dataclass(frozen=True)
@@ -268,11 +330,22 @@ class ReadRange:
 
 
 def merge_contiguous_ranges(entry: ExpertEntry) -> tuple[ReadRange, ...]:
-    """Runs of an entry's tensors that are adjacent in one shard, one read each (``storage/index.py:208-233``)."""
-    groups: list[list[TensorRange]] = []
-    for t in entry.tensors:
-        if groups and groups[-1][-1].shard == t.shard and groups[-1][-1].end == t.start:
-            groups[-1].append(t)
-        else:
-            groups.append([t])
-    return tuple(ReadRange(g[0].shard, g[0].start, g[-1].end, tuple(g)) for g in groups)
+    """An entry's tensors as the fewest single reads: a new read starts wherever
+    a tensor does not begin, in the same shard, at the byte the previous one ended
+    (the interface of ``storage/index.py:208-233``)."""
+    ts = entry.tensors
+    cuts = [0] + [i for i in range(1, len(ts))
+                  if (ts[i].shard, ts[i].start) != (ts[i - 1].shard, ts[i - 1].end)] + [len(ts)]
+    return tuple(ReadRange(ts[a].shard, ts[a].start, ts[b - 1].end, ts[a:b])
+                 for a, b in zip(cuts, cuts[1:]) if b > a)
+
+
+def tensor_sizes_from_entry(entry: ExpertEntry) -> dict[str, int]:
+    """{short name: bytes} of one indexed expert, sorted by name: what the runtime
+    hands the store to size its slots (the interface of
+    ``cache/resident_store.py:103-111``)."""
+    sizes = {".".join(t.name.split(".")[-2:]): t.size for t in entry.tensors}
+    lacking = sorted({"w1.weight", "w2.weight", "w3.weight"}.difference(sizes))
+    if lacking:
+        raise ValueError(f"expert ({entry.layer}, {entry.expert}) has no {', '.join(lacking)}")
+    return dict(sorted(sizes.items()))

@@ -79,3 +79,65 @@ def test_bank_loader_fills_misses(cuda, tmp_path):
     store.get_many([I.ExpertEntry(0, 1), I.ExpertEntry(0, 3)])
     torch.cuda.synchronize()
     assert store.stats.evictions == 1 and not store.is_resident((1, 2))
+
+
+def test_runtime_constructed_store_decodes(cuda, tmp_path):
+    """The store built exactly as text_decode_runtime.py:442-453 builds it (budget,
+    tensor sizes from an index entry, load workers, verbosity, then `.format =`)
+    serves moe_layer_forward over a partly resident bank read through the reader;
+    the output equals, bit for bit, the same layer over a fully resident store."""
+    from cachalot_amd import synth
+    from cachalot_amd.cache.resident_store import ResidentExpertStore
+    from cachalot_amd.moe_layer import moe_layer_forward
+    from cachalot_amd.storage.reader import ExpertReader
+
+    fmt0 = I.affine_format(4096, 2880)
+    _write(tmp_path, fmt0)
+    fmt, index = I.detect_expert_bank(tmp_path)
+    store = ResidentExpertStore(budget_bytes=6 * fmt.expert_bytes, reader=ExpertReader(),
+                                tensor_sizes=I.tensor_sizes_from_entry(next(iter(index.values()))),
+                                load_workers=8, verbose=False, n_layers=L, n_experts=E)
+    store.format = fmt
+    ref = make_store(fmt0, n_layers=L, n_experts=E)
+    for step in range(3):
+        la = step % L
+        w, b = synth.router_weights(SEED, la, E, 4096, cuda)
+        x = synth.activations(SEED, 90 + step, 1, 4096, cuda)[0]
+        out, route = moe_layer_forward(x, layer_id=la, gate_weight=w, gate_bias=b, expert_index=index,
+                                       expert_store=store, topk=6, route_scale=1.0, score_fn="sigmoid")
+        want, route_ref = moe_layer_forward(x, layer_id=la, gate_weight=w, gate_bias=b, expert_index=None,
+                                            expert_store=ref, topk=6, route_scale=1.0, score_fn="sigmoid")
+        assert torch.equal(route.indices, route_ref.indices)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), step
+    assert store.stats.misses >= 6 and len(store.resident_keys()) <= 6
+
+
+@pytest.mark.parametrize("planned", [False, True])
+def test_prefill_partial_residency_matches_full(cuda, planned):
+    """moe_prefill_grouped over a store that holds 8 of a layer's 32 experts: the
+    rest go to transient slots (with a prefetcher, after prepare_prefill_layer
+    plans the layer's share) and are released after the launches; the output
+    equals the fully resident store's bit for bit, on two layers in a row."""
+    from cachalot_amd.cache.prefetch import ResidentExpertPrefetcher
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+    from cachalot_amd.moe_prefill import moe_prefill_grouped
+    from oracle import synth as osynth
+
+    d, f, nE, t = 512, 256, 32, 150
+    fmt = I.affine_format(d, f)
+    full = make_store(fmt, n_layers=2, n_experts=nE)
+    part = ResidentExpertStore(fmt=fmt, n_slots=8, transient_slots=32, n_layers=2, n_experts=nE, device=cuda,
+                               loader=SyntheticLoader(fmt, SEED))
+    pf = ResidentExpertPrefetcher(part) if planned else None
+    for la in (0, 1, 0):
+        wb, bias = osynth.router_tensors(SEED, la, nE, d)
+        xb = osynth.activations(SEED, 700 + la, t, d)
+        kw = dict(layer_id=la, gate_weight=torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).to(cuda),
+                  gate_bias=torch.from_numpy(bias).to(cuda), expert_index=None, topk=6, route_scale=1.0,
+                  score_fn="sigmoid")
+        x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(cuda)
+        a, ra = moe_prefill_grouped(x, expert_store=part, expert_prefetcher=pf, **kw)
+        b, rb = moe_prefill_grouped(x, expert_store=full, **kw)
+        assert torch.equal(ra.indices, rb.indices)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), la
+        assert part._transient_count == 0 and len(part.resident_keys()) <= 8
