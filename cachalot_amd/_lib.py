@@ -39,9 +39,23 @@ c_uint64 = ctypes.c_uint64
 
 
 class ExpertLayout(ctypes.Structure):
-    """cachalot_expert_layout: record stride and nine tensor offsets."""
+    """cachalot_expert_layout: record stride, nine tensor offsets and the 2-bit bank's
+    scale / bias storage type (SCALE_BF16 or SCALE_F16)."""
 
-    _fields_ = [("record_bytes", c_int64), ("offset", c_int64 * 9)]
+    _fields_ = [("record_bytes", c_int64), ("offset", c_int64 * 9), ("scale_dtype", ctypes.c_int32)]
+
+
+SCALE_BF16 = 0
+SCALE_F16 = 1
+SCALE_DTYPES = {"bfloat16": SCALE_BF16, "float16": SCALE_F16}
+
+
+def scale_dtype_code(name: str) -> int:
+    """The C ABI's code for a 2-bit bank's scale dtype name; other types are refused."""
+    try:
+        return SCALE_DTYPES[name]
+    except KeyError:
+        raise ValueError(f"2-bit bank scales/biases must be bfloat16 or float16, got {name!r}") from None
 
 
 class CachalotError(RuntimeError):
@@ -113,10 +127,11 @@ _SIGNATURES = {
                                            c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_size_t, c_void_p]),
     "cachalot_copy_records": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "cachalot_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
-    "cachalot_requant_fp4_to_q2": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "cachalot_requant_fp4_to_q2": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
+                                           c_void_p]),
     "cachalot_dequant_fp4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
-    "cachalot_dequant_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
-                                    c_void_p]),
+    "cachalot_dequant_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                    c_void_p, c_void_p]),
 }
 
 _lib = None

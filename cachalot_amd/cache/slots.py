@@ -94,6 +94,7 @@ class HBMSlotPool:
         fmt = self.expert_format()
         lay = _lib.ExpertLayout()
         lay.record_bytes = self.record_bytes
+        lay.scale_dtype = _lib.scale_dtype_code(fmt.dtypes["w1.scales"]) if fmt.kind == "affine" else _lib.SCALE_BF16
         for i, canonical in enumerate(KERNEL_ORDER):
             name = kernel_tensor_name(fmt, canonical)
             lay.offset[i] = self.offsets[name] if name is not None else 0

@@ -43,6 +43,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Round-to-nearest-even fp32 -> fp16 bits (the hardware conversion).
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// A 2-bit bank's scale or bias as stored: bf16 bits, or fp16 bits when `f16`
+// (both convert to fp32 exactly).
+__device__ __forceinline__ float scale_bits_to_f32(uint16_t b, bool f16) {
+  return f16 ? (float)__builtin_bit_cast(_Float16, b) : bf16_to_f32(b);
+}
+
 __device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t u) {
   return __builtin_bit_cast(bf16x2_t, u);
 }

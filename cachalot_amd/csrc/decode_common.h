@@ -12,6 +12,7 @@ constexpr int KMAX = 8;     // max experts per token
 struct Layout {
   int64_t record_bytes;
   int64_t off[9];
+  bool f16;   // 2-bit banks: scales and biases stored as fp16 (else bf16)
 };
 
 inline int make_layout(const cachalot_expert_layout* layout, int n_tensors, const int* used, Layout& L,
@@ -21,6 +22,12 @@ inline int make_layout(const cachalot_expert_layout* layout, int n_tensors, cons
     return fail(CACHALOT_EINVAL, "%s: record_bytes %lld must be a positive multiple of 16", who,
                 (long long)L.record_bytes);
   for (int i = 0; i < 9; ++i) L.off[i] = layout->offset[i];
+  if (layout->scale_dtype != CACHALOT_SCALE_BF16 && layout->scale_dtype != CACHALOT_SCALE_F16)
+    return fail(CACHALOT_EINVAL, "%s: scale_dtype %d (0 = bf16, 1 = fp16)", who, (int)layout->scale_dtype);
+  // FP4 records (six tensors) carry E8M0 scales: the flag has no meaning there
+  if (n_tensors != 9 && layout->scale_dtype != CACHALOT_SCALE_BF16)
+    return fail(CACHALOT_EINVAL, "%s: an FP4 bank has E8M0 scales, scale_dtype must be 0", who);
+  L.f16 = layout->scale_dtype == CACHALOT_SCALE_F16;
   for (int t = 0; t < n_tensors; ++t) {
     const int i = used[t];
     if (L.off[i] < 0 || L.off[i] % 16 != 0 || L.off[i] >= L.record_bytes)
@@ -81,18 +88,14 @@ struct RouteTail {
 };
 
 // Workspace layout of one decode call:
-//   [counters 256 B][grid-barrier block 4224 B][k slots][k weights][hidden]
-// each region 256-byte aligned, the first two at fixed offsets whatever k and F
-// are, so calls of different shapes on one workspace never overlap another's
+//   [counters 256 B][k slots][k weights][hidden]
+// each region 256-byte aligned, the counters at offset 0 whatever k and F are,
+// so calls of different shapes on one workspace never overlap another's
 // counters.  The counters must be zero before the first call on a workspace (a
-// zero-filled allocation); every call leaves them zero.  The grid-barrier block
-// of the one-launch decode keeps a generation count instead (never reset).  The
-// rest is scratch: nothing in it survives a call.
-constexpr size_t WS_SYNC_OFF = 256;
-constexpr size_t WS_SYNC_BYTES = 4352;
-
+// zero-filled allocation); every call leaves them zero.  The rest is scratch:
+// nothing in it survives a call.
 struct WsOffsets {
-  size_t counter, sync, slots, weights, hidden, total;
+  size_t counter, slots, weights, hidden, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -100,8 +103,7 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 inline WsOffsets ws_offsets(size_t hidden_bytes) {
   WsOffsets o;
   o.counter = 0;
-  o.sync = WS_SYNC_OFF;
-  o.slots = WS_SYNC_OFF + WS_SYNC_BYTES;
+  o.slots = 256;
   o.weights = o.slots + align256(KMAX * sizeof(int32_t));
   o.hidden = o.weights + align256(KMAX * sizeof(float));
   o.total = o.hidden + align256(hidden_bytes);

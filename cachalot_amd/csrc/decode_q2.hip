@@ -201,8 +201,8 @@ __global__ void __launch_bounds__(64 * GU_WAVES) q2_gate_up_kernel(
     group_steps2(xm, aoff, wg[b], wu[b], cg, cu);
     const float gs = gv[b] ? xs[gi[b]] : 0.0f;
     const int si = j * GT + gi[b];
-    accg = accg + (bf16_to_f32(s1[si]) * cg[0] + bf16_to_f32(b1[si]) * gs);
-    accu = accu + (bf16_to_f32(s3[si]) * cu[0] + bf16_to_f32(b3[si]) * gs);
+    accg = accg + (scale_bits_to_f32(s1[si], L.f16) * cg[0] + scale_bits_to_f32(b1[si], L.f16) * gs);
+    accu = accu + (scale_bits_to_f32(s3[si], L.f16) * cu[0] + scale_bits_to_f32(b3[si], L.f16) * gs);
   }
   accg = sum_lane_groups(accg);
   accu = sum_lane_groups(accu);
@@ -307,7 +307,7 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) q2_down_kernel(
       const f32x4_t c = group_steps1(hm, aoff, wd[b]);
       const float gs = gv[b] ? hsum[e * GK + gi[b]] : 0.0f;
       const int si = j * GK + gi[b];
-      acc = acc + (bf16_to_f32(s2[si]) * c[0] + bf16_to_f32(b2[si]) * gs);
+      acc = acc + (scale_bits_to_f32(s2[si], L.f16) * c[0] + scale_bits_to_f32(b2[si], L.f16) * gs);
     }
   }
   acc = sum_lane_groups(acc);
@@ -330,19 +330,12 @@ __global__ void __launch_bounds__(64 * KMAX * DN_HALVES) q2_down_kernel(
 
 }  // namespace
 
-size_t q2_fused_region_bytes(int F, int k);
-int q2_fused_grid(int D, int F, int k);
-int launch_q2_decode_fused(int G, const uint16_t* x, const uint8_t* pool, const Layout& L, const ExpertSource& src,
-                           const int32_t* ws_slots, const float* ws_w, int D, int F, int k, float limit,
-                           const uint16_t* addend, float* routed, uint16_t* out, uint8_t* sync, uint8_t* hid,
-                           hipStream_t s);
-
-// [two-kernel layout (counters, grid-barrier block, slots, weights, hidden)]
-// [matrix-core paths: hidden plane blocks][matrix-core two-kernel path: x plane blocks]
+// [decode layout (counters, slots, weights, bf16 hidden)]
+// [matrix-core path: hidden plane blocks, k x ceil(F/128) x 320 B][x plane blocks, ceil(D/128) x 320 B]
 static size_t xplanes_bytes(int D) { return align256((size_t)(D + 127) / 128 * 320); }
+static size_t hplanes_bytes(int F, int k) { return align256((size_t)k * ((F + 127) / 128) * 320); }
 size_t q2_workspace_bytes(int D, int F, int k) {
-  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total + q2_fused_region_bytes(F, k) +
-         xplanes_bytes(D);
+  return ws_offsets((size_t)k * hidden_stride(F) * sizeof(uint16_t)).total + hplanes_bytes(F, k) + xplanes_bytes(D);
 }
 
 // Validates, then launches [router + top-k tail], gate/up and down on stream s.
@@ -390,10 +383,9 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   uint16_t* hp = reinterpret_cast<uint16_t*>(ws + wo.hidden);
   int32_t* ws_slots = reinterpret_cast<int32_t*>(ws + wo.slots);
   float* ws_w = reinterpret_cast<float*>(ws + wo.weights);
-  const int G = q2_fused_grid(D, F, k);
-  const bool mx = G == 0 && q2mx_supported(D, F, k) && !bf16_requested();
-  uint8_t* xplanes = ws + wo.total + q2_fused_region_bytes(F, k);
-  if (router && G == 0) {   // scores only; the gate/up workgroups select the experts
+  const bool mx = q2mx_supported(D, F, k) && !bf16_requested();
+  uint8_t* xplanes = ws + wo.total + hplanes_bytes(F, k);
+  if (router && mx) {   // scores only; the gate/up workgroups select the experts
     rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
                               router->scores, s, nullptr, mx ? xplanes : nullptr);
     if (rc) return rc;
@@ -429,9 +421,6 @@ int launch_q2_decode(const uint16_t* x, const uint8_t* pool, const cachalot_expe
   if (mx)
     return launch_q2mx_decode(x, router != nullptr, xplanes, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit,
                               addend, routed, out, ws + wo.total, s, nullptr, nullptr);
-  if (G > 0)
-    return launch_q2_decode_fused(G, x, pool, L, src, ws_slots, ws_w, D, F, k, swiglu_limit, addend, routed, out,
-                                  ws + wo.sync, ws + wo.total, s);
   const int GT = D / GROUP;
   const int nb_gu = ((GT + GU_WAVES - 1) / GU_WAVES + 3) / 4;
   const int xi = (D / 16 + 255) / 256;

@@ -187,8 +187,8 @@ __device__ __forceinline__ void q2mx_gate_up_body(GuLds& s, const int bid, const
     a3 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c3[m][1].z, c3[m][1].w), a3, ch.sa, mx::E8M0_TWO);
     const float sx = piece_sums(s.planes + (4 * q + kg) * PB_BYTES, mx::PIECES);
     const int si = j * GT + 4 * q + kg;
-    const float v1 = bf16_to_f32(s.sc[0][si]) * dot4(a1) + bf16_to_f32(s.sc[1][si]) * sx;
-    const float v3 = bf16_to_f32(s.sc[2][si]) * dot4(a3) + bf16_to_f32(s.sc[3][si]) * sx;
+    const float v1 = scale_bits_to_f32(s.sc[0][si], L.f16) * dot4(a1) + scale_bits_to_f32(s.sc[1][si], L.f16) * sx;
+    const float v3 = scale_bits_to_f32(s.sc[2][si], L.f16) * dot4(a3) + scale_bits_to_f32(s.sc[3][si], L.f16) * sx;
     const float r1 = tile::sum_lane_groups(v1);
     const float r3 = tile::sum_lane_groups(v3);
     if (lane < 16) {
@@ -301,7 +301,7 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_gate_up_shared_kernel(const u
 template <int NI, int MAXM>
 __device__ __forceinline__ void down_items(DnLds& s, const uint4 (&c2)[MAXM][2], const int (&it_e)[MAXM],
                                            const int (&it_q)[MAXM], const bool (&on)[MAXM], int m0,
-                                           const ARole& ro, int GK, int FT, int j, int kg, int lane) {
+                                           const ARole& ro, int GK, int FT, int j, int kg, int lane, bool f16) {
   Chain ch[NI];
   f32x4_t acc[NI];
 #pragma unroll
@@ -334,7 +334,8 @@ __device__ __forceinline__ void down_items(DnLds& s, const uint4 (&c2)[MAXM][2],
     const int g2 = 4 * q2 + kg;
     const float sh = g2 < GK ? piece_sums(s.planes + (e * GK + g2) * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
     const int si = j * GK + min(g2, GK - 1);
-    float v = g2 < GK ? bf16_to_f32(s.sc[e][0][si]) * dot4(acc[i]) + bf16_to_f32(s.sc[e][1][si]) * sh : 0.0f;
+    float v = g2 < GK ? scale_bits_to_f32(s.sc[e][0][si], f16) * dot4(acc[i]) + scale_bits_to_f32(s.sc[e][1][si], f16) * sh
+                      : 0.0f;
     v = tile::sum_lane_groups(v);
     if (on[m] && lane < 16) s.red[e][q2][lane] = v;
   }
@@ -442,10 +443,10 @@ __global__ void __launch_bounds__(DN_THREADS) q2mx_down_kernel(const uint8_t* __
   //         valid (clamped) data and are discarded.
   const ARole ro = a_role(lane);
   if constexpr (MAXM <= 3) {
-    down_items<MAXM>(s, c2, it_e, it_q, on, 0, ro, GK, FT, j, kg, lane);
+    down_items<MAXM>(s, c2, it_e, it_q, on, 0, ro, GK, FT, j, kg, lane, L.f16);
   } else {
-    down_items<2>(s, c2, it_e, it_q, on, 0, ro, GK, FT, j, kg, lane);
-    down_items<MAXM - 2>(s, c2, it_e, it_q, on, 2, ro, GK, FT, j, kg, lane);
+    down_items<2>(s, c2, it_e, it_q, on, 0, ro, GK, FT, j, kg, lane, L.f16);
+    down_items<MAXM - 2>(s, c2, it_e, it_q, on, 2, ro, GK, FT, j, kg, lane, L.f16);
   }
   if constexpr (SH) tile::wait_vmem();   // the shared rows
   lds_sync();
@@ -687,8 +688,8 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bgu_kernel(BatchArgs a) {
       a3 = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c3[m][1].z, c3[m][1].w), a3, ch.sa, mx::E8M0_TWO);
       const float sx = piece_sums(planes + (4 * q + kg) * PB_BYTES, mx::PIECES);
       const int si = j * GT + 4 * q + kg;
-      const float v1 = bf16_to_f32(s.sc[0][si]) * dot4(a1) + bf16_to_f32(s.sc[1][si]) * sx;
-      const float v3 = bf16_to_f32(s.sc[2][si]) * dot4(a3) + bf16_to_f32(s.sc[3][si]) * sx;
+      const float v1 = scale_bits_to_f32(s.sc[0][si], a.L.f16) * dot4(a1) + scale_bits_to_f32(s.sc[1][si], a.L.f16) * sx;
+      const float v3 = scale_bits_to_f32(s.sc[2][si], a.L.f16) * dot4(a3) + scale_bits_to_f32(s.sc[3][si], a.L.f16) * sx;
       const float s1 = tile::sum_lane_groups(v1);
       const float s3 = tile::sum_lane_groups(v3);
       if (lane < 16) {
@@ -830,7 +831,9 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn4_kernel(BatchArgs a) {
       acc = mx::mfma_fp8_fp4<3>(ch.a[3], mx::q2_spread(c2[m][1].z, c2[m][1].w), acc, ch.sa, mx::E8M0_TWO);
       const float sh = g2 < GK ? piece_sums(planes + g2 * PB_BYTES, min(8, FT - 8 * g2)) : 0.0f;
       const int si = j * GK + min(g2, GK - 1);
-      float v = g2 < GK ? bf16_to_f32(s.sc[wave][0][si]) * dot4(acc) + bf16_to_f32(s.sc[wave][1][si]) * sh : 0.0f;
+      float v = g2 < GK ? scale_bits_to_f32(s.sc[wave][0][si], a.L.f16) * dot4(acc) +
+                              scale_bits_to_f32(s.sc[wave][1][si], a.L.f16) * sh
+                        : 0.0f;
       yv = yv + tile::sum_lane_groups(v);
     }
     // the previous row's outputs go out now: their stores then overlap this row's work

@@ -47,7 +47,7 @@ __global__ void dequant_fp4_kernel(const uint32_t* __restrict__ packed, const ui
 // one thread per 32-bit word of codes (16 values)
 __global__ void dequant_q2_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ scales,
                                   const uint16_t* __restrict__ biases, int N, int K, int row_words, int groups,
-                                  int group, float* __restrict__ out) {
+                                  int group, bool f16, float* __restrict__ out) {
   const int kw = (K + 15) / 16;
   const int64_t total = (int64_t)N * kw;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -70,8 +70,8 @@ __global__ void dequant_q2_kernel(const uint32_t* __restrict__ w, const uint16_t
     q[4 * b + 3] = __uint_as_float(po[b] & 0xffff0000u);
   }
   const int g = (j * 16) / group;
-  const float s = bf16_to_f32(scales[n * groups + g]);
-  const float b = bf16_to_f32(biases[n * groups + g]);
+  const float s = scale_bits_to_f32(scales[n * groups + g], f16);
+  const float b = scale_bits_to_f32(biases[n * groups + g], f16);
 #pragma unroll
   for (int t = 0; t < 16; ++t) {
     const int k = j * 16 + t;
@@ -95,16 +95,20 @@ extern "C" int cachalot_dequant_fp4(const uint8_t* packed, const uint8_t* scales
 }
 
 extern "C" int cachalot_dequant_q2(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
-                                   int row_words, int groups, int group, float* out, cachalot_stream_t stream) {
+                                   int row_words, int groups, int group, int scale_dtype, float* out,
+                                   cachalot_stream_t stream) {
   using namespace cachalot;
   CACHALOT_REQUIRE(w && scales && biases && out, "dequant_q2: null pointer");
   CACHALOT_REQUIRE(N >= 1 && K >= 1 && group >= 16 && group % 16 == 0, "dequant_q2: bad shape N=%d K=%d group=%d",
                    N, K, group);
   CACHALOT_REQUIRE(row_words * 16 >= K && groups * group >= K, "dequant_q2: row_words %d / groups %d too small",
                    row_words, groups);
+  CACHALOT_REQUIRE(scale_dtype == CACHALOT_SCALE_BF16 || scale_dtype == CACHALOT_SCALE_F16,
+                   "dequant_q2: scale_dtype %d (0 = bf16, 1 = fp16)", scale_dtype);
   const int64_t total = (int64_t)N * ((K + 15) / 16);
   const int threads = 256;
   hipLaunchKernelGGL(dequant_q2_kernel, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0,
-                     (hipStream_t)stream, w, scales, biases, N, K, row_words, groups, group, out);
+                     (hipStream_t)stream, w, scales, biases, N, K, row_words, groups, group,
+                     scale_dtype == CACHALOT_SCALE_F16, out);
   return check_launch("dequant_q2_kernel");
 }

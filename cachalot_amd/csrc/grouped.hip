@@ -358,9 +358,9 @@ __device__ __forceinline__ void chunk_mma(const uint8_t* abuf, const float* sums
 // Scale of (row j of the workgroup, chunk c) for tensor q: 2-bit bf16 scale/bias of
 // group c; FP4 E8M0 of block 4c + kg.
 template <int KIND>
-__device__ __forceinline__ float staged_scale(const uint8_t* sc, int q, int j, int c, int kg, int per_row) {
+__device__ __forceinline__ float staged_scale(const uint8_t* sc, int q, int j, int c, int kg, int per_row, bool f16) {
   if constexpr (KIND == KIND_Q2) {
-    return bf16_to_f32(reinterpret_cast<const uint16_t*>(sc)[(q * NT + j) * per_row + c]);
+    return scale_bits_to_f32(reinterpret_cast<const uint16_t*>(sc)[(q * NT + j) * per_row + c], f16);
   } else {
     // blocks past K (the last chunk of K = 2880) meet zero activations: any finite scale
     return 4 * c + kg < per_row ? e8m0_to_f32(sc[(q * NT + j) * per_row + 4 * c + kg]) : 1.0f;
@@ -436,8 +436,8 @@ __device__ __forceinline__ bool grouped_main(const GroupedArgs& g, uint8_t* lds,
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       // 2-bit: tensor slots 2m (scales) and 2m+1 (biases); FP4: slot 2m (E8M0)
-      scale[m] = staged_scale<KIND>(sc, KIND == KIND_Q2 ? 2 * m : m, wave * 16 + (lane & 15), c, kg, per_row);
-      bias[m] = KIND == KIND_Q2 ? staged_scale<KIND>(sc, 2 * m + 1, wave * 16 + (lane & 15), c, kg, per_row) : 0.0f;
+      scale[m] = staged_scale<KIND>(sc, KIND == KIND_Q2 ? 2 * m : m, wave * 16 + (lane & 15), c, kg, per_row, g.L.f16);
+      bias[m] = KIND == KIND_Q2 ? staged_scale<KIND>(sc, 2 * m + 1, wave * 16 + (lane & 15), c, kg, per_row, g.L.f16) : 0.0f;
     }
     chunk_mma<KIND, MT, NM>(abuf[cur], sums[cur], bc, scale, bias, lane, acc);
     if (more) {

@@ -10,7 +10,9 @@
 //   skipped, in order) replaces the best when its error is strictly smaller;
 //   error = sum over the group in index order of (scale q + bias - w)^2 with
 //   q = clip(rint((w - bias) / scale), 0, 3);
-// then scale and bias are rounded to bf16, the codes recomputed against them
+// then scale and bias are rounded (RNE) to the bank's storage type, bf16 or
+// fp16, the codes recomputed against them (an fp16 scale that rounds to zero,
+// a constant group, gives code 0)
 // and packed 16 per word, low field first.  Every operation is a single fp32
 // operation in the written order (the library is built without contraction),
 // so the result equals a float32 evaluation in the same order bit for bit.
@@ -30,8 +32,9 @@ struct Args {
   const uint8_t* s;      // [N, K/32] E8M0
   int N, K;
   uint32_t* q;           // [N, G * 8] 2-bit codes
-  uint16_t* scales;      // [N, G] bf16
-  uint16_t* biases;      // [N, G] bf16
+  uint16_t* scales;      // [N, G] bf16 or fp16 (f16)
+  uint16_t* biases;      // [N, G] bf16 or fp16
+  bool f16;
 };
 
 __device__ __forceinline__ float level(float w, float scale, float bias) {
@@ -104,8 +107,9 @@ __global__ __launch_bounds__(256) void requant_fp4_q2_kernel(Args p) {
     }
   }
 
-  const uint16_t sb = f32_to_bf16(best_s), bb = f32_to_bf16(best_b);
-  const float s16 = bf16_to_f32(sb), b16 = bf16_to_f32(bb);
+  const uint16_t sb = p.f16 ? f32_to_f16(best_s) : f32_to_bf16(best_s);
+  const uint16_t bb = p.f16 ? f32_to_f16(best_b) : f32_to_bf16(best_b);
+  const float s16 = scale_bits_to_f32(sb, p.f16), b16 = scale_bits_to_f32(bb, p.f16);
   uint32_t words[GROUP / 16];
 #pragma unroll
   for (int j = 0; j < GROUP / 16; ++j) {
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(256) void requant_fp4_q2_kernel(Args p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int k = 16 * j + i;
-      const uint32_t q = k < nvalid ? (uint32_t)level(w[k], s16, b16) : 0u;
+      const uint32_t q = k < nvalid && s16 != 0.0f ? (uint32_t)level(w[k], s16, b16) : 0u;
       v |= q << (2 * i);
     }
     words[j] = v;
@@ -131,13 +135,16 @@ __global__ __launch_bounds__(256) void requant_fp4_q2_kernel(Args p) {
 using namespace cachalot;
 
 extern "C" int cachalot_requant_fp4_to_q2(const uint8_t* w_fp4, const uint8_t* s_fp4, int N, int K, uint32_t* q,
-                                          uint16_t* scales, uint16_t* biases, cachalot_stream_t stream) {
+                                          uint16_t* scales, uint16_t* biases, int scale_dtype,
+                                          cachalot_stream_t stream) {
   CACHALOT_REQUIRE(w_fp4 && s_fp4 && q && scales && biases, "requant_fp4_to_q2: null pointer");
   CACHALOT_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "requant_fp4_to_q2: N=%d, K=%d (K a positive multiple of 32)", N, K);
   CACHALOT_REQUIRE(((uintptr_t)w_fp4 & 15u) == 0 && ((uintptr_t)q & 15u) == 0,
                    "requant_fp4_to_q2: w_fp4 and q must be 16-byte aligned");
   const long groups = (long)N * ((K + requant::GROUP - 1) / requant::GROUP);
-  requant::Args a{w_fp4, s_fp4, N, K, q, scales, biases};
+  CACHALOT_REQUIRE(scale_dtype == CACHALOT_SCALE_BF16 || scale_dtype == CACHALOT_SCALE_F16,
+                   "requant_fp4_to_q2: scale_dtype %d (0 = bf16, 1 = fp16)", scale_dtype);
+  requant::Args a{w_fp4, s_fp4, N, K, q, scales, biases, scale_dtype == CACHALOT_SCALE_F16};
   hipLaunchKernelGGL(requant::requant_fp4_q2_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, a);
   return check_launch("requant_fp4_to_q2");

@@ -4,7 +4,7 @@
 // (Steele, Lea & Flood, OOPSLA 2014).  Kinds and their exact arithmetic are
 // fixed so that a host re-implementation can regenerate any element bit for
 // bit: every float step is one IEEE operation in double, then one rounding
-// to fp32 (and RNE to bf16).
+// to fp32 (and RNE to bf16 or fp16).
 #include "common.h"
 
 namespace cachalot {
@@ -52,6 +52,14 @@ __global__ void fill_kernel(void* dst, int64_t n, int64_t start, uint64_t key, i
       case 3:
         ((uint16_t*)dst)[i] = f32_to_bf16((float)irwin_hall(r, p1));
         break;
+      case 5: {
+        const double t = (double)(r >> 40) * 0x1p-24;
+        ((uint16_t*)dst)[i] = f32_to_f16((float)(p0 + p1 * t));
+        break;
+      }
+      case 6:
+        ((uint16_t*)dst)[i] = f32_to_f16((float)irwin_hall(r, p1));
+        break;
       default:
         ((float*)dst)[i] = (float)irwin_hall(r, p1);
         break;
@@ -68,10 +76,10 @@ extern "C" int cachalot_fill_synthetic(void* dst, int64_t n, int64_t start, uint
   using namespace cachalot;
   CACHALOT_REQUIRE(dst != nullptr || n == 0, "fill: null destination");
   CACHALOT_REQUIRE(n >= 0 && start >= 0, "fill: negative size");
-  CACHALOT_REQUIRE(kind >= 0 && kind <= 4, "fill: unknown kind %d", kind);
+  CACHALOT_REQUIRE(kind >= 0 && kind <= 6, "fill: unknown kind %d", kind);
   CACHALOT_REQUIRE(kind != 1 || (p0 >= 0 && p1 <= 255 && p0 <= p1), "fill: E8M0 range [%g, %g]", p0, p1);
   if (n == 0) return CACHALOT_OK;
-  // kinds 3/4 take the Irwin-Hall scale c = sigma / std in p1 (the host computes it)
+  // kinds 3/4/6 take the Irwin-Hall scale c = sigma / std in p1 (the host computes it)
   const int threads = 256;
   int64_t blocks = (n + threads - 1) / threads;
   if (blocks > 65536) blocks = 65536;

@@ -20,9 +20,10 @@ from .storage.index import ExpertFormat, affine_format, detect_expert_bank
 PROJS = ("w1", "w2", "w3")
 
 
-def requantize_fp4_matrix(w_fp4: torch.Tensor, s_fp4: torch.Tensor, k: int, *, group_size: int = 128):
+def requantize_fp4_matrix(w_fp4: torch.Tensor, s_fp4: torch.Tensor, k: int, *, group_size: int = 128,
+                          scale_dtype: str = "bfloat16"):
     """w_fp4 uint8 [N, K/2], s_fp4 uint8 [N, K/32] (device) -> (codes int32 [N, Kp/16] (uint32 bits),
-    scales int16 [N, Kp/128] (bf16 bits), biases int16) on the same device."""
+    scales int16 [N, Kp/128] (bf16 or fp16 bits, ``scale_dtype``), biases int16) on the same device."""
     if group_size != 128:
         raise ValueError("the requantizer writes the g128 bank")
     n = w_fp4.shape[0]
@@ -37,7 +38,8 @@ def requantize_fp4_matrix(w_fp4: torch.Tensor, s_fp4: torch.Tensor, k: int, *, g
     s = torch.empty((n, g), dtype=torch.int16, device=dev)
     b = torch.empty((n, g), dtype=torch.int16, device=dev)
     rc = _lib.lib().cachalot_requant_fp4_to_q2(w_fp4.data_ptr(), s_fp4.data_ptr(), n, k, q.data_ptr(), s.data_ptr(),
-                                               b.data_ptr(), _lib.stream_handle(dev))
+                                               b.data_ptr(), _lib.scale_dtype_code(scale_dtype),
+                                               _lib.stream_handle(dev))
     _lib.check(rc, "requant_fp4_to_q2")
     return q, s, b
 
@@ -52,7 +54,8 @@ def requantize_expert(src: dict[str, torch.Tensor], src_fmt: ExpertFormat, dst: 
     for proj in PROJS:
         rows, half_k = src_fmt.shapes[f"{proj}.weight"]
         q, s, b = requantize_fp4_matrix(src[f"{proj}.weight"].view(rows, half_k),
-                                        src[f"{proj}.scale"].view(rows, -1), 2 * half_k)
+                                        src[f"{proj}.scale"].view(rows, -1), 2 * half_k,
+                                        scale_dtype=dst_fmt.dtypes[f"{proj}.scales"])
         for name, t in ((f"{proj}.weight", q), (f"{proj}.scales", s), (f"{proj}.biases", b)):
             dst[name].view(torch.uint8).copy_(t.view(torch.uint8).reshape(-1))
 

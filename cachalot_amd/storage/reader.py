@@ -35,7 +35,8 @@ def check_kernel_format(fmt: ExpertFormat) -> None:
     """The kernels read the layouts of ``affine_format`` / ``fp4_format``; a bank whose tensors differ
     (another group count, fp32 scales, a truncated last group) is rejected before any byte moves."""
     if fmt.kind == "affine":
-        want = affine_format(fmt.d_model, fmt.d_ff, bits=fmt.bits, group_size=fmt.group_size)
+        want = affine_format(fmt.d_model, fmt.d_ff, bits=fmt.bits, group_size=fmt.group_size,
+                             scale_dtype=fmt.dtypes.get("w1.scales", "bfloat16"))
     elif fmt.kind == "fp4":
         want = fp4_format(fmt.d_model, fmt.d_ff)
     else:

@@ -30,6 +30,8 @@ KIND_E8M0 = 1
 KIND_BF16_UNIFORM = 2
 KIND_BF16_NORMAL = 3
 KIND_F32_NORMAL = 4
+KIND_F16_UNIFORM = 5
+KIND_F16_NORMAL = 6
 IRWIN_HALL_STD = math.sqrt((65536.0 ** 2 - 1.0) / 3.0)
 
 TENSOR_IDS = {
@@ -61,10 +63,11 @@ def fill(dst: torch.Tensor, kind: int, key: int, p0: float = 0.0, p1: float = 0.
          row_total: int = 0, row_valid: int = 0, start: int = 0, n: int | None = None) -> None:
     """Fill `dst` (a contiguous device tensor) element-wise; element size follows the kind."""
     _lib.require_cuda(dst)
-    item = {KIND_U32: 4, KIND_E8M0: 1, KIND_BF16_UNIFORM: 2, KIND_BF16_NORMAL: 2, KIND_F32_NORMAL: 4}[kind]
+    item = {KIND_U32: 4, KIND_E8M0: 1, KIND_BF16_UNIFORM: 2, KIND_BF16_NORMAL: 2, KIND_F32_NORMAL: 4,
+            KIND_F16_UNIFORM: 2, KIND_F16_NORMAL: 2}[kind]
     if n is None:
         n = dst.numel() * dst.element_size() // item
-    if kind in (KIND_BF16_NORMAL, KIND_F32_NORMAL):
+    if kind in (KIND_BF16_NORMAL, KIND_F32_NORMAL, KIND_F16_NORMAL):
         p1 = p0 / IRWIN_HALL_STD
     rc = _lib.lib().cachalot_fill_synthetic(dst.data_ptr(), n, start, key, kind, float(p0), float(p1),
                                             row_total, row_valid, _lib.stream_handle(dst.device))
@@ -85,8 +88,10 @@ def tensor_specs(fmt: ExpertFormat, *, e8m0_lo: int = 119, e8m0_hi: int = 127, s
         row_valid = k * fmt.bits // 32
         pad = row_valid != row_total
         specs.append((f"{proj}.weight", KIND_U32, 0.0, 0.0, row_total if pad else 0, row_valid if pad else 0))
-        specs.append((f"{proj}.scales", KIND_BF16_UNIFORM, float(scale_lo), float(scale_hi) - float(scale_lo), 0, 0))
-        specs.append((f"{proj}.biases", KIND_BF16_NORMAL, float(bias_sigma), 0.0, 0, 0))
+        f16 = fmt.dtypes[f"{proj}.scales"] == "float16"
+        specs.append((f"{proj}.scales", KIND_F16_UNIFORM if f16 else KIND_BF16_UNIFORM, float(scale_lo),
+                      float(scale_hi) - float(scale_lo), 0, 0))
+        specs.append((f"{proj}.biases", KIND_F16_NORMAL if f16 else KIND_BF16_NORMAL, float(bias_sigma), 0.0, 0, 0))
     return specs
 
 

@@ -44,15 +44,24 @@ typedef struct ihipStream_t* cachalot_stream_t; /* == hipStream_t */
 #define CACHALOT_ORDER_ASCENDING 0     /* argsort(sel)[-k:]: router_mlx.py:197-202    */
 #define CACHALOT_ORDER_RANK 1          /* argpartition(-sel): minimax/gpu_select.py:81-106 */
 
+/* Storage type of a 2-bit affine bank's scales and biases: the bank's
+ * ExpertFormat.dtypes entry ("bfloat16" / "float16", src/cachalot/storage/index.py:18,153;
+ * oQ3e banks carry fp16, src/cachalot/model/expert_affine.py:1-10). */
+#define CACHALOT_SCALE_BF16 0
+#define CACHALOT_SCALE_F16 1
+
 /* Byte layout of one expert record inside an HBM slot pool.  A slot's record
  * starts at pool + slot * record_bytes; tensor t sits at offset[t].
  * Tensor order: w1.weight, w1.scale(s), w1.biases, w2.weight, w2.scale(s),
  * w2.biases, w3.weight, w3.scale(s), w3.biases (biases unused for FP4).
+ * scale_dtype: CACHALOT_SCALE_BF16 or CACHALOT_SCALE_F16 for 2-bit banks;
+ * 0 for FP4 banks (their scales are E8M0).
  * Mirrors SlabSlotPool's fixed per-tensor record offsets
  * (src/cachalot/cache/slots.py:185-216). */
 typedef struct cachalot_expert_layout {
   int64_t record_bytes;
   int64_t offset[9];
+  int32_t scale_dtype;
 } cachalot_expert_layout;
 
 /* Library identity and last error (thread-local). */
@@ -315,30 +324,33 @@ int cachalot_stream_read(const void* src, size_t bytes, uint32_t* sink, int bloc
 
 /* FP4 -> 2-bit affine g128 requantization (the searched fit) of one weight
  * matrix: w_fp4 [N, K/2] packed E2M1 + s_fp4 [N, K/32] E8M0 -> q [N, Kp/16] u32
- * codes (16 per word, low field first), scales / biases [N, Kp/128] bf16,
- * Kp = K rounded up to 128.  Per group: the min/max fit, then 24 shrunk ranges
- * (SHRINKS x SHRINKS), the least squared error kept (strictly smaller wins,
- * error summed in index order), scale and bias rounded to bf16, codes
+ * codes (16 per word, low field first), scales / biases [N, Kp/128] bf16 or fp16
+ * (scale_dtype, CACHALOT_SCALE_*), Kp = K rounded up to 128.  Per group: the
+ * min/max fit, then 24 shrunk ranges (SHRINKS x SHRINKS), the least squared
+ * error kept (strictly smaller wins, error summed in index order), scale and
+ * bias rounded (RNE) to the storage type, codes
  * recomputed against them; a partial last group fits its real elements and
  * pads with code 0.  Replaces quantize_affine(fit=fit_search) over the FP4
  * checkpoint (benchmarks/quant_affine.py:157-205,330-359,
  * build_affine_bank.py:165-189). */
 int cachalot_requant_fp4_to_q2(const uint8_t* w_fp4, const uint8_t* s_fp4, int N, int K, uint32_t* q,
-                               uint16_t* scales, uint16_t* biases, cachalot_stream_t stream);
+                               uint16_t* scales, uint16_t* biases, int scale_dtype,
+                               cachalot_stream_t stream);
 
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32
  *   (replaces dequantize_fp4_weight / dequantize_fp4_dense,
  *    src/cachalot/model/fp4.py:67-109, fp4_dequant_metal.py:43-69);
  *   as_bf16 != 0 converts through the bf16 path the GEMV/GEMM kernels use.
- * 2-bit: w [N, row_words] u32, scales/biases [N, groups] bf16 -> out [N, K] fp32,
- *   value fl(fl(s*q)+b) (replaces mx.dequantize on the affine views,
+ * 2-bit: w [N, row_words] u32, scales/biases [N, groups] bf16 or fp16
+ *   (scale_dtype, CACHALOT_SCALE_*) -> out [N, K] fp32, value fl(fl(s*q)+b)
+ *   (replaces mx.dequantize on the affine views,
  *   src/cachalot/model/expert_affine.py:26-51). */
 int cachalot_dequant_fp4(const uint8_t* packed, const uint8_t* scales, int N, int K, int as_bf16,
                          float* out, cachalot_stream_t stream);
 int cachalot_dequant_q2(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                        int N, int K, int row_words, int groups, int group, float* out,
-                        cachalot_stream_t stream);
+                        int N, int K, int row_words, int groups, int group, int scale_dtype,
+                        float* out, cachalot_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,9 @@
   own ``tests/test_quant_affine.py:45-51`` against ``mx.quantize``);
 * dequantised value ``w = scale * q + bias`` per ``group``-element group along K
   (``benchmarks/quant_affine.py:11-15``), scales/biases stored bf16
-  (``benchmarks/build_affine_bank.py:76,165-174``);
+  (``benchmarks/build_affine_bank.py:76,165-174``) or fp16 (the oQ3e banks,
+  ``src/cachalot/model/expert_affine.py:1-10``; ``ExpertFormat.dtypes`` carries
+  which, ``storage/index.py:18,153``);
 * ``quantized_matmul(x, w, s, b, transpose=True)``: per group
   ``s * sum(x_i q_i) + b * sum(x_i)`` with fp32 accumulation
   (MLX ``qdot``, shown at ``src/cachalot/minimax/codes_qmv.py:86-100``).
@@ -46,25 +48,38 @@ def unpack_2bit(w, k: int | None = None) -> np.ndarray:
     return q if k is None else q[..., :k]
 
 
-def dequantize_affine(w, scales_bits, biases_bits, *, k: int, group: int = 128) -> np.ndarray:
-    """[N, K] fp32 with the declared rounding ``fl(fl(s * q) + b)`` (s, b exact from bf16)."""
+def scale_values(bits, dtype: str = "bfloat16") -> np.ndarray:
+    """Stored scale / bias bits -> exact fp32 values (bf16: the high half of an
+    fp32; fp16: IEEE half precision, subnormals included)."""
+    bits = np.asarray(bits, dtype=np.uint16)
+    if dtype == "bfloat16":
+        return bf16_bits_to_f32(bits)
+    if dtype == "float16":
+        return bits.view(np.float16).astype(np.float32)
+    raise ValueError(f"scale dtype {dtype!r}")
+
+
+def dequantize_affine(w, scales_bits, biases_bits, *, k: int, group: int = 128,
+                      scale_dtype: str = "bfloat16") -> np.ndarray:
+    """[N, K] fp32 with the declared rounding ``fl(fl(s * q) + b)`` (s, b exact from their storage type)."""
     q = unpack_2bit(w, k).astype(np.float32)
-    s = np.repeat(bf16_bits_to_f32(scales_bits), group, axis=-1)[..., :k]
-    b = np.repeat(bf16_bits_to_f32(biases_bits), group, axis=-1)[..., :k]
+    s = np.repeat(scale_values(scales_bits, scale_dtype), group, axis=-1)[..., :k]
+    b = np.repeat(scale_values(biases_bits, scale_dtype), group, axis=-1)[..., :k]
     return (s * q) + b
 
 
-def dequantize_affine64(w, scales_bits, biases_bits, *, k: int, group: int = 128) -> np.ndarray:
+def dequantize_affine64(w, scales_bits, biases_bits, *, k: int, group: int = 128,
+                        scale_dtype: str = "bfloat16") -> np.ndarray:
     q = unpack_2bit(w, k).astype(np.float64)
-    s = np.repeat(bf16_bits_to_f32(scales_bits).astype(np.float64), group, axis=-1)[..., :k]
-    b = np.repeat(bf16_bits_to_f32(biases_bits).astype(np.float64), group, axis=-1)[..., :k]
+    s = np.repeat(scale_values(scales_bits, scale_dtype).astype(np.float64), group, axis=-1)[..., :k]
+    b = np.repeat(scale_values(biases_bits, scale_dtype).astype(np.float64), group, axis=-1)[..., :k]
     return s * q + b
 
 
-def qmv64(x, w, scales_bits, biases_bits, *, k: int, group: int = 128) -> np.ndarray:
+def qmv64(x, w, scales_bits, biases_bits, *, k: int, group: int = 128, scale_dtype: str = "bfloat16") -> np.ndarray:
     """x [M, K] (bf16-exact values) -> float64 [M, N] = sum_g s_g*sum(x q) + b_g*sum(x).
 
-    s*q+b is exact in float64 for bf16 s, b and q in 0..3, so this equals
-    x @ dequant(W)^T evaluated in float64."""
+    s*q+b is exact in float64 for bf16 or fp16 s, b and q in 0..3, so this
+    equals x @ dequant(W)^T evaluated in float64."""
     x = np.asarray(x, dtype=np.float64)
-    return x @ dequantize_affine64(w, scales_bits, biases_bits, k=k, group=group).T
+    return x @ dequantize_affine64(w, scales_bits, biases_bits, k=k, group=group, scale_dtype=scale_dtype).T

@@ -15,8 +15,11 @@ the FP4 checkpoint dequantized to fp32 (``benchmarks/expert_requant_error.py:68-
   ``scale = max((new_hi - new_lo) / 3, 1e-8)``, ``bias = new_lo``; taken when its
   error is strictly below the best so far;
 * error: ``sum((scale * q + bias - w)^2)`` with ``q = clip(round_half_even((w - bias) / scale), 0, 3)``;
-* output: scale and bias rounded to bf16, codes recomputed against the rounded
-  pair, packed 16 per uint32, low field first.
+* output: scale and bias rounded to bf16 (the reference bank's type,
+  ``build_affine_bank.py:76``), or RNE to fp16 for an fp16 bank; codes
+  recomputed against the rounded pair (code 0 where an fp16 scale rounds to
+  zero: only a constant group, whose min/max scale is 1e-8, does), packed 16
+  per uint32, low field first.
 
 Two things the reference leaves open are fixed here and stated:
 * the error sum runs over the group's elements in index order (MLX's reduction
@@ -77,8 +80,9 @@ def fit_search(w, valid):
     return best_s, best_b
 
 
-def requantize(dense: np.ndarray, group: int = 128):
-    """dense float32 [N, K] -> (packed uint32 [N, Kp/16], scales bf16 bits [N, Kp/g], biases bf16 bits)."""
+def requantize(dense: np.ndarray, group: int = 128, scale_dtype: str = "bfloat16"):
+    """dense float32 [N, K] -> (packed uint32 [N, Kp/16], scale bits [N, Kp/g], bias bits), the bits
+    bf16 or fp16 (``scale_dtype``)."""
     n, k = dense.shape
     groups = -(-k // group)
     kp = groups * group
@@ -89,9 +93,14 @@ def requantize(dense: np.ndarray, group: int = 128):
     g = w.reshape(-1, group)
     v = valid.reshape(-1, group)
     s, b = fit_search(g, v)
-    sb = f32_to_bf16_bits(s)
-    bb = f32_to_bf16_bits(b)
-    s16 = bf16_bits_to_f32(sb)
-    b16 = bf16_bits_to_f32(bb)
-    q = np.where(v, _q(g, s16, b16), F32(0)).astype(np.uint8)
+    if scale_dtype == "bfloat16":
+        sb, bb = f32_to_bf16_bits(s), f32_to_bf16_bits(b)
+        s16, b16 = bf16_bits_to_f32(sb), bf16_bits_to_f32(bb)
+    elif scale_dtype == "float16":
+        sb, bb = s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+        s16, b16 = sb.view(np.float16).astype(F32), bb.view(np.float16).astype(F32)
+    else:
+        raise ValueError(f"scale dtype {scale_dtype!r}")
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(v & (s16 != 0), _q(g, s16, b16), F32(0)).astype(np.uint8)
     return pack_2bit(q.reshape(n, kp)), sb.reshape(n, groups), bb.reshape(n, groups)

@@ -38,6 +38,8 @@ KIND_E8M0 = 1
 KIND_BF16_UNIFORM = 2
 KIND_BF16_NORMAL = 3
 KIND_F32_NORMAL = 4
+KIND_F16_UNIFORM = 5
+KIND_F16_NORMAL = 6
 
 IRWIN_HALL_STD = math.sqrt((65536.0 ** 2 - 1.0) / 3.0)
 
@@ -105,6 +107,11 @@ def fill(kind: int, n: int, key: int, p0: float = 0.0, p1: float = 0.0,
         return f32_to_bf16_bits(_normal_f64(r, p0).astype(np.float32))
     if kind == KIND_F32_NORMAL:
         return _normal_f64(r, p0).astype(np.float32)
+    if kind == KIND_F16_UNIFORM:     # fp64 -> fp32 -> fp16 (RNE), as the GPU fill
+        t = (r >> np.uint64(40)).astype(np.float64) * (2.0 ** -24)
+        return (p0 + p1 * t).astype(np.float32).astype(np.float16).view(np.uint16)
+    if kind == KIND_F16_NORMAL:
+        return _normal_f64(r, p0).astype(np.float32).astype(np.float16).view(np.uint16)
     raise ValueError(f"unknown kind {kind}")
 
 
@@ -122,8 +129,10 @@ def fp4_tensor_specs(d_model: int, d_ff: int, e8m0_lo: int = 119, e8m0_hi: int =
 
 
 def q2_tensor_specs(d_model: int, d_ff: int, group: int = 128,
-                    scale_lo: float = 0.005, scale_hi: float = 0.05, bias_sigma: float = 0.02):
-    """2-bit affine expert (MLX layout): weight [N, Kp/16] u32, scales/biases [N, Kp/g] bf16.
+                    scale_lo: float = 0.005, scale_hi: float = 0.05, bias_sigma: float = 0.02,
+                    scale_dtype: str = "bfloat16"):
+    """2-bit affine expert (MLX layout): weight [N, Kp/16] u32, scales/biases [N, Kp/g] bf16
+    (or fp16 with ``scale_dtype="float16"``, BASELINE config 1's "fp16 scale and bias").
 
     Kp is K rounded up to a whole group; codes past K are zero."""
     specs = []
@@ -134,9 +143,11 @@ def q2_tensor_specs(d_model: int, d_ff: int, group: int = 128,
         row_valid = k // 16 if kp != k else 0
         specs.append((f"{proj}.weight", (n, row_total), np.uint32, KIND_U32, 0.0, 0.0,
                       row_total if row_valid else 0, row_valid))
-        specs.append((f"{proj}.scales", (n, groups), np.uint16, KIND_BF16_UNIFORM,
+        f16 = scale_dtype == "float16"
+        specs.append((f"{proj}.scales", (n, groups), np.uint16, KIND_F16_UNIFORM if f16 else KIND_BF16_UNIFORM,
                       float(scale_lo), float(scale_hi) - float(scale_lo), 0, 0))
-        specs.append((f"{proj}.biases", (n, groups), np.uint16, KIND_BF16_NORMAL, float(bias_sigma), 0.0, 0, 0))
+        specs.append((f"{proj}.biases", (n, groups), np.uint16, KIND_F16_NORMAL if f16 else KIND_BF16_NORMAL,
+                      float(bias_sigma), 0.0, 0, 0))
     return specs
 
 

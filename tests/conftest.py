@@ -31,13 +31,12 @@ def cuda():
     return torch.device("cuda:0")
 
 
-@pytest.fixture(params=["two_kernel_mx", "two_kernel_bf16", "one_launch"])
+@pytest.fixture(params=["two_kernel_mx", "two_kernel_bf16"])
 def q2_path(request, monkeypatch):
     """The 2-bit decode runs as two kernels on the block-scaled fp8 x fp4 matrix
-    cores by default; the bf16-MFMA kernel pair is selected with
-    CACHALOT_DECODE_BF16=1 and the one-launch persistent kernel with
-    CACHALOT_DECODE_FUSED=1.  All three are pinned."""
-    monkeypatch.setenv("CACHALOT_DECODE_FUSED", "1" if request.param == "one_launch" else "0")
+    cores by default; the bf16-MFMA kernel pair (the path for shapes outside the
+    matrix-core kernels' envelope) is selected with CACHALOT_DECODE_BF16=1.  Both
+    are pinned."""
     monkeypatch.setenv("CACHALOT_DECODE_BF16", "1" if request.param == "two_kernel_bf16" else "0")
     return request.param
 

@@ -32,17 +32,19 @@ def oracle_tensors(fmt, layer, expert, seed=SEED):
     if fmt.kind == "fp4":
         specs = osynth.fp4_tensor_specs(fmt.d_model, fmt.d_ff)
     else:
-        specs = osynth.q2_tensor_specs(fmt.d_model, fmt.d_ff, fmt.group_size)
+        specs = osynth.q2_tensor_specs(fmt.d_model, fmt.d_ff, fmt.group_size,
+                                       scale_dtype=fmt.dtypes.get("w1.scales", "bfloat16"))
     return osynth.expert_tensors(seed, layer, expert, specs)
 
 
 def q2_mats(fmt, tensors):
     """(mm1, mm3, mm2): float64 products with W1^T, W3^T, W2^T of one 2-bit expert."""
     g = fmt.group_size
+    sd = fmt.dtypes.get("w1.scales", "bfloat16")
 
     def mm(proj, k):
         w, s, b = tensors[f"{proj}.weight"], tensors[f"{proj}.scales"], tensors[f"{proj}.biases"]
-        return lambda x: qmv64(x, w, s, b, k=k, group=g)
+        return lambda x: qmv64(x, w, s, b, k=k, group=g, scale_dtype=sd)
 
     return mm("w1", fmt.d_model), mm("w3", fmt.d_model), mm("w2", fmt.d_ff)
 

@@ -63,7 +63,7 @@ def test_dequant_golden(cuda):
     ds = torch.from_numpy(g["scales"].view(np.int16)).to(cuda)
     db = torch.from_numpy(g["biases"].view(np.int16)).to(cuda)
     _lib.check(_lib.lib().cachalot_dequant_q2(dw.data_ptr(), ds.data_ptr(), db.data_ptr(), n, k, row_words,
-                                              g["scales"].shape[1], 128, out.data_ptr(), _lib.stream_handle(cuda)))
+                                              g["scales"].shape[1], 128, 0, out.data_ptr(), _lib.stream_handle(cuda)))
     assert np.array_equal(_np(out).view(np.uint32), g["dense"].view(np.uint32))
 
 

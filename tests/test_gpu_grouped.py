@@ -114,13 +114,17 @@ def test_permute_errors(cuda):
     assert "E=2000" in _lib.last_error()
 
 
-@pytest.mark.parametrize("kind", ["affine", "fp4"])
+@pytest.mark.parametrize("kind", ["affine", "fp4", "affine_f16"])
 def test_grouped_experts_prefill_tiles(cuda, kind, prefill_path):
-    """64-row tiles (T*k >= 4E): an expert with more rows than one tile, ragged tails."""
+    """64-row tiles (T*k >= 4E): an expert with more rows than one tile, ragged tails
+    (2-bit banks with bf16 and with fp16 scales / biases)."""
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format, fp4_format
 
-    fmt = affine_format(4096, 2880) if kind == "affine" else fp4_format(4096, 2880)
+    if kind == "affine_f16" and prefill_path != "mx":
+        pytest.skip("the prefill path switch selects FP4 kernels only")
+    fmt = (fp4_format(4096, 2880) if kind == "fp4" else
+           affine_format(4096, 2880, scale_dtype="float16" if kind == "affine_f16" else "bfloat16"))
     E = 8
     store = make_store(fmt, n_layers=1, n_experts=E)
     rng = np.random.default_rng(11)
@@ -139,13 +143,14 @@ def test_grouped_experts_prefill_tiles(cuda, kind, prefill_path):
                   + bf16_ulp(want))
 
 
-@pytest.mark.parametrize("kind", ["affine", "fp4"])
+@pytest.mark.parametrize("kind", ["affine", "fp4", "affine_f16"])
 def test_grouped_experts_batched_decode(cuda, kind):
     """16-row tiles (few rows per expert, BASELINE config 2 shape), a missing expert, an addend."""
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format, fp4_format
 
-    fmt = affine_format(4096, 2880) if kind == "affine" else fp4_format(4096, 2880)
+    fmt = (fp4_format(4096, 2880) if kind == "fp4" else
+           affine_format(4096, 2880, scale_dtype="float16" if kind == "affine_f16" else "bfloat16"))
     rng = np.random.default_rng(12)
     t, k = 4, 6
     experts = [3, 17, 100, 101, 250, 383, 42, 7]

@@ -45,7 +45,9 @@ def test_fill_matches_oracle_every_kind(cuda):
              (synth.KIND_E8M0, torch.uint8, 777, 119.0, 127.0, 0, 0),
              (synth.KIND_BF16_UNIFORM, torch.int16, 1001, 0.005, 0.045, 0, 0),
              (synth.KIND_BF16_NORMAL, torch.int16, 1003, 0.02, 0.0, 0, 0),
-             (synth.KIND_F32_NORMAL, torch.float32, 1005, 1.0, 0.0, 0, 0)]
+             (synth.KIND_F32_NORMAL, torch.float32, 1005, 1.0, 0.0, 0, 0),
+             (synth.KIND_F16_UNIFORM, torch.int16, 1007, 0.005, 0.045, 0, 0),
+             (synth.KIND_F16_NORMAL, torch.int16, 1009, 0.02, 0.0, 0, 0)]
     for kind, dt, n, p0, p1, rt, rv in cases:
         for start in (0, 12345):
             t = torch.empty(n, dtype=dt, device=cuda)
@@ -55,11 +57,12 @@ def test_fill_matches_oracle_every_kind(cuda):
             assert np.array_equal(got.view(want.dtype), want), (kind, start)
 
 
-@pytest.mark.parametrize("kind", ["affine", "fp4"])
+@pytest.mark.parametrize("kind", ["affine", "fp4", "affine_f16"])
 def test_whole_expert_bytes_match_oracle(cuda, kind):
     from cachalot_amd.storage.index import affine_format, fp4_format
 
-    fmt = affine_format(4096, 2880) if kind == "affine" else fp4_format(4096, 2880)
+    fmt = (fp4_format(4096, 2880) if kind == "fp4" else
+           affine_format(4096, 2880, scale_dtype="float16" if kind == "affine_f16" else "bfloat16"))
     store = make_store(fmt, n_layers=2, n_experts=4, keys=[(1, 3)])
     slot = store.pool.slot(store.layer_table(1)[3].item())
     want = oracle_tensors(fmt, 1, 3)
@@ -100,11 +103,12 @@ def test_dequant_fp4_special_scales(cuda):
         assert np.array_equal(_np(out), dequantize_fp4_weight(packed, scales)), as_bf16
 
 
-def test_dequant_q2_bit_exact(cuda):
+@pytest.mark.parametrize("scale_dtype", ["bfloat16", "float16"])
+def test_dequant_q2_bit_exact(cuda, scale_dtype):
     from cachalot_amd import _lib
     from cachalot_amd.storage.index import affine_format
 
-    fmt = affine_format(4096, 2880)
+    fmt = affine_format(4096, 2880, scale_dtype=scale_dtype)
     t = oracle_tensors(fmt, 0, 9)
     for proj, k in (("w1", 4096), ("w2", 2880)):
         w, s, b = t[f"{proj}.weight"], t[f"{proj}.scales"], t[f"{proj}.biases"]
@@ -115,8 +119,9 @@ def test_dequant_q2_bit_exact(cuda):
         db = torch.from_numpy(b.view(np.int16)).to(cuda)
         out = torch.empty((n, k), dtype=torch.float32, device=cuda)
         _lib.check(_lib.lib().cachalot_dequant_q2(dw.data_ptr(), dsc.data_ptr(), db.data_ptr(), n, k, row_words,
-                                                  groups, 128, out.data_ptr(), _lib.stream_handle(cuda)))
-        want = dequantize_affine(w, s, b, k=k, group=128)
+                                                  groups, 128, _lib.scale_dtype_code(scale_dtype),
+                                                  out.data_ptr(), _lib.stream_handle(cuda)))
+        want = dequantize_affine(w, s, b, k=k, group=128, scale_dtype=scale_dtype)
         assert np.array_equal(_np(out).view(np.uint32), want.view(np.uint32)), proj
 
 

@@ -23,23 +23,24 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-def _check_matrix(cuda, w, s):
+def _check_matrix(cuda, w, s, scale_dtype="bfloat16"):
     from cachalot_amd.requant import requantize_fp4_matrix
 
     k = w.shape[1] * 2
-    q, sc, bi = requantize_fp4_matrix(torch.from_numpy(w).to(cuda), torch.from_numpy(s).to(cuda), k)
-    wq, ws, wb = orq.requantize(dequantize_fp4_weight(w, s).astype(np.float32))
+    q, sc, bi = requantize_fp4_matrix(torch.from_numpy(w).to(cuda), torch.from_numpy(s).to(cuda), k,
+                                      scale_dtype=scale_dtype)
+    wq, ws, wb = orq.requantize(dequantize_fp4_weight(w, s).astype(np.float32), scale_dtype=scale_dtype)
     assert np.array_equal(_np(q).view(np.uint32), wq)
     assert np.array_equal(_np(sc).view(np.uint16), ws)
     assert np.array_equal(_np(bi).view(np.uint16), wb)
 
 
-@pytest.mark.parametrize("proj", ["w1", "w2"])
-def test_requant_matrix_bit_exact_synthetic(cuda, proj):
+@pytest.mark.parametrize("proj,scale_dtype", [("w1", "bfloat16"), ("w2", "bfloat16"), ("w2", "float16")])
+def test_requant_matrix_bit_exact_synthetic(cuda, proj, scale_dtype):
     fmt = I.fp4_format(1024, 2880)                   # w2: K = 2880, a partial last group
     t = oracle_tensors(fmt, 0, 3)
     rows = 640 if proj == "w1" else 512
-    _check_matrix(cuda, t[f"{proj}.weight"][:rows], t[f"{proj}.scale"][:rows])
+    _check_matrix(cuda, t[f"{proj}.weight"][:rows], t[f"{proj}.scale"][:rows], scale_dtype)
 
 
 def test_requant_matrix_bit_exact_gaussian(cuda):
@@ -56,6 +57,9 @@ def test_requant_matrix_bit_exact_gaussian(cuda):
     w = (code[:, 0::2] | (code[:, 1::2] << 4)).astype(np.uint8)
     s = (e + 127).astype(np.uint8)
     _check_matrix(cuda, w, s)
+    _check_matrix(cuda, w, s, "float16")
+    w[:4] = 0                                        # constant groups: the fp16 scale rounds to zero, codes 0
+    _check_matrix(cuda, w, s, "float16")
 
 
 def test_requantize_store_and_bank_file(cuda, tmp_path):

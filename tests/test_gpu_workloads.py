@@ -104,16 +104,19 @@ def _check_decode(what, fmt, layer, xf, idx, w, routed, out, terms, addend=None)
     return st
 
 
-@pytest.mark.parametrize("shape", [(4096, 2880), (5120, 2304)])
-def test_decode_q2_terms_exact_up_to_flips(cuda, shape, q2_path):
+@pytest.mark.parametrize("shape,scale_dtype", [((4096, 2880), "bfloat16"), ((5120, 2304), "bfloat16"),
+                                               ((4096, 2880), "float16")])
+def test_decode_q2_terms_exact_up_to_flips(cuda, shape, scale_dtype, q2_path):
     """Config 1 decode: the k-expert call's routed vector is the route-order fp32
     sum of its own per-expert terms (bit for bit), every term is the oracle's
-    bf16 cast up to counted boundary flips, and out = bf16(routed + addend)."""
+    bf16 cast up to counted boundary flips, and out = bf16(routed + addend).
+    Config 1 as BASELINE states it ("fp16 scale and bias") is the float16 case;
+    the reference's own bank stores bf16."""
     from cachalot_amd.moe_decode import decode_experts
     from cachalot_amd.storage.index import affine_format
 
     D, F = shape
-    fmt = affine_format(D, F)
+    fmt = affine_format(D, F, scale_dtype=scale_dtype)
     rng = np.random.default_rng(21)
     toks = [(rng.choice(384, size=6, replace=False).tolist(), rng.dirichlet(np.ones(6)).astype(np.float32))
             for _ in range(3)]
@@ -127,7 +130,7 @@ def test_decode_q2_terms_exact_up_to_flips(cuda, shape, q2_path):
                                                                                        device=cuda),
                                      torch.tensor(w, device=cuda), addend=a)
         terms = _decode_terms(cuda, store, 0, x, idx, w)
-        _check_decode(f"decode {q2_path} {D}x{F} token {t}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed),
+        _check_decode(f"decode {q2_path} {D}x{F} {scale_dtype} token {t}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed),
                       _f32(out), terms, bf16_bits_to_f32(ab))
 
 

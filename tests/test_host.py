@@ -242,3 +242,17 @@ def test_prediction_entries_strongest_first():
     assert [(e.layer, e.expert) for e in got] == [(3, 5), (3, 9), (3, 2), (4, 7), (4, 1), (4, 8)]
     index = {(3, 5): ExpertEntry(3, 5), (3, 2): ExpertEntry(3, 2)}
     assert [(e.layer, e.expert) for e in prediction_entries(pred[:1], index, "ascending")] == [(3, 2), (3, 5)]
+
+
+def test_layout_carries_the_scale_dtype():
+    """The record descriptor tells the kernels how a 2-bit bank stores its scales;
+    FP4 banks (E8M0 scales) send 0; other storage types are refused."""
+    from cachalot_amd import _lib
+    from cachalot_amd.cache.slots import HBMSlotPool
+    from cachalot_amd.storage.index import affine_format, fp4_format
+
+    for fmt, code in ((affine_format(256, 128), 0), (affine_format(256, 128, scale_dtype="float16"), 1),
+                      (fp4_format(256, 128), 0)):
+        assert HBMSlotPool(fmt, 1, device="cpu").layout().scale_dtype == code
+    with pytest.raises(ValueError, match="bfloat16 or float16"):
+        _lib.scale_dtype_code("float32")

@@ -122,3 +122,66 @@ def test_round_bf16_matches_torch():
     want = torch.from_numpy(vals).to(torch.bfloat16).float().numpy()
     got = round_bf16(vals)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_fp16_scale_values_known_bits():
+    """fp16 scale / bias storage (the oQ3e banks): IEEE half bits,
+    subnormals included; bf16 bits are the high half of an fp32."""
+    from oracle.affine2 import scale_values
+
+    got = scale_values(np.array([0x3C00, 0xC000, 0x0001, 0x3555, 0x7BFF], np.uint16), "float16")
+    assert got.tolist() == [1.0, -2.0, 2.0 ** -24, 0.333251953125, 65504.0]
+    assert scale_values(np.array([0x3F80, 0xBF00], np.uint16)).tolist() == [1.0, -0.5]
+    with pytest.raises(ValueError):
+        scale_values(np.array([0], np.uint16), "float32")
+
+
+def test_dequantize_affine_fp16_known_words():
+    from oracle.affine2 import dequantize_affine, pack_2bit
+
+    q = np.tile(np.arange(4, dtype=np.uint8), 4)[None, :]          # 0 1 2 3 0 1 2 3 ...
+    w = pack_2bit(q)
+    s = np.array([[0x3800]], np.uint16)                              # 0.5
+    b = np.array([[0xBC00]], np.uint16)                              # -1.0
+    got = dequantize_affine(w, s, b, k=16, group=16, scale_dtype="float16")
+    assert got[0, :4].tolist() == [-1.0, -0.5, 0.0, 0.5]
+
+
+def test_requant_fp16_rounds_the_same_fit():
+    """The fp16 bank's (scale, bias) are the RNE-to-fp16 of the searched fit the bf16
+    bank rounds to bf16; codes follow the rounded pair; a constant group's fp16 scale
+    rounds to zero and its codes are 0 (its bias then equals the constant)."""
+    from oracle import requant as orq
+    from oracle.affine2 import dequantize_affine
+
+    rng = np.random.default_rng(3)
+    dense = (rng.standard_normal((6, 256)) * 0.05).astype(np.float32)
+    dense[5, 128:] = 0.25                                             # one constant group
+    g = dense.reshape(-1, 128)
+    s, b = orq.fit_search(g, np.ones_like(g, bool))
+    q16, s16, b16 = orq.requantize(dense, scale_dtype="float16")
+    assert np.array_equal(s16.reshape(-1), s.reshape(-1).astype(np.float16).view(np.uint16))
+    assert np.array_equal(b16.reshape(-1), b.reshape(-1).astype(np.float16).view(np.uint16))
+    assert s16.reshape(-1)[-1] == 0 and not (q16.reshape(6, -1)[5, 8:]).any()
+    back = dequantize_affine(q16, s16, b16, k=256, group=128, scale_dtype="float16")
+    assert np.array_equal(back[5, 128:], dense[5, 128:])
+    # fp16 keeps 3 more significand bits than bf16: the fit's error is no larger on average
+    qb, sb, bb = orq.requantize(dense)
+    err16 = np.abs(back - dense).mean()
+    errb = np.abs(dequantize_affine(qb, sb, bb, k=256, group=128) - dense).mean()
+    assert err16 <= errb * 1.01
+
+
+def test_fp16_synthetic_kinds_follow_the_bf16_stream():
+    """The fp16 fill kinds draw the same fp32 values as the bf16 kinds and round them
+    to half precision: each pair lies within one bf16 step of each other."""
+    from oracle import synth as osynth
+    from oracle.affine2 import scale_values
+
+    key = osynth.stream_key(5, 1, 2, 3)
+    for kb, kf, p0, p1 in ((osynth.KIND_BF16_UNIFORM, osynth.KIND_F16_UNIFORM, 0.005, 0.045),
+                           (osynth.KIND_BF16_NORMAL, osynth.KIND_F16_NORMAL, 0.02, 0.0)):
+        vb = scale_values(osynth.fill(kb, 4000, key, p0, p1))
+        vf = scale_values(osynth.fill(kf, 4000, key, p0, p1), "float16")
+        assert np.all(np.abs(vb - vf) <= np.abs(vb) * 2.0 ** -8 + 2.0 ** -24)
+        assert not np.array_equal(vb, vf)
