@@ -348,11 +348,13 @@ def test_moe_layer_forward_end_to_end(cuda, q2_path):
         assert bf16_terms_ok(bf16_bits_to_f32(_bf16_np(out)), want, np.concatenate([ys, want[None]]), TOL)
 
 
-@pytest.mark.parametrize("kind", ["affine", "fp4"])
-def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind, q2_path):
+@pytest.mark.parametrize("kind,score", [("affine", "sqrt_softplus"), ("fp4", "sqrt_softplus"), ("fp4", "sigmoid")])
+def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind, score, q2_path):
     """Device-routed decode (scores -> top-k in the gate/up prologue -> down with the
     counter-based combine): ids bit-exact, outputs within the bar, and repeated calls
-    on one workspace (counters reset by the kernels) give identical results."""
+    on one workspace (counters reset by the kernels) give identical results.  The
+    FP4 / sigmoid case is config 0 as BASELINE states it (sigmoid scores, top-6
+    renormalised, route scale 1)."""
     from cachalot_amd import synth
     from cachalot_amd.moe_decode import moe_layer_decode
     from cachalot_amd.storage.index import affine_format, fp4_format
@@ -360,13 +362,16 @@ def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind, q2_path):
     fmt = affine_format(4096, 2880) if kind == "affine" else fp4_format(4096, 2880)
     store = make_store(fmt, n_layers=1, n_experts=384)
     w, b = synth.router_weights(SEED, 0, 384, 4096, cuda)
+    rs = 1.5 if score == "sqrt_softplus" else 1.0
+    sfn = orouter.SCORE_SQRT_SOFTPLUS if score == "sqrt_softplus" else orouter.SCORE_SIGMOID
     first = None
     for t in range(3):
         x = synth.activations(SEED, 60 + t, 1, 4096, cuda)[0]
-        routed, out, route = moe_layer_decode(x, w, b, store.pool, store.layer_table(0), topk=6, route_scale=1.5,
-                                              score_fn="sqrt_softplus", addend=x, want_routed=True)
+        routed, out, route = moe_layer_decode(x, w, b, store.pool, store.layer_table(0), topk=6, route_scale=rs,
+                                              score_fn=score, addend=x, want_routed=True)
         xf = bf16_bits_to_f32(_bf16_np(x))
-        oi, ow, osc = orouter.route(xf[None], bf16_bits_to_f32(_bf16_np(w)), _np(b), topk=6, route_scale=1.5)
+        oi, ow, osc = orouter.route(xf[None], bf16_bits_to_f32(_bf16_np(w)), _np(b), topk=6, route_scale=rs,
+                                    score=sfn)
         assert np.array_equal(_np(route.indices), oi[0])
         assert np.array_equal(_np(route.weights).view(np.uint32), ow[0].view(np.uint32))
         assert np.array_equal(_np(route.scores).view(np.uint32), osc[0].view(np.uint32))
@@ -384,8 +389,8 @@ def test_layer_decode_fused_routing_and_repeat_calls(cuda, kind, q2_path):
             first = (x, routed.clone(), out.clone())
     x0, r0, o0 = first
     for _ in range(3):
-        r, o, _ = moe_layer_decode(x0, w, b, store.pool, store.layer_table(0), topk=6, route_scale=1.5, addend=x0,
-                                   want_routed=True)
+        r, o, _ = moe_layer_decode(x0, w, b, store.pool, store.layer_table(0), topk=6, route_scale=rs, addend=x0,
+                                   score_fn=score, want_routed=True)
         assert torch.equal(r, r0) and torch.equal(o, o0)
 
 

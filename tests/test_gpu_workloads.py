@@ -302,6 +302,91 @@ def test_config3_prefill_workload(cuda, prefill_path):
            experts_touched=int((counts > 0).sum()))
 
 
+@pytest.mark.parametrize("B", [16, 32])
+def test_config2_batched_decode_router_union(cuda, B):
+    """Config 2 itself: B tokens through the seeded router over 384 experts (the
+    union of their routes, ~85 / ~150 experts, about 1.3-1.6 rows each), then the
+    grouped 2-bit decode over that union.  Ids and weights bit-exact for every
+    token; every route of 8 sampled experts against the oracle term by term; the
+    combine of all B tokens bit for bit over the GPU's terms."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.router import route_topk_rows
+    from cachalot_amd.storage.index import affine_format
+
+    D, F, E, K = 4096, 2880, 384, 6
+    fmt = affine_format(D, F)
+    store = make_store(fmt, n_layers=1, n_experts=E)
+    w, b = synth.router_weights(SEED, 0, E, D, cuda)
+    x = synth.activations(SEED, 2000 + B, B, D, cuda)
+    a = synth.activations(SEED, 2100 + B, B, D, cuda)
+    idx, wt, _ = route_topk_rows(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+    xf = _f32(x)
+    oi, ow, _ = orouter.route(xf, _f32(w), _np(b), topk=K, route_scale=1.0, score=orouter.SCORE_SIGMOID)
+    assert np.array_equal(_np(idx), oi) and np.array_equal(_np(wt).view(np.uint32), ow.view(np.uint32))
+    union = np.unique(oi)
+    assert len(union) > 3 * B // 2, len(union)
+    routed, out, y = grouped_experts(x, idx, wt, store.pool, store.layer_table(0), addend=a, want_routed=True,
+                                     want_terms=True)
+    rng = np.random.default_rng(B)
+    sample = rng.choice(union, size=8, replace=False)
+    _grouped_check(f"config2 B={B} union {len(union)}", fmt, 0, xf, oi, ow, _np(routed), _f32(out), _f32(y), E,
+                   rows_of={int(e): slice(None) for e in sample}, addend=_f32(a))
+
+
+def test_config4_full_residency_chain(cuda):
+    """Config 4 at full residency: 40 x 384 2-bit experts (154 GB) in HBM, one
+    token through all 40 layers (device routing, residual as the addend).  Ids
+    bit-exact at every layer against the oracle router fed the GPU's own input;
+    two sampled layers' outputs term by term; a captured 40-layer graph replays
+    identically to the eager chain, three times, with eager work between."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_decode import moe_layer_decode
+    from cachalot_amd.storage.index import affine_format
+
+    L, E = 40, 384
+    fmt = affine_format(4096, 2880)
+    store = make_store(fmt, n_layers=L, n_experts=E)
+    table = store.track_slots()
+    gates = [synth.router_weights(SEED, la, E, 4096, cuda) for la in range(L)]
+    x0 = synth.activations(SEED, 4040, 1, 4096, cuda)[0]
+
+    def chain(x, record=None):
+        for la in range(L):
+            w, bias = gates[la]
+            routed, out, route = moe_layer_decode(x, w, bias, store.pool, table[la], topk=6, route_scale=1.0,
+                                                  score_fn="sigmoid", addend=x, want_routed=True)
+            if record is not None:
+                record.append((x, routed, out, route))
+            x = out
+        return x
+
+    steps = []
+    eager = chain(x0, steps)
+    torch.cuda.synchronize()
+    for la, (x, routed, out, route) in enumerate(steps):
+        w, bias = gates[la]
+        xf = _f32(x)
+        oi, ow, _ = orouter.route(xf[None], _f32(w), _np(bias), topk=6, route_scale=1.0, score=orouter.SCORE_SIGMOID)
+        assert np.array_equal(_np(route.indices), oi[0]), la
+        assert np.array_equal(_np(route.weights).view(np.uint32), ow[0].view(np.uint32)), la
+        if la in (0, 39):
+            terms = _decode_terms(cuda, store, la, x, oi[0], ow[0])
+            _check_decode(f"config4 full residency layer {la}", fmt, la, xf, oi[0], ow[0], _np(routed), _f32(out),
+                          terms, xf)
+    xbuf = x0.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = chain(xbuf)
+    for _ in range(3):
+        xbuf.copy_(x0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        _ = chain(x0)
+        torch.cuda.synchronize()
+
+
 # ------------------------------------------------------- partial residency ---
 def _partial_layer(cuda, resident_of):
     """A 2-bit layer whose store holds only some experts (loader for misses), its router,
