@@ -129,6 +129,22 @@ _SIGNATURES = {
     "cachalot_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
     "cachalot_requant_fp4_to_q2": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
                                            c_void_p]),
+    "cachalot_moe_decode_affine_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "cachalot_moe_decode_affine": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
+                                           c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p,
+                                           c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "cachalot_moe_layer_decode_affine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float,
+                                                 c_float, c_int, c_int, c_void_p, ctypes.POINTER(ExpertLayout),
+                                                 c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                                 c_void_p]),
+    "cachalot_grouped_experts_affine_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "cachalot_grouped_experts_affine": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p,
+                                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                                c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_size_t,
+                                                c_void_p]),
+    "cachalot_dequant_affine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                        c_int, c_void_p, c_void_p]),
     "cachalot_dequant_fp4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
     "cachalot_dequant_q2": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                     c_void_p, c_void_p]),

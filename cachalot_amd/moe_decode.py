@@ -21,6 +21,12 @@ from .storage.index import ExpertFormat
 _WORKSPACES: dict[tuple, torch.Tensor] = {}
 
 
+def is_q2_g128(fmt: ExpertFormat) -> bool:
+    """The 2-bit g128 bank, which has matrix-core kernels; other affine widths (3 / 4 bits,
+    groups of 32 / 64) take the generic affine kernels (csrc/affine.hip)."""
+    return fmt.kind == "affine" and fmt.bits == 2 and fmt.group_size == 128
+
+
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """The decode scratch workspace, cached per device (grown on demand).
 
@@ -71,7 +77,15 @@ def decode_experts(x: torch.Tensor, pool: HBMSlotPool, slot_table: torch.Tensor,
     layout = pool.layout()
     stream = _lib.stream_handle(dev)
     e = int(slot_table.numel())
-    if fmt.kind == "affine":
+    if fmt.kind == "affine" and not is_q2_g128(fmt):
+        nbytes = L.cachalot_moe_decode_affine_workspace_bytes(d, f, k)
+        ws = workspace(dev, nbytes)
+        rc = L.cachalot_moe_decode_affine(x.data_ptr(), pool.storage.data_ptr(), layout, slot_table.data_ptr(),
+                                          idx.data_ptr(), weights.data_ptr(), d, f, e, k, fmt.bits, fmt.group_size,
+                                          float(swiglu_limit), _lib.ptr(addend), _lib.ptr(routed), _lib.ptr(out),
+                                          ws.data_ptr(), nbytes, stream)
+        _lib.check(rc, "moe_decode_affine")
+    elif fmt.kind == "affine":
         nbytes = L.cachalot_moe_decode_q2_workspace_bytes(d, f, k)
         ws = workspace(dev, nbytes)
         rc = L.cachalot_moe_decode_q2(x.data_ptr(), pool.storage.data_ptr(), layout, slot_table.data_ptr(),
@@ -139,6 +153,16 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
                   slot_table.data_ptr(), d, f)
     tail = (_lib.ptr(addend), idx.data_ptr(), w.data_ptr(), scores.data_ptr(), _lib.ptr(routed), _lib.ptr(out))
     stream = _lib.stream_handle(dev)
+    if shared is not None and fmt.kind == "affine" and not is_q2_g128(fmt):
+        # the generic affine kernels carry no shared tiles: the shared expert runs first
+        # and enters as the addend (the same out = bf16(routed + y_sh))
+        from .shared_expert import shared_expert_forward
+
+        if addend is not None:
+            raise ValueError("pass either the shared expert weights or addend, not both")
+        addend = shared_expert_forward(x, **shared, swiglu_limit=swiglu_limit)
+        tail = (_lib.ptr(addend),) + tail[1:]
+        shared = None
     if shared is not None:
         if fmt.kind not in ("affine", "fp4"):
             raise ValueError(f"unknown expert format {fmt.kind!r}")
@@ -161,6 +185,11 @@ def moe_layer_decode(x: torch.Tensor, gate_weight: torch.Tensor, gate_bias: torc
             ws = workspace(dev, nbytes)
             rc = L.cachalot_moe_layer_decode_fp4_shared(*args_route, float(swiglu_limit), *ptrs, sw[6], *tail[1:],
                                                         ws.data_ptr(), nbytes, stream)
+    elif fmt.kind == "affine" and not is_q2_g128(fmt):
+        nbytes = L.cachalot_moe_decode_affine_workspace_bytes(d, f, topk)
+        ws = workspace(dev, nbytes)
+        rc = L.cachalot_moe_layer_decode_affine(*args_route, fmt.bits, fmt.group_size, float(swiglu_limit), *tail,
+                                                ws.data_ptr(), nbytes, stream)
     elif fmt.kind == "affine":
         nbytes = L.cachalot_moe_decode_q2_workspace_bytes(d, f, topk)
         ws = workspace(dev, nbytes)

@@ -97,9 +97,21 @@ def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tenso
     L = _lib.lib()
     stream = _lib.stream_handle(dev)
     y = torch.empty((t, k, d), dtype=torch.bfloat16, device=dev)
-    nbytes = L.cachalot_grouped_experts_workspace_bytes(t, k, n_experts, d, f)
+    generic = fmt.kind == "affine" and not (fmt.bits == 2 and fmt.group_size == 128)
+    if generic:
+        nbytes = L.cachalot_grouped_experts_affine_workspace_bytes(t, k, n_experts, f)
+    else:
+        nbytes = L.cachalot_grouped_experts_workspace_bytes(t, k, n_experts, d, f)
     ws = _workspace(dev, nbytes)
-    if fmt.kind == "affine":
+    if generic:
+        # 3- / 4-bit codes or groups of 32 / 64: the generic affine kernels (csrc/affine.hip)
+        offsets, row_token, row_slot, row_w = permute(indices, weights, n_experts)
+        rc = L.cachalot_grouped_experts_affine(x.data_ptr(), pool.storage.data_ptr(), pool.layout(),
+                                               slot_table.data_ptr(), offsets.data_ptr(), row_token.data_ptr(),
+                                               row_slot.data_ptr(), row_w.data_ptr(), t, d, f, n_experts, k, fmt.bits,
+                                               fmt.group_size, float(swiglu_limit), y.data_ptr(), ws.data_ptr(),
+                                               nbytes, stream)
+    elif fmt.kind == "affine":
         # the routes go in as they are: a batched decode permutes them inside its prep launch
         if indices.ndim != 2 or tuple(weights.shape) != tuple(indices.shape):
             raise ValueError(f"indices {tuple(indices.shape)} / weights {tuple(weights.shape)} must be [T, k]")

@@ -109,9 +109,12 @@ def fp4_format(d_model: int, d_ff: int) -> ExpertFormat:
 
 def affine_format(d_model: int, d_ff: int, *, bits: int = 2, group_size: int = 128,
                   scale_dtype: str = "bfloat16") -> ExpertFormat:
-    """Stacked-affine bank format (``storage/index.py:167-174``) for one model shape."""
-    if bits != 2:
-        raise ValueError(f"only the 2-bit affine bank is implemented (bits={bits})")
+    """Stacked-affine bank format (``storage/index.py:167-174``) for one model shape: 2, 3 or
+    4 bits per code in groups of 32, 64 or 128 (the widths ``build_affine_bank.py:266-267``
+    writes; oQ3e is 3-bit g64 with fp16 scales, ``expert_affine.py:1-4``)."""
+    if bits not in (2, 3, 4) or group_size not in (32, 64, 128):
+        raise ValueError(f"affine banks have 2, 3 or 4 bits in groups of 32, 64 or 128 "
+                         f"(bits={bits}, group_size={group_size})")
     if scale_dtype not in ("bfloat16", "float16"):
         raise ValueError(f"scale dtype {scale_dtype}")
     shapes, dtypes = {}, {}

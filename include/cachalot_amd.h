@@ -337,6 +337,46 @@ int cachalot_requant_fp4_to_q2(const uint8_t* w_fp4, const uint8_t* s_fp4, int N
                                uint16_t* scales, uint16_t* biases, int scale_dtype,
                                cachalot_stream_t stream);
 
+/* Affine banks of the other widths the reference's bank tool writes
+ * (benchmarks/build_affine_bank.py:266-267): bits 2, 3 or 4 per code, groups of
+ * 32, 64 or 128 (the 2-bit g128 bank has the dedicated entry points above), bf16
+ * or fp16 scales and biases (layout->scale_dtype) -- e.g. oQ3e, 3-bit g64 fp16
+ * (src/cachalot/model/expert_affine.py:1-10).  Codes: each row one little-endian
+ * bit stream, code i at bits [i*bits, (i+1)*bits) (benchmarks/quant_affine.py:
+ * 69-105), K padded to whole groups with zero codes.  Same rounding points,
+ * outputs and errors as cachalot_moe_decode_q2 / cachalot_moe_layer_decode_q2 /
+ * cachalot_grouped_experts_q2, the group formula s*sum(x q) + b*sum(x) in fp32
+ * (replacing mx.quantized_matmul at these widths, expert_affine.py:65-99,
+ * 117-152).  Workspaces from the *_workspace_bytes functions. */
+size_t cachalot_moe_decode_affine_workspace_bytes(int D, int F, int k);
+int cachalot_moe_decode_affine(const uint16_t* x, const uint8_t* pool,
+                               const cachalot_expert_layout* layout /* host */,
+                               const int32_t* slot_table, const int32_t* idx, const float* w,
+                               int D, int F, int E, int k, int bits, int group, float swiglu_limit,
+                               const uint16_t* addend, float* routed, uint16_t* out,
+                               void* workspace, size_t workspace_bytes, cachalot_stream_t stream);
+int cachalot_moe_layer_decode_affine(const uint16_t* x, const uint16_t* gate_weight, const float* gate_bias,
+                                     int E, int k, int score_fn, float gate_temp, float route_scale, int norm,
+                                     int order, const uint8_t* pool,
+                                     const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                     int D, int F, int bits, int group, float swiglu_limit,
+                                     const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
+                                     float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                     cachalot_stream_t stream);
+size_t cachalot_grouped_experts_affine_workspace_bytes(int T, int k, int E, int F);
+int cachalot_grouped_experts_affine(const uint16_t* x, const uint8_t* pool,
+                                    const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
+                                    const int32_t* offsets, const int32_t* row_token, const int32_t* row_slot,
+                                    const float* row_w, int T, int D, int F, int E, int k, int bits, int group,
+                                    float swiglu_limit, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                    cachalot_stream_t stream);
+/* Dense dequantisation of one affine matrix of any bank width: w [N, row_words]
+ * u32, scales / biases [N, groups] (scale_dtype) -> out [N, K] fp32, fl(fl(s*q)+b)
+ * (replaces mx.dequantize on the affine views, expert_affine.py:26-51). */
+int cachalot_dequant_affine(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
+                            int row_words, int groups, int group, int bits, int scale_dtype, float* out,
+                            cachalot_stream_t stream);
+
 /* Dense dequantisation (bit-exact weight checks and debugging).
  * FP4: packed [N, K/2] u8, scales [N, K/32] u8 -> out [N, K] fp32
  *   (replaces dequantize_fp4_weight / dequantize_fp4_dense,

@@ -1,8 +1,11 @@
-"""MLX affine 2-bit g128 layout and group formula, restated.
+"""MLX affine layouts (2-bit g128 and the other widths) and the group formula, restated.
 
 * packing: 16 codes per uint32, least-significant field first
   (``benchmarks/quant_affine.py:11-16,60-66``; layout pinned by the reference's
-  own ``tests/test_quant_affine.py:45-51`` against ``mx.quantize``);
+  own ``tests/test_quant_affine.py:45-51`` against ``mx.quantize``); at 3 and 4
+  bits (``pack_bits``, ``quant_affine.py:69-105``) a row's codes are one
+  little-endian bit stream, code i at bits [i b, (i+1) b), a code straddling a
+  word boundary split between the two words;
 * dequantised value ``w = scale * q + bias`` per ``group``-element group along K
   (``benchmarks/quant_affine.py:11-15``), scales/biases stored bf16
   (``benchmarks/build_affine_bank.py:76,165-174``) or fp16 (the oQ3e banks,
@@ -59,27 +62,56 @@ def scale_values(bits, dtype: str = "bfloat16") -> np.ndarray:
     raise ValueError(f"scale dtype {dtype!r}")
 
 
+def pack_bits(q, bits: int) -> np.ndarray:
+    """[..., K] codes in 0 .. 2^bits - 1 -> [..., K * bits / 32] uint32: the row as one
+    little-endian bit stream (numpy's little-endian bit packing of the code bits,
+    each code least significant bit first)."""
+    q = np.asarray(q, dtype=np.uint32)
+    if (q.shape[-1] * bits) % 32:
+        raise ValueError(f"K={q.shape[-1]} at {bits} bits is not a whole number of words")
+    if bits == 2:
+        return pack_2bit(q)
+    bitplane = ((q[..., None] >> np.arange(bits, dtype=np.uint32)) & 1).astype(np.uint8)
+    stream = bitplane.reshape(*q.shape[:-1], -1)                       # bit i*bits + j = bit j of code i
+    by = np.packbits(stream, axis=-1, bitorder="little")               # byte m = stream bits 8m .. 8m+7
+    return np.ascontiguousarray(by).view("<u4").astype(np.uint32)
+
+
+def unpack_bits(w, bits: int, k: int | None = None) -> np.ndarray:
+    """Inverse of ``pack_bits``: [..., W] uint32 -> [..., k] uint8 codes (k defaults to 32 W / bits)."""
+    if bits == 2:
+        return unpack_2bit(w, k)
+    w = np.ascontiguousarray(np.asarray(w, dtype="<u4"))
+    stream = np.unpackbits(w.view(np.uint8), axis=-1, bitorder="little")
+    n = stream.shape[-1] // bits
+    codes = stream[..., : n * bits].reshape(*w.shape[:-1], n, bits).astype(np.uint32)
+    q = (codes << np.arange(bits, dtype=np.uint32)).sum(axis=-1).astype(np.uint8)
+    return q if k is None else q[..., :k]
+
+
 def dequantize_affine(w, scales_bits, biases_bits, *, k: int, group: int = 128,
-                      scale_dtype: str = "bfloat16") -> np.ndarray:
+                      scale_dtype: str = "bfloat16", bits: int = 2) -> np.ndarray:
     """[N, K] fp32 with the declared rounding ``fl(fl(s * q) + b)`` (s, b exact from their storage type)."""
-    q = unpack_2bit(w, k).astype(np.float32)
+    q = unpack_bits(w, bits, k).astype(np.float32)
     s = np.repeat(scale_values(scales_bits, scale_dtype), group, axis=-1)[..., :k]
     b = np.repeat(scale_values(biases_bits, scale_dtype), group, axis=-1)[..., :k]
     return (s * q) + b
 
 
 def dequantize_affine64(w, scales_bits, biases_bits, *, k: int, group: int = 128,
-                        scale_dtype: str = "bfloat16") -> np.ndarray:
-    q = unpack_2bit(w, k).astype(np.float64)
+                        scale_dtype: str = "bfloat16", bits: int = 2) -> np.ndarray:
+    q = unpack_bits(w, bits, k).astype(np.float64)
     s = np.repeat(scale_values(scales_bits, scale_dtype).astype(np.float64), group, axis=-1)[..., :k]
     b = np.repeat(scale_values(biases_bits, scale_dtype).astype(np.float64), group, axis=-1)[..., :k]
     return s * q + b
 
 
-def qmv64(x, w, scales_bits, biases_bits, *, k: int, group: int = 128, scale_dtype: str = "bfloat16") -> np.ndarray:
+def qmv64(x, w, scales_bits, biases_bits, *, k: int, group: int = 128, scale_dtype: str = "bfloat16",
+          bits: int = 2) -> np.ndarray:
     """x [M, K] (bf16-exact values) -> float64 [M, N] = sum_g s_g*sum(x q) + b_g*sum(x).
 
-    s*q+b is exact in float64 for bf16 or fp16 s, b and q in 0..3, so this
+    s*q+b is exact in float64 for bf16 or fp16 s, b and q below 2^bits, so this
     equals x @ dequant(W)^T evaluated in float64."""
     x = np.asarray(x, dtype=np.float64)
-    return x @ dequantize_affine64(w, scales_bits, biases_bits, k=k, group=group, scale_dtype=scale_dtype).T
+    return x @ dequantize_affine64(w, scales_bits, biases_bits, k=k, group=group, scale_dtype=scale_dtype,
+                                   bits=bits).T

@@ -130,17 +130,21 @@ def fp4_tensor_specs(d_model: int, d_ff: int, e8m0_lo: int = 119, e8m0_hi: int =
 
 def q2_tensor_specs(d_model: int, d_ff: int, group: int = 128,
                     scale_lo: float = 0.005, scale_hi: float = 0.05, bias_sigma: float = 0.02,
-                    scale_dtype: str = "bfloat16"):
-    """2-bit affine expert (MLX layout): weight [N, Kp/16] u32, scales/biases [N, Kp/g] bf16
-    (or fp16 with ``scale_dtype="float16"``, BASELINE config 1's "fp16 scale and bias").
+                    scale_dtype: str = "bfloat16", bits: int = 2):
+    """Affine expert (MLX layout): weight [N, Kp * bits / 32] u32 (uniform random words: every
+    code uniform), scales/biases [N, Kp/g] bf16 (or fp16 with ``scale_dtype="float16"``,
+    BASELINE config 1's "fp16 scale and bias").
 
-    Kp is K rounded up to a whole group; codes past K are zero."""
+    Kp is K rounded up to a whole group; codes past K are zero (K * bits is a whole
+    number of words for every shape used)."""
     specs = []
     for proj, (n, k) in (("w1", (d_ff, d_model)), ("w2", (d_model, d_ff)), ("w3", (d_ff, d_model))):
         groups = -(-k // group)
         kp = groups * group
-        row_total = kp // 16
-        row_valid = k // 16 if kp != k else 0
+        if (k * bits) % 32:
+            raise ValueError(f"K={k} at {bits} bits ends inside a word")
+        row_total = kp * bits // 32
+        row_valid = k * bits // 32 if kp != k else 0
         specs.append((f"{proj}.weight", (n, row_total), np.uint32, KIND_U32, 0.0, 0.0,
                       row_total if row_valid else 0, row_valid))
         f16 = scale_dtype == "float16"

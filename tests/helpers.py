@@ -33,7 +33,7 @@ def oracle_tensors(fmt, layer, expert, seed=SEED):
         specs = osynth.fp4_tensor_specs(fmt.d_model, fmt.d_ff)
     else:
         specs = osynth.q2_tensor_specs(fmt.d_model, fmt.d_ff, fmt.group_size,
-                                       scale_dtype=fmt.dtypes.get("w1.scales", "bfloat16"))
+                                       scale_dtype=fmt.dtypes.get("w1.scales", "bfloat16"), bits=fmt.bits)
     return osynth.expert_tensors(seed, layer, expert, specs)
 
 
@@ -44,7 +44,7 @@ def q2_mats(fmt, tensors):
 
     def mm(proj, k):
         w, s, b = tensors[f"{proj}.weight"], tensors[f"{proj}.scales"], tensors[f"{proj}.biases"]
-        return lambda x: qmv64(x, w, s, b, k=k, group=g, scale_dtype=sd)
+        return lambda x: qmv64(x, w, s, b, k=k, group=g, scale_dtype=sd, bits=fmt.bits)
 
     return mm("w1", fmt.d_model), mm("w3", fmt.d_model), mm("w2", fmt.d_ff)
 

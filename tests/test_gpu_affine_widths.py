@@ -1,0 +1,114 @@
+"""Affine banks of the other widths (3 / 4 bits, groups of 32 / 64, bf16 or fp16
+scales): oQ3e is 3-bit g64 with fp16 scales (expert_affine.py:1-10), and the bank
+tool writes bits 2/3/4 x groups 32/64/128 (build_affine_bank.py:266-267).
+
+* dequantisation bit-exact against oracle/affine2.py (the MLX bit-stream layout);
+* decode at the layer's shape, per-expert terms against the oracle's rounding
+  points (helpers.term_flips), routed = the route-order sum bit for bit,
+  out = bf16(routed + addend) bit for bit; the device-routed layer with ids
+  bit-exact;
+* grouped (prefill / batched) rows against the oracle, dropped ids giving zeros.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import SEED, make_store, oracle_tensors, q2_mats
+from oracle import router as orouter
+from oracle import synth as osynth
+from oracle.affine2 import dequantize_affine
+from oracle.bf16 import bf16_bits_to_f32
+from test_gpu_workloads import TERM_TOL, _bf16, _check_decode, _decode_terms, _f32, _grouped_check, _np
+
+pytestmark = pytest.mark.gpu
+
+WIDTHS = [(3, 64, "float16"), (4, 32, "bfloat16"), (3, 128, "bfloat16"), (2, 64, "float16")]
+
+
+def _fmt(bits, group, sd, d=4096, f=2880):
+    from cachalot_amd.storage.index import affine_format
+
+    return affine_format(d, f, bits=bits, group_size=group, scale_dtype=sd)
+
+
+@pytest.mark.parametrize("bits,group,sd", WIDTHS)
+def test_affine_dequant_and_fill_bit_exact(cuda, bits, group, sd):
+    from cachalot_amd import _lib
+
+    fmt = _fmt(bits, group, sd)
+    t = oracle_tensors(fmt, 0, 7)
+    for proj, k in (("w1", 4096), ("w2", 2880)):
+        w, s, b = t[f"{proj}.weight"], t[f"{proj}.scales"], t[f"{proj}.biases"]
+        n, row_words = w.shape
+        out = torch.empty((n, k), dtype=torch.float32, device=cuda)
+        dw = torch.from_numpy(w.view(np.int32)).to(cuda)
+        ds = torch.from_numpy(s.view(np.int16)).to(cuda)
+        db = torch.from_numpy(b.view(np.int16)).to(cuda)
+        _lib.check(_lib.lib().cachalot_dequant_affine(dw.data_ptr(), ds.data_ptr(), db.data_ptr(), n, k, row_words,
+                                                      s.shape[1], group, bits, _lib.scale_dtype_code(sd),
+                                                      out.data_ptr(), _lib.stream_handle(cuda)))
+        want = dequantize_affine(w, s, b, k=k, group=group, scale_dtype=sd, bits=bits)
+        assert np.array_equal(_np(out).view(np.uint32), want.view(np.uint32)), (proj, bits, group)
+    store = make_store(fmt, n_layers=1, n_experts=8, keys=[(0, 7)])
+    slot = store.pool.slot(store.layer_table(0)[7].item())
+    for name, arr in t.items():
+        assert np.array_equal(_np(slot.arrays[name]), arr.view(np.uint8).reshape(-1)), name
+
+
+@pytest.mark.parametrize("bits,group,sd", WIDTHS[:2])
+def test_affine_decode_terms(cuda, bits, group, sd):
+    """Given experts (two tokens) and the device-routed layer (one token)."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_decode import decode_experts, moe_layer_decode
+
+    fmt = _fmt(bits, group, sd)
+    store = make_store(fmt, n_layers=1, n_experts=384)
+    rng = np.random.default_rng(bits * 100 + group)
+    for tk in range(2):
+        idx = rng.choice(384, size=6, replace=False).tolist()
+        w = rng.dirichlet(np.ones(6)).astype(np.float32)
+        xb = osynth.activations(SEED, 3000 + tk, 1, 4096)[0]
+        ab = osynth.activations(SEED, 3100 + tk, 1, 4096)[0]
+        x, a = _bf16(xb, cuda), _bf16(ab, cuda)
+        routed, out = decode_experts(x, store.pool, store.layer_table(0), torch.tensor(idx, dtype=torch.int32,
+                                                                                       device=cuda),
+                                     torch.tensor(w, device=cuda), addend=a)
+        terms = _decode_terms(cuda, store, 0, x, idx, w)
+        _check_decode(f"affine {bits}-bit g{group} {sd} token {tk}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
+                      _np(routed), _f32(out), terms, bf16_bits_to_f32(ab))
+    gw, gb = synth.router_weights(SEED, 0, 384, 4096, cuda)
+    x = synth.activations(SEED, 3200, 1, 4096, cuda)[0]
+    routed, out, route = moe_layer_decode(x, gw, gb, store.pool, store.layer_table(0), topk=6, route_scale=1.0,
+                                          score_fn="sigmoid", addend=x, want_routed=True)
+    xf = _f32(x)
+    oi, ow, _ = orouter.route(xf[None], _f32(gw), _np(gb), topk=6, route_scale=1.0, score=orouter.SCORE_SIGMOID)
+    assert np.array_equal(_np(route.indices), oi[0])
+    assert np.array_equal(_np(route.weights).view(np.uint32), ow[0].view(np.uint32))
+    terms = _decode_terms(cuda, store, 0, x, oi[0], ow[0])
+    _check_decode(f"affine {bits}-bit g{group} layer", fmt, 0, xf, oi[0], ow[0], _np(routed), _f32(out), terms, xf)
+
+
+@pytest.mark.parametrize("bits,group,sd", WIDTHS[:2])
+def test_affine_grouped_rows(cuda, bits, group, sd):
+    """37 tokens x top-6 over 16 experts (uneven rows, tiles of 4), three dropped ids."""
+    from cachalot_amd.moe_prefill import grouped_experts
+
+    fmt = _fmt(bits, group, sd)
+    E, t, k = 16, 37, 6
+    store = make_store(fmt, n_layers=1, n_experts=E)
+    rng = np.random.default_rng(7 + bits)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(t)]).astype(np.int32)
+    idx[0, 1], idx[5, 5], idx[t - 1, 0] = -1, E + 2, 1 << 29
+    w = rng.dirichlet(np.ones(k), size=t).astype(np.float32)
+    xb = osynth.activations(SEED, 3300, t, 4096)
+    ab = osynth.activations(SEED, 3301, t, 4096)
+    for _ in range(2):   # y reused from a previous call must not leak into the dropped rows
+        routed, out, y = grouped_experts(_bf16(xb, cuda), torch.from_numpy(idx).to(cuda),
+                                         torch.from_numpy(w).to(cuda), store.pool, store.layer_table(0),
+                                         addend=_bf16(ab, cuda), want_routed=True, want_terms=True)
+        yf = _f32(y)
+        assert not yf[0, 1].any() and not yf[5, 5].any() and not yf[t - 1, 0].any()
+        _grouped_check(f"grouped affine {bits}-bit g{group}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed),
+                       _f32(out), yf, E, addend=bf16_bits_to_f32(ab))

@@ -185,3 +185,65 @@ def test_fp16_synthetic_kinds_follow_the_bf16_stream():
         vf = scale_values(osynth.fill(kf, 4000, key, p0, p1), "float16")
         assert np.all(np.abs(vb - vf) <= np.abs(vb) * 2.0 ** -8 + 2.0 ** -24)
         assert not np.array_equal(vb, vf)
+
+
+def test_pack_bits_3bit_known_words():
+    """MLX's 3-bit layout (quant_affine.py:69-105): one little-endian bit stream, code i
+    at bits [3i, 3i+3); code 10 straddles words 0 and 1 (bits 30..32)."""
+    from oracle.affine2 import pack_bits, unpack_bits
+
+    q = np.zeros(32, np.uint8)
+    q[0], q[1], q[10], q[11], q[31] = 7, 5, 6, 1, 3
+    w = pack_bits(q, 3)
+    assert w.shape == (3,)
+    # word 0: 7 | 5 << 3 | (6 & 3) << 30 ; word 1: 6 >> 2 = 1 in bit 0, code 11 at bits 1..3
+    assert int(w[0]) == (7 | (5 << 3) | ((6 & 3) << 30))
+    assert int(w[1]) == (1 | (1 << 1))
+    assert int(w[2]) == 3 << 29                     # code 31 at stream bits 93..95
+    assert np.array_equal(unpack_bits(w, 3), q)
+
+
+def test_pack_bits_round_trip_and_2bit_agreement():
+    from oracle.affine2 import pack_2bit, pack_bits, unpack_bits
+
+    rng = np.random.default_rng(4)
+    for bits in (2, 3, 4):
+        q = rng.integers(0, 1 << bits, size=(5, 256), dtype=np.uint8)
+        w = pack_bits(q, bits)
+        assert w.shape == (5, 256 * bits // 32)
+        assert np.array_equal(unpack_bits(w, bits), q)
+    q = rng.integers(0, 4, size=(3, 128), dtype=np.uint8)
+    assert np.array_equal(pack_bits(q, 2), pack_2bit(q))
+    # 4-bit: eight codes per word, low nibble first (byte-aligned, so also the nibble order)
+    q = np.arange(8, dtype=np.uint8)
+    assert int(pack_bits(q, 4)[0]) == 0x76543210
+
+
+def test_affine_widths_qmv_equals_dense_product():
+    """3-bit g64 with fp16 scales (oQ3e) and 4-bit g32: the group formula equals the
+    dense product of the dequantised matrix."""
+    from oracle.affine2 import dequantize_affine, dequantize_affine64, pack_bits, qmv64
+
+    rng = np.random.default_rng(5)
+    for bits, group, sd in ((3, 64, "float16"), (4, 32, "bfloat16")):
+        n, k = 12, 160                                  # 2.5 groups of 64, 5 of 32
+        kp = -(-k // group) * group
+        q = rng.integers(0, 1 << bits, size=(n, kp), dtype=np.uint8)
+        q[:, k:] = 0
+        w = pack_bits(q, bits)
+        s = rng.uniform(0.005, 0.05, size=(n, kp // group)).astype(np.float32)
+        b = rng.normal(0, 0.02, size=(n, kp // group)).astype(np.float32)
+        if sd == "float16":
+            sb, bb = s.astype(np.float16).view(np.uint16), b.astype(np.float16).view(np.uint16)
+            sv, bv = sb.view(np.float16).astype(np.float64), bb.view(np.float16).astype(np.float64)
+        else:
+            sb, bb = f32_to_bf16_bits(s), f32_to_bf16_bits(b)
+            sv, bv = bf16_bits_to_f32(sb).astype(np.float64), bf16_bits_to_f32(bb).astype(np.float64)
+        dense = q[:, :k] * np.repeat(sv, group, axis=1)[:, :k] + np.repeat(bv, group, axis=1)[:, :k]
+        assert np.array_equal(dequantize_affine64(w, sb, bb, k=k, group=group, scale_dtype=sd, bits=bits), dense)
+        x = rng.normal(size=(3, k))
+        assert np.allclose(qmv64(x, w, sb, bb, k=k, group=group, scale_dtype=sd, bits=bits), x @ dense.T,
+                           rtol=1e-12, atol=1e-12)
+        f32 = dequantize_affine(w, sb, bb, k=k, group=group, scale_dtype=sd, bits=bits)
+        assert np.array_equal(f32, (q[:, :k].astype(np.float32) * np.repeat(sv, group, axis=1)[:, :k].astype(
+            np.float32)) + np.repeat(bv, group, axis=1)[:, :k].astype(np.float32))
