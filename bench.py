@@ -49,7 +49,7 @@ def parse():
                     help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared", "sharedfp8"),
+    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared", "sharedfp8", "widths"),
                     help="profiling aid: run one secondary measurement alone (config 3 prefill, config 2 "
                          "batched decode over --layers resident layers, config 0 FP4 decode, config 1's layer "
                          "with the FP8 shared expert, or the shared expert alone), print its JSON and exit")
@@ -306,24 +306,23 @@ def batched_decode(args, store, gates, log_fn):
     return out
 
 
-def fp4_decode_config0(args, dev, log_fn):
-    """BASELINE config 0: one token through one FP4 MoE layer (router + 6 FP4 experts), chained over 8
-    resident FP4 layers (58 GB, so the 256 MB MALL holds nothing between visits)."""
+def chained_decode(args, dev, log_fn, fmt, L, seed_off, label, note, with_shared=False):
+    """One token through one MoE layer of `fmt` (router + 6 experts, device routing), chained over
+    L resident layers of 384 experts (graph replays of 8 L steps; each layer comes back only after
+    the L - 1 others, so the 256 MB MALL holds nothing between visits)."""
     import torch
 
     from cachalot_amd import synth
     from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
     from cachalot_amd.moe_decode import moe_layer_decode
-    from cachalot_amd.storage.index import fp4_format
 
-    D, F, E, K, L = 4096, 2880, 384, 6, 8
-    fmt = fp4_format(D, F)
-    loader = SyntheticLoader(fmt, args.seed + 11)
+    D, E, K = fmt.d_model, 384, 6
+    loader = SyntheticLoader(fmt, args.seed + seed_off)
     store = ResidentExpertStore(fmt=fmt, n_slots=L * E, n_layers=L, n_experts=E, device=dev)
     store.preload([(la, e) for la in range(L) for e in range(E)], loader.fill_key)
     table = store.track_slots()
-    gates = [synth.router_weights(args.seed + 11, la, E, D, dev) for la in range(L)]
-    x0 = synth.activations(args.seed + 11, 0, 1, D, dev)[0]
+    gates = [synth.router_weights(args.seed + seed_off, la, E, D, dev) for la in range(L)]
+    x0 = synth.activations(args.seed + seed_off, 0, 1, D, dev)[0]
 
     def step(x, s):
         w, b = gates[s % L]
@@ -358,14 +357,43 @@ def fp4_decode_config0(args, dev, log_fn):
     res = {"us_per_step": round(us, 2), "tok_per_s": round(1e6 / us, 1),
            "expert_GBps": round(expert_bytes / (us * 1e-6) / 1e9, 1),
            "hbm_frac_step": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-           "note": "chained layer steps (router + FP4 gate/up + down), graph replays; FP4 decode computes in fp32 "
-                   "(bf16 hi/lo MFMA), the reference's FP4 rounding points"}
-    log_fn(f"config 0 FP4 decode: {us:.2f} us/step, {res['expert_GBps']:.0f} GB/s expert bytes")
-    # the same FP4 layers with the FP8 shared expert (moe_layer_forward, independent steps)
-    res["layer_with_shared"] = layer_with_shared(args, store, gates, log_fn)
+           "expert_bytes": fmt.algorithmic_bytes, "resident_layers": L, "note": note}
+    log_fn(f"{label}: {us:.2f} us/step, {res['expert_GBps']:.0f} GB/s expert bytes")
+    if with_shared:
+        # the same layers with the FP8 shared expert (moe_layer_forward, independent steps)
+        res["layer_with_shared"] = layer_with_shared(args, store, gates, log_fn)
     del store
     torch.cuda.empty_cache()
     return res
+
+
+def fp4_decode_config0(args, dev, log_fn):
+    """BASELINE config 0: one token through one FP4 MoE layer (router + 6 FP4 experts), chained over 8
+    resident FP4 layers (58 GB)."""
+    from cachalot_amd.storage.index import fp4_format
+
+    return chained_decode(args, dev, log_fn, fp4_format(4096, 2880), 8, 11, "config 0 FP4 decode",
+                          "chained layer steps (router + FP4 gate/up + down), graph replays; FP4 decode computes in "
+                          "fp32 (bf16 hi/lo MFMA), the reference's FP4 rounding points", with_shared=True)
+
+
+def affine_width_decodes(args, dev, log_fn):
+    """Config 1 with the scale type BASELINE states (fp16 scales and biases), and the oQ3e bank
+    (3-bit codes, groups of 64, fp16 scales: expert_affine.py:1-10), each chained over 8 resident
+    layers."""
+    from cachalot_amd.storage.index import affine_format
+
+    out = {}
+    out["config1_fp16_scales"] = chained_decode(
+        args, dev, log_fn, affine_format(4096, 2880, scale_dtype="float16"), 8, 13, "config 1 fp16 scales",
+        "2-bit g128 bank with fp16 scales / biases (BASELINE config 1 as stated); the same matrix-core kernels, "
+        "the scales converted from fp16")
+    out["oq3e_3bit_g64_fp16"] = chained_decode(
+        args, dev, log_fn, affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"), 8, 17,
+        "oQ3e 3-bit g64 decode",
+        "3-bit g64 fp16 bank (oQ3e) on the generic affine kernels (one lane per group, VALU), not the "
+        "matrix-core 2-bit path")
+    return out
 
 
 def prefill_config3(args, dev, log_fn):
@@ -722,6 +750,10 @@ def main() -> int:
         _lib.lib()
         print(json.dumps(fp4_decode_config0(args, dev, log)), flush=True)
         return 0
+    if args.only == "widths":
+        _lib.lib()
+        print(json.dumps(affine_width_decodes(args, dev, log)), flush=True)
+        return 0
     if args.only == "sharedfp8":
         _lib.lib()
         print(json.dumps(shared_expert_fp8(args, dev, log)), flush=True)
@@ -932,6 +964,7 @@ def main() -> int:
     result["roofline"]["frac_of_stream_ceiling"] = round(achieved / ceiling["60MB"]["GBps"], 4)
     if not args.no_extra:
         result["config0_fp4_decode"] = fp4_decode_config0(args, dev, log)
+        result["affine_widths"] = affine_width_decodes(args, dev, log)
         result["config2_batched_decode"] = batched_decode(args, store, gates, log)
         result["config1_layer_with_shared_expert"] = layer_with_shared(args, store, gates, log)
         result["config3_prefill"] = prefill_config3(args, dev, log)

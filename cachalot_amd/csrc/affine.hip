@@ -27,6 +27,8 @@
 //     route order summed into routed / out; grouped, one expert's TB rows into
 //     y[token, slot, :].
 //   aff_dequant_kernel  dense fp32 weights (bit-exact checks).
+#include <algorithm>
+
 #include "decode_common.h"
 #include "router_launch.h"
 
@@ -49,58 +51,121 @@ __device__ __forceinline__ uint32_t code_of(const uint32_t* w, int i) {
   return v & ((1u << BITS) - 1u);
 }
 
-// s * sum(x q) + b * sum(x) over one group; x: the group's G values (fp32, LDS).
-template <int BITS, int G>
-__device__ __forceinline__ float group_value(const uint32_t (&w)[G * BITS / 32], const float* x, float s, float b) {
-  float sxq = 0.0f, sx = 0.0f;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const float xi = x[i];
-    sxq = sxq + xi * (float)code_of<BITS>(w, i);
-    sx = sx + xi;
-  }
-  return s * sxq + b * sx;
-}
+// Rows are read in units of 32 codes -- BITS whole words -- dealt to the lanes
+// (unit u to lane u % 64); unit u lies in group 32 u / G.  A lane's value for a
+// row is the sum over its units of s * sum(x q), plus b * sum(x) for each group
+// whose first unit it holds (sum(x) per group precomputed once per activation
+// row); the wave butterfly then adds the lanes.  All of a wave's rows are loaded
+// before any is used, so their loads are in flight together.
+constexpr int UNIT = 32;
 
-template <int BITS, int G>
-__device__ __forceinline__ void load_group(const uint8_t* row, int g, uint32_t (&w)[G * BITS / 32]) {
-  constexpr int WORDS = G * BITS / 32;
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(row) + (size_t)g * WORDS;
-  if constexpr (WORDS % 4 == 0) {
-#pragma unroll
-    for (int q = 0; q < WORDS / 4; ++q) {
-      const uint4 v = reinterpret_cast<const uint4*>(p)[q];
-      w[4 * q] = v.x;
-      w[4 * q + 1] = v.y;
-      w[4 * q + 2] = v.z;
-      w[4 * q + 3] = v.w;
-    }
+template <int BITS>
+struct Unit {
+  uint32_t w[BITS];
+};
+
+template <int BITS>
+__device__ __forceinline__ Unit<BITS> load_unit(const uint8_t* row, int u) {
+  Unit<BITS> r;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(row) + (size_t)u * BITS;
+  if constexpr (BITS == 2) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else if constexpr (BITS == 4) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+    r.w[3] = v.w;
   } else {
 #pragma unroll
-    for (int q = 0; q < WORDS; ++q) w[q] = p[q];
+    for (int i = 0; i < BITS; ++i) r.w[i] = p[i];
   }
+  return r;
 }
 
-// The dot products of one weight row (words [Gn * WORDS], scales / biases [Gn])
-// with NT activation rows x[t * ld ..] held in LDS: lane l takes groups l, l + 64,
-// ..; the sums are combined by the wave butterfly and returned to every lane.
-template <int BITS, int G, int NT>
-__device__ __forceinline__ void row_dots(const uint8_t* wrow, const uint16_t* srow, const uint16_t* brow, bool f16,
-                                         int Gn, const float* x, int ld, int nt, float (&out)[NT]) {
+// R rows' units (UPL per lane), scales and group biases, loaded together.
+template <int BITS, int G, int R, int UPL>
+struct Rows {
+  Unit<BITS> w[R][UPL];
+  float s[R][UPL], b[R][UPL];
+};
+
+template <int BITS, int G, int R, int UPL>
+__device__ __forceinline__ void load_rows(const uint8_t* const (&wrow)[R], const uint16_t* const (&srow)[R],
+                                          const uint16_t* const (&brow)[R], bool f16, int nunits,
+                                          Rows<BITS, G, R, UPL>& o) {
   const int lane = threadIdx.x & 63;
-  float acc[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
-  for (int g = lane; g < Gn; g += 64) {
-    uint32_t w[G * BITS / 32];
-    load_group<BITS, G>(wrow, g, w);
-    const float s = scale_bits_to_f32(srow[g], f16), b = scale_bits_to_f32(brow[g], f16);
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (t < nt) acc[t] = acc[t] + group_value<BITS, G>(w, x + t * ld + g * G, s, b);
+    for (int j = 0; j < UPL; ++j) {
+      const int u = min(lane + 64 * j, nunits - 1);
+      o.w[r][j] = load_unit<BITS>(wrow[r], u);
+      const int g = u * UNIT / G;
+      o.s[r][j] = scale_bits_to_f32(srow[r][g], f16);
+      o.b[r][j] = scale_bits_to_f32(brow[r][g], f16);
+    }
+}
+
+// out[r] = the rows' dot products with one activation row x (fp32, LDS), xsum its
+// per-group sums; returned to every lane.
+template <int BITS, int G, int R, int UPL>
+__device__ __forceinline__ void dot_rows(const Rows<BITS, G, R, UPL>& o, int nunits, const float* x,
+                                         const float* xsum, float (&out)[R]) {
+  const int lane = threadIdx.x & 63;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = lane + 64 * j;
+    if (u >= nunits) break;
+    const float4* xv = reinterpret_cast<const float4*>(x + u * UNIT);
+    const bool first = (u * UNIT) % G == 0;
+    const float gs = first ? xsum[u * UNIT / G] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float d = 0.0f;
+#pragma unroll
+      for (int i4 = 0; i4 < UNIT / 4; ++i4) {
+        const float4 xx = xv[i4];
+        d = __builtin_fmaf(xx.x, (float)code_of<BITS>(o.w[r][j].w, 4 * i4), d);
+        d = __builtin_fmaf(xx.y, (float)code_of<BITS>(o.w[r][j].w, 4 * i4 + 1), d);
+        d = __builtin_fmaf(xx.z, (float)code_of<BITS>(o.w[r][j].w, 4 * i4 + 2), d);
+        d = __builtin_fmaf(xx.w, (float)code_of<BITS>(o.w[r][j].w, 4 * i4 + 3), d);
+      }
+      acc[r] = acc[r] + (o.s[r][j] * d + o.b[r][j] * gs);
+    }
   }
 #pragma unroll
-  for (int t = 0; t < NT; ++t) out[t] = wave_sum(acc[t]);
+  for (int r = 0; r < R; ++r) out[r] = wave_sum(acc[r]);
+}
+
+// Per-group sums of NT activation rows (x [t][ld], padding zero) into xsum [t][ld / G]:
+// G / 16 consecutive threads per group, 16 values each, then a butterfly inside the
+// thread group (every thread of the workgroup takes part in every pass).
+template <int G>
+__device__ __forceinline__ void group_sums(const float* x, int ld, int nt, float* xsum) {
+  constexpr int P = G / 16;   // threads per group (2, 4 or 8: aligned inside a quad pair)
+  const int ng = ld / G, total = nt * ng * P;
+  for (int i0 = 0; i0 < total; i0 += blockDim.x) {
+    const int i = i0 + threadIdx.x;
+    const int q = min(i, total - 1), grp = q / P, part = q - grp * P;
+    const int t = grp / ng, g = grp - t * ng;
+    const float4* p = reinterpret_cast<const float4*>(x + t * ld + g * G + 16 * part);
+    float sum = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 f = p[v];
+      sum = sum + f.x + f.y + f.z + f.w;
+    }
+    sum = sum + __uint_as_float(xor1_u32(__float_as_uint(sum)));
+    if constexpr (P >= 4) sum = sum + __uint_as_float(xor2_u32(__float_as_uint(sum)));
+    if constexpr (P >= 8) sum = sum + __uint_as_float(mirror8_u32(__float_as_uint(sum)));
+    if (i < total && part == 0) xsum[grp] = sum;
+  }
 }
 
 // Where a gate/up or down workgroup finds its rows.  Decode: route e of one
@@ -175,9 +240,10 @@ __global__ void __launch_bounds__(256) aff_drop_kernel(const int32_t* __restrict
 }
 
 // grid.x = k * F / 16 (decode) or max_tiles * F / 16 (grouped).
-template <int BITS, int G, bool GROUPED>
+template <int BITS, int G, int UPL, bool GROUPED>
 __global__ void __launch_bounds__(THREADS) aff_gate_up_kernel(Args a) {
   extern __shared__ float xs[];   // [TB or 1][Dp] fp32
+  __shared__ float xsum[TB * MAX_K / UNIT];
   __shared__ int top_i[KMAX], top_s[KMAX];
   __shared__ float top_v[KMAX], top_w[KMAX];
   __shared__ float red[2][16][TB];
@@ -191,38 +257,72 @@ __global__ void __launch_bounds__(THREADS) aff_gate_up_kernel(Args a) {
     slot = a.slot_table[e];
   } else {
     e = unit;
-    if (wave == 0) {
+    if (wave == 0) {   // the expert's slot (the top-k itself, given scores) while the x rows are staged
       const int sl = route_slot(a.src, a.ws_slots, e, top_i, top_v, top_s);
       if (lane == 0) s_slot = sl;
     }
-    __syncthreads();
-    slot = s_slot;
   }
   const int NT = GROUPED ? nr : 1;
-  // activation rows into LDS (fp32; the padding past D is zero)
+  // activation rows into LDS (fp32; the padding past D is zero), 8 values per thread and step
   for (int t = 0; t < NT; ++t) {
     const int tok = GROUPED ? a.row_token[r0 + t] : 0;
-    for (int i = tid; i < Dp; i += THREADS) xs[t * Dp + i] = i < a.D ? bf16_to_f32(a.x[(size_t)tok * a.D + i]) : 0.0f;
+    const uint16_t* xr = a.x + (size_t)tok * a.D;
+    for (int i = 8 * tid; i < Dp; i += 8 * THREADS) {
+      float v[8];
+      if (i + 8 <= a.D) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(xr + i);
+        const uint32_t ww[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[2 * q] = __uint_as_float(ww[q] << 16);
+          v[2 * q + 1] = __uint_as_float(ww[q] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = i + q < a.D ? bf16_to_f32(xr[i + q]) : 0.0f;
+      }
+      float4* d = reinterpret_cast<float4*>(xs + t * Dp + i);
+      d[0] = make_float4(v[0], v[1], v[2], v[3]);
+      d[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
   }
   __syncthreads();
+  if constexpr (!GROUPED) slot = s_slot;
   const int Gn = Dp / G;
   if (slot >= 0) {
     const uint8_t* base = a.pool + (int64_t)slot * a.L.record_bytes;
     const int wb = Dp * BITS / 8;   // bytes per weight row
-    // wave w: rows 4w .. 4w + 3 of W1 and W3
-    for (int r = 0; r < 4; ++r) {
-      const int n = row0 + 4 * wave + r;
+    // wave w: rows 4w .. 4w + 3 of W1 (r < 4) and of W3 (r >= 4); grouped tiles (several
+    // activation rows) take the two matrices in turn, so fewer rows stay live
+    constexpr int R = GROUPED ? 4 : 8;
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int tq = m == 0 ? 0 : 6;
-        const uint8_t* wrow = base + a.L.off[tq] + (int64_t)n * wb;
-        const uint16_t* srow = reinterpret_cast<const uint16_t*>(base + a.L.off[tq + 1]) + (int64_t)n * Gn;
-        const uint16_t* brow = reinterpret_cast<const uint16_t*>(base + a.L.off[tq + 2]) + (int64_t)n * Gn;
-        float v[GROUPED ? TB : 1];
-        row_dots<BITS, G, GROUPED ? TB : 1>(wrow, srow, brow, a.L.f16, Gn, xs, Dp, NT, v);
+    for (int pass = 0; pass < 8 / R; ++pass) {
+      const uint8_t* wrow[R];
+      const uint16_t* srow[R];
+      const uint16_t* brow[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int rr = pass * R + r;
+        const int n = row0 + 4 * wave + (rr & 3), tq = rr < 4 ? 0 : 6;
+        wrow[r] = base + a.L.off[tq] + (int64_t)n * wb;
+        srow[r] = reinterpret_cast<const uint16_t*>(base + a.L.off[tq + 1]) + (int64_t)n * Gn;
+        brow[r] = reinterpret_cast<const uint16_t*>(base + a.L.off[tq + 2]) + (int64_t)n * Gn;
+      }
+      Rows<BITS, G, R, UPL> rw;
+      load_rows<BITS, G, R, UPL>(wrow, srow, brow, a.L.f16, Dp / UNIT, rw);
+      if (pass == 0) {   // the group sums while the first rows' loads are in flight
+        group_sums<G>(xs, Dp, NT, xsum);
+        __syncthreads();
+      }
+      for (int t = 0; t < NT; ++t) {
+        float v[R];
+        dot_rows<BITS, G, R, UPL>(rw, Dp / UNIT, xs + t * Dp, xsum + t * Gn, v);
         if (lane == 0)
 #pragma unroll
-          for (int t = 0; t < (GROUPED ? TB : 1); ++t) red[m][4 * wave + r][t] = v[t];
+          for (int r = 0; r < R; ++r) {
+            const int rr = pass * R + r;
+            red[rr >> 2][4 * wave + (rr & 3)][t] = v[r];
+          }
       }
     }
   }
@@ -256,9 +356,10 @@ __global__ void __launch_bounds__(THREADS) aff_gate_up_kernel(Args a) {
 }
 
 // grid.x = D / 16 (decode) or (D / 16) x max_tiles (grouped: blockIdx.y = tile).
-template <int BITS, int G, bool GROUPED>
+template <int BITS, int G, int UPL, bool GROUPED>
 __global__ void __launch_bounds__(THREADS) aff_down_kernel(Args a) {
   extern __shared__ float hs[];   // [TB][Fp] fp32
+  __shared__ float hsum[TB * MAX_K / UNIT];
   __shared__ float yv[KMAX][16][TB];
   __shared__ int slots[KMAX];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -272,26 +373,47 @@ __global__ void __launch_bounds__(THREADS) aff_down_kernel(Args a) {
   if (tid < ne) slots[tid] = GROUPED ? a.slot_table[e0] : expert_slot(a.src, a.ws_slots, tid);
   for (int x = 0; x < ne; ++x) {
     const int NT = GROUPED ? nr : 1;
-    __syncthreads();
-    for (int t = 0; t < NT; ++t) {
-      const uint16_t* hrow = a.h + (size_t)(GROUPED ? r0 + t : x) * Fp;
-      for (int i = tid; i < Fp; i += THREADS) hs[t * Fp + i] = bf16_to_f32(hrow[i]);
-    }
-    __syncthreads();
+    __syncthreads();   // slots written; the previous expert's h no longer read
     const int slot = slots[x];
+    // this expert's rows first, so their loads fly while h is staged and summed
+    Rows<BITS, G, 4, UPL> rw;
     if (slot >= 0) {
       const uint8_t* base = a.pool + (int64_t)slot * a.L.record_bytes;
       const int wb = Fp * BITS / 8;
+      const uint8_t* wrow[4];
+      const uint16_t* srow[4];
+      const uint16_t* brow[4];
+#pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = row0 + 4 * wave + r;
-        const uint8_t* wrow = base + a.L.off[3] + (int64_t)n * wb;
-        const uint16_t* srow = reinterpret_cast<const uint16_t*>(base + a.L.off[4]) + (int64_t)n * Gn;
-        const uint16_t* brow = reinterpret_cast<const uint16_t*>(base + a.L.off[5]) + (int64_t)n * Gn;
-        float v[GROUPED ? TB : 1];
-        row_dots<BITS, G, GROUPED ? TB : 1>(wrow, srow, brow, a.L.f16, Gn, hs, Fp, NT, v);
+        wrow[r] = base + a.L.off[3] + (int64_t)n * wb;
+        srow[r] = reinterpret_cast<const uint16_t*>(base + a.L.off[4]) + (int64_t)n * Gn;
+        brow[r] = reinterpret_cast<const uint16_t*>(base + a.L.off[5]) + (int64_t)n * Gn;
+      }
+      load_rows<BITS, G, 4, UPL>(wrow, srow, brow, a.L.f16, Fp / UNIT, rw);
+    }
+    for (int t = 0; t < NT; ++t) {
+      const uint16_t* hrow = a.h + (size_t)(GROUPED ? r0 + t : x) * Fp;
+      for (int i = 8 * tid; i < Fp; i += 8 * THREADS) {   // padded with zeros by the gate/up kernel
+        const uint4 raw = *reinterpret_cast<const uint4*>(hrow + i);
+        const uint32_t ww[4] = {raw.x, raw.y, raw.z, raw.w};
+        float4* d = reinterpret_cast<float4*>(hs + t * Fp + i);
+        d[0] = make_float4(__uint_as_float(ww[0] << 16), __uint_as_float(ww[0] & 0xffff0000u),
+                           __uint_as_float(ww[1] << 16), __uint_as_float(ww[1] & 0xffff0000u));
+        d[1] = make_float4(__uint_as_float(ww[2] << 16), __uint_as_float(ww[2] & 0xffff0000u),
+                           __uint_as_float(ww[3] << 16), __uint_as_float(ww[3] & 0xffff0000u));
+      }
+    }
+    __syncthreads();
+    group_sums<G>(hs, Fp, NT, hsum);
+    __syncthreads();
+    if (slot >= 0) {
+      for (int t = 0; t < NT; ++t) {
+        float v[4];
+        dot_rows<BITS, G, 4, UPL>(rw, Fp / UNIT, hs + t * Fp, hsum + t * Gn, v);
         if (lane == 0)
 #pragma unroll
-          for (int t = 0; t < (GROUPED ? TB : 1); ++t) yv[x][4 * wave + r][t] = v[t];
+          for (int r = 0; r < 4; ++r) yv[x][4 * wave + r][t] = v[r];
       }
     } else if (lane == 0) {
       for (int r = 0; r < 4; ++r)
@@ -316,7 +438,7 @@ __global__ void __launch_bounds__(THREADS) aff_down_kernel(Args a) {
   }
 }
 
-// One thread per group of a row: w [N, row_words], scales / biases [N, groups].
+// One thread per 32-code unit of a row: w [N, row_words], scales / biases [N, groups].
 template <int BITS, int G>
 __global__ void __launch_bounds__(256) aff_dequant_kernel(const uint32_t* __restrict__ w,
                                                           const uint16_t* __restrict__ scales,
@@ -324,17 +446,16 @@ __global__ void __launch_bounds__(256) aff_dequant_kernel(const uint32_t* __rest
                                                           int row_words, int groups, bool f16,
                                                           float* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int gk = (K + G - 1) / G;
-  if (i >= (int64_t)N * gk) return;
-  const int64_t n = i / gk;
-  const int g = (int)(i - n * gk);
-  uint32_t words[G * BITS / 32];
-  load_group<BITS, G>(reinterpret_cast<const uint8_t*>(w + n * row_words), g, words);
+  const int nu = (K + UNIT - 1) / UNIT;
+  if (i >= (int64_t)N * nu) return;
+  const int64_t n = i / nu;
+  const int u = (int)(i - n * nu), g = u * UNIT / G;
+  const Unit<BITS> c = load_unit<BITS>(reinterpret_cast<const uint8_t*>(w + n * row_words), u);
   const float s = scale_bits_to_f32(scales[n * groups + g], f16), b = scale_bits_to_f32(biases[n * groups + g], f16);
 #pragma unroll
-  for (int t = 0; t < G; ++t) {
-    const int k = g * G + t;
-    if (k < K) out[n * K + k] = s * (float)code_of<BITS>(words, t) + b;
+  for (int t = 0; t < UNIT; ++t) {
+    const int k = u * UNIT + t;
+    if (k < K) out[n * K + k] = s * (float)code_of<BITS>(c.w, t) + b;
   }
 }
 
@@ -357,32 +478,40 @@ int dispatch(int bits, int group, A... args) {
               "32/64/128)", bits, group);
 }
 
+template <int BITS, int G, int UPL>
+int run_decode(const Args& a, bool grouped, hipStream_t s) {
+  const int Dp = (a.D + G - 1) / G * G, Fp = (a.F + G - 1) / G * G;
+  const int nt = grouped ? TB : 1;
+  const size_t lds_gu = (size_t)nt * Dp * 4, lds_dn = (size_t)nt * Fp * 4;
+  const void* kgu = grouped ? reinterpret_cast<const void*>(aff_gate_up_kernel<BITS, G, UPL, true>)
+                            : reinterpret_cast<const void*>(aff_gate_up_kernel<BITS, G, UPL, false>);
+  const void* kdn = grouped ? reinterpret_cast<const void*>(aff_down_kernel<BITS, G, UPL, true>)
+                            : reinterpret_cast<const void*>(aff_down_kernel<BITS, G, UPL, false>);
+  if (hipFuncSetAttribute(kgu, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu) != hipSuccess ||
+      hipFuncSetAttribute(kdn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_dn) != hipSuccess)
+    return fail(CACHALOT_EHIP, "affine: cannot grant %zu / %zu bytes of LDS", lds_gu, lds_dn);
+  if (grouped) {
+    hipLaunchKernelGGL((aff_gate_up_kernel<BITS, G, UPL, true>), dim3((unsigned)(a.max_tiles * (a.F / 16))),
+                       dim3(THREADS), lds_gu, s, a);
+    if (int rc = check_launch("aff_gate_up_kernel")) return rc;
+    hipLaunchKernelGGL((aff_down_kernel<BITS, G, UPL, true>), dim3((unsigned)(a.D / 16), (unsigned)a.max_tiles),
+                       dim3(THREADS), lds_dn, s, a);
+    return check_launch("aff_down_kernel");
+  }
+  hipLaunchKernelGGL((aff_gate_up_kernel<BITS, G, UPL, false>), dim3((unsigned)(a.k * (a.F / 16))), dim3(THREADS),
+                     lds_gu, s, a);
+  if (int rc = check_launch("aff_gate_up_kernel")) return rc;
+  hipLaunchKernelGGL((aff_down_kernel<BITS, G, UPL, false>), dim3((unsigned)(a.D / 16)), dim3(THREADS), lds_dn, s,
+                     a);
+  return check_launch("aff_down_kernel");
+}
+
+// UPL = units per lane for the longer K: 2 up to 4096, 4 up to MAX_K.
 template <int BITS, int G>
 struct Decode {
   static int run(const Args& a, bool grouped, hipStream_t s) {
-    const int Dp = (a.D + G - 1) / G * G, Fp = (a.F + G - 1) / G * G;
-    const int nt = grouped ? TB : 1;
-    const size_t lds_gu = (size_t)nt * Dp * 4, lds_dn = (size_t)nt * Fp * 4;
-    const void* kgu = grouped ? reinterpret_cast<const void*>(aff_gate_up_kernel<BITS, G, true>)
-                              : reinterpret_cast<const void*>(aff_gate_up_kernel<BITS, G, false>);
-    const void* kdn = grouped ? reinterpret_cast<const void*>(aff_down_kernel<BITS, G, true>)
-                              : reinterpret_cast<const void*>(aff_down_kernel<BITS, G, false>);
-    if (hipFuncSetAttribute(kgu, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu) != hipSuccess ||
-        hipFuncSetAttribute(kdn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_dn) != hipSuccess)
-      return fail(CACHALOT_EHIP, "affine: cannot grant %zu / %zu bytes of LDS", lds_gu, lds_dn);
-    if (grouped) {
-      hipLaunchKernelGGL((aff_gate_up_kernel<BITS, G, true>), dim3((unsigned)(a.max_tiles * (a.F / 16))),
-                         dim3(THREADS), lds_gu, s, a);
-      if (int rc = check_launch("aff_gate_up_kernel")) return rc;
-      hipLaunchKernelGGL((aff_down_kernel<BITS, G, true>), dim3((unsigned)(a.D / 16), (unsigned)a.max_tiles),
-                         dim3(THREADS), lds_dn, s, a);
-      return check_launch("aff_down_kernel");
-    }
-    hipLaunchKernelGGL((aff_gate_up_kernel<BITS, G, false>), dim3((unsigned)(a.k * (a.F / 16))), dim3(THREADS),
-                       lds_gu, s, a);
-    if (int rc = check_launch("aff_gate_up_kernel")) return rc;
-    hipLaunchKernelGGL((aff_down_kernel<BITS, G, false>), dim3((unsigned)(a.D / 16)), dim3(THREADS), lds_dn, s, a);
-    return check_launch("aff_down_kernel");
+    const int kmax = std::max((a.D + G - 1) / G * G, (a.F + G - 1) / G * G);
+    return kmax <= 64 * 2 * UNIT ? run_decode<BITS, G, 2>(a, grouped, s) : run_decode<BITS, G, 4>(a, grouped, s);
   }
 };
 
@@ -390,7 +519,7 @@ template <int BITS, int G>
 struct Dequant {
   static int run(const uint32_t* w, const uint16_t* sc, const uint16_t* bi, int N, int K, int row_words, int groups,
                  bool f16, float* out, hipStream_t s) {
-    const int64_t total = (int64_t)N * ((K + G - 1) / G);
+    const int64_t total = (int64_t)N * ((K + UNIT - 1) / UNIT);
     hipLaunchKernelGGL((aff_dequant_kernel<BITS, G>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, w, sc,
                        bi, N, K, row_words, groups, f16, out);
     return check_launch("aff_dequant_kernel");
