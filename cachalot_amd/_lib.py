@@ -129,6 +129,8 @@ _SIGNATURES = {
     "cachalot_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
     "cachalot_requant_fp4_to_q2": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
                                            c_void_p]),
+    "cachalot_requant_fp4_to_affine": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p,
+                                               c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "cachalot_moe_decode_affine_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "cachalot_moe_decode_affine": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p, c_void_p,
                                            c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p,

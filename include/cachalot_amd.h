@@ -331,11 +331,33 @@ int cachalot_stream_read(const void* src, size_t bytes, uint32_t* sink, int bloc
  * bias rounded (RNE) to the storage type, codes
  * recomputed against them; a partial last group fits its real elements and
  * pads with code 0.  Replaces quantize_affine(fit=fit_search) over the FP4
- * checkpoint (benchmarks/quant_affine.py:157-205,330-359,
- * build_affine_bank.py:165-189). */
+ * checkpoint (benchmarks/quant_affine.py:138-186,303-329,
+ * build_affine_bank.py:162-189). */
 int cachalot_requant_fp4_to_q2(const uint8_t* w_fp4, const uint8_t* s_fp4, int N, int K, uint32_t* q,
                                uint16_t* scales, uint16_t* biases, int scale_dtype,
                                cachalot_stream_t stream);
+
+/* The bank tool's fits (benchmarks/build_affine_bank.py:74-75, FITS; "mlx",
+ * MLX's own quantizer, is not offered). */
+#define CACHALOT_FIT_MINMAX 0     /* fit_minmax, quant_affine.py:138-149 */
+#define CACHALOT_FIT_SEARCH 1     /* fit_search over SHRINKS (5 x 5), :155-186 */
+#define CACHALOT_FIT_SEARCH_LSQ 2 /* fit_search, then 4 least-squares refits, :207-261 */
+#define CACHALOT_FIT_WIDE_LSQ 3   /* fit_search over SHRINKS_WIDE (9 x 9), then the refits, :281-287 */
+
+/* FP4 -> affine requantization at every width the bank tool writes: bits 2, 3
+ * or 4, groups of 32, 64 or 128, fit CACHALOT_FIT_*, optionally weighted per
+ * column by importance [K] fp32 (device; null = unweighted), the activation
+ * weighting of quantize_affine(importance=...) (quant_affine.py:126-135,303-329).
+ * q [N, Kp*bits/32] u32 (each row one little-endian bit stream), scales /
+ * biases [N, Kp/group] bf16 or fp16 (scale_dtype), Kp = K rounded up to the
+ * group.  A refit step rounds its pair to the storage type and keeps the
+ * previous pair where the normal equations are singular or the new scale is not
+ * positive; the best iterate (strictly smaller error) is the fit.  Replaces
+ * quantize_affine(w, group, bits, FITS[fit], importance) over the FP4
+ * checkpoint (build_affine_bank.py:162-189). */
+int cachalot_requant_fp4_to_affine(const uint8_t* w_fp4, const uint8_t* s_fp4, int N, int K, int bits, int group,
+                                   int fit, const float* importance, uint32_t* q, uint16_t* scales,
+                                   uint16_t* biases, int scale_dtype, cachalot_stream_t stream);
 
 /* Affine banks of the other widths the reference's bank tool writes
  * (benchmarks/build_affine_bank.py:266-267): bits 2, 3 or 4 per code, groups of

@@ -97,3 +97,78 @@ def test_partial_last_group_fits_real_elements_only():
     # the last group's fit equals the fit of its 32 real values alone
     s, b = R.fit_search(dense[:, 128:], np.ones((8, 32), bool))
     assert np.array_equal(sb[:, 1], f32_to_bf16_bits(s[:, 0])) and np.array_equal(bb[:, 1], f32_to_bf16_bits(b[:, 0]))
+
+
+def _rel(dense, packed, sb, bb, group, bits):
+    from oracle.affine2 import dequantize_affine
+
+    got = dequantize_affine(packed, sb, bb, k=dense.shape[1], group=group, bits=bits).astype(np.float64)
+    return float(np.linalg.norm(got - dense) / np.linalg.norm(dense))
+
+
+def test_lsq_refinement_never_loses_to_the_grid_it_refines():
+    """The reference's own pin (tests/test_quant_affine.py:112-126): per group the refinement
+    keeps the grid's fit unless it beats it, so search-lsq <= search and wide-lsq <= search-lsq
+    on Gaussian weights; levels stay inside the width."""
+    from oracle.affine2 import unpack_bits
+
+    rng = np.random.default_rng(15)
+    w = rng.standard_normal((32, 512)).astype(np.float32)
+    for group in (64, 128):
+        err = {f: _rel(w, *R.requantize(w, group, fit_name=f), group, 2) for f in ("search", "search-lsq", "wide-lsq")}
+        assert err["search-lsq"] <= err["search"] and err["wide-lsq"] <= err["search-lsq"], err
+    packed, _, _ = R.requantize(w, 128, fit_name="wide-lsq")
+    assert unpack_bits(packed, 2).max() <= 3
+
+
+def test_lsq_step_is_the_least_squares_line():
+    """With the levels fixed, the refit is the float64 least-squares line through (q, w)
+    (numpy.polyfit), rounded to bf16 -- an independent closed form."""
+    rng = np.random.default_rng(3)
+    w = rng.standard_normal((6, 64)).astype(np.float32)
+    v = np.ones_like(w, bool)
+    s, b = R.fit_search(w, v)
+    ns, nb = R.lsq_step(w, v, s, b)
+    q = R._q(w, s, b)
+    for i in range(6):
+        slope, icpt = np.polyfit(q[i].astype(np.float64), w[i].astype(np.float64), 1)
+        assert abs(ns[i, 0] - slope) <= 2 ** -7 * abs(slope) + 1e-6
+        assert abs(nb[i, 0] - icpt) <= 2 ** -7 * abs(icpt) + 1e-6
+
+
+def test_search_fit_beats_minmax_every_width_and_group():
+    """tests/test_quant_affine.py:70-86 and :206-220 at 2 and 3 bits, every group size; 4 bits too."""
+    rng = np.random.default_rng(13)
+    w = rng.standard_normal((32, 512)).astype(np.float32)
+    for bits in (2, 3, 4):
+        for group in (32, 64, 128):
+            e_s = _rel(w, *R.requantize(w, group, bits=bits), group, bits)
+            e_m = _rel(w, *R.requantize(w, group, bits=bits, fit_name="minmax"), group, bits)
+            assert e_s < e_m, (bits, group)
+    e2 = _rel(w, *R.requantize(w, 64, bits=2), 64, 2)
+    e3 = _rel(w, *R.requantize(w, 64, bits=3), 64, 3)
+    e4 = _rel(w, *R.requantize(w, 64, bits=4), 64, 4)
+    assert e4 < e3 < e2
+
+
+def test_importance_weighting():
+    """quant_affine.py:125-134: unit importance is the unweighted fit bit for bit; columns of
+    zero importance do not move the fit; the weighted error on the important columns is no
+    worse than the unweighted fit's."""
+    rng = np.random.default_rng(21)
+    w = rng.standard_normal((8, 256)).astype(np.float32)
+    for f in ("search", "search-lsq", "wide-lsq"):
+        a = R.requantize(w, 64, fit_name=f)
+        b = R.requantize(w, 64, fit_name=f, importance=np.ones(256, np.float32))
+        assert all(np.array_equal(x, y) for x, y in zip(a, b)), f
+    # the weighted search picks, among the same candidates, the one of least weighted error:
+    # never worse (in its own float32 error) than the unweighted winner
+    imp = rng.uniform(0.0, 2.0, size=256).astype(np.float32)
+    g = w.reshape(-1, 64)
+    v = np.ones_like(g, bool)
+    wts = np.tile(imp.reshape(-1, 64), (8, 1))
+    s_u, b_u = R.fit_search(g, v)
+    s_w, b_w = R.fit_search(g, v, weights=wts)
+    e_u = R.group_error(g, v, s_u, b_u, weights=wts)
+    e_w = R.group_error(g, v, s_w, b_w, weights=wts)
+    assert np.all(e_w <= e_u) and np.any(e_w < e_u)
