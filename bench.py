@@ -49,10 +49,11 @@ def parse():
                     help="measurement aid: time plain streaming reads of 24, 60 and 288 MB and print them (JSON)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="profiling aid: three plain 1 GiB device copies (HBM counter calibration) and exit")
-    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared", "sharedfp8", "widths"),
+    ap.add_argument("--only", choices=("prefill", "batched", "fp4", "shared", "sharedfp8", "widths", "requant"),
                     help="profiling aid: run one secondary measurement alone (config 3 prefill, config 2 "
                          "batched decode over --layers resident layers, config 0 FP4 decode, config 1's layer "
-                         "with the FP8 shared expert, or the shared expert alone), print its JSON and exit")
+                         "with the FP8 shared expert, the shared expert alone, the other affine widths, or the requantizer), "
+                         "print its JSON and exit")
     return ap.parse_args()
 
 
@@ -563,8 +564,9 @@ def shared_expert_fp8(args, dev, log_fn):
 
 
 def requant_bank(args, dev, log_fn):
-    """FP4 -> 2-bit g128 requantization (searched fit) of whole experts at the layer's shape, on the GPU:
-    time per expert and the implied time for the 40 x 384 bank (device work only, no disk)."""
+    """FP4 -> affine requantization of whole experts at the layer's shape, on the GPU: time per expert and
+    the implied time for the 40 x 384 bank (device work only, no disk).  The default bank (2-bit g128,
+    searched fit), then the other fits and the oQ3e width as side lines."""
     import torch
 
     from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
@@ -572,32 +574,43 @@ def requant_bank(args, dev, log_fn):
     from cachalot_amd.storage.index import affine_format, fp4_format
 
     D, F, N = 4096, 2880, 8
-    sf, df = fp4_format(D, F), affine_format(D, F)
+    sf = fp4_format(D, F)
     src = ResidentExpertStore(fmt=sf, n_slots=N, n_layers=1, n_experts=N, device=dev)
     src.preload([(0, e) for e in range(N)], SyntheticLoader(sf, args.seed + 5).fill_key)
-    dst = ResidentExpertStore(fmt=df, n_slots=N, n_layers=1, n_experts=N, device=dev)
-    slots = [dst.pool.acquire_index(e) for e in range(N)]
 
-    def run():
-        for e in range(N):
-            requantize_expert(src._items[(0, e)].arrays, sf, slots[e].arrays, df)
+    def time_fit(df, fit):
+        dst = ResidentExpertStore(fmt=df, n_slots=N, n_layers=1, n_experts=N, device=dev)
+        slots = [dst.pool.acquire_index(e) for e in range(N)]
 
-    run()
-    torch.cuda.synchronize()
-    reps = 3
-    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(reps):
+        def run():
+            for e in range(N):
+                requantize_expert(src._items[(0, e)].arrays, sf, slots[e].arrays, df, fit=fit)
+
         run()
-    e.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(e) / (reps * N)
+        torch.cuda.synchronize()
+        reps = 3
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            run()
+        e.record()
+        torch.cuda.synchronize()
+        del dst
+        return a.elapsed_time(e) / (reps * N)
+
+    ms = time_fit(affine_format(D, F), "search")
     res = {"ms_per_expert": round(ms, 3), "experts_per_s": round(1e3 / ms, 1),
            "bank_40x384_s": round(ms * 40 * 384 / 1e3, 1),
            "note": "per expert: three matrices, 3 x 2880 x 32 groups of 128 (w2 23 groups per row), 25 fit "
-                   "candidates each; device work only"}
+                   "candidates each; device work only", "other_fits": {}}
     log_fn(f"requant FP4 -> 2-bit: {ms:.3f} ms/expert, bank {res['bank_40x384_s']} s")
-    del src, dst
+    for name, bits, group, sd, fit in (("2-bit g128 bf16, search-lsq", 2, 128, "bfloat16", "search-lsq"),
+                                       ("2-bit g128 bf16, wide-lsq", 2, 128, "bfloat16", "wide-lsq"),
+                                       ("3-bit g64 fp16 (oQ3e), search", 3, 64, "float16", "search")):
+        m = time_fit(affine_format(D, F, bits=bits, group_size=group, scale_dtype=sd), fit)
+        res["other_fits"][name] = {"ms_per_expert": round(m, 3), "bank_40x384_s": round(m * 40 * 384 / 1e3, 1)}
+        log_fn(f"requant FP4 -> {name}: {m:.3f} ms/expert")
+    del src
     torch.cuda.empty_cache()
     return res
 
@@ -749,6 +762,10 @@ def main() -> int:
     if args.only == "fp4":
         _lib.lib()
         print(json.dumps(fp4_decode_config0(args, dev, log)), flush=True)
+        return 0
+    if args.only == "requant":
+        _lib.lib()
+        print(json.dumps(requant_bank(args, dev, log)), flush=True)
         return 0
     if args.only == "widths":
         _lib.lib()

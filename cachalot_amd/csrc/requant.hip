@@ -64,7 +64,7 @@ __device__ __forceinline__ float weight_at(const float* a, int i, int nvalid) {
   return a && i < nvalid ? a[i] : 1.0f;
 }
 
-template <int G>
+template <int G, bool W>
 __device__ __forceinline__ float group_error(const float (&w)[G], const float* a, int nvalid, float scale,
                                              float bias, float levels) {
   float err = 0.0f;
@@ -72,14 +72,14 @@ __device__ __forceinline__ float group_error(const float (&w)[G], const float* a
   for (int i = 0; i < G; ++i) {
     const float d = scale * level(w[i], scale, bias, levels) + bias - w[i];
     float sq = d * d;
-    if (a) sq = weight_at(a, i, nvalid) * sq;
+    if constexpr (W) sq = weight_at(a, i, nvalid) * sq;
     if (i < nvalid) err = err + sq;
   }
   return err;
 }
 
 // One assign-then-refit step.
-template <int G>
+template <int G, bool W>
 __device__ __forceinline__ void lsq_step(const float (&w)[G], const float* a, int nvalid, float& scale,
                                          float& bias, float levels, bool f16) {
   float n = 0.0f, sq = 0.0f, sqq = 0.0f, sw = 0.0f, sqw = 0.0f;
@@ -87,7 +87,7 @@ __device__ __forceinline__ void lsq_step(const float (&w)[G], const float* a, in
   for (int i = 0; i < G; ++i) {
     if (i < nvalid) {
       const float q = level(w[i], scale, bias, levels);
-      const float ai = weight_at(a, i, nvalid);
+      const float ai = W ? weight_at(a, i, nvalid) : 1.0f;
       const float aq = ai * q;
       n = n + ai;
       sq = sq + aq;
@@ -107,7 +107,7 @@ __device__ __forceinline__ void lsq_step(const float (&w)[G], const float* a, in
   }
 }
 
-template <int BITS, int G>
+template <int BITS, int G, bool W>
 __global__ __launch_bounds__(256) void requant_kernel(Args p) {
   constexpr float LEVELS = (float)((1 << BITS) - 1);
   constexpr int WORDS = G * BITS / 32;
@@ -155,14 +155,14 @@ __global__ __launch_bounds__(256) void requant_kernel(Args p) {
     const bool wide = p.fit == CACHALOT_FIT_WIDE_LSQ;
     const float* shr = wide ? kShrinksWide : kShrinks;
     const int ns = wide ? 9 : 5;
-    float best = group_error<G>(w, a, nvalid, best_s, best_b, LEVELS);
+    float best = group_error<G, W>(w, a, nvalid, best_s, best_b, LEVELS);
     for (int x = 0; x < ns; ++x) {
       for (int y = 0; y < ns; ++y) {
         if (x == 0 && y == 0) continue;
         const float new_lo = mid + (lo - mid) * shr[x];
         const float new_hi = mid + (hi - mid) * shr[y];
         const float s = fmaxf((new_hi - new_lo) / LEVELS, 1e-8f);
-        const float err = group_error<G>(w, a, nvalid, s, new_lo, LEVELS);
+        const float err = group_error<G, W>(w, a, nvalid, s, new_lo, LEVELS);
         if (err < best) {
           best_s = s;
           best_b = new_lo;
@@ -175,10 +175,10 @@ __global__ __launch_bounds__(256) void requant_kernel(Args p) {
     float s = store_round(best_s, p.f16), b = store_round(best_b, p.f16);
     best_s = s;
     best_b = b;
-    float best = group_error<G>(w, a, nvalid, s, b, LEVELS);
+    float best = group_error<G, W>(w, a, nvalid, s, b, LEVELS);
     for (int it = 0; it < LSQ_ITERS; ++it) {
-      lsq_step<G>(w, a, nvalid, s, b, LEVELS, p.f16);
-      const float err = group_error<G>(w, a, nvalid, s, b, LEVELS);
+      lsq_step<G, W>(w, a, nvalid, s, b, LEVELS, p.f16);
+      const float err = group_error<G, W>(w, a, nvalid, s, b, LEVELS);
       if (err < best) {
         best_s = s;
         best_b = b;
@@ -210,7 +210,9 @@ __global__ __launch_bounds__(256) void requant_kernel(Args p) {
 template <int BITS, int G>
 int launch(const Args& a, hipStream_t s) {
   const long groups = (long)a.N * ((a.K + G - 1) / G);
-  hipLaunchKernelGGL((requant_kernel<BITS, G>), dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, a);
+  const dim3 grid((unsigned)((groups + 255) / 256));
+  if (a.importance) hipLaunchKernelGGL((requant_kernel<BITS, G, true>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((requant_kernel<BITS, G, false>), grid, dim3(256), 0, s, a);
   return check_launch("requant_fp4_to_affine");
 }
 

@@ -3,8 +3,12 @@
 // reproducible bit for bit; reference: src/cachalot/model/router_mlx.py:29-37,
 // minimax/language.py:280-292):
 //   * D is cut into 64 contiguous chunks of D/64; lane l owns chunk l and adds
-//     its bf16*bf16 products (exact in fp32) sequentially in fp32 (an fma rounds
-//     the same exact sum once, so it is the same operation);
+//     its bf16*bf16 products sequentially in fp32 with fma.  A product of two bf16
+//     values has 16 significant bits, so it is exact in fp32 unless it falls below
+//     the normal range (|x w| < 2^-126); then a multiply-then-add rounds it and the
+//     fma does not, and the two can differ in the last bit.  Activations and gate
+//     weights of a real layer (|x|, |w| far above 2^-63) never come near that;
+//     the CPU restatement multiplies then adds;
 //   * the 64 partials are combined by the xor butterfly 1, 2, 4, 8, 16, 32;
 //   * logit = sum / gate_temp (fp32);
 //   * score functions use only IEEE basic operations (Cody-Waite exp with a

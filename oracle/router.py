@@ -22,7 +22,10 @@ The reference leaves the fp32 summation order of the logit dot product to MLX.
 This build fixes one so ids are reproducible bit for bit on any device:
 
 * D is split into 64 contiguous chunks (one per lane of a wave64); each chunk
-  is summed sequentially in fp32 from 0 (bf16 x bf16 products are exact in fp32);
+  is summed sequentially in fp32 from 0 (bf16 x bf16 products are exact in fp32
+  unless |x w| < 2^-126: there a separate multiply rounds the product and the
+  GPU's fma does not, so such inputs may differ in the last bit -- far outside
+  any real activation and gate weight);
 * the 64 partials are combined by the butterfly ``p[i] + p[i ^ s]`` for
   s = 1, 2, 4, 8, 16, 32 (pairwise summation over the chunks in natural order);
 * ``logit = tree / gate_temp`` in fp32.

@@ -169,9 +169,10 @@ def test_grouped_experts_batched_decode(cuda, kind):
                   + bf16_ulp(want + a))
 
 
-@pytest.mark.parametrize("t", [1, 4, 7])
+@pytest.mark.parametrize("t", [1, 4, 7, 200])
 def test_grouped_batched_routes_outside_range(cuda, t):
-    """The batched 2-bit decode permutes its routes inside the prep launch: ids outside
+    """The batched 2-bit decode permutes its routes inside the prep launch (up to 1,024
+    routes; T = 200, 1,200 routes, goes through the separate permute first): ids outside
     [0, E) are dropped (zero y rows, after every expert) and the rest match the oracle."""
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format
@@ -183,6 +184,9 @@ def test_grouped_batched_routes_outside_range(cuda, t):
     idx, w = _zipf_routes(rng, t, k, experts)
     idx[0, 1] = -3
     idx[t - 1, k - 1] = 384
+    if t > 7:
+        idx[t // 2, 0] = -3
+        idx[t // 3, 2] = 384
     store = make_store(fmt, n_layers=1, n_experts=384, keys=[(0, e) for e in experts], n_slots=len(experts))
     xb = osynth.activations(SEED, 410 + t, t, 4096)
     routed, _ = grouped_experts(_bf16(xb, cuda), torch.from_numpy(idx).to(cuda), torch.from_numpy(w).to(cuda),
