@@ -379,16 +379,16 @@ def fp4_decode_config0(args, dev, log_fn):
 
 
 def affine_width_decodes(args, dev, log_fn):
-    """Config 1 with the scale type BASELINE states (fp16 scales and biases), and the oQ3e bank
+    """Config 1 with the other scale type (bf16, the reference bank tool's), and the oQ3e bank
     (3-bit codes, groups of 64, fp16 scales: expert_affine.py:1-10), each chained over 8 resident
     layers."""
     from cachalot_amd.storage.index import affine_format
 
     out = {}
-    out["config1_fp16_scales"] = chained_decode(
-        args, dev, log_fn, affine_format(4096, 2880, scale_dtype="float16"), 8, 13, "config 1 fp16 scales",
-        "2-bit g128 bank with fp16 scales / biases (BASELINE config 1 as stated); the same matrix-core kernels, "
-        "the scales converted from fp16")
+    out["config1_bf16_scales"] = chained_decode(
+        args, dev, log_fn, affine_format(4096, 2880), 8, 13, "config 1 bf16 scales",
+        "2-bit g128 bank with bf16 scales / biases (the type of the reference's shipped bank, "
+        "build_affine_bank.py:76); the same matrix-core kernels as the fp16 headline")
     out["oq3e_3bit_g64_fp16"] = chained_decode(
         args, dev, log_fn, affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"), 8, 17,
         "oQ3e 3-bit g64 decode",
@@ -778,7 +778,7 @@ def main() -> int:
     _lib.lib()
     D, F, E, K = 4096, 2880, 384, 6
     L = args.layers
-    fmt = affine_format(D, F)
+    fmt = affine_format(D, F, scale_dtype="float16")   # configs[1]: fp16 scale and bias per group
     log(f"filling {L} layers x {E} experts ({L * E * fmt.expert_bytes / 1e9:.1f} GB) in HBM")
     t0 = time.time()
     loader = SyntheticLoader(fmt, args.seed)
@@ -954,10 +954,10 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded 2-bit affine g128 bank, sigmoid router; BASELINE configs[1])",
+        "data": "synthetic (seeded 2-bit affine g128 bank with fp16 scales / biases, sigmoid router; BASELINE configs[1])",
         "config": {
             "workload": "configs[1]: one MoE layer decode, B=1, d_model 4096, 384 experts top-6, d_ff 2880, "
-                        "2-bit affine g128 bank (bf16 scales/biases), chained over "
+                        "2-bit affine g128 bank (fp16 scales/biases), chained over "
                         f"{L} resident layers",
             "d_model": D, "d_ff": F, "experts": E, "topk": K, "batch": 1, "resident_layers": L,
             "parallelism": "single GPU",

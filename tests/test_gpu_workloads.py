@@ -14,8 +14,8 @@ in order in fp32 (``expert_affine.py:81,149-151``, ``moe_prefill_grouped.py:
 * the layer output against the oracle's own bf16 output, in bf16 ulps
   (reported, and bounded by the flips).
 
-Workloads: config 1's decode (two-kernel matrix-core, bf16-MFMA and one-launch
-paths), config 3's 4096-token Zipf prefill on the FP4 bank (tiled router at
+Workloads: config 1's decode (matrix-core and bf16-MFMA paths, bf16 and fp16
+scales), config 2 with a router-driven union, config 3's 4096-token Zipf prefill on the FP4 bank (tiled router at
 E = 384, experts spanning many 128-row tiles), config 4's chained decode over
 layers whose slots lie beyond 2^32 bytes, and the grouped path with experts of
 several tiles and with out-of-range route ids.

@@ -172,3 +172,18 @@ def test_importance_weighting():
     e_u = R.group_error(g, v, s_u, b_u, weights=wts)
     e_w = R.group_error(g, v, s_w, b_w, weights=wts)
     assert np.all(e_w <= e_u) and np.any(e_w < e_u)
+
+
+def test_lsq_step_keeps_the_pair_where_the_line_is_not_defined():
+    """A group whose levels collapse (every code equal: |den| < 1e-12) and a group whose
+    importance is zero throughout (a zero weight total) keep the pair they came in with."""
+    w = np.full((1, 64), 0.75, np.float32)
+    v = np.ones_like(w, bool)
+    s0, b0 = np.array([[0.25]], np.float32), np.array([[0.5]], np.float32)
+    ns, nb = R.lsq_step(w, v, s0, b0)
+    assert ns[0, 0] == s0[0, 0] and nb[0, 0] == b0[0, 0]
+    rng = np.random.default_rng(4)
+    w = rng.standard_normal((1, 64)).astype(np.float32)
+    s, b = R.fit_search(w, v)
+    ns, nb = R.lsq_step(w, v, s, b, weights=np.zeros_like(w))
+    assert ns[0, 0] == s[0, 0] and nb[0, 0] == b[0, 0]
