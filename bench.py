@@ -27,7 +27,7 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per decode (gate/up + down kernels) at config 1, from two rocprofv3
 # counter passes (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
 # plain 1 GiB device copy (read x 2.0, write x 1.0); summary under profiles/.
-PAIR_TRAFFIC_BYTES = 61_412_659
+PAIR_TRAFFIC_BYTES = 61_418_804
 METRIC = "MoE-layer decode tok/s + expert-byte HBM GB/s (B=1); prefill grouped-GEMM TFLOPS"
 
 
