@@ -33,7 +33,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     Decode calls on one device share it and must therefore be ordered (one
     stream, or streams that wait on each other); a HIP-graph capture must be
     preceded by an eager call of the same shape so that the workspace exists
-    before capture.  A new workspace is zero-filled: the fused layer calls keep
+    before capture.  A new workspace is zero-filled: the bf16-MFMA layer decode keeps
     a completion counter in its first bytes that must start at zero (every call
     leaves it zero)."""
     key = (device.index,)

@@ -112,3 +112,48 @@ def test_affine_grouped_rows(cuda, bits, group, sd):
         assert not yf[0, 1].any() and not yf[5, 5].any() and not yf[t - 1, 0].any()
         _grouped_check(f"grouped affine {bits}-bit g{group}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed),
                        _f32(out), yf, E, addend=bf16_bits_to_f32(ab))
+
+
+def test_affine_missing_slot_and_graph_replays(cuda):
+    """oQ3e (3-bit g64 fp16): an expert without a slot contributes exact zeros (routed = the route-order
+    sum of the other experts' one-expert terms, bit for bit), and a captured chain of device-routed layer
+    decodes replays identically, three times, with eager work and synchronisation between replays."""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_decode import decode_experts, moe_layer_decode
+    from helpers import route_order_sum
+    from test_gpu_workloads import _decode_terms
+
+    fmt = _fmt(3, 64, "float16")
+    store = make_store(fmt, n_layers=2, n_experts=384)
+    idx = [5, 77, 300, 12, 250, 199]
+    w = np.full(6, 1 / 6, np.float32)
+    x = synth.activations(SEED, 3400, 1, 4096, cuda)[0]
+    terms = _decode_terms(cuda, store, 0, x, idx, w)
+    store.track_slots()[0, 77] = -1
+    routed, _ = decode_experts(x, store.pool, store.layer_table(0), torch.tensor(idx, dtype=torch.int32, device=cuda),
+                               torch.from_numpy(w).to(cuda))
+    terms[1] = 0.0
+    assert np.array_equal(_np(routed).view(np.uint32), route_order_sum(terms).view(np.uint32))
+    gates = [synth.router_weights(SEED, la, 384, 4096, cuda) for la in range(2)]
+
+    def chain(x):
+        for s in range(4):
+            gw, gb = gates[s % 2]
+            _, x, _ = moe_layer_decode(x, gw, gb, store.pool, store.layer_table(1), topk=6, route_scale=1.0,
+                                       score_fn="sigmoid", addend=x)
+        return x
+
+    x0 = synth.activations(SEED, 3401, 1, 4096, cuda)[0]
+    eager = chain(x0)
+    torch.cuda.synchronize()
+    xbuf = x0.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = chain(xbuf)
+    for _ in range(3):
+        xbuf.copy_(x0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        _ = chain(x0)
+        torch.cuda.synchronize()
