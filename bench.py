@@ -392,8 +392,8 @@ def affine_width_decodes(args, dev, log_fn):
     out["oq3e_3bit_g64_fp16"] = chained_decode(
         args, dev, log_fn, affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"), 8, 17,
         "oQ3e 3-bit g64 decode",
-        "3-bit g64 fp16 bank (oQ3e) on the generic affine kernels (one lane per group, VALU), not the "
-        "matrix-core 2-bit path")
+        "3-bit g64 fp16 bank (oQ3e) on the block-scaled matrix cores (decode_affine_mx.hip: codes split into "
+        "low and high bit pairs, two fp4 instructions per 32 codes)")
     return out
 
 

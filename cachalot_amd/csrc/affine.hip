@@ -31,8 +31,18 @@
 
 #include "decode_common.h"
 #include "router_launch.h"
+#include "mx_tile.h"
 
 namespace cachalot {
+
+// decode_affine_mx.hip
+bool affine_mx_supported(int bits, int group, int D, int F, int k);
+size_t affine_mx_hidden_bytes(int k, int D, int F);
+int launch_affine_mx(const uint16_t* x, bool planes_ready, uint8_t* hid, uint8_t* xplanes, const uint8_t* pool,
+                     const decode::Layout& L, const decode::ExpertSource& src, int32_t* ws_slots, float* ws_w, int D,
+                     int F, int k, int bits, int group, float limit, const uint16_t* addend, float* routed,
+                     uint16_t* out, hipStream_t s);
+
 namespace aff {
 
 using namespace decode;
@@ -539,6 +549,19 @@ int check_shape(const char* who, int D, int F, int bits, int group) {
 
 size_t hidden_bytes(int rows, int F) { return align256((size_t)rows * ((F + 127) / 128 * 128) * 2); }
 
+// The decode workspace's hidden region: the VALU kernels' bf16 h rows or the
+// matrix-core kernels' plane blocks (h, then x), whichever is larger.
+size_t decode_hidden_bytes(int k, int D, int F) {
+  return std::max(hidden_bytes(k, F), affine_mx_hidden_bytes(k, D, F));
+}
+
+// The VALU kernels stay selectable for the widths the matrix-core kernels take
+// (CACHALOT_AFFINE_VALU=1), so that the tests hold both to the oracle.
+bool valu_requested() {
+  const char* env = getenv("CACHALOT_AFFINE_VALU");
+  return env && env[0] == '1';
+}
+
 int decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout, ExpertSource src,
            const RouterCall* router, int D, int F, int k, int bits, int group, float limit, const uint16_t* addend,
            float* routed, uint16_t* out, void* workspace, size_t workspace_bytes, hipStream_t s) {
@@ -547,13 +570,28 @@ int decode(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout*
   CACHALOT_REQUIRE(k >= 1 && k <= KMAX, "moe_decode_affine: k=%d outside 1..%d", k, KMAX);
   CACHALOT_REQUIRE(src.E >= 1 && src.E <= 1024, "moe_decode_affine: E=%d outside 1..1024", src.E);
   if (int rc = check_shape("moe_decode_affine", D, F, bits, group)) return rc;
-  const WsOffsets wo = ws_offsets(hidden_bytes(k, F));
+  const WsOffsets wo = ws_offsets(decode_hidden_bytes(k, D, F));
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "moe_decode_affine: workspace %zu < %zu bytes", workspace_bytes, wo.total);
   Args a{};
   static const int used[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
   if (int rc = make_layout(layout, 9, used, a.L, "moe_decode_affine")) return rc;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
+  if (affine_mx_supported(bits, group, D, F, k) && !valu_requested()) {
+    // the block-scaled matrix-core kernels (decode_affine_mx.hip): h planes, then x planes,
+    // which the router launch writes when there is one
+    uint8_t* hid = ws + wo.hidden;
+    uint8_t* xplanes = hid + align256((size_t)k * ((F + 127) / 128) * mx::PB_BYTES);
+    if (router) {
+      if (int rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
+                                        router->scores, s, nullptr, xplanes))
+        return rc;
+      src = route_source(src, *router);
+    }
+    return launch_affine_mx(x, router != nullptr, hid, xplanes, pool, a.L, src,
+                            reinterpret_cast<int32_t*>(ws + wo.slots), reinterpret_cast<float*>(ws + wo.weights), D,
+                            F, k, bits, group, limit, addend, routed, out, s);
+  }
   if (router) {
     if (int rc = launch_router_scores(x, router->gate_weight, 1, D, src.E, router->gate_temp, router->score_fn,
                                       router->scores, s))
@@ -583,7 +621,7 @@ using namespace cachalot;
 
 extern "C" size_t cachalot_moe_decode_affine_workspace_bytes(int D, int F, int k) {
   if (D <= 0 || F <= 0 || k <= 0 || k > decode::KMAX) return 0;
-  return decode::ws_offsets(aff::hidden_bytes(k, F)).total;
+  return decode::ws_offsets(aff::decode_hidden_bytes(k, D, F)).total;
 }
 
 extern "C" int cachalot_moe_decode_affine(const uint16_t* x, const uint8_t* pool, const cachalot_expert_layout* layout,

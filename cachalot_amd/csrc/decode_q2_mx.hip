@@ -79,14 +79,7 @@ struct DnLds {
   float y[KMAX][16];
 };
 
-// Copy `bytes` (a multiple of 16) into LDS with untracked direct-to-LDS loads
-// (tile::lds_load16_untracked): 1 KiB chunks c = part, part + parts, ...  The
-// caller waits (wait_vmem) before the data is read.
-__device__ __forceinline__ void copy_to_lds_untracked(const uint8_t* src, uint8_t* dst, int bytes, int part,
-                                                      int parts, int lane) {
-  for (int c = part * 1024; c < bytes; c += parts * 1024)
-    if (c + 16 * lane < bytes) tile::lds_load16_untracked(src + c + 16 * lane, dst + c);
-}
+using tile::copy_to_lds_untracked;
 
 // x (one token) as fp8 plane blocks, for calls whose experts are given (no router launch).
 __global__ void __launch_bounds__(256) x_planes_kernel(const uint16_t* __restrict__ x, int D,
@@ -850,6 +843,12 @@ __global__ void __launch_bounds__(GU_THREADS) q2mx_bdn4_kernel(BatchArgs a) {
 }
 
 }  // namespace
+
+// x (one token) as plane blocks, for decode calls whose router launch did not write them.
+int launch_x_planes(const uint16_t* x, int D, uint8_t* xplanes, hipStream_t s) {
+  hipLaunchKernelGGL(x_planes_kernel, dim3((D / 4 + 255) / 256), dim3(256), 0, s, x, D, xplanes);
+  return check_launch("x_planes_kernel");
+}
 
 // The shapes the matrix-core path takes (the rest use the bf16 kernels).
 bool q2mx_supported(int D, int F, int k) {

@@ -145,6 +145,19 @@ __device__ __forceinline__ void lds_load16_untracked(const void* src, void* lds)
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(src) : "memory", "m0");
 }
 
+// Copy `bytes` (a multiple of 16) into LDS with untracked direct-to-LDS loads: 1 KiB
+// chunks c = part, part + parts, ...  The caller waits (wait_vmem, or a wait count
+// for register loads issued later) before the data is read.
+__device__ __forceinline__ void copy_to_lds_untracked(const uint8_t* src, uint8_t* dst, int bytes, int part,
+                                                      int parts, int lane) {
+  for (int c = part * 1024; c < bytes; c += parts * 1024)
+    if (c + 16 * lane < bytes) lds_load16_untracked(src + c + 16 * lane, dst + c);
+}
+
+// s_waitcnt immediate (gfx9 encoding) for "at most n vector-memory loads of this wave
+// still outstanding", expcnt and lgkmcnt unconstrained; n < 64.
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 // Wait until every vector-memory load of this wave has landed (registers and LDS).
 // (The builtin, unlike inline asm, is visible to the compiler's wait-count tracking, so
 // it knows that LDS written by direct-to-LDS loads is complete after it.)

@@ -246,6 +246,37 @@ __device__ __forceinline__ void chain_load(Chain& ch, const uint8_t* blk, const 
   if (ro.scale) ch.sa = lds32(blk + PB_SCALE + (ro.halfR * 2 + ro.planeR) * 4);
 }
 
+// mfma_fp8_fp4 with the A scale byte chosen by a step index (a constant once the
+// caller's step loop is unrolled).
+__device__ __forceinline__ f32x4_t mfma_fp8_fp4_sel(int step, const i32x8_t& a, const i32x8_t& b, f32x4_t c,
+                                                    uint32_t sa, uint32_t sb) {
+  switch (step & 3) {
+    case 0: return mfma_fp8_fp4<0>(a, b, c, sa, sb);
+    case 1: return mfma_fp8_fp4<1>(a, b, c, sa, sb);
+    case 2: return mfma_fp8_fp4<2>(a, b, c, sa, sb);
+    default: return mfma_fp8_fp4<3>(a, b, c, sa, sb);
+  }
+}
+
+// One step of a chain into a single persistent operand `a` (set up like a chain's
+// registers: zeros, written once): only the lane's data half is rewritten, from
+// chunk c's 16 bytes of the plane block.  The step scales come from chain_scales.
+__device__ __forceinline__ void chain_load_step(i32x8_t& a, const uint8_t* blk, const ARole& ro, int c) {
+  const uint8_t* src = blk + (ro.halfR * 2 + ro.planeR) * 64 + 16 * c;
+  if (ro.lo) {
+    const uint4 d = lds16(src);
+    a[0] = (int)d.x; a[1] = (int)d.y; a[2] = (int)d.z; a[3] = (int)d.w;
+  }
+  if (ro.hi) {
+    const uint4 d = lds16(src);
+    a[4] = (int)d.x; a[5] = (int)d.y; a[6] = (int)d.z; a[7] = (int)d.w;
+  }
+}
+// The scale lanes' four chunk scales of a plane block (byte c for chunk c).
+__device__ __forceinline__ void chain_scales(uint32_t& sa, const uint8_t* blk, const ARole& ro) {
+  if (ro.scale) sa = lds32(blk + PB_SCALE + (ro.halfR * 2 + ro.planeR) * 4);
+}
+
 __device__ __forceinline__ float dot4(const f32x4_t& d) { return (d[0] + d[1]) + (d[2] + d[3]); }
 
 // Sum of the first `npieces` piece sums of a plane block (fixed order).

@@ -3,8 +3,9 @@ scales): oQ3e is 3-bit g64 with fp16 scales (expert_affine.py:1-10), and the ban
 tool writes bits 2/3/4 x groups 32/64/128 (build_affine_bank.py:266-267).
 
 * dequantisation bit-exact against oracle/affine2.py (the MLX bit-stream layout);
-* decode at the layer's shape, per-expert terms against the oracle's rounding
-  points (helpers.term_flips), routed = the route-order sum bit for bit,
+* decode at the layer's shape (block-scaled matrix-core kernels for every width,
+  and the VALU kernels), per-expert terms against the oracle's rounding points
+  (helpers.term_flips), routed = the route-order sum bit for bit,
   out = bf16(routed + addend) bit for bit; the device-routed layer with ids
   bit-exact;
 * grouped (prefill / batched) rows against the oracle, dropped ids giving zeros.
@@ -57,12 +58,21 @@ def test_affine_dequant_and_fill_bit_exact(cuda, bits, group, sd):
         assert np.array_equal(_np(slot.arrays[name]), arr.view(np.uint8).reshape(-1)), name
 
 
-@pytest.mark.parametrize("bits,group,sd", WIDTHS[:2])
-def test_affine_decode_terms(cuda, bits, group, sd):
-    """Given experts (two tokens) and the device-routed layer (one token)."""
+DECODE_CASES = [(3, 64, "float16", "mx"), (4, 32, "bfloat16", "mx"), (3, 128, "bfloat16", "mx"),
+                (2, 64, "float16", "mx"), (4, 128, "float16", "mx"), (2, 32, "bfloat16", "mx"),
+                (3, 32, "float16", "mx"), (4, 64, "bfloat16", "mx"),
+                (3, 64, "float16", "valu"), (4, 32, "bfloat16", "valu")]
+
+
+@pytest.mark.parametrize("bits,group,sd,path", DECODE_CASES)
+def test_affine_decode_terms(cuda, bits, group, sd, path, monkeypatch):
+    """Given experts (two tokens) and the device-routed layer (one token), on the block-scaled
+    matrix-core kernels (the default at these shapes) and the VALU kernels
+    (CACHALOT_AFFINE_VALU=1)."""
     from cachalot_amd import synth
     from cachalot_amd.moe_decode import decode_experts, moe_layer_decode
 
+    monkeypatch.setenv("CACHALOT_AFFINE_VALU", "1" if path == "valu" else "0")
     fmt = _fmt(bits, group, sd)
     store = make_store(fmt, n_layers=1, n_experts=384)
     rng = np.random.default_rng(bits * 100 + group)
@@ -76,7 +86,7 @@ def test_affine_decode_terms(cuda, bits, group, sd):
                                                                                        device=cuda),
                                      torch.tensor(w, device=cuda), addend=a)
         terms = _decode_terms(cuda, store, 0, x, idx, w)
-        _check_decode(f"affine {bits}-bit g{group} {sd} token {tk}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
+        _check_decode(f"affine {bits}-bit g{group} {sd} {path} token {tk}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
                       _np(routed), _f32(out), terms, bf16_bits_to_f32(ab))
     gw, gb = synth.router_weights(SEED, 0, 384, 4096, cuda)
     x = synth.activations(SEED, 3200, 1, 4096, cuda)[0]
@@ -87,7 +97,7 @@ def test_affine_decode_terms(cuda, bits, group, sd):
     assert np.array_equal(_np(route.indices), oi[0])
     assert np.array_equal(_np(route.weights).view(np.uint32), ow[0].view(np.uint32))
     terms = _decode_terms(cuda, store, 0, x, oi[0], ow[0])
-    _check_decode(f"affine {bits}-bit g{group} layer", fmt, 0, xf, oi[0], ow[0], _np(routed), _f32(out), terms, xf)
+    _check_decode(f"affine {bits}-bit g{group} {path} layer", fmt, 0, xf, oi[0], ow[0], _np(routed), _f32(out), terms, xf)
 
 
 @pytest.mark.parametrize("bits,group,sd", WIDTHS[:2])
