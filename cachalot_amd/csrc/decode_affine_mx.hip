@@ -64,7 +64,6 @@ struct Geo {
   static constexpr int STEPS = G / 32;                  // instructions (per part) per group
   static constexpr int W = G * BITS / 32;               // u32 words of one group of one row
   static constexpr int LDI = W % 4 == 0 ? W / 4 : (W % 2 == 0 ? W / 2 : W);   // load instructions per group
-  static constexpr int PARTS = BITS == 2 ? 1 : 2;       // instructions per step and matrix
 };
 
 // The W words of one group of one row (16-, 8- or 4-byte loads as the group's
