@@ -381,7 +381,7 @@ def fp4_decode_config0(args, dev, log_fn):
 def affine_width_decodes(args, dev, log_fn):
     """Config 1 with the other scale type (bf16, the reference bank tool's), and the oQ3e bank
     (3-bit codes, groups of 64, fp16 scales: expert_affine.py:1-10), each chained over 8 resident
-    layers."""
+    layers; config 3's prefill over the 2-bit g128 and the oQ3e banks."""
     from cachalot_amd.storage.index import affine_format
 
     out = {}
@@ -389,12 +389,58 @@ def affine_width_decodes(args, dev, log_fn):
         args, dev, log_fn, affine_format(4096, 2880), 8, 13, "config 1 bf16 scales",
         "2-bit g128 bank with bf16 scales / biases (the type of the reference's shipped bank, "
         "build_affine_bank.py:76); the same matrix-core kernels as the fp16 headline")
+    for key, f, note in (("prefill_4096_2bit_g128", affine_format(4096, 2880),
+                          "2-bit g128 bf16 bank: bf16 matrix cores with the codes converted in registers"),
+                         ("prefill_4096_oq3e", affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"),
+                          "oQ3e bank: the same bf16-MFMA grouped kernels, 3-bit codes converted per step")):
+        out[key] = prefill_affine(args, dev, log_fn, f, key, note)
     out["oq3e_3bit_g64_fp16"] = chained_decode(
         args, dev, log_fn, affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"), 8, 17,
         "oQ3e 3-bit g64 decode",
         "3-bit g64 fp16 bank (oQ3e) on the block-scaled matrix cores (decode_affine_mx.hip: codes split into "
         "low and high bit pairs, two fp4 instructions per 32 codes)")
     return out
+
+
+def prefill_affine(args, dev, log_fn, fmt, label, note):
+    """Config 3's prefill (4096 tokens, Zipf-skewed routing, one layer: router, permute, grouped
+    gate/up and down, combine) over an affine bank."""
+    import torch
+
+    from cachalot_amd import synth
+    from cachalot_amd.cache.resident_store import ResidentExpertStore, SyntheticLoader
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.router import route_topk_rows
+
+    D, F, E, K, T = fmt.d_model, fmt.d_ff, 384, 6, 4096
+    store = ResidentExpertStore(fmt=fmt, n_slots=E, n_layers=1, n_experts=E, device=dev)
+    store.preload([(0, e) for e in range(E)], SyntheticLoader(fmt, args.seed + 3).fill_key)
+    w, b = synth.router_weights(args.seed + 3, 0, E, D, dev)
+    b = b + torch.tensor(synth.zipf_bias(E, seed=args.seed), dtype=torch.float32, device=dev)
+    x = synth.activations(args.seed + 3, 0, T, D, dev)
+    table = store.layer_table(0)
+
+    def layer():
+        idx, wt, _ = route_topk_rows(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+        return grouped_experts(x, idx, wt, store.pool, table)
+
+    layer()
+    torch.cuda.synchronize()
+    reps = 3
+    a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        layer()
+    e.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(e) / reps
+    tflops = 2.0 * T * K * 3 * D * F / (ms * 1e-3) / 1e12
+    res = {"ms_per_layer": round(ms, 3), "tflops": round(tflops, 1), "frac_bf16_mfma_peak": round(tflops / 2500.0, 4),
+           "expert_bytes": fmt.algorithmic_bytes, "note": note}
+    log_fn(f"{label}: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s")
+    del store
+    torch.cuda.empty_cache()
+    return res
 
 
 def prefill_config3(args, dev, log_fn):
@@ -450,8 +496,9 @@ def prefill_config3(args, dev, log_fn):
                         "note": "1.739 TFLOP over >= the touched experts' FP4 bytes: 256 FLOP/B, below the MXFP4 "
                                 "ridge (1,250 FLOP/B), so the attainable bound is HBM"},
            "_counts": counts.cpu().tolist(),
-           "note": "block-scaled fp8 x fp4 matrix cores (x and h as two exact fp8 planes, FP4 codes and E8M0 "
-                   "scales as stored), routing + permute + grouped gate/up + down + combine, eager launches"}
+           "note": "block-scaled fp8 x fp4 matrix cores (x and h as two fp8 planes per 32-element block, exact for "
+                   "values within 2^13 of the block's largest; FP4 codes and E8M0 scales as stored), routing + "
+                   "permute + grouped gate/up + down + combine, eager launches"}
     log_fn(f"config 3 prefill: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s, {touched} experts touched, "
            f"max {int(counts.max())} rows/expert")
     res["layer_with_shared_fp8"] = prefill_layer_with_shared(x, w, b, store, dev, args.seed + 3)

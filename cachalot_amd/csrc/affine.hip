@@ -43,6 +43,14 @@ int launch_affine_mx(const uint16_t* x, bool planes_ready, uint8_t* hid, uint8_t
                      int F, int k, int bits, int group, float limit, const uint16_t* addend, float* routed,
                      uint16_t* out, hipStream_t s);
 
+// grouped.hip: the other widths on the bf16-MFMA grouped kernels
+size_t grouped_affine_ws_bytes(int T, int k, int E, int F);
+int launch_grouped_affine(int bits, int group, const uint16_t* x, const uint8_t* pool,
+                          const cachalot_expert_layout* layout, const int32_t* slot_table, const int32_t* offsets,
+                          const int32_t* row_token, const int32_t* row_slot, const float* row_w, int T, int D, int F,
+                          int E, int k, float limit, uint16_t* y, void* workspace, size_t workspace_bytes,
+                          hipStream_t s);
+
 namespace aff {
 
 using namespace decode;
@@ -661,7 +669,8 @@ extern "C" int cachalot_moe_layer_decode_affine(const uint16_t* x, const uint16_
 
 extern "C" size_t cachalot_grouped_experts_affine_workspace_bytes(int T, int k, int E, int F) {
   if (T <= 0 || k <= 0 || E <= 0 || F <= 0) return 0;
-  return aff::align256((size_t)(E + 1) * 4) + aff::hidden_bytes(T * k, F);
+  return std::max(aff::align256((size_t)(E + 1) * 4) + aff::hidden_bytes(T * k, F),
+                  grouped_affine_ws_bytes(T, k, E, F));
 }
 
 extern "C" int cachalot_grouped_experts_affine(const uint16_t* x, const uint8_t* pool,
@@ -678,6 +687,11 @@ extern "C" int cachalot_grouped_experts_affine(const uint16_t* x, const uint8_t*
   if (workspace == nullptr || workspace_bytes < need)
     return fail(CACHALOT_ESPACE, "grouped_experts_affine: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
+  // the bf16 matrix cores (grouped.hip) where their tiling fits; the VALU kernels otherwise
+  // and with CACHALOT_AFFINE_VALU=1
+  if (D % 128 == 0 && F % 64 == 0 && D <= 8192 && F <= 8192 && k <= decode::KMAX && !aff::valu_requested())
+    return launch_grouped_affine(bits, group, x, pool, layout, slot_table, offsets, row_token, row_slot, row_w, T, D,
+                                 F, E, k, swiglu_limit, y, workspace, workspace_bytes, s);
   aff::Args a{};
   static const int used[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
   if (int rc = decode::make_layout(layout, 9, used, a.L, "grouped_experts_affine")) return rc;

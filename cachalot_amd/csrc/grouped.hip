@@ -65,6 +65,17 @@ using namespace tile;
 
 constexpr int KIND_Q2 = 0;
 constexpr int KIND_FP4 = 1;
+// Affine banks of the other widths (3- and 4-bit codes, groups of 32 / 64 / 128, 2-bit
+// codes in groups of 32 / 64): KIND_AFF + 10 bits + group / 32.  Their K chunk of 128
+// holds 128 / G groups; a step of the bf16 matrix cores covers 32 contiguous codes
+// (lane group kg: codes 32 s + 8 kg ..), so a group is G / 32 whole steps and its
+// formula s * sum(x q) + b * sum(x) is applied after its last step.
+constexpr int KIND_AFF = 100;
+template <int BITS, int G>
+constexpr int aff_kind = KIND_AFF + 10 * BITS + G / 32;
+constexpr bool is_aff(int kind) { return kind >= KIND_AFF; }
+constexpr int aff_bits(int kind) { return (kind - KIND_AFF) / 10; }
+constexpr int aff_group(int kind) { return ((kind - KIND_AFF) % 10) * 32; }
 constexpr int NT = 64;                 // weight rows per workgroup (4 waves x 16)
 constexpr int KC = 128;                // K chunk
 constexpr int A_ROW_BYTES = 272;       // one staged A row: 128 bf16 + 16 bytes padding
@@ -230,15 +241,19 @@ struct GroupedArgs {
 
 // LDS: A double buffer (MT rows x 272 B), per-row chunk sums (2-bit), then the
 // staged scales (2-bit: scales and biases of each matrix; FP4: E8M0 bytes).
-template <int MT>
+// Activation sums per staged row and chunk: one per group (2-bit g128: one).
+constexpr int sums_per_row(int kind) { return is_aff(kind) ? KC / aff_group(kind) : 1; }
+template <int KIND, int MT>
 struct GroupedLds {
   static constexpr int A = 2 * MT * A_ROW_BYTES;
-  static constexpr int SUMS = 2 * MT * 4;
+  static constexpr int SUMS = 2 * MT * sums_per_row(KIND) * 4;
 };
 inline size_t grouped_lds_bytes(int kind, int MT, int NM, int K) {
-  const int per_row = kind == KIND_Q2 ? (K + KC - 1) / KC : K / 32;
-  const size_t scales = kind == KIND_Q2 ? (size_t)2 * NM * NT * per_row * 2 : (size_t)NM * NT * per_row;
-  return (size_t)2 * MT * A_ROW_BYTES + (size_t)2 * MT * 4 + scales;
+  const bool affine = kind == KIND_Q2 || is_aff(kind);
+  const int g = kind == KIND_Q2 ? KC : (is_aff(kind) ? aff_group(kind) : 32);
+  const int per_row = (K + g - 1) / g;
+  const size_t scales = affine ? (size_t)2 * NM * NT * per_row * 2 : (size_t)NM * NT * per_row;
+  return (size_t)2 * MT * A_ROW_BYTES + (size_t)2 * MT * sums_per_row(kind) * 4 + scales;
 }
 
 // Stage chunk c of the tile's A rows: MT rows x 128 values, 16 values per item
@@ -278,6 +293,14 @@ struct AStage {
         pairs_mfma(v[i][1].z, v[i][1].w, hi.z, hi.w);
         const float s = sum8_lanes(sum_bf16x8(lo) + sum_bf16x8(hi));
         if (item < MT * 8 && (item & 7) == 0) sums[r] = s;
+      } else if constexpr (is_aff(KIND)) {
+        // natural order; the sum of each group's G / 16 items (aligned lanes)
+        constexpr int P = aff_group(KIND) / 16;
+        float s = sum_bf16x8(lo) + sum_bf16x8(hi);
+        s = s + __uint_as_float(xor1_u32(__float_as_uint(s)));
+        if constexpr (P >= 4) s = s + __uint_as_float(xor2_u32(__float_as_uint(s)));
+        if constexpr (P >= 8) s = s + __uint_as_float(mirror8_u32(__float_as_uint(s)));
+        if (item < MT * 8 && (item % P) == 0) sums[r * (8 / P) + (item & 7) / P] = s;
       }
       if (item < MT * 8) {
         uint4* d = reinterpret_cast<uint4*>(abuf + r * A_ROW_BYTES + (item & 7) * 32);
@@ -291,8 +314,47 @@ struct AStage {
 // The lane's codes of chunk c for weight row `row` of one matrix.
 // 2-bit: lane group kg owns codes [32kg, 32kg+32) of the group = 8 bytes.
 // FP4: lane group kg owns block kg of the chunk = 16 bytes.
+// Other affine widths: at step s lane group kg takes codes 32 s + 8 kg .. + 7 of the
+// chunk (BITS bytes of the row's bit stream), loaded for all four steps at once.
+template <int KIND, bool AFF = is_aff(KIND)>
+struct BChunk;
+
 template <int KIND>
-struct BChunk {
+struct BChunk<KIND, true> {
+  static constexpr int BITS = aff_bits(KIND);
+  uint32_t p[4];   // the eight codes of each step, low field first
+  __device__ __forceinline__ void load(const uint8_t* wrow, int c, int kg, int row_bytes) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int m = 16 * c + 4 * s + kg;   // piece index: BITS bytes each
+      if constexpr (BITS == 2) {
+        p[s] = *reinterpret_cast<const uint16_t*>(wrow + min(2 * m, row_bytes - 2));
+      } else if constexpr (BITS == 4) {
+        p[s] = *reinterpret_cast<const uint32_t*>(wrow + min(4 * m, row_bytes - 4));
+      } else {   // 3 bytes at 3 m: the two words around them
+        const int bit = 24 * m, wb = (bit >> 5) * 4;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(wrow + min(wb, row_bytes - 4));
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(wrow + min(wb + 4, row_bytes - 4));
+        p[s] = __builtin_amdgcn_alignbit(w1, w0, bit & 31) & 0xFFFFFFu;
+      }
+    }
+  }
+  // codes 0..15 are exact in bf16 (the float's upper half)
+  __device__ __forceinline__ bf16x8_t step(int s, float) const {
+    constexpr uint32_t MASK = (1u << BITS) - 1u;
+    uint32_t o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float f0 = (float)((p[s] >> (BITS * 2 * t)) & MASK);
+      const float f1 = (float)((p[s] >> (BITS * (2 * t + 1))) & MASK);
+      o[t] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+    }
+    return __builtin_bit_cast(bf16x8_t, o);
+  }
+};
+
+template <int KIND>
+struct BChunk<KIND, false> {
   uint4 v;
   __device__ __forceinline__ void load(const uint8_t* wrow, int c, int kg, int row_bytes) {
     if constexpr (KIND == KIND_Q2) {
@@ -355,11 +417,57 @@ __device__ __forceinline__ void chunk_mma(const uint8_t* abuf, const float* sums
   }
 }
 
+// Other affine widths: the chunk's 128 / G groups in turn, each G / 32 steps (A read at
+// codes 32 s + 8 kg, natural order), the group formula after each group's last step;
+// ngroups: the chunk's groups inside the row (the last chunk of a K that is not a whole
+// number of chunks holds fewer; the rest see zero activations and are skipped).
+template <int KIND, int MT, int NM>
+__device__ __forceinline__ void chunk_mma_aff(const uint8_t* abuf, const float* sums, const BChunk<KIND> (&b)[NM],
+                                              const float (&scale)[NM][4], const float (&bias)[NM][4], int ngroups,
+                                              int lane, f32x4_t (&acc)[NM][MT / 16]) {
+  constexpr int SPG = aff_group(KIND) / 32, NGC = KC / aff_group(KIND);
+  const int i = lane & 15, kg = lane >> 4;
+  f32x4_t c[NM][MT / 16];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int tb = 0; tb < MT / 16; ++tb) c[m][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    bf16x8_t bv[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) bv[m] = b[m].step(s, 1.0f);
+#pragma unroll
+    for (int tb = 0; tb < MT / 16; ++tb) {
+      const bf16x8_t a = lds_a(abuf, (tb * 16 + i) * A_ROW_BYTES + s * 64 + kg * 16);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) c[m][tb] = mfma(a, bv[m], c[m][tb]);
+    }
+    if ((s + 1) % SPG == 0) {
+      const int grp = s / SPG;
+      if (grp < ngroups) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int tb = 0; tb < MT / 16; ++tb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[m][tb][r] = acc[m][tb][r] +
+                              (scale[m][grp] * c[m][tb][r] + bias[m][grp] * sums[(tb * 16 + 4 * kg + r) * NGC + grp]);
+      }
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int tb = 0; tb < MT / 16; ++tb) c[m][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+}
+
 // Scale of (row j of the workgroup, chunk c) for tensor q: 2-bit bf16 scale/bias of
 // group c; FP4 E8M0 of block 4c + kg.
 template <int KIND>
 __device__ __forceinline__ float staged_scale(const uint8_t* sc, int q, int j, int c, int kg, int per_row, bool f16) {
-  if constexpr (KIND == KIND_Q2) {
+  if constexpr (KIND == KIND_Q2 || is_aff(KIND)) {   // c: the group
     return scale_bits_to_f32(reinterpret_cast<const uint16_t*>(sc)[(q * NT + j) * per_row + c], f16);
   } else {
     // blocks past K (the last chunk of K = 2880) meet zero activations: any finite scale
@@ -372,7 +480,8 @@ __device__ __forceinline__ float staged_scale(const uint8_t* sc, int q, int j, i
 template <int KIND, int MT, int NM>
 __device__ __forceinline__ bool grouped_main(const GroupedArgs& g, uint8_t* lds, const int (&tq)[NM], int& e,
                                              int& row0, int& rows, f32x4_t (&acc)[NM][MT / 16]) {
-  using Lds = GroupedLds<MT>;
+  using Lds = GroupedLds<KIND, MT>;
+  constexpr bool AQ = KIND == KIND_Q2 || is_aff(KIND);   // affine: scales and biases per group
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int kg = lane >> 4;
@@ -390,14 +499,16 @@ __device__ __forceinline__ bool grouped_main(const GroupedArgs& g, uint8_t* lds,
   if (slot < 0) return true;   // not resident: zero rows
 
   uint8_t* abuf[2] = {lds, lds + MT * A_ROW_BYTES};
-  float* sums[2] = {reinterpret_cast<float*>(lds + Lds::A), reinterpret_cast<float*>(lds + Lds::A) + MT};
+  float* sums[2] = {reinterpret_cast<float*>(lds + Lds::A),
+                    reinterpret_cast<float*>(lds + Lds::A) + MT * sums_per_row(KIND)};
   uint8_t* sc = lds + Lds::A + Lds::SUMS;
   const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
   const int nchunks = (g.K + KC - 1) / KC;
   // bytes per weight row and per scale row
-  const int groups = nchunks;                                   // 2-bit: stored groups per row
-  const int row_bytes = KIND == KIND_Q2 ? groups * 32 : g.K / 2;
-  const int per_row = KIND == KIND_Q2 ? groups : g.K / 32;      // scale entries per row
+  constexpr int GRP = is_aff(KIND) ? aff_group(KIND) : KC;
+  const int groups = (g.K + GRP - 1) / GRP;                     // affine: stored groups per row
+  const int row_bytes = KIND == KIND_Q2 ? groups * 32 : (is_aff(KIND) ? groups * GRP * aff_bits(KIND) / 8 : g.K / 2);
+  const int per_row = AQ ? groups : g.K / 32;                   // scale entries per row
   const int row = n0 + wave * 16 + (lane & 15);
   const uint8_t* wrow[NM];
 #pragma unroll
@@ -405,13 +516,13 @@ __device__ __forceinline__ bool grouped_main(const GroupedArgs& g, uint8_t* lds,
 
   // scales (and biases) of the 64 weight rows: contiguous runs, straight into LDS
   {
-    const int run = NT * per_row * (KIND == KIND_Q2 ? 2 : 1);
+    const int run = NT * per_row * (AQ ? 2 : 1);
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       // 2-bit: slot 2m = scales, 2m+1 = biases; FP4: slot m = E8M0 bytes
-      const int q = KIND == KIND_Q2 ? 2 * m : m;
+      const int q = AQ ? 2 * m : m;
       dma_to_lds(base + g.L.off[tq[m] + 1] + (int64_t)n0 * run / NT, sc + q * run, run, (wave + m) & 3, 4, lane);
-      if constexpr (KIND == KIND_Q2)
+      if constexpr (AQ)
         dma_to_lds(base + g.L.off[tq[m] + 2] + (int64_t)n0 * run / NT, sc + (q + 1) * run, run, (wave + m + 2) & 3,
                    4, lane);
     }
@@ -432,14 +543,29 @@ __device__ __forceinline__ bool grouped_main(const GroupedArgs& g, uint8_t* lds,
 #pragma unroll
       for (int m = 0; m < NM; ++m) bn[m].load(wrow[m], c + 1, kg, row_bytes);
     }
-    float scale[NM], bias[NM];
+    if constexpr (is_aff(KIND)) {
+      constexpr int NGC = KC / GRP;
+      const int g0 = c * NGC, ng = min(NGC, groups - g0);
+      float scale[NM][4], bias[NM][4];
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      // 2-bit: tensor slots 2m (scales) and 2m+1 (biases); FP4: slot 2m (E8M0)
-      scale[m] = staged_scale<KIND>(sc, KIND == KIND_Q2 ? 2 * m : m, wave * 16 + (lane & 15), c, kg, per_row, g.L.f16);
-      bias[m] = KIND == KIND_Q2 ? staged_scale<KIND>(sc, 2 * m + 1, wave * 16 + (lane & 15), c, kg, per_row, g.L.f16) : 0.0f;
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int q = 0; q < NGC; ++q) {
+          const int gi = min(g0 + q, groups - 1);
+          scale[m][q] = staged_scale<KIND>(sc, 2 * m, wave * 16 + (lane & 15), gi, kg, per_row, g.L.f16);
+          bias[m][q] = staged_scale<KIND>(sc, 2 * m + 1, wave * 16 + (lane & 15), gi, kg, per_row, g.L.f16);
+        }
+      chunk_mma_aff<KIND, MT, NM>(abuf[cur], sums[cur], bc, scale, bias, ng, lane, acc);
+    } else {
+      float scale[NM], bias[NM];
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        // 2-bit: tensor slots 2m (scales) and 2m+1 (biases); FP4: slot 2m (E8M0)
+        scale[m] = staged_scale<KIND>(sc, KIND == KIND_Q2 ? 2 * m : m, wave * 16 + (lane & 15), c, kg, per_row, g.L.f16);
+        bias[m] = KIND == KIND_Q2 ? staged_scale<KIND>(sc, 2 * m + 1, wave * 16 + (lane & 15), c, kg, per_row, g.L.f16) : 0.0f;
+      }
+      chunk_mma<KIND, MT, NM>(abuf[cur], sums[cur], bc, scale, bias, lane, acc);
     }
-    chunk_mma<KIND, MT, NM>(abuf[cur], sums[cur], bc, scale, bias, lane, acc);
     if (more) {
       as.store(abuf[cur ^ 1], sums[cur ^ 1]);
 #pragma unroll
@@ -899,14 +1025,17 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
                    "%s: D=%d must be a multiple of 64 in 128..8192", who, D);
   CACHALOT_REQUIRE(F % NT == 0 && F >= 64 && F <= KC * MAX_GROUPS, "%s: F=%d must be a multiple of 64 in 64..8192",
                    who, F);
-  if (KIND == KIND_Q2) CACHALOT_REQUIRE(D % KC == 0, "%s: D=%d must be a multiple of the 128-code group", who, D);
-  const GroupedWs wo = grouped_ws(T, k, E, D, F);
+  if (KIND == KIND_Q2 || is_aff(KIND))
+    CACHALOT_REQUIRE(D % KC == 0, "%s: D=%d must be a multiple of the 128-code chunk", who, D);
+  // (the other affine widths use neither the x planes nor the block-scaled prefill region)
+  const GroupedWs wo = grouped_ws(T, k, E, is_aff(KIND) ? 0 : D, F);
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "%s: workspace %zu < %zu bytes", who, workspace_bytes, wo.total);
   Layout L;
   static const int used_q2[9] = {0, 1, 2, 3, 4, 5, 6, 7, 8};
   static const int used_fp4[6] = {0, 1, 3, 4, 6, 7};
-  int rc = KIND == KIND_Q2 ? make_layout(layout, 9, used_q2, L, who) : make_layout(layout, 6, used_fp4, L, who);
+  int rc = KIND == KIND_Q2 || is_aff(KIND) ? make_layout(layout, 9, used_q2, L, who)
+                                           : make_layout(layout, 6, used_fp4, L, who);
   if (rc) return rc;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   int32_t* tiles_n = reinterpret_cast<int32_t*>(ws + wo.tiles_n);
@@ -969,6 +1098,31 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
 }
 
 }  // namespace
+
+// The other affine widths on the bf16-MFMA grouped kernels (called by
+// cachalot_grouped_experts_affine, affine.hip): workspace and launch.
+size_t grouped_affine_ws_bytes(int T, int k, int E, int F) { return grouped_ws(T, k, E, 0, F).total; }
+
+int launch_grouped_affine(int bits, int group, const uint16_t* x, const uint8_t* pool,
+                          const cachalot_expert_layout* layout, const int32_t* slot_table, const int32_t* offsets,
+                          const int32_t* row_token, const int32_t* row_slot, const float* row_w, int T, int D, int F,
+                          int E, int k, float limit, uint16_t* y, void* workspace, size_t workspace_bytes,
+                          hipStream_t s) {
+  const char* who = "grouped_experts_affine";
+  if (bits == 2 && group == KC)
+    return launch_grouped<KIND_Q2>(x, pool, layout, slot_table, offsets, row_token, row_slot, row_w, T, D, F, E, k,
+                                   limit, y, workspace, workspace_bytes, s, who);
+#define CACHALOT_GAFF(B, G)                                                                                      \
+  if (bits == B && group == G)                                                                                   \
+    return launch_grouped<aff_kind<B, G>>(x, pool, layout, slot_table, offsets, row_token, row_slot, row_w, T, D, F, \
+                                          E, k, limit, y, workspace, workspace_bytes, s, who);
+  CACHALOT_GAFF(2, 32) CACHALOT_GAFF(2, 64)
+  CACHALOT_GAFF(3, 32) CACHALOT_GAFF(3, 64) CACHALOT_GAFF(3, 128)
+  CACHALOT_GAFF(4, 32) CACHALOT_GAFF(4, 64) CACHALOT_GAFF(4, 128)
+#undef CACHALOT_GAFF
+  return fail(CACHALOT_EINVAL, "%s: %d-bit codes in groups of %d", who, bits, group);
+}
+
 }  // namespace cachalot
 
 extern "C" int cachalot_permute(const int32_t* idx, const float* w, int T, int k, int E, int32_t* offsets,

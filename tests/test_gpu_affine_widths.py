@@ -8,7 +8,8 @@ tool writes bits 2/3/4 x groups 32/64/128 (build_affine_bank.py:266-267).
   (helpers.term_flips), routed = the route-order sum bit for bit,
   out = bf16(routed + addend) bit for bit; the device-routed layer with ids
   bit-exact;
-* grouped (prefill / batched) rows against the oracle, dropped ids giving zeros.
+* grouped (prefill / batched) rows against the oracle on the bf16-MFMA grouped kernels and
+  the VALU kernels, dropped ids giving zeros.
 """
 from __future__ import annotations
 
@@ -100,17 +101,29 @@ def test_affine_decode_terms(cuda, bits, group, sd, path, monkeypatch):
     _check_decode(f"affine {bits}-bit g{group} {path} layer", fmt, 0, xf, oi[0], ow[0], _np(routed), _f32(out), terms, xf)
 
 
-@pytest.mark.parametrize("bits,group,sd", WIDTHS[:2])
-def test_affine_grouped_rows(cuda, bits, group, sd):
-    """37 tokens x top-6 over 16 experts (uneven rows, tiles of 4), three dropped ids."""
+GROUPED_CASES = [(3, 64, "float16", "mfma", 37, 16), (4, 32, "bfloat16", "mfma", 37, 16),
+                 (3, 128, "bfloat16", "mfma", 37, 16), (2, 64, "float16", "mfma", 37, 16),
+                 (4, 128, "float16", "mfma", 200, 8), (2, 32, "bfloat16", "mfma", 4, 16),
+                 (3, 32, "float16", "mfma", 4, 16), (4, 64, "bfloat16", "mfma", 37, 16),
+                 (3, 64, "float16", "valu", 37, 16), (4, 32, "bfloat16", "valu", 37, 16)]
+
+
+@pytest.mark.parametrize("bits,group,sd,path,t,E", GROUPED_CASES)
+def test_affine_grouped_rows(cuda, bits, group, sd, path, t, E, monkeypatch):
+    """t tokens x top-6 over E experts (uneven rows), three dropped ids, on the bf16-MFMA grouped
+    kernels (64-row tiles; 16-row tiles at t = 4; T = 200 over 8 experts: experts of several
+    tiles) and on the VALU kernels (CACHALOT_AFFINE_VALU=1)."""
     from cachalot_amd.moe_prefill import grouped_experts
 
+    monkeypatch.setenv("CACHALOT_AFFINE_VALU", "1" if path == "valu" else "0")
     fmt = _fmt(bits, group, sd)
-    E, t, k = 16, 37, 6
+    k = 6
     store = make_store(fmt, n_layers=1, n_experts=E)
-    rng = np.random.default_rng(7 + bits)
+    rng = np.random.default_rng(7 + bits + t)
     idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(t)]).astype(np.int32)
-    idx[0, 1], idx[5, 5], idx[t - 1, 0] = -1, E + 2, 1 << 29
+    drops = [(0, 1), (t // 2, k - 1), (t - 1, 0)]
+    for (r, c), v in zip(drops, (-1, E + 2, 1 << 29)):
+        idx[r, c] = v
     w = rng.dirichlet(np.ones(k), size=t).astype(np.float32)
     xb = osynth.activations(SEED, 3300, t, 4096)
     ab = osynth.activations(SEED, 3301, t, 4096)
@@ -119,9 +132,9 @@ def test_affine_grouped_rows(cuda, bits, group, sd):
                                          torch.from_numpy(w).to(cuda), store.pool, store.layer_table(0),
                                          addend=_bf16(ab, cuda), want_routed=True, want_terms=True)
         yf = _f32(y)
-        assert not yf[0, 1].any() and not yf[5, 5].any() and not yf[t - 1, 0].any()
-        _grouped_check(f"grouped affine {bits}-bit g{group}", fmt, 0, bf16_bits_to_f32(xb), idx, w, _np(routed),
-                       _f32(out), yf, E, addend=bf16_bits_to_f32(ab))
+        assert not any(yf[r, c].any() for r, c in drops)
+        _grouped_check(f"grouped affine {bits}-bit g{group} {path} T={t}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
+                       _np(routed), _f32(out), yf, E, addend=bf16_bits_to_f32(ab))
 
 
 def test_affine_missing_slot_and_graph_replays(cuda):
