@@ -180,3 +180,25 @@ def test_affine_missing_slot_and_graph_replays(cuda):
         assert torch.equal(y, eager)
         _ = chain(x0)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("bits,group,sd,d,f,k", [(3, 32, "float16", 4096, 2880, 8), (4, 64, "bfloat16", 5120, 2304, 6),
+                                                (4, 128, "float16", 5120, 3072, 8), (2, 32, "bfloat16", 1024, 512, 3)])
+def test_affine_decode_other_shapes(cuda, bits, group, sd, d, f, k):
+    """The matrix-core decode's other register budgets: k = 8 (more down items per wave), D = 5120
+    (more gate/up items per wave), F = 3072 (the largest K of the down kernel), a small layer."""
+    from cachalot_amd.moe_decode import decode_experts
+
+    fmt = _fmt(bits, group, sd, d=d, f=f)
+    store = make_store(fmt, n_layers=1, n_experts=64)
+    rng = np.random.default_rng(bits * 1000 + group + d + k)
+    idx = rng.choice(64, size=k, replace=False).tolist()
+    w = rng.dirichlet(np.ones(k)).astype(np.float32)
+    xb = osynth.activations(SEED, 3500 + d, 1, d)[0]
+    ab = osynth.activations(SEED, 3600 + d, 1, d)[0]
+    x, a = _bf16(xb, cuda), _bf16(ab, cuda)
+    routed, out = decode_experts(x, store.pool, store.layer_table(0), torch.tensor(idx, dtype=torch.int32, device=cuda),
+                                 torch.tensor(w, device=cuda), addend=a)
+    terms = _decode_terms(cuda, store, 0, x, idx, w)
+    _check_decode(f"affine {bits}-bit g{group} D={d} F={f} k={k}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
+                  _np(routed), _f32(out), terms, bf16_bits_to_f32(ab))
