@@ -390,7 +390,8 @@ def affine_width_decodes(args, dev, log_fn):
         "2-bit g128 bank with bf16 scales / biases (the type of the reference's shipped bank, "
         "build_affine_bank.py:76); the same matrix-core kernels as the fp16 headline")
     for key, f, note in (("prefill_4096_2bit_g128", affine_format(4096, 2880),
-                          "2-bit g128 bf16 bank: bf16 matrix cores with the codes converted in registers"),
+                          "2-bit g128 bf16 bank: the block-scaled prefill kernels of config 3 (x and h as fp8 "
+                          "planes, codes as fp4 operands), the group formula folded per 128-code chunk"),
                          ("prefill_4096_oq3e", affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"),
                           "oQ3e bank: the same bf16-MFMA grouped kernels, 3-bit codes converted per step")):
         out[key] = prefill_affine(args, dev, log_fn, f, key, note)

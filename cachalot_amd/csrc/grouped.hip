@@ -57,6 +57,12 @@ int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decod
                       const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
                       int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
                       int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s);
+bool prefill_mx_q2_supported(int D, int F);
+int launch_prefill_mx_q2(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
+                         const int32_t* slot_table, const int32_t* offsets, const int2* tiles,
+                         const int32_t* tiles_n, int max_tiles, const int32_t* row_token, const int32_t* row_slot,
+                         const float* row_w, int D, int F, int k, float limit, uint8_t* ws, uint16_t* y,
+                         hipStream_t s);
 
 namespace {
 
@@ -1001,8 +1007,9 @@ inline bool small_tiles_requested() {
   return env && env[0] == '1';
 }
 
-// FP4 prefill runs on the block-scaled matrix cores (prefill_mx.hip) unless
-// CACHALOT_PREFILL_BF16=1 selects the bf16-MFMA kernels (g2_fp4_kernel).
+// FP4 and 2-bit g128 prefill run on the block-scaled matrix cores (prefill_mx.hip)
+// unless CACHALOT_PREFILL_BF16=1 selects the bf16-MFMA kernels (g2_fp4_kernel, the
+// 64-row grouped kernels).
 inline bool prefill_bf16_requested() {
   const char* env = getenv("CACHALOT_PREFILL_BF16");
   return env && env[0] == '1';
@@ -1070,6 +1077,15 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
     if (rc) return rc;
     return launch_prefill_mx(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,
                              row_w, D, F, k, limit, ws + wo.mx, y, s);
+  }
+  if (KIND == KIND_Q2 && MT == 64 && prefill_mx_q2_supported(D, F) && !small_tiles_requested() &&
+      !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
+    // 2-bit g128 prefill on the block-scaled matrix cores (prefill_mx.hip)
+    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, prefill_mx_mt(), tiles, tiles_n, zeros);
+    rc = check_launch("tile_list_kernel");
+    if (rc) return rc;
+    return launch_prefill_mx_q2(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,
+                                row_w, D, F, k, limit, ws + wo.mx, y, s);
   }
   const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested() &&
                      max_tiles <= (1 << 20);

@@ -39,6 +39,17 @@
 // 3.64 with a three-stage ring (two chunks ahead), which left room for two.  Workgroups
 // go to the XCDs round-robin by launch index; the mapping gives every slice of
 // one tile to one XCD, so the tile's A rows are fetched into that XCD's L2 once.
+//
+// 2-bit affine g128 banks (Q2 = true) run the same kernels: a 128-code group is one
+// K chunk, its codes q go in as the fp4 operand (E2M1 of q / 2 with B scale 2, spread
+// into natural nibble order), and the group formula s * sum(x q) + b * sum(x) is
+// applied per chunk: each chunk's two plane instructions accumulate into a zeroed
+// tile, which is folded into the fp32 accumulators with the weight row's scale and
+// bias and the token row's chunk sum of x (or h).  The chunk sums come from the plane
+// writers (x_planes_rows_kernel; the gate/up epilogue for h, whose workgroup holds one
+// whole 128-column chunk of h).
+#include <type_traits>
+
 #include "decode_common.h"
 #include "mfma_tile.h"
 #include "mx_tile.h"
@@ -83,6 +94,8 @@ struct MxArgs {
   uint8_t* hs;                // gate/up: h scales [rows][hsb]
   int hsb, hkch;
   uint16_t* y;                // down: [T, k, N]
+  const float* asum;          // 2-bit: chunk sums of the A source rows [source rows][kch]
+  float* hsum;                // 2-bit gate/up: chunk sums of h [rows][hkch]
 };
 
 __host__ __device__ inline int scale_row_bytes(int K) { return (K / 32 * 2 + 15) / 16 * 16; }
@@ -143,7 +156,7 @@ __device__ __forceinline__ int plane_exp(float m) {
 // threads of an aligned lane quad hold one 32-element block.
 __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __restrict__ x, int T, int D,
                                                             uint8_t* __restrict__ xp, uint8_t* __restrict__ xs,
-                                                            int sb) {
+                                                            int sb, float* __restrict__ xsum) {
   const int64_t t8 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // index of an 8-value group
   const int per_row = D / 8;
   const bool live = t8 < (int64_t)T * per_row;
@@ -165,7 +178,13 @@ __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __re
   const int E = plane_exp(m);
   uint2 hi, lo;
   encode8(v, __uint_as_float((uint32_t)(127 - E) << 23), hi, lo);
+  // the 128-value chunk sums (16 threads per chunk; 2-bit banks' group formula)
+  float cs = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) cs = cs + v[j];
+  cs = row16_sum(cs);
   if (!live) return;
+  if (xsum != nullptr && (g8 & 15) == 0) xsum[(size_t)t * (D / 128) + (g8 >> 4)] = cs;
   const int col = 8 * g8, ch = col >> 7, byte = col & 127;
   uint8_t* dst = xp + ((size_t)t * (D / 128) + ch) * P3_ROWB + byte;
   *reinterpret_cast<uint2*>(dst) = hi;
@@ -179,6 +198,7 @@ __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __re
 template <int NM, int NF>
 struct P3Chunk {
   uint4 codes[NM][NF];
+  uint32_t sb[NM][NF];   // 2-bit: the weight row's scale | bias << 16 bits for the chunk's group
 };
 
 template <int NM, int NF>
@@ -193,6 +213,37 @@ __device__ __forceinline__ void p3_issue(uint8_t* stage, const uint8_t* (&asrc)[
 #pragma unroll
     for (int f = 0; f < NF; ++f)
       out.codes[m][f] = *reinterpret_cast<const uint4*>(wrow[m][f] + min(c * 64 + kg * 16, row_bytes - 16));
+}
+
+// 2-bit: block kg of the chunk's group (32 codes, 8 bytes) and the group's scale and
+// bias, per (matrix, fragment); rows as 32-bit offsets from the slot record (a
+// uniform base), so no 64-bit address per row stays live.
+template <int NM, int NF>
+__device__ __forceinline__ void p3_issue_q2(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
+                                            const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
+                                            const int (&nrow)[NF], int c, int kg, int wave, int row_bytes, int kch,
+                                            P3Chunk<NM, NF>& out) {
+#pragma unroll
+  for (int q = 0; q < P3_ASLOTS; ++q)
+    tile::lds_load16_untracked(asrc[q] + (size_t)c * P3_ROWB, stage + (P3_ASLOTS * wave + q) * 1024);
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint2 v = *reinterpret_cast<const uint2*>(base + woff[m] + nrow[f] * row_bytes + c * 32 + kg * 8);
+      out.codes[m][f] = make_uint4(v.x, v.y, 0u, 0u);
+      const int si = (nrow[f] * kch + c) * 2;
+      out.sb[m][f] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
+                     ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
+    }
+}
+
+// Sixteen 2-bit codes (the low or high half of a word) one per nibble in natural
+// order, nibble n = E2M1 of code n / 2.
+__device__ __forceinline__ uint32_t q2_nibbles(uint32_t v16) {
+  uint32_t t = (v16 & 0xFFu) | ((v16 & 0xFF00u) << 8);
+  t = (t & 0x000F000Fu) | ((t & 0x00F000F0u) << 4);
+  return (t & 0x03030303u) | ((t & 0x0C0C0C0Cu) << 2);
 }
 
 // B scales of chunk c = 4 g + J from the group registers (lane (i, p) holds the 16
@@ -247,13 +298,66 @@ __device__ __forceinline__ void p3_compute(const uint8_t* ab, const uint8_t* sbu
   }
 }
 
-// grid = slices * tiles rounded up to 8; dynamic LDS = P3_STAGES * P3_ABYTES + P3_MT * (sb + 16).
+// 2-bit chunk: per token block, the two plane instructions of every (matrix, fragment)
+// into zeroed tiles, then the group formula folded into the fp32 accumulators.
 template <int NM, int NF>
+__device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* sbuf, int sbs, const float* sxs,
+                                              const P3Chunk<NM, NF>& ch, int c, int i, int kg, int ntb, bool f16,
+                                              float (&acc)[NM][NF][P3_TB][4]) {
+  i32x8_t b[NM][NF];
+  float sc[NM][NF], bi[NM][NF];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint4 w = ch.codes[m][f];
+      b[m][f] = i32x8_t{(int)q2_nibbles(w.x & 0xFFFFu), (int)q2_nibbles(w.x >> 16), (int)q2_nibbles(w.y & 0xFFFFu),
+                        (int)q2_nibbles(w.y >> 16), 0, 0, 0, 0};
+      sc[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f] & 0xFFFFu), f16);
+      bi[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f] >> 16), f16);
+    }
+#pragma unroll
+  for (int tb = 0; tb < P3_TB; ++tb) {
+    if (tb >= ntb) break;
+    const int row = tb * 16 + i;
+    const uint8_t* ar = ab + row * P3_ROWB;
+    const uint4 h0 = mx::lds16(ar + ((kg ^ i) << 4));
+    const uint4 h1 = mx::lds16(ar + (((4 + kg) ^ i) << 4));
+    const uint4 l0 = mx::lds16(ar + (((8 + kg) ^ i) << 4));
+    const uint4 l1 = mx::lds16(ar + (((12 + kg) ^ i) << 4));
+    const uint32_t sa = *reinterpret_cast<const uint16_t*>(sbuf + row * sbs + (4 * c + kg) * 2);
+    const float4 sx = *reinterpret_cast<const float4*>(sxs + c * P3_MT + tb * 16 + 4 * kg);
+    const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+    const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+    f32x4_t d[NM][NF];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0>(ahi, b[m][f], mx::zero_acc(), sa, mx::E8M0_TWO);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<1>(alo, b[m][f], d[m][f], sa, mx::E8M0_TWO);
+    const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[m][f][tb][r] = acc[m][f][tb][r] + (sc[m][f] * d[m][f][r] + bi[m][f] * sxv[r]);
+  }
+}
+
+// grid = slices * tiles rounded up to 8; dynamic LDS = P3_STAGES * P3_ABYTES + P3_MT * (sb + 16)
+// (+ the tile's chunk sums, P3_MT * kch floats, for 2-bit banks).
+template <bool Q2, int NM, int NF>
 __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
   extern __shared__ __align__(16) uint8_t p3_lds[];
   uint8_t* abuf = p3_lds;
   uint8_t* sbuf = p3_lds + P3_STAGES * P3_ABYTES;
   const int sbs = g.sb + 16;   // LDS row stride of the A scales (bank spread)
+  float* sxs = reinterpret_cast<float*>(sbuf + P3_MT * sbs);   // 2-bit: the tile's chunk sums [kch][MT]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, kg = lane >> 4;
@@ -268,15 +372,19 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
   const int slot = g.slot_table[e];
   constexpr int WN = 16 * NF;                            // weight rows per wave and matrix
   const int nw0 = slice * (P3_WAVES * WN) + WN * wave;   // the wave's first weight row
-  f32x4_t acc[NM][NF][P3_TB];
+  // FP4: fp32 tiles in AGPRs fed by the instruction; 2-bit: fp32 in VGPRs, folded per chunk
+  using AccT = typename std::conditional<Q2, float[4], f32x4_t>::type;
+  AccT acc[NM][NF][P3_TB];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
-      for (int tb = 0; tb < P3_TB; ++tb) acc[m][f][tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int tb = 0; tb < P3_TB; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = 0.0f;
   if (slot >= 0) {
-    const int row_bytes = g.K / 2, blocks = g.K / 32;
+    const int row_bytes = Q2 ? g.kch * 32 : g.K / 2, blocks = g.K / 32;
     // the tile's A scales into LDS for the whole K loop (rows past the tile: its last row)
     const int sq = g.sb / 16;
     for (int it = threadIdx.x; it < P3_MT * sq; it += P3_THREADS) {
@@ -285,6 +393,14 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
       const int src = g.a_gather ? g.a_gather[rr] : rr;
       *reinterpret_cast<uint4*>(sbuf + r * sbs + q * 16) =
           *reinterpret_cast<const uint4*>(g.as + (size_t)src * g.sb + q * 16);
+    }
+    if constexpr (Q2) {   // and the tile's chunk sums of A
+      for (int it = threadIdx.x; it < P3_MT * g.kch; it += P3_THREADS) {
+        const int ch = it / P3_MT, r = it - ch * P3_MT;
+        const int rr = row0 + min(r, rows - 1);
+        const int src = g.a_gather ? g.a_gather[rr] : rr;
+        sxs[it] = g.asum[(size_t)src * g.kch + ch];
+      }
     }
     // A plane sources of the lane's slots: slot S = 64 (P3_ASLOTS wave + q) + lane holds
     // row S / 16, physical 16-byte column S % 16 = logical column ^ (row % 16)
@@ -301,14 +417,18 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
     const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
     const int tq[2] = {NM == 2 ? 0 : 3, 6};   // w1, w3 (gate/up) or w2 (down)
     const uint8_t* wrow[NM][NF];
+    int woff[NM], soff[NM], boff[NM], nrow[NF];   // 2-bit: offsets in the record (< 2^31: one expert)
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int f = 0; f < NF; ++f) nrow[f] = min(nw0 + 16 * f + i, g.N - 1);   // rows past N: clamped (discarded)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        const int n = min(nw0 + 16 * f + i, g.N - 1);   // rows past N: clamped (discarded)
-        wrow[m][f] = base + g.L.off[tq[m]] + (int64_t)n * row_bytes;
-      }
-    // B scales: lane (i, p), p = kg = (m, f) pair, loads 16 E8M0 bytes (4 chunks) of its
+    for (int m = 0; m < NM; ++m) {
+      woff[m] = (int)g.L.off[tq[m]];
+      soff[m] = (int)g.L.off[tq[m] + 1];
+      boff[m] = (int)g.L.off[tq[m] + 2];
+#pragma unroll
+      for (int f = 0; f < NF; ++f) wrow[m][f] = base + g.L.off[tq[m]] + (int64_t)nrow[f] * row_bytes;
+    }
+    // FP4 B scales: lane (i, p), p = kg = (m, f) pair, loads 16 E8M0 bytes (4 chunks) of its
     // pair's weight row i at a time (NM * NF == 4); p3_scales hands them out.  A group
     // past the row's last block reads into what follows the tensor in the record (the
     // host checks that something does); those bytes are never used.
@@ -321,8 +441,9 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
     uint4 sgrp[2];
     // every issue is unconditional (a chunk past the end re-reads the last one into a
     // stage nothing reads again), so each wait is for exactly the loads it needs
-    sgrp[0] = *reinterpret_cast<const uint4*>(sgp);
-    p3_issue<NM, NF>(abuf, asrc, wrow, 0, kg, wave, row_bytes, ring[0]);
+    if constexpr (!Q2) sgrp[0] = *reinterpret_cast<const uint4*>(sgp);
+    if constexpr (Q2) p3_issue_q2<NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kg, wave, row_bytes, nch, ring[0]);
+    else p3_issue<NM, NF>(abuf, asrc, wrow, 0, kg, wave, row_bytes, ring[0]);
     // eight chunks per trip: A stage and code ring index u % 2, scale group buffer (u / 4) % 2
     for (int c0 = 0; c0 < nch; c0 += 8) {
 #pragma unroll
@@ -330,16 +451,29 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
         const int c = c0 + u;
         // this wave's loads of chunk c have landed (its last code load is consumed
         // here; its earlier direct-to-LDS loads complete first), then every wave's
-        asm volatile("" ::"v"(ring[u % 2].codes[NM - 1][NF - 1].w) : "memory");
+        // (2-bit: the pair's bias is the last load of a chunk; the first barrier also
+        // publishes the chunk sums stored above)
+        if constexpr (Q2) asm volatile("" ::"v"(ring[u % 2].sb[NM - 1][NF - 1]) : "memory");
+        else asm volatile("" ::"v"(ring[u % 2].codes[NM - 1][NF - 1].w) : "memory");
         lds_sync();
-        if ((u + 1) % 4 == 0)   // the scale group of chunk c + 1
-          sgrp[((u + 1) / 4) % 2] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 1) / 4, ngrp - 1));
-        p3_issue<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, wrow, min(c + 1, nch - 1), kg, wave, row_bytes,
-                         ring[(u + 1) % 2]);
+        if constexpr (!Q2)
+          if ((u + 1) % 4 == 0)   // the scale group of chunk c + 1
+            sgrp[((u + 1) / 4) % 2] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 1) / 4, ngrp - 1));
+        if constexpr (Q2)
+          p3_issue_q2<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
+                              min(c + 1, nch - 1), kg, wave, row_bytes, nch, ring[(u + 1) % 2]);
+        else
+          p3_issue<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, wrow, min(c + 1, nch - 1), kg, wave, row_bytes,
+                           ring[(u + 1) % 2]);
         if (c < nch) {
-          uint32_t bs[NM][NF];
-          p3_scales<NM, NF>(sgrp[(u / 4) % 2], u % 4, c, i, kg, blocks, bs);
-          p3_compute<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, ring[u % 2], bs, c, i, kg, ntb, acc);
+          if constexpr (Q2) {
+            p3_compute_q2<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], c, i, kg, ntb, g.L.f16,
+                                  acc);
+          } else {
+            uint32_t bs[NM][NF];
+            p3_scales<NM, NF>(sgrp[(u / 4) % 2], u % 4, c, i, kg, blocks, bs);
+            p3_compute<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, ring[u % 2], bs, c, i, kg, ntb, acc);
+          }
         }
       }
     }
@@ -349,6 +483,9 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
   }
   // epilogue: lane holds rows tb*16 + 4kg + r (tile rows) x weight rows nw0 + 16f + i
   if constexpr (NM == 2) {
+    // 2-bit: every wave is past its last A reads before the ring holds the h sums
+    float* red = reinterpret_cast<float*>(abuf);   // [P3_WAVES][P3_MT]
+    if constexpr (Q2) lds_sync();
     // h = bf16(silu(min(g, L)) * clip(u) * w), written as the planes of its 32-element
     // block (the wave's 32 weight rows are one block of h's columns)
 #pragma unroll
@@ -390,7 +527,24 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
           const uint32_t sc = (uint32_t)(E + 127) | ((uint32_t)(E + 123) << 8);
           *reinterpret_cast<uint16_t*>(g.hs + (size_t)prow * g.hsb + (nw0 / 32) * 2) = (uint16_t)sc;
         }
+        if constexpr (Q2) {   // the wave's 32 h values of the row, summed (f, then the 16 lanes)
+          float hsv = 0.0f;
+#pragma unroll
+          for (int f = 0; f < NF; ++f) hsv = hsv + hv[f];
+          hsv = row16_sum(hsv);
+          if (i == 0) red[wave * P3_MT + tr] = hsv;
+        }
       }
+    if constexpr (Q2) {   // the workgroup's 128 columns are one chunk of h: its sum per row, waves in order
+      lds_sync();
+      if ((int)threadIdx.x < rows) {
+        const int tr = threadIdx.x;
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < P3_WAVES; ++w) t = t + red[w * P3_MT + tr];
+        g.hsum[(size_t)(row0 + tr) * g.hkch + slice] = t;
+      }
+    }
   } else {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -418,7 +572,7 @@ size_t prefill_mx_ws_bytes(int T, int k, int D, int F) {
   const int fch = (F + 127) / 128;
   auto a256 = [](size_t v) { return (v + 255) & ~size_t(255); };
   return a256((size_t)T * D * 2) + a256((size_t)T * scale_row_bytes(D)) + a256(rows * fch * P3_ROWB) +
-         a256(rows * scale_row_bytes(fch * 128));
+         a256(rows * scale_row_bytes(fch * 128)) + a256((size_t)T * (D / 128) * 4) + a256(rows * fch * 4);
 }
 
 // Shapes and slot layouts the kernels take.  Their B-scale loads read 16 bytes per
@@ -436,11 +590,19 @@ bool prefill_mx_supported(int D, int F, const decode::Layout& L) {
   return room(1, F, D / 32) && room(7, F, D / 32) && room(4, D, F / 32);
 }
 
-// tiles / tiles_n: the 64-row tile list (tile_list_kernel with MT = 64), max_tiles its bound.
-int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
-                      const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
-                      int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
-                      int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s) {
+// 2-bit g128 banks: any shape of the FP4 envelope (the rows' groups are padded to whole
+// chunks in the bank; scales and biases are read one per chunk).
+bool prefill_mx_q2_supported(int D, int F) {
+  return D % 128 == 0 && D >= 512 && D <= 8192 && F % 32 == 0 && F >= 512 && F <= 8192;
+}
+
+namespace {
+
+template <bool Q2>
+int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L, const int32_t* slot_table,
+              const int32_t* offsets, const int2* tiles, const int32_t* tiles_n, int max_tiles,
+              const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k, float limit,
+              uint8_t* ws, uint16_t* y, hipStream_t s) {
   auto a256 = [](size_t v) { return (v + 255) & ~size_t(255); };
   const size_t rows = (size_t)T * k;
   const int fch = (F + 127) / 128;
@@ -449,17 +611,20 @@ int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decod
   uint8_t* xs = xp + a256((size_t)T * D * 2);
   uint8_t* hp = xs + a256((size_t)T * sbx);
   uint8_t* hs = hp + a256(rows * fch * P3_ROWB);
+  float* xsum = reinterpret_cast<float*>(hs + a256(rows * sbh));
+  float* hsum = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xsum) + a256((size_t)T * (D / 128) * 4));
   const int64_t groups = (int64_t)T * D / 8;
   hipLaunchKernelGGL(x_planes_rows_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, x, T, D, xp, xs,
-                     sbx);
+                     sbx, Q2 ? xsum : nullptr);
   int rc = check_launch("x_planes_rows_kernel");
   if (rc) return rc;
   const int tiles8 = (max_tiles + 7) / 8 * 8;
   MxArgs gu{xp, xs, sbx, D / 128, row_token, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot,
-            row_w, D, F, k, limit, hp, hs, sbh, fch, nullptr};
+            row_w, D, F, k, limit, hp, hs, sbh, fch, nullptr, xsum, hsum};
   const int s_gu = (fch * 128) / (P3_WAVES * 32);   // h's padded columns, 128 per workgroup
-  const size_t lds_gu = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbx + 16);
-  auto kgu = p3_kernel<2, 2>;
+  const size_t lds_gu = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbx + 16) +
+                        (Q2 ? (size_t)P3_MT * (D / 128) * 4 : 0);
+  auto kgu = p3_kernel<Q2, 2, 2>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds_gu) != hipSuccess)
     return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_gu);
@@ -467,15 +632,37 @@ int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decod
   rc = check_launch("p3_kernel<2,2>");
   if (rc) return rc;
   MxArgs dn{hp, hs, sbh, fch, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
-            F, D, k, limit, nullptr, nullptr, 0, 0, y};
+            F, D, k, limit, nullptr, nullptr, 0, 0, y, hsum, nullptr};
   const int s_dn = (D + P3_WAVES * 64 - 1) / (P3_WAVES * 64);
-  const size_t lds_dn = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbh + 16);
-  auto kdn = p3_kernel<1, 4>;
+  const size_t lds_dn = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbh + 16) +
+                        (Q2 ? (size_t)P3_MT * fch * 4 : 0);
+  auto kdn = p3_kernel<Q2, 1, 4>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kdn), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds_dn) != hipSuccess)
     return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_dn);
   hipLaunchKernelGGL(kdn, dim3(s_dn * tiles8), dim3(P3_THREADS), lds_dn, s, dn, s_dn);
   return check_launch("p3_kernel<1,4>");
+}
+
+}  // namespace
+
+// tiles / tiles_n: the 64-row tile list (tile_list_kernel with MT = 64), max_tiles its bound.
+int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
+                      const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
+                      int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
+                      int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s) {
+  return launch_p3<false>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot, row_w,
+                          D, F, k, limit, ws, y, s);
+}
+
+// The same launches over a 2-bit g128 bank.
+int launch_prefill_mx_q2(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
+                         const int32_t* slot_table, const int32_t* offsets, const int2* tiles,
+                         const int32_t* tiles_n, int max_tiles, const int32_t* row_token, const int32_t* row_slot,
+                         const float* row_w, int D, int F, int k, float limit, uint8_t* ws, uint16_t* y,
+                         hipStream_t s) {
+  return launch_p3<true>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot, row_w,
+                         D, F, k, limit, ws, y, s);
 }
 
 }  // namespace cachalot

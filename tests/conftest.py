@@ -43,7 +43,8 @@ def q2_path(request, monkeypatch):
 
 @pytest.fixture(params=["mx", "bf16"])
 def prefill_path(request, monkeypatch):
-    """FP4 prefill runs on the block-scaled fp8 x fp4 matrix cores by default; the
-    bf16-MFMA kernels are selected with CACHALOT_PREFILL_BF16=1.  Both are pinned."""
+    """FP4 and 2-bit g128 prefill run on the block-scaled fp8 x fp4 matrix cores by
+    default; the bf16-MFMA kernels are selected with CACHALOT_PREFILL_BF16=1.  Both are
+    pinned."""
     monkeypatch.setenv("CACHALOT_PREFILL_BF16", "1" if request.param == "bf16" else "0")
     return request.param

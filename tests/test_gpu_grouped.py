@@ -121,8 +121,6 @@ def test_grouped_experts_prefill_tiles(cuda, kind, prefill_path):
     from cachalot_amd.moe_prefill import grouped_experts
     from cachalot_amd.storage.index import affine_format, fp4_format
 
-    if kind == "affine_f16" and prefill_path != "mx":
-        pytest.skip("the prefill path switch selects FP4 kernels only")
     fmt = (fp4_format(4096, 2880) if kind == "fp4" else
            affine_format(4096, 2880, scale_dtype="float16" if kind == "affine_f16" else "bfloat16"))
     E = 8
