@@ -28,6 +28,10 @@
 //       its (token, route slot) place: y [T, k, D] bf16.
 //   combine_kernel     out[t] = bf16(0 + y[t,0] + ... + y[t,k-1] (+ addend));
 //                      combine8_kernel the same with 16-byte accesses.
+// The grouped kernels also take the other affine widths (aff_kind<BITS, G>: 3- and
+// 4-bit codes, groups of 32 / 64 / 128, 2-bit codes in groups of 32 / 64), with the
+// codes read per step and the group formula applied per group (see chunk_mma_aff).
+// FP4 and 2-bit g128 prefill go to the block-scaled kernels of prefill_mx.hip.
 #include "decode_common.h"
 #include "mfma_tile.h"
 #include "permute_small.h"
