@@ -140,7 +140,7 @@ _SIGNATURES = {
                                                  c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
                                                  c_void_p]),
-    "cachalot_grouped_experts_affine_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "cachalot_grouped_experts_affine_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "cachalot_grouped_experts_affine": (c_int, [c_void_p, c_void_p, ctypes.POINTER(ExpertLayout), c_void_p,
                                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                                 c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_size_t,

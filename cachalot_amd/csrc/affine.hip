@@ -44,7 +44,7 @@ int launch_affine_mx(const uint16_t* x, bool planes_ready, uint8_t* hid, uint8_t
                      uint16_t* out, hipStream_t s);
 
 // grouped.hip: the other widths on the bf16-MFMA grouped kernels
-size_t grouped_affine_ws_bytes(int T, int k, int E, int F);
+size_t grouped_affine_ws_bytes(int T, int k, int E, int D, int F);
 int launch_grouped_affine(int bits, int group, const uint16_t* x, const uint8_t* pool,
                           const cachalot_expert_layout* layout, const int32_t* slot_table, const int32_t* offsets,
                           const int32_t* row_token, const int32_t* row_slot, const float* row_w, int T, int D, int F,
@@ -667,10 +667,10 @@ extern "C" int cachalot_moe_layer_decode_affine(const uint16_t* x, const uint16_
                      workspace_bytes, (hipStream_t)stream);
 }
 
-extern "C" size_t cachalot_grouped_experts_affine_workspace_bytes(int T, int k, int E, int F) {
-  if (T <= 0 || k <= 0 || E <= 0 || F <= 0) return 0;
+extern "C" size_t cachalot_grouped_experts_affine_workspace_bytes(int T, int k, int E, int D, int F) {
+  if (T <= 0 || k <= 0 || E <= 0 || D <= 0 || F <= 0) return 0;
   return std::max(aff::align256((size_t)(E + 1) * 4) + aff::hidden_bytes(T * k, F),
-                  grouped_affine_ws_bytes(T, k, E, F));
+                  grouped_affine_ws_bytes(T, k, E, D, F));
 }
 
 extern "C" int cachalot_grouped_experts_affine(const uint16_t* x, const uint8_t* pool,
@@ -683,7 +683,7 @@ extern "C" int cachalot_grouped_experts_affine(const uint16_t* x, const uint8_t*
                    "grouped_experts_affine: null pointer");
   CACHALOT_REQUIRE(T >= 1 && k >= 1 && E >= 1 && E <= 1024, "grouped_experts_affine: T=%d k=%d E=%d", T, k, E);
   if (int rc = aff::check_shape("grouped_experts_affine", D, F, bits, group)) return rc;
-  const size_t need = cachalot_grouped_experts_affine_workspace_bytes(T, k, E, F);
+  const size_t need = cachalot_grouped_experts_affine_workspace_bytes(T, k, E, D, F);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(CACHALOT_ESPACE, "grouped_experts_affine: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;

@@ -92,13 +92,6 @@ __device__ __forceinline__ void load_words(const uint8_t* p, uint32_t (&w)[W]) {
   }
 }
 
-// Eight 3-bit codes (a 24-bit run, code i at bits 3i) one per nibble, nibble i = code i.
-__device__ __forceinline__ uint32_t spread3(uint32_t v) {
-  const uint32_t a = (v & 0xFFFu) | ((v << 4) & 0x0FFF0000u);       // four codes per 16-bit half
-  const uint32_t b = (a & 0x003F003Fu) | ((a << 2) & 0x3F003F00u);   // two per byte
-  return (b & 0x07070707u) | ((b << 1) & 0x70707070u);               // one per nibble
-}
-
 // Nibble registers of codes (8 t .. 8 t + 7) in natural order -> the even codes of a
 // pair (lo, hi) of such registers, then the odd ones, as the plane blocks order a
 // 16-code piece: even(lo, hi) nibbles = codes 0, 2, 4, 6 of lo, then of hi.
@@ -124,10 +117,10 @@ __device__ __forceinline__ void step_operands(const uint32_t (&w)[W], int s, i32
       for (int t = 0; t < 4; ++t) n[t] = w[4 * s + t];
     } else {
       const uint32_t w0 = w[3 * s], w1 = w[3 * s + 1], w2 = w[3 * s + 2];
-      n[0] = spread3(w0 & 0xFFFFFFu);
-      n[1] = spread3(__builtin_amdgcn_alignbit(w1, w0, 24) & 0xFFFFFFu);
-      n[2] = spread3(__builtin_amdgcn_alignbit(w2, w1, 16) & 0xFFFFFFu);
-      n[3] = spread3(w2 >> 8);
+      n[0] = mx::spread3(w0 & 0xFFFFFFu);
+      n[1] = mx::spread3(__builtin_amdgcn_alignbit(w1, w0, 24) & 0xFFFFFFu);
+      n[2] = mx::spread3(__builtin_amdgcn_alignbit(w2, w1, 16) & 0xFFFFFFu);
+      n[3] = mx::spread3(w2 >> 8);
     }
     const uint32_t p[4] = {even_nibbles(n[0], n[1]), odd_nibbles(n[0], n[1]), even_nibbles(n[2], n[3]),
                            odd_nibbles(n[2], n[3])};

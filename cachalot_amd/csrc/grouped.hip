@@ -57,6 +57,12 @@ int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const dec
 size_t prefill_mx_ws_bytes(int T, int k, int D, int F);
 bool prefill_mx_supported(int D, int F, const decode::Layout& L);
 int prefill_mx_mt();
+bool prefill_mx_aff_supported(int bits, int group, int D, int F);
+int launch_prefill_mx_aff(int bits, int group, const uint16_t* x, int T, const uint8_t* pool,
+                          const decode::Layout& L, const int32_t* slot_table, const int32_t* offsets,
+                          const int2* tiles, const int32_t* tiles_n, int max_tiles, const int32_t* row_token,
+                          const int32_t* row_slot, const float* row_w, int D, int F, int k, float limit, uint8_t* ws,
+                          uint16_t* y, hipStream_t s);
 int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
                       const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
                       int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
@@ -1038,8 +1044,7 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
                    who, F);
   if (KIND == KIND_Q2 || is_aff(KIND))
     CACHALOT_REQUIRE(D % KC == 0, "%s: D=%d must be a multiple of the 128-code chunk", who, D);
-  // (the other affine widths use neither the x planes nor the block-scaled prefill region)
-  const GroupedWs wo = grouped_ws(T, k, E, is_aff(KIND) ? 0 : D, F);
+  const GroupedWs wo = grouped_ws(T, k, E, D, F);
   if (workspace == nullptr || workspace_bytes < wo.total)
     return fail(CACHALOT_ESPACE, "%s: workspace %zu < %zu bytes", who, workspace_bytes, wo.total);
   Layout L;
@@ -1091,6 +1096,15 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
     return launch_prefill_mx_q2(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,
                                 row_w, D, F, k, limit, ws + wo.mx, y, s);
   }
+  if (is_aff(KIND) && MT == 64 && prefill_mx_aff_supported(aff_bits(KIND), aff_group(KIND), D, F) &&
+      !small_tiles_requested() && !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
+    // 2-bit g64, 3- and 4-bit g64 / g128 prefill on the block-scaled matrix cores
+    hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, prefill_mx_mt(), tiles, tiles_n, zeros);
+    rc = check_launch("tile_list_kernel");
+    if (rc) return rc;
+    return launch_prefill_mx_aff(aff_bits(KIND), aff_group(KIND), x, T, pool, L, slot_table, offsets, tiles, tiles_n,
+                                 max_tiles, row_token, row_slot, row_w, D, F, k, limit, ws + wo.mx, y, s);
+  }
   const bool large = KIND == KIND_FP4 && MT == 64 && D % 128 == 0 && F % 32 == 0 && !small_tiles_requested() &&
                      max_tiles <= (1 << 20);
   hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, large ? G2_MT : MT, tiles, tiles_n,
@@ -1121,7 +1135,7 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
 
 // The other affine widths on the bf16-MFMA grouped kernels (called by
 // cachalot_grouped_experts_affine, affine.hip): workspace and launch.
-size_t grouped_affine_ws_bytes(int T, int k, int E, int F) { return grouped_ws(T, k, E, 0, F).total; }
+size_t grouped_affine_ws_bytes(int T, int k, int E, int D, int F) { return grouped_ws(T, k, E, D, F).total; }
 
 int launch_grouped_affine(int bits, int group, const uint16_t* x, const uint8_t* pool,
                           const cachalot_expert_layout* layout, const int32_t* slot_table, const int32_t* offsets,

@@ -114,6 +114,22 @@ __device__ __forceinline__ i32x8_t q2_spread(uint32_t w0, uint32_t w1) {
   return b;
 }
 
+// Eight 3-bit codes (a 24-bit run, code i at bits 3i) one per nibble, nibble i = code i.
+__device__ __forceinline__ uint32_t spread3(uint32_t v) {
+  const uint32_t a = (v & 0xFFFu) | ((v << 4) & 0x0FFF0000u);       // four codes per 16-bit half
+  const uint32_t b = (a & 0x003F003Fu) | ((a << 2) & 0x3F003F00u);   // two per byte
+  return (b & 0x07070707u) | ((b << 1) & 0x70707070u);               // one per nibble
+}
+
+// Eight nibble codes (nibble i = code i) one per byte, in order: bytes 0..3 of lo =
+// codes 0..3, of hi = codes 4..7.
+__device__ __forceinline__ void nibbles_to_bytes(uint32_t n, uint32_t& lo, uint32_t& hi) {
+  const uint32_t e = n & 0x0F0F0F0Fu;          // codes 0, 2, 4, 6
+  const uint32_t o = (n >> 4) & 0x0F0F0F0Fu;   // codes 1, 3, 5, 7
+  lo = __builtin_amdgcn_perm(o, e, 0x05010400u);
+  hi = __builtin_amdgcn_perm(o, e, 0x07030602u);
+}
+
 // Byte position of element i (0..15) of a piece in its plane.
 __device__ __forceinline__ int piece_pos(int i) { return (i & 1) ? 8 + (i >> 1) : (i >> 1); }
 

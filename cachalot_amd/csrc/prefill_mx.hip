@@ -71,6 +71,19 @@ constexpr int P3_ASLOTS = P3_ABYTES / 16 / P3_THREADS;   // 16-byte A slots per 
 typedef __attribute__((ext_vector_type(8))) int i32x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
+// Weight kinds of p3_kernel (AK): FP4; 2-bit g128 with the codes as fp4 operands;
+// (BITS << 8) | G for affine codes as fp8 operands (code q as the E4M3 byte q, which
+// is q * 2^-9 -- subnormal below 8 -- with B scale 2^9).
+constexpr int AK_FP4 = 0;
+constexpr int AK_Q2 = 1;
+constexpr int ak_aff(int bits, int g) { return (bits << 8) | g; }
+constexpr bool ak_fold(int ak) { return ak != AK_FP4; }       // group formula per group
+constexpr bool ak_bytes(int ak) { return ak > AK_Q2; }        // codes as fp8 bytes
+constexpr int ak_bits(int ak) { return ak == AK_Q2 ? 2 : ak >> 8; }
+constexpr int ak_group(int ak) { return ak == AK_Q2 ? 128 : (ak & 255); }
+constexpr int ak_gpc(int ak) { return ak_fold(ak) ? 128 / ak_group(ak) : 1; }   // groups per K chunk
+constexpr uint32_t E8M0_2P9 = 136u;                            // 2^9
+
 struct MxArgs {
   const uint8_t* ap;          // A planes [source rows][kch][256]
   const uint8_t* as;          // A scales [source rows][sb]
@@ -106,13 +119,19 @@ __host__ __device__ inline int scale_row_bytes(int K) { return (K / 32 * 2 + 15)
 // VGPRs, so they cannot overlap it), and keeps A and B live until the result exists;
 // pinning it to VGPRs instead makes the compiler copy it out of and back into AGPRs
 // around every instruction.
-template <int OPSEL_A>
+// B_FP8: B is fp8 (E4M3, all eight registers) instead of fp4 (the first four).
+template <int OPSEL_A, bool B_FP8 = false>
 __device__ __forceinline__ f32x4_t mfma_plane(const i32x8_t& a, const i32x8_t& b, f32x4_t c, uint32_t sa,
                                               uint32_t sb) {
   typedef __attribute__((ext_vector_type(4))) int i32x4_t;
-  f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 4, OPSEL_A, (int)sa, 0, (int)sb);
-  const i32x4_t b4 = __builtin_shufflevector(b, b, 0, 1, 2, 3);
-  asm volatile("" : "+a"(d) : "v"(a), "v"(b4));
+  f32x4_t d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, B_FP8 ? 0 : 4, OPSEL_A, (int)sa, 0,
+                                                                (int)sb);
+  if constexpr (B_FP8) {
+    asm volatile("" : "+a"(d) : "v"(a), "v"(b));
+  } else {
+    const i32x4_t b4 = __builtin_shufflevector(b, b, 0, 1, 2, 3);
+    asm volatile("" : "+a"(d) : "v"(a), "v"(b4));
+  }
   return d;
 }
 
@@ -156,7 +175,7 @@ __device__ __forceinline__ int plane_exp(float m) {
 // threads of an aligned lane quad hold one 32-element block.
 __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __restrict__ x, int T, int D,
                                                             uint8_t* __restrict__ xp, uint8_t* __restrict__ xs,
-                                                            int sb, float* __restrict__ xsum) {
+                                                            int sb, float* __restrict__ xsum, int gsum) {
   const int64_t t8 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // index of an 8-value group
   const int per_row = D / 8;
   const bool live = t8 < (int64_t)T * per_row;
@@ -178,13 +197,18 @@ __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __re
   const int E = plane_exp(m);
   uint2 hi, lo;
   encode8(v, __uint_as_float((uint32_t)(127 - E) << 23), hi, lo);
-  // the 128-value chunk sums (16 threads per chunk; 2-bit banks' group formula)
+  // the group sums of affine banks' group formula (gsum = 128: 16 threads per group,
+  // 64: 8 threads)
   float cs = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) cs = cs + v[j];
-  cs = row16_sum(cs);
+  cs = cs + __uint_as_float(xor1_u32(__float_as_uint(cs)));
+  cs = cs + __uint_as_float(xor2_u32(__float_as_uint(cs)));
+  cs = cs + __uint_as_float(mirror8_u32(__float_as_uint(cs)));
+  if (gsum == 128) cs = cs + __uint_as_float(mirror16_u32(__float_as_uint(cs)));
   if (!live) return;
-  if (xsum != nullptr && (g8 & 15) == 0) xsum[(size_t)t * (D / 128) + (g8 >> 4)] = cs;
+  const int tpg = gsum / 8;   // threads per group
+  if (xsum != nullptr && g8 % tpg == 0) xsum[(size_t)t * (D / gsum) + g8 / tpg] = cs;
   const int col = 8 * g8, ch = col >> 7, byte = col & 127;
   uint8_t* dst = xp + ((size_t)t * (D / 128) + ch) * P3_ROWB + byte;
   *reinterpret_cast<uint2*>(dst) = hi;
@@ -198,7 +222,7 @@ __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __re
 template <int NM, int NF>
 struct P3Chunk {
   uint4 codes[NM][NF];
-  uint32_t sb[NM][NF];   // 2-bit: the weight row's scale | bias << 16 bits for the chunk's group
+  uint32_t sb[NM][NF][2];   // affine: the weight row's scale | bias << 16 bits per group of the chunk
 };
 
 template <int NM, int NF>
@@ -233,7 +257,7 @@ __device__ __forceinline__ void p3_issue_q2(uint8_t* stage, const uint8_t* (&asr
       const uint2 v = *reinterpret_cast<const uint2*>(base + woff[m] + nrow[f] * row_bytes + c * 32 + kg * 8);
       out.codes[m][f] = make_uint4(v.x, v.y, 0u, 0u);
       const int si = (nrow[f] * kch + c) * 2;
-      out.sb[m][f] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
+      out.sb[m][f][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
                      ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
     }
 }
@@ -313,8 +337,8 @@ __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* 
       const uint4 w = ch.codes[m][f];
       b[m][f] = i32x8_t{(int)q2_nibbles(w.x & 0xFFFFu), (int)q2_nibbles(w.x >> 16), (int)q2_nibbles(w.y & 0xFFFFu),
                         (int)q2_nibbles(w.y >> 16), 0, 0, 0, 0};
-      sc[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f] & 0xFFFFu), f16);
-      bi[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f] >> 16), f16);
+      sc[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f][0] & 0xFFFFu), f16);
+      bi[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f][0] >> 16), f16);
     }
 #pragma unroll
   for (int tb = 0; tb < P3_TB; ++tb) {
@@ -349,15 +373,150 @@ __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* 
   }
 }
 
+// Affine codes as fp8 operands.  Lane group kg of the instruction's fp8 operand holds
+// elements 16 kg .. 16 kg + 15 of the chunk (registers 0..3) and 64 + 16 kg .. (4..7),
+// the A planes' order; the matching codes are the two runs of 16 codes at those
+// elements, 2 BITS bytes each: run 0 at byte 2 BITS kg of the row's chunk, run 1 at
+// 8 BITS + 2 BITS kg.  Each run is loaded as whole words (3-bit: the 8 bytes from the
+// 4-byte boundary below it) into codes[m][f] (run 0: x / y, run 1: z / w); with the
+// group's scale and bias (sb) per group of the chunk.  Loads past the row (the half
+// of a last chunk that holds no group, for K not a whole number of chunks) read the
+// row's last words instead; their group is skipped.
+template <int AK, int NM, int NF>
+__device__ __forceinline__ void p3_issue_aff(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
+                                             const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
+                                             const int (&nrow)[NF], int c, int kg, int wave, int row_bytes,
+                                             int groups, P3Chunk<NM, NF>& out) {
+  constexpr int BITS = ak_bits(AK), GPC = ak_gpc(AK), CB = 16 * BITS;
+  constexpr int LB = BITS == 2 ? 4 : 8;   // bytes per run load
+#pragma unroll
+  for (int q = 0; q < P3_ASLOTS; ++q)
+    tile::lds_load16_untracked(asrc[q] + (size_t)c * P3_ROWB, stage + (P3_ASLOTS * wave + q) * 1024);
+  const int r0 = (2 * BITS * kg) & ~3, r1 = r0 + 8 * BITS;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint8_t* row = base + woff[m] + nrow[f] * row_bytes;
+      const int o0 = min(c * CB + r0, row_bytes - LB), o1 = min(c * CB + r1, row_bytes - LB);
+      if constexpr (BITS == 2) {
+        out.codes[m][f] = make_uint4(*reinterpret_cast<const uint32_t*>(row + o0),
+                                     *reinterpret_cast<const uint32_t*>(row + o1), 0u, 0u);
+      } else {
+        const uint2 a = *reinterpret_cast<const uint2*>(row + o0);
+        const uint2 b = *reinterpret_cast<const uint2*>(row + o1);
+        out.codes[m][f] = make_uint4(a.x, a.y, b.x, b.y);
+      }
+    }
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int h = 0; h < GPC; ++h) {
+        const int si = (nrow[f] * groups + min(c * GPC + h, groups - 1)) * 2;
+        out.sb[m][f][h] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
+                          ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
+      }
+}
+
+// The fp8 B operand of a lane from its two code runs (one code per byte).
+template <int BITS>
+__device__ __forceinline__ i32x8_t aff_code_bytes(const uint4& w, int kg) {
+  uint32_t o[8];
+  if constexpr (BITS == 4) {
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx::nibbles_to_bytes(v[j], o[2 * j], o[2 * j + 1]);
+  } else if constexpr (BITS == 2) {
+    const uint32_t v[2] = {w.x, w.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      mx::nibbles_to_bytes(q2_nibbles(v[j] & 0xFFFFu), o[4 * j], o[4 * j + 1]);
+      mx::nibbles_to_bytes(q2_nibbles(v[j] >> 16), o[4 * j + 2], o[4 * j + 3]);
+    }
+  } else {
+    const uint32_t sh = (uint32_t)(2 * BITS * kg & 3) * 8;   // the run's offset in its first word
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t lo = __builtin_amdgcn_alignbit(v[2 * j + 1], v[2 * j], sh);
+      const uint32_t hi = v[2 * j + 1] >> sh;
+      mx::nibbles_to_bytes(mx::spread3(lo & 0xFFFFFFu), o[4 * j], o[4 * j + 1]);
+      mx::nibbles_to_bytes(mx::spread3(__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFFFFFu), o[4 * j + 2],
+                           o[4 * j + 3]);
+    }
+  }
+  return i32x8_t{(int)o[0], (int)o[1], (int)o[2], (int)o[3], (int)o[4], (int)o[5], (int)o[6], (int)o[7]};
+}
+
+// Affine chunk with fp8 codes: per token block, per group h of the chunk, the two
+// plane instructions into a zeroed tile, then the group formula folded in.  With two
+// groups per chunk (G = 64) both instructions take the whole operand and the B scale
+// keeps one group: 2^9 on the group's two blocks (lane groups 2h, 2h + 1), 2^-127 (E8M0
+// 0) on the other's, whose terms then lie below 2^-120 of the result's scale.
+template <int AK, int NM, int NF>
+__device__ __forceinline__ void p3_compute_aff(const uint8_t* ab, const uint8_t* sbuf, int sbs, const float* sxs,
+                                               const P3Chunk<NM, NF>& ch, int c, int i, int kg, int ntb, int groups,
+                                               bool f16, float (&acc)[NM][NF][P3_TB][4]) {
+  constexpr int GPC = ak_gpc(AK);
+  i32x8_t b[NM][NF];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int f = 0; f < NF; ++f) b[m][f] = aff_code_bytes<ak_bits(AK)>(ch.codes[m][f], kg);
+  const int nh = min(GPC, groups - c * GPC);   // the chunk's groups inside the row
+#pragma unroll
+  for (int tb = 0; tb < P3_TB; ++tb) {
+    if (tb >= ntb) break;
+    const int row = tb * 16 + i;
+    const uint8_t* ar = ab + row * P3_ROWB;
+    const uint4 h0 = mx::lds16(ar + ((kg ^ i) << 4));
+    const uint4 h1 = mx::lds16(ar + (((4 + kg) ^ i) << 4));
+    const uint4 l0 = mx::lds16(ar + (((8 + kg) ^ i) << 4));
+    const uint4 l1 = mx::lds16(ar + (((12 + kg) ^ i) << 4));
+    const uint32_t sa = *reinterpret_cast<const uint16_t*>(sbuf + row * sbs + (4 * c + kg) * 2);
+    const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+    const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+    for (int h = 0; h < GPC; ++h) {
+      if (h >= nh) break;
+      const uint32_t bsc = GPC == 1 || (kg >> 1) == h ? E8M0_2P9 : 0u;
+      f32x4_t d[NM][NF];
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0, true>(ahi, b[m][f], mx::zero_acc(), sa, bsc);
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<1, true>(alo, b[m][f], d[m][f], sa, bsc);
+      const float4 sx = *reinterpret_cast<const float4*>(sxs + (c * GPC + h) * P3_MT + tb * 16 + 4 * kg);
+      const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const float sc = scale_bits_to_f32((uint16_t)(ch.sb[m][f][h] & 0xFFFFu), f16);
+          const float bi = scale_bits_to_f32((uint16_t)(ch.sb[m][f][h] >> 16), f16);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = acc[m][f][tb][r] + (sc * d[m][f][r] + bi * sxv[r]);
+        }
+    }
+  }
+}
+
 // grid = slices * tiles rounded up to 8; dynamic LDS = P3_STAGES * P3_ABYTES + P3_MT * (sb + 16)
 // (+ the tile's chunk sums, P3_MT * kch floats, for 2-bit banks).
-template <bool Q2, int NM, int NF>
+template <int AK, int NM, int NF>
 __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
+  constexpr bool Q2 = ak_fold(AK);   // affine: the group formula per group
+  constexpr int GPC = ak_gpc(AK);
   extern __shared__ __align__(16) uint8_t p3_lds[];
   uint8_t* abuf = p3_lds;
   uint8_t* sbuf = p3_lds + P3_STAGES * P3_ABYTES;
   const int sbs = g.sb + 16;   // LDS row stride of the A scales (bank spread)
-  float* sxs = reinterpret_cast<float*>(sbuf + P3_MT * sbs);   // 2-bit: the tile's chunk sums [kch][MT]
+  float* sxs = reinterpret_cast<float*>(sbuf + P3_MT * sbs);   // affine: the tile's group sums [kch * GPC][MT]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 15, kg = lane >> 4;
@@ -384,7 +543,9 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = 0.0f;
   if (slot >= 0) {
-    const int row_bytes = Q2 ? g.kch * 32 : g.K / 2, blocks = g.K / 32;
+    // affine rows hold whole groups (the bank pads the last one)
+    const int groups = (g.K + ak_group(AK) - 1) / ak_group(AK);
+    const int row_bytes = !Q2 ? g.K / 2 : groups * ak_group(AK) * ak_bits(AK) / 8, blocks = g.K / 32;
     // the tile's A scales into LDS for the whole K loop (rows past the tile: its last row)
     const int sq = g.sb / 16;
     for (int it = threadIdx.x; it < P3_MT * sq; it += P3_THREADS) {
@@ -394,12 +555,13 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
       *reinterpret_cast<uint4*>(sbuf + r * sbs + q * 16) =
           *reinterpret_cast<const uint4*>(g.as + (size_t)src * g.sb + q * 16);
     }
-    if constexpr (Q2) {   // and the tile's chunk sums of A
-      for (int it = threadIdx.x; it < P3_MT * g.kch; it += P3_THREADS) {
+    if constexpr (Q2) {   // and the tile's group sums of A
+      const int ns = g.kch * GPC;
+      for (int it = threadIdx.x; it < P3_MT * ns; it += P3_THREADS) {
         const int ch = it / P3_MT, r = it - ch * P3_MT;
         const int rr = row0 + min(r, rows - 1);
         const int src = g.a_gather ? g.a_gather[rr] : rr;
-        sxs[it] = g.asum[(size_t)src * g.kch + ch];
+        sxs[it] = g.asum[(size_t)src * ns + ch];
       }
     }
     // A plane sources of the lane's slots: slot S = 64 (P3_ASLOTS wave + q) + lane holds
@@ -442,7 +604,10 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
     // every issue is unconditional (a chunk past the end re-reads the last one into a
     // stage nothing reads again), so each wait is for exactly the loads it needs
     if constexpr (!Q2) sgrp[0] = *reinterpret_cast<const uint4*>(sgp);
-    if constexpr (Q2) p3_issue_q2<NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kg, wave, row_bytes, nch, ring[0]);
+    if constexpr (ak_bytes(AK))
+      p3_issue_aff<AK, NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kg, wave, row_bytes, groups, ring[0]);
+    else if constexpr (Q2)
+      p3_issue_q2<NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kg, wave, row_bytes, nch, ring[0]);
     else p3_issue<NM, NF>(abuf, asrc, wrow, 0, kg, wave, row_bytes, ring[0]);
     // eight chunks per trip: A stage and code ring index u % 2, scale group buffer (u / 4) % 2
     for (int c0 = 0; c0 < nch; c0 += 8) {
@@ -453,20 +618,26 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
         // here; its earlier direct-to-LDS loads complete first), then every wave's
         // (2-bit: the pair's bias is the last load of a chunk; the first barrier also
         // publishes the chunk sums stored above)
-        if constexpr (Q2) asm volatile("" ::"v"(ring[u % 2].sb[NM - 1][NF - 1]) : "memory");
+        if constexpr (Q2) asm volatile("" ::"v"(ring[u % 2].sb[NM - 1][NF - 1][GPC - 1]) : "memory");
         else asm volatile("" ::"v"(ring[u % 2].codes[NM - 1][NF - 1].w) : "memory");
         lds_sync();
         if constexpr (!Q2)
           if ((u + 1) % 4 == 0)   // the scale group of chunk c + 1
             sgrp[((u + 1) / 4) % 2] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 1) / 4, ngrp - 1));
-        if constexpr (Q2)
+        if constexpr (ak_bytes(AK))
+          p3_issue_aff<AK, NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
+                                   min(c + 1, nch - 1), kg, wave, row_bytes, groups, ring[(u + 1) % 2]);
+        else if constexpr (Q2)
           p3_issue_q2<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
                               min(c + 1, nch - 1), kg, wave, row_bytes, nch, ring[(u + 1) % 2]);
         else
           p3_issue<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, wrow, min(c + 1, nch - 1), kg, wave, row_bytes,
                            ring[(u + 1) % 2]);
         if (c < nch) {
-          if constexpr (Q2) {
+          if constexpr (ak_bytes(AK)) {
+            p3_compute_aff<AK, NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], c, i, kg, ntb, groups,
+                                       g.L.f16, acc);
+          } else if constexpr (Q2) {
             p3_compute_q2<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], c, i, kg, ntb, g.L.f16,
                                   acc);
           } else {
@@ -535,14 +706,18 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
           if (i == 0) red[wave * P3_MT + tr] = hsv;
         }
       }
-    if constexpr (Q2) {   // the workgroup's 128 columns are one chunk of h: its sum per row, waves in order
+    if constexpr (Q2) {   // the workgroup's 128 columns are one chunk of h: its group sums per row,
+                          // waves in order (G = 64: waves 0, 1 and 2, 3)
       lds_sync();
       if ((int)threadIdx.x < rows) {
         const int tr = threadIdx.x;
-        float t = 0.0f;
 #pragma unroll
-        for (int w = 0; w < P3_WAVES; ++w) t = t + red[w * P3_MT + tr];
-        g.hsum[(size_t)(row0 + tr) * g.hkch + slice] = t;
+        for (int h = 0; h < GPC; ++h) {
+          float t = 0.0f;
+#pragma unroll
+          for (int w = h * P3_WAVES / GPC; w < (h + 1) * P3_WAVES / GPC; ++w) t = t + red[w * P3_MT + tr];
+          g.hsum[(size_t)(row0 + tr) * g.hkch * GPC + slice * GPC + h] = t;
+        }
       }
     }
   } else {
@@ -566,13 +741,14 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
 }  // namespace
 
 // Workspace of the block-scaled prefill beyond the tile list: x planes [T][D/128][256]
-// and scales [T][sb(D)], h planes [rows][F_pad/128][256] and scales [rows][sb(F_pad)].
+// and scales [T][sb(D)], h planes [rows][F_pad/128][256] and scales [rows][sb(F_pad)],
+// affine group sums of x [T][D/64 or D/128] and of h [rows][2 or 1 per 128 columns].
 size_t prefill_mx_ws_bytes(int T, int k, int D, int F) {
   const size_t rows = (size_t)T * k;
   const int fch = (F + 127) / 128;
   auto a256 = [](size_t v) { return (v + 255) & ~size_t(255); };
   return a256((size_t)T * D * 2) + a256((size_t)T * scale_row_bytes(D)) + a256(rows * fch * P3_ROWB) +
-         a256(rows * scale_row_bytes(fch * 128)) + a256((size_t)T * (D / 128) * 4) + a256(rows * fch * 4);
+         a256(rows * scale_row_bytes(fch * 128)) + a256((size_t)T * (D / 64) * 4) + a256(rows * fch * 2 * 4);
 }
 
 // Shapes and slot layouts the kernels take.  Their B-scale loads read 16 bytes per
@@ -598,7 +774,7 @@ bool prefill_mx_q2_supported(int D, int F) {
 
 namespace {
 
-template <bool Q2>
+template <int AK>
 int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L, const int32_t* slot_table,
               const int32_t* offsets, const int2* tiles, const int32_t* tiles_n, int max_tiles,
               const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k, float limit,
@@ -612,10 +788,12 @@ int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layou
   uint8_t* hp = xs + a256((size_t)T * sbx);
   uint8_t* hs = hp + a256(rows * fch * P3_ROWB);
   float* xsum = reinterpret_cast<float*>(hs + a256(rows * sbh));
-  float* hsum = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xsum) + a256((size_t)T * (D / 128) * 4));
+  float* hsum = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xsum) + a256((size_t)T * (D / 64) * 4));
+  constexpr bool Q2 = ak_fold(AK);
+  constexpr int GPC = ak_gpc(AK);
   const int64_t groups = (int64_t)T * D / 8;
   hipLaunchKernelGGL(x_planes_rows_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, x, T, D, xp, xs,
-                     sbx, Q2 ? xsum : nullptr);
+                     sbx, Q2 ? xsum : nullptr, 128 / GPC);
   int rc = check_launch("x_planes_rows_kernel");
   if (rc) return rc;
   const int tiles8 = (max_tiles + 7) / 8 * 8;
@@ -623,8 +801,8 @@ int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layou
             row_w, D, F, k, limit, hp, hs, sbh, fch, nullptr, xsum, hsum};
   const int s_gu = (fch * 128) / (P3_WAVES * 32);   // h's padded columns, 128 per workgroup
   const size_t lds_gu = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbx + 16) +
-                        (Q2 ? (size_t)P3_MT * (D / 128) * 4 : 0);
-  auto kgu = p3_kernel<Q2, 2, 2>;
+                        (Q2 ? (size_t)P3_MT * (D / 128) * GPC * 4 : 0);
+  auto kgu = p3_kernel<AK, 2, 2>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds_gu) != hipSuccess)
     return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_gu);
@@ -635,8 +813,8 @@ int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layou
             F, D, k, limit, nullptr, nullptr, 0, 0, y, hsum, nullptr};
   const int s_dn = (D + P3_WAVES * 64 - 1) / (P3_WAVES * 64);
   const size_t lds_dn = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbh + 16) +
-                        (Q2 ? (size_t)P3_MT * fch * 4 : 0);
-  auto kdn = p3_kernel<Q2, 1, 4>;
+                        (Q2 ? (size_t)P3_MT * fch * GPC * 4 : 0);
+  auto kdn = p3_kernel<AK, 1, 4>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kdn), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds_dn) != hipSuccess)
     return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_dn);
@@ -651,7 +829,7 @@ int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decod
                       const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
                       int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
                       int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s) {
-  return launch_p3<false>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot, row_w,
+  return launch_p3<AK_FP4>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot, row_w,
                           D, F, k, limit, ws, y, s);
 }
 
@@ -661,8 +839,30 @@ int launch_prefill_mx_q2(const uint16_t* x, int T, const uint8_t* pool, const de
                          const int32_t* tiles_n, int max_tiles, const int32_t* row_token, const int32_t* row_slot,
                          const float* row_w, int D, int F, int k, float limit, uint8_t* ws, uint16_t* y,
                          hipStream_t s) {
-  return launch_p3<true>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot, row_w,
-                         D, F, k, limit, ws, y, s);
+  return launch_p3<AK_Q2>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot, row_w,
+                          D, F, k, limit, ws, y, s);
+}
+
+// The other affine widths the kernels take: 2-bit codes in groups of 64, 3- and 4-bit
+// codes in groups of 64 or 128 (groups of 32 would need four instructions per plane
+// and chunk), in the shapes of the FP4 envelope with F a multiple of 64.
+bool prefill_mx_aff_supported(int bits, int group, int D, int F) {
+  const bool kind = (bits == 2 && group == 64) || ((bits == 3 || bits == 4) && (group == 64 || group == 128));
+  return kind && D % 128 == 0 && D >= 512 && D <= 8192 && F % 64 == 0 && F >= 512 && F <= 8192;
+}
+
+int launch_prefill_mx_aff(int bits, int group, const uint16_t* x, int T, const uint8_t* pool,
+                          const decode::Layout& L, const int32_t* slot_table, const int32_t* offsets,
+                          const int2* tiles, const int32_t* tiles_n, int max_tiles, const int32_t* row_token,
+                          const int32_t* row_slot, const float* row_w, int D, int F, int k, float limit, uint8_t* ws,
+                          uint16_t* y, hipStream_t s) {
+#define CACHALOT_P3AFF(B, G)                                                                                       \
+  if (bits == B && group == G)                                                                                     \
+    return launch_p3<ak_aff(B, G)>(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token,      \
+                                   row_slot, row_w, D, F, k, limit, ws, y, s);
+  CACHALOT_P3AFF(2, 64) CACHALOT_P3AFF(3, 64) CACHALOT_P3AFF(3, 128) CACHALOT_P3AFF(4, 64) CACHALOT_P3AFF(4, 128)
+#undef CACHALOT_P3AFF
+  return fail(CACHALOT_EINVAL, "prefill (block-scaled): %d-bit codes in groups of %d", bits, group);
 }
 
 }  // namespace cachalot

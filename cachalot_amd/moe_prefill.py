@@ -99,7 +99,7 @@ def grouped_experts(x: torch.Tensor, indices: torch.Tensor, weights: torch.Tenso
     y = torch.empty((t, k, d), dtype=torch.bfloat16, device=dev)
     generic = fmt.kind == "affine" and not (fmt.bits == 2 and fmt.group_size == 128)
     if generic:
-        nbytes = L.cachalot_grouped_experts_affine_workspace_bytes(t, k, n_experts, f)
+        nbytes = L.cachalot_grouped_experts_affine_workspace_bytes(t, k, n_experts, d, f)
     else:
         nbytes = L.cachalot_grouped_experts_workspace_bytes(t, k, n_experts, d, f)
     ws = _workspace(dev, nbytes)

@@ -385,7 +385,7 @@ int cachalot_moe_layer_decode_affine(const uint16_t* x, const uint16_t* gate_wei
                                      const uint16_t* addend, int32_t* idx_out, float* w_out, float* scores,
                                      float* routed, uint16_t* out, void* workspace, size_t workspace_bytes,
                                      cachalot_stream_t stream);
-size_t cachalot_grouped_experts_affine_workspace_bytes(int T, int k, int E, int F);
+size_t cachalot_grouped_experts_affine_workspace_bytes(int T, int k, int E, int D, int F);
 int cachalot_grouped_experts_affine(const uint16_t* x, const uint8_t* pool,
                                     const cachalot_expert_layout* layout /* host */, const int32_t* slot_table,
                                     const int32_t* offsets, const int32_t* row_token, const int32_t* row_slot,

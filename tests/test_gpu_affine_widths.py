@@ -74,6 +74,7 @@ def test_affine_decode_terms(cuda, bits, group, sd, path, monkeypatch):
     from cachalot_amd.moe_decode import decode_experts, moe_layer_decode
 
     monkeypatch.setenv("CACHALOT_AFFINE_VALU", "1" if path == "valu" else "0")
+    monkeypatch.setenv("CACHALOT_PREFILL_BF16", "1" if path == "bf16" else "0")
     fmt = _fmt(bits, group, sd)
     store = make_store(fmt, n_layers=1, n_experts=384)
     rng = np.random.default_rng(bits * 100 + group)
@@ -101,21 +102,27 @@ def test_affine_decode_terms(cuda, bits, group, sd, path, monkeypatch):
     _check_decode(f"affine {bits}-bit g{group} {path} layer", fmt, 0, xf, oi[0], ow[0], _np(routed), _f32(out), terms, xf)
 
 
+# path: "mfma" = the default kernels (64-row tiles: the block-scaled prefill kernels for
+# 2-bit g64 and 3- / 4-bit g64 / g128, the bf16-MFMA grouped kernels for groups of 32;
+# 16-row tiles at t = 4), "bf16" = the bf16-MFMA grouped kernels (CACHALOT_PREFILL_BF16=1),
+# "valu" = the VALU kernels (CACHALOT_AFFINE_VALU=1)
 GROUPED_CASES = [(3, 64, "float16", "mfma", 37, 16), (4, 32, "bfloat16", "mfma", 37, 16),
                  (3, 128, "bfloat16", "mfma", 37, 16), (2, 64, "float16", "mfma", 37, 16),
                  (4, 128, "float16", "mfma", 200, 8), (2, 32, "bfloat16", "mfma", 4, 16),
                  (3, 32, "float16", "mfma", 4, 16), (4, 64, "bfloat16", "mfma", 37, 16),
+                 (3, 64, "float16", "mfma", 200, 8), (3, 64, "bfloat16", "bf16", 37, 16),
+                 (4, 128, "float16", "bf16", 200, 8),
                  (3, 64, "float16", "valu", 37, 16), (4, 32, "bfloat16", "valu", 37, 16)]
 
 
 @pytest.mark.parametrize("bits,group,sd,path,t,E", GROUPED_CASES)
 def test_affine_grouped_rows(cuda, bits, group, sd, path, t, E, monkeypatch):
-    """t tokens x top-6 over E experts (uneven rows), three dropped ids, on the bf16-MFMA grouped
-    kernels (64-row tiles; 16-row tiles at t = 4; T = 200 over 8 experts: experts of several
-    tiles) and on the VALU kernels (CACHALOT_AFFINE_VALU=1)."""
+    """t tokens x top-6 over E experts (uneven rows), three dropped ids, on each kernel family
+    (T = 200 over 8 experts: experts of several tiles)."""
     from cachalot_amd.moe_prefill import grouped_experts
 
     monkeypatch.setenv("CACHALOT_AFFINE_VALU", "1" if path == "valu" else "0")
+    monkeypatch.setenv("CACHALOT_PREFILL_BF16", "1" if path == "bf16" else "0")
     fmt = _fmt(bits, group, sd)
     k = 6
     store = make_store(fmt, n_layers=1, n_experts=E)
