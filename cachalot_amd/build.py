@@ -36,13 +36,18 @@ CFLAGS = [
 ]
 
 
+# Per-file flags.  prefill_affine_mx.hip: matrix-core results in VGPRs, where its
+# per-group fold reads them (the other kernels keep their accumulators in AGPRs).
+FILE_FLAGS = {"prefill_affine_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr[-6000:]}")

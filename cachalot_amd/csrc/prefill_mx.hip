@@ -53,65 +53,18 @@
 #include "decode_common.h"
 #include "mfma_tile.h"
 #include "mx_tile.h"
+#include "prefill_mx.h"
 
 namespace cachalot {
+
+// affine groups of 64 (prefill_affine_mx.hip)
+int launch_prefill_affine_g64(int ak, const pmx::MxArgs& gu, int s_gu, size_t lds_gu, const pmx::MxArgs& dn,
+                              int s_dn, size_t lds_dn, int tiles8, hipStream_t s);
+
 namespace {
 
 using namespace decode;
-
-constexpr int P3_THREADS = 256;
-constexpr int P3_WAVES = 4;
-constexpr int P3_MT = 64;                     // token rows per tile
-constexpr int P3_TB = P3_MT / 16;             // token fragments
-constexpr int P3_STAGES = 2;
-constexpr int P3_ROWB = 256;                  // one row's chunk: hi 128 B | lo 128 B
-constexpr int P3_ABYTES = P3_MT * P3_ROWB;    // 16 KiB per stage
-constexpr int P3_ASLOTS = P3_ABYTES / 16 / P3_THREADS;   // 16-byte A slots per lane and chunk (4)
-
-typedef __attribute__((ext_vector_type(8))) int i32x8_t;
-typedef __attribute__((ext_vector_type(4))) float f32x4_t;
-
-// Weight kinds of p3_kernel (AK): FP4; 2-bit g128 with the codes as fp4 operands;
-// (BITS << 8) | G for affine codes as fp8 operands (code q as the E4M3 byte q, which
-// is q * 2^-9 -- subnormal below 8 -- with B scale 2^9).
-constexpr int AK_FP4 = 0;
-constexpr int AK_Q2 = 1;
-constexpr int ak_aff(int bits, int g) { return (bits << 8) | g; }
-constexpr bool ak_fold(int ak) { return ak != AK_FP4; }       // group formula per group
-constexpr bool ak_bytes(int ak) { return ak > AK_Q2; }        // codes as fp8 bytes
-constexpr int ak_bits(int ak) { return ak == AK_Q2 ? 2 : ak >> 8; }
-constexpr int ak_group(int ak) { return ak == AK_Q2 ? 128 : (ak & 255); }
-constexpr int ak_gpc(int ak) { return ak_fold(ak) ? 128 / ak_group(ak) : 1; }   // groups per K chunk
-constexpr uint32_t E8M0_2P9 = 136u;                            // 2^9
-
-struct MxArgs {
-  const uint8_t* ap;          // A planes [source rows][kch][256]
-  const uint8_t* as;          // A scales [source rows][sb]
-  int sb;                     // A scale bytes per source row
-  int kch;                    // 128-element chunks along K (K_pad / 128)
-  const int32_t* a_gather;    // source row of a tile row (row_token) or null (the row itself)
-  const uint8_t* pool;
-  Layout L;
-  const int32_t* slot_table;
-  const int32_t* offsets;
-  const int2* tiles;
-  const int32_t* tiles_n;
-  const int32_t* row_token;
-  const int32_t* row_slot;
-  const float* row_w;
-  int K;                      // real K (D or F)
-  int N;                      // weight rows per matrix (F or D)
-  int k;
-  float limit;
-  uint8_t* hp;                // gate/up: h planes [rows][hkch][256]
-  uint8_t* hs;                // gate/up: h scales [rows][hsb]
-  int hsb, hkch;
-  uint16_t* y;                // down: [T, k, N]
-  const float* asum;          // 2-bit: chunk sums of the A source rows [source rows][kch]
-  float* hsum;                // 2-bit gate/up: chunk sums of h [rows][hkch]
-};
-
-__host__ __device__ inline int scale_row_bytes(int K) { return (K / 32 * 2 + 15) / 16 * 16; }
+using namespace pmx;
 
 // D += A (fp8 plane, row scales = byte OPSEL_A of sa) x B (fp4 codes, column scales = byte 0 of sb).
 // The destination must not share registers with A or B (see mx_tile.h).  The empty
@@ -161,14 +114,6 @@ __device__ __forceinline__ void encode8(const float (&v)[8], float inv, uint2& h
   l1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r[6], r[7], (int)l1, true);
   hi = make_uint2(h0, h1);
   lo = make_uint2(l0, l1);
-}
-
-// Plane scale exponent of a block whose largest magnitude is m: E = e(m) - 7,
-// clamped so that both E8M0 bytes (E + 127, E + 123) are finite scales.
-__device__ __forceinline__ int plane_exp(float m) {
-  const int e = (int)((__float_as_uint(m) >> 23) & 0xffu) - 127;   // zero / subnormal max: -127
-  const int E = e - 7;
-  return E < -123 ? -123 : (E > 120 ? 120 : E);
 }
 
 // x [T, D] bf16 -> planes and scales per token.  One thread = 8 values; the four
@@ -260,14 +205,6 @@ __device__ __forceinline__ void p3_issue_q2(uint8_t* stage, const uint8_t* (&asr
       out.sb[m][f][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
                      ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
     }
-}
-
-// Sixteen 2-bit codes (the low or high half of a word) one per nibble in natural
-// order, nibble n = E2M1 of code n / 2.
-__device__ __forceinline__ uint32_t q2_nibbles(uint32_t v16) {
-  uint32_t t = (v16 & 0xFFu) | ((v16 & 0xFF00u) << 8);
-  t = (t & 0x000F000Fu) | ((t & 0x00F000F0u) << 4);
-  return (t & 0x03030303u) | ((t & 0x0C0C0C0Cu) << 2);
 }
 
 // B scales of chunk c = 4 g + J from the group registers (lane (i, p) holds the 16
@@ -369,7 +306,7 @@ __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* 
       for (int f = 0; f < NF; ++f)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          acc[m][f][tb][r] = acc[m][f][tb][r] + (sc[m][f] * d[m][f][r] + bi[m][f] * sxv[r]);
+          acc[m][f][tb][r] = fmaf(sc[m][f], d[m][f][r], fmaf(bi[m][f], sxv[r], acc[m][f][tb][r]));
   }
 }
 
@@ -418,36 +355,6 @@ __device__ __forceinline__ void p3_issue_aff(uint8_t* stage, const uint8_t* (&as
         out.sb[m][f][h] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
                           ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
       }
-}
-
-// The fp8 B operand of a lane from its two code runs (one code per byte).
-template <int BITS>
-__device__ __forceinline__ i32x8_t aff_code_bytes(const uint4& w, int kg) {
-  uint32_t o[8];
-  if constexpr (BITS == 4) {
-    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) mx::nibbles_to_bytes(v[j], o[2 * j], o[2 * j + 1]);
-  } else if constexpr (BITS == 2) {
-    const uint32_t v[2] = {w.x, w.y};
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      mx::nibbles_to_bytes(q2_nibbles(v[j] & 0xFFFFu), o[4 * j], o[4 * j + 1]);
-      mx::nibbles_to_bytes(q2_nibbles(v[j] >> 16), o[4 * j + 2], o[4 * j + 3]);
-    }
-  } else {
-    const uint32_t sh = (uint32_t)(2 * BITS * kg & 3) * 8;   // the run's offset in its first word
-    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t lo = __builtin_amdgcn_alignbit(v[2 * j + 1], v[2 * j], sh);
-      const uint32_t hi = v[2 * j + 1] >> sh;
-      mx::nibbles_to_bytes(mx::spread3(lo & 0xFFFFFFu), o[4 * j], o[4 * j + 1]);
-      mx::nibbles_to_bytes(mx::spread3(__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFFFFFu), o[4 * j + 2],
-                           o[4 * j + 3]);
-    }
-  }
-  return i32x8_t{(int)o[0], (int)o[1], (int)o[2], (int)o[3], (int)o[4], (int)o[5], (int)o[6], (int)o[7]};
 }
 
 // Affine chunk with fp8 codes: per token block, per group h of the chunk, the two
@@ -500,7 +407,7 @@ __device__ __forceinline__ void p3_compute_aff(const uint8_t* ab, const uint8_t*
           const float sc = scale_bits_to_f32((uint16_t)(ch.sb[m][f][h] & 0xFFFFu), f16);
           const float bi = scale_bits_to_f32((uint16_t)(ch.sb[m][f][h] >> 16), f16);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = acc[m][f][tb][r] + (sc * d[m][f][r] + bi * sxv[r]);
+          for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = fmaf(sc, d[m][f][r], fmaf(bi, sxv[r], acc[m][f][tb][r]));
         }
     }
   }
@@ -738,295 +645,6 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
   }
 }
 
-// ---------------------------------------------------------------------------------
-// Affine codes in groups of 64 or 128 on v_mfma_scale_f32_32x32x64_f8f6f4: one
-// instruction per plane covers one 64-element half of a K chunk, so a group of 64 is
-// one instruction and nothing is masked (the 16 x 16 x 128 form above spends half of
-// each instruction on the other group).  Operand layout (fp8, measured): lane l holds
-// row (A) or column (B) l & 31; its registers 0..3 carry elements 16 (l >> 5) .. + 15 of
-// the 64, registers 4..7 elements 32 + 16 (l >> 5) .. + 15; the scale of block b
-// (elements 32 b .. 32 b + 31) of row r comes from lane 32 b + r.  Result register j of
-// lane l: row 8 (j / 4) + 4 (l >> 5) + (j & 3), column l & 31.
-//
-// One 256-thread workgroup = the 64-row M tile x 32 NF weight rows per wave of each of
-// NM matrices (gate/up: NM = 2, NF = 1; down: NM = 1, NF = 2); the A ring, the tile
-// mapping and the plane writers are those of p3_kernel.
-typedef __attribute__((ext_vector_type(16))) float f32x16_t;
-constexpr int P4_TB = P3_MT / 32;   // 32-row token blocks
-
-__device__ __forceinline__ f32x16_t zero16() {
-  f32x16_t z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-  asm volatile("" : "+a"(z));
-  return z;
-}
-
-template <int OPSEL_A>
-__device__ __forceinline__ f32x16_t mfma32_plane(const i32x8_t& a, const i32x8_t& b, f32x16_t c, uint32_t sa) {
-  f32x16_t d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, OPSEL_A, (int)sa, 0, (int)E8M0_2P9);
-  asm volatile("" : "+a"(d) : "v"(a), "v"(b));
-  return d;
-}
-
-template <int NP>
-struct P4Chunk {
-  uint4 codes[NP][2];   // per (matrix, weight block) pair and half of the chunk: the lane's two runs
-  uint32_t sb[NP][2];   // scale | bias << 16 of the group of each half
-};
-
-// Codes of half h of chunk c for lane half kh: runs at elements 64 h + 16 kh and + 32,
-// 2 BITS bytes each, loaded as whole words as in p3_issue_aff.
-template <int AK, int NM, int NF>
-__device__ __forceinline__ void p4_issue(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
-                                         const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
-                                         const int (&nrow)[NF], int c, int kh, int wave, int row_bytes, int groups,
-                                         P4Chunk<NM * NF>& out) {
-  constexpr int BITS = ak_bits(AK), GPC = ak_gpc(AK), CB = 16 * BITS;
-  constexpr int LB = BITS == 2 ? 4 : 8;
-#pragma unroll
-  for (int q = 0; q < P3_ASLOTS; ++q)
-    tile::lds_load16_untracked(asrc[q] + (size_t)c * P3_ROWB, stage + (P3_ASLOTS * wave + q) * 1024);
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const uint8_t* row = base + woff[m] + nrow[f] * row_bytes;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int r0 = (2 * BITS * (4 * h + kh)) & ~3, r1 = (2 * BITS * (4 * h + kh) + 4 * BITS) & ~3;
-        const int o0 = min(c * CB + r0, row_bytes - LB), o1 = min(c * CB + r1, row_bytes - LB);
-        if constexpr (BITS == 2) {
-          out.codes[m * NF + f][h] = make_uint4(*reinterpret_cast<const uint32_t*>(row + o0),
-                                                *reinterpret_cast<const uint32_t*>(row + o1), 0u, 0u);
-        } else {
-          const uint2 a = *reinterpret_cast<const uint2*>(row + o0);
-          const uint2 b = *reinterpret_cast<const uint2*>(row + o1);
-          out.codes[m * NF + f][h] = make_uint4(a.x, a.y, b.x, b.y);
-        }
-      }
-    }
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int h = 0; h < GPC; ++h) {
-        const int si = (nrow[f] * groups + min(c * GPC + h, groups - 1)) * 2;
-        out.sb[m * NF + f][h] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
-                                ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
-      }
-}
-
-// One chunk: per token block and half h, the two plane instructions of every pair;
-// the group formula after each group (G = 64: each half; G = 128: the second half).
-// The token blocks run one after the other, so one block's tiles are live at a time.
-template <int AK, int NP>
-__device__ __forceinline__ void p4_compute(const uint8_t* ab, const uint8_t* sbuf, int sbs, const float* sxs,
-                                           const P4Chunk<NP>& ch, int c, int lane, int ntb, int groups, bool f16,
-                                           float (&acc)[NP][P4_TB][16]) {
-  constexpr int GPC = ak_gpc(AK);
-  const int r32 = lane & 31, kh = lane >> 5;
-  const int nh = GPC == 2 ? min(2, groups - 2 * c) : 2;   // halves inside the row's groups
-#pragma unroll
-  for (int tb = 0; tb < P4_TB; ++tb) {
-    if (tb >= ntb) break;
-    const int row = tb * 32 + r32;
-    const uint8_t* ar = ab + row * P3_ROWB;
-    f32x16_t d[NP];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (h >= nh) break;
-      const int gl = GPC == 2 ? h : 0;   // the half's group in the chunk
-      i32x8_t b[NP];
-#pragma unroll
-      for (int p = 0; p < NP; ++p) b[p] = aff_code_bytes<ak_bits(AK)>(ch.codes[p][h], kh);
-      const int c0 = 4 * h + kh, c1 = 4 * h + 2 + kh;   // 16-byte columns of the hi plane
-      const uint4 h0 = mx::lds16(ar + ((c0 ^ (row & 15)) << 4));
-      const uint4 h1 = mx::lds16(ar + ((c1 ^ (row & 15)) << 4));
-      const uint4 l0 = mx::lds16(ar + (((8 + c0) ^ (row & 15)) << 4));
-      const uint4 l1 = mx::lds16(ar + (((8 + c1) ^ (row & 15)) << 4));
-      const uint32_t sa = *reinterpret_cast<const uint16_t*>(sbuf + row * sbs + (4 * c + 2 * h + kh) * 2);
-      const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-      const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
-#pragma unroll
-      for (int p = 0; p < NP; ++p) d[p] = mfma32_plane<0>(ahi, b[p], GPC == 1 && h == 1 ? d[p] : zero16(), sa);
-#pragma unroll
-      for (int p = 0; p < NP; ++p) d[p] = mfma32_plane<1>(alo, b[p], d[p], sa);
-      if (GPC == 2 || h == 1) {
-        float sx[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 v = *reinterpret_cast<const float4*>(sxs + (c * GPC + gl) * P3_MT + tb * 32 + 8 * q + 4 * kh);
-          sx[4 * q] = v.x;
-          sx[4 * q + 1] = v.y;
-          sx[4 * q + 2] = v.z;
-          sx[4 * q + 3] = v.w;
-        }
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const float sc = scale_bits_to_f32((uint16_t)(ch.sb[p][gl] & 0xFFFFu), f16);
-          const float bi = scale_bits_to_f32((uint16_t)(ch.sb[p][gl] >> 16), f16);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) acc[p][tb][j] = acc[p][tb][j] + (sc * d[p][j] + bi * sx[j]);
-        }
-      }
-    }
-  }
-}
-
-template <int AK, int NM, int NF>
-__global__ void __launch_bounds__(P3_THREADS) p4_kernel(MxArgs g, int slices) {
-  constexpr int GPC = ak_gpc(AK), NP = NM * NF;
-  extern __shared__ __align__(16) uint8_t p3_lds[];
-  uint8_t* abuf = p3_lds;
-  uint8_t* sbuf = p3_lds + P3_STAGES * P3_ABYTES;
-  const int sbs = g.sb + 16;
-  float* sxs = reinterpret_cast<float*>(sbuf + P3_MT * sbs);   // the tile's group sums [kch * GPC][MT]
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r32 = lane & 31, kh = lane >> 5;
-  const int b8 = blockIdx.x >> 3;
-  const int slice = b8 % slices;
-  const int tile_id = (b8 / slices) * 8 + (int)(blockIdx.x & 7);
-  if (tile_id >= g.tiles_n[0]) return;
-  const int2 tl = g.tiles[tile_id];
-  const int e = tl.x, row0 = tl.y;
-  const int rows = min(P3_MT, g.offsets[e + 1] - row0);
-  const int ntb = __builtin_amdgcn_readfirstlane((rows + 31) >> 5);
-  const int slot = g.slot_table[e];
-  constexpr int WN = 32 * NF;                            // weight rows per wave and matrix
-  const int nw0 = slice * (P3_WAVES * WN) + WN * wave;
-  float acc[NP][P4_TB][16];
-#pragma unroll
-  for (int p = 0; p < NP; ++p)
-#pragma unroll
-    for (int tb = 0; tb < P4_TB; ++tb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[p][tb][j] = 0.0f;
-  if (slot >= 0) {
-    const int groups = (g.K + ak_group(AK) - 1) / ak_group(AK);
-    const int row_bytes = groups * ak_group(AK) * ak_bits(AK) / 8;
-    const int sq = g.sb / 16;
-    for (int it = threadIdx.x; it < P3_MT * sq; it += P3_THREADS) {
-      const int r = it / sq, q = it - r * sq;
-      const int rr = row0 + min(r, rows - 1);
-      const int src = g.a_gather ? g.a_gather[rr] : rr;
-      *reinterpret_cast<uint4*>(sbuf + r * sbs + q * 16) =
-          *reinterpret_cast<const uint4*>(g.as + (size_t)src * g.sb + q * 16);
-    }
-    {
-      const int ns = g.kch * GPC;
-      for (int it = threadIdx.x; it < P3_MT * ns; it += P3_THREADS) {
-        const int ch = it / P3_MT, r = it - ch * P3_MT;
-        const int rr = row0 + min(r, rows - 1);
-        const int src = g.a_gather ? g.a_gather[rr] : rr;
-        sxs[it] = g.asum[(size_t)src * ns + ch];
-      }
-    }
-    const uint8_t* asrc[P3_ASLOTS];
-#pragma unroll
-    for (int q = 0; q < P3_ASLOTS; ++q) {
-      const int S = 64 * (P3_ASLOTS * wave + q) + lane;
-      const int r = S >> 4;
-      const int col = (S & 15) ^ (r & 15);
-      const int rr = row0 + min(r, rows - 1);
-      const int src = g.a_gather ? g.a_gather[rr] : rr;
-      asrc[q] = g.ap + (size_t)src * g.kch * P3_ROWB + col * 16;
-    }
-    const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
-    const int tq[2] = {NM == 2 ? 0 : 3, 6};   // w1, w3 (gate/up) or w2 (down)
-    int woff[NM], soff[NM], boff[NM], nrow[NF];
-#pragma unroll
-    for (int f = 0; f < NF; ++f) nrow[f] = min(nw0 + 32 * f + r32, g.N - 1);   // rows past N: clamped (discarded)
-#pragma unroll
-    for (int m = 0; m < NM; ++m) {
-      woff[m] = (int)g.L.off[tq[m]];
-      soff[m] = (int)g.L.off[tq[m] + 1];
-      boff[m] = (int)g.L.off[tq[m] + 2];
-    }
-    const int nch = g.kch;
-    P4Chunk<NP> ring[P3_STAGES];
-    p4_issue<AK, NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kh, wave, row_bytes, groups, ring[0]);
-    for (int c0 = 0; c0 < nch; c0 += 2) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int c = c0 + u;
-        // this wave's loads of chunk c have landed (the last scale load is consumed
-        // here), then every wave's; the first barrier also publishes the staged sums
-        asm volatile("" ::"v"(ring[u].sb[NP - 1][GPC - 1]) : "memory");
-        lds_sync();
-        p4_issue<AK, NM, NF>(abuf + (1 - u) * P3_ABYTES, asrc, base, woff, soff, boff, nrow, min(c + 1, nch - 1), kh,
-                             wave, row_bytes, groups, ring[1 - u]);
-        if (c < nch)
-          p4_compute<AK, NP>(abuf + u * P3_ABYTES, sbuf, sbs, sxs, ring[u], c, lane, ntb, groups, g.L.f16, acc);
-      }
-    }
-    tile::wait_vmem();
-  }
-  if constexpr (NM == 2) {
-    float* red = reinterpret_cast<float*>(abuf);   // [P3_WAVES][P3_MT]
-    lds_sync();
-    const int n = nw0 + r32;
-#pragma unroll
-    for (int tb = 0; tb < P4_TB; ++tb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int tr = tb * 32 + 8 * (j / 4) + 4 * kh + (j & 3);   // the same in the 32 lanes of a half
-        if (tr >= rows) continue;
-        const int prow = row0 + tr;
-        const float wr = g.row_w[prow];
-        float gv = round_bf16(acc[0][tb][j]);
-        float uv = round_bf16(acc[1][tb][j]);
-        if (g.limit > 0.0f) {
-          uv = fminf(fmaxf(uv, -g.limit), g.limit);
-          gv = fminf(gv, g.limit);
-        }
-        const float hv = n < g.N ? round_bf16((silu_f32(gv) * uv) * wr) : 0.0f;
-        float m = mx::row16_max(fabsf(hv));
-        m = fmaxf(m, xor_f<16>(m));
-        const int E = plane_exp(m);
-        const float s = hv * __uint_as_float((uint32_t)(127 - E) << 23);
-        const uint32_t hi = mx::f32_to_e4m3(s);
-        const uint32_t lo = mx::f32_to_e4m3((s - mx::e4m3_to_f32(hi)) * 16.0f);
-        uint8_t* p = g.hp + ((size_t)prow * g.hkch + (n >> 7)) * P3_ROWB + (n & 127);
-        p[0] = (uint8_t)hi;
-        p[128] = (uint8_t)lo;
-        float hs = row16_sum(hv);
-        hs = hs + xor_f<16>(hs);
-        if (r32 == 0) {
-          const uint32_t sc = (uint32_t)(E + 127) | ((uint32_t)(E + 123) << 8);
-          *reinterpret_cast<uint16_t*>(g.hs + (size_t)prow * g.hsb + (nw0 / 32) * 2) = (uint16_t)sc;
-          red[wave * P3_MT + tr] = hs;
-        }
-      }
-    lds_sync();
-    if ((int)threadIdx.x < rows) {
-      const int tr = threadIdx.x;
-#pragma unroll
-      for (int h = 0; h < GPC; ++h) {
-        float t = 0.0f;
-#pragma unroll
-        for (int w = h * P3_WAVES / GPC; w < (h + 1) * P3_WAVES / GPC; ++w) t = t + red[w * P3_MT + tr];
-        g.hsum[(size_t)(row0 + tr) * g.hkch * GPC + slice * GPC + h] = t;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const int n = nw0 + 32 * f + r32;
-      if (n >= g.N) continue;
-#pragma unroll
-      for (int tb = 0; tb < P4_TB; ++tb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int tr = tb * 32 + 8 * (j / 4) + 4 * kh + (j & 3);
-          if (tr >= rows) continue;
-          const int rr = row0 + tr;
-          g.y[((size_t)g.row_token[rr] * g.k + g.row_slot[rr]) * g.N + n] = f32_to_bf16(acc[f][tb][j]);
-        }
-    }
-  }
-}
-
 }  // namespace
 
 // Workspace of the block-scaled prefill beyond the tile list: x planes [T][D/128][256]
@@ -1064,17 +682,6 @@ bool prefill_mx_q2_supported(int D, int F) {
 namespace {
 
 template <int AK>
-auto gu_kernel() {
-  if constexpr (ak_bytes(AK) && ak_group(AK) == 64) return p4_kernel<AK, 2, 1>;
-  else return p3_kernel<AK, 2, 2>;
-}
-template <int AK>
-auto dn_kernel() {
-  if constexpr (ak_bytes(AK) && ak_group(AK) == 64) return p4_kernel<AK, 1, 2>;
-  else return p3_kernel<AK, 1, 4>;
-}
-
-template <int AK>
 int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L, const int32_t* slot_table,
               const int32_t* offsets, const int2* tiles, const int32_t* tiles_n, int max_tiles,
               const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D, int F, int k, float limit,
@@ -1102,25 +709,27 @@ int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layou
   const int s_gu = (fch * 128) / (P3_WAVES * 32);   // h's padded columns, 128 per workgroup
   const size_t lds_gu = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbx + 16) +
                         (Q2 ? (size_t)P3_MT * (D / 128) * GPC * 4 : 0);
-  // affine fp8 codes in groups of 64: the 32 x 32 x 64 kernels; the others 16 x 16 x 128
-  auto kgu = gu_kernel<AK>();
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)lds_gu) != hipSuccess)
-    return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_gu);
-  hipLaunchKernelGGL(kgu, dim3(s_gu * tiles8), dim3(P3_THREADS), lds_gu, s, gu, s_gu);
-  rc = check_launch(ak_bytes(AK) && ak_group(AK) == 64 ? "p4_kernel<2,1>" : "p3_kernel<2,2>");
-  if (rc) return rc;
   MxArgs dn{hp, hs, sbh, fch, nullptr, pool, L, slot_table, offsets, tiles, tiles_n, row_token, row_slot, row_w,
             F, D, k, limit, nullptr, nullptr, 0, 0, y, hsum, nullptr};
   const int s_dn = (D + P3_WAVES * 64 - 1) / (P3_WAVES * 64);
   const size_t lds_dn = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbh + 16) +
                         (Q2 ? (size_t)P3_MT * fch * GPC * 4 : 0);
-  auto kdn = dn_kernel<AK>();
+  // affine fp8 codes in groups of 64: the 32 x 32 x 64 kernels (prefill_affine_mx.hip)
+  if constexpr (ak_bytes(AK) && ak_group(AK) == 64)
+    return launch_prefill_affine_g64(AK, gu, s_gu, lds_gu, dn, s_dn, lds_dn, tiles8, s);
+  auto kgu = p3_kernel<AK, 2, 2>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds_gu) != hipSuccess)
+    return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_gu);
+  hipLaunchKernelGGL(kgu, dim3(s_gu * tiles8), dim3(P3_THREADS), lds_gu, s, gu, s_gu);
+  rc = check_launch("p3_kernel<2,2>");
+  if (rc) return rc;
+  auto kdn = p3_kernel<AK, 1, 4>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kdn), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds_dn) != hipSuccess)
     return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_dn);
   hipLaunchKernelGGL(kdn, dim3(s_dn * tiles8), dim3(P3_THREADS), lds_dn, s, dn, s_dn);
-  return check_launch(ak_bytes(AK) && ak_group(AK) == 64 ? "p4_kernel<1,2>" : "p3_kernel<1,4>");
+  return check_launch("p3_kernel<1,4>");
 }
 
 }  // namespace
