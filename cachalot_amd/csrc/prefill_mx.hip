@@ -294,7 +294,7 @@ __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* 
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0>(ahi, b[m][f], mx::zero_acc(), sa, mx::E8M0_TWO);
+      for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0>(ahi, b[m][f], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, sa, mx::E8M0_TWO);
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -393,7 +393,7 @@ __device__ __forceinline__ void p3_compute_aff(const uint8_t* ab, const uint8_t*
 #pragma unroll
       for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0, true>(ahi, b[m][f], mx::zero_acc(), sa, bsc);
+        for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0, true>(ahi, b[m][f], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, sa, bsc);
 #pragma unroll
       for (int m = 0; m < NM; ++m)
 #pragma unroll
