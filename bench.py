@@ -393,7 +393,9 @@ def affine_width_decodes(args, dev, log_fn):
                           "2-bit g128 bf16 bank: the block-scaled prefill kernels of config 3 (x and h as fp8 "
                           "planes, codes as fp4 operands), the group formula folded per 128-code chunk"),
                          ("prefill_4096_oq3e", affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"),
-                          "oQ3e bank: the same bf16-MFMA grouped kernels, 3-bit codes converted per step")):
+                          ("oQ3e bank: block-scaled 32 x 32 x 64 matrix-core kernels (prefill_affine_mx.hip): x and h as fp8 "
+                           "planes, 3-bit codes as fp8 bytes, one instruction per plane and 64-code group, the group "
+                           "formula folded per group"))):
         out[key] = prefill_affine(args, dev, log_fn, f, key, note)
     out["oq3e_3bit_g64_fp16"] = chained_decode(
         args, dev, log_fn, affine_format(4096, 2880, bits=3, group_size=64, scale_dtype="float16"), 8, 17,
