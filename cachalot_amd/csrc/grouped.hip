@@ -57,7 +57,7 @@ int launch_q2mx_batched(const uint16_t* x, int T, const uint8_t* pool, const dec
 size_t prefill_mx_ws_bytes(int T, int k, int D, int F);
 bool prefill_mx_supported(int D, int F, const decode::Layout& L);
 int prefill_mx_mt();
-bool prefill_mx_aff_supported(int bits, int group, int D, int F);
+bool prefill_mx_aff_supported(int bits, int group, int D, int F, const decode::Layout& L);
 int launch_prefill_mx_aff(int bits, int group, const uint16_t* x, int T, const uint8_t* pool,
                           const decode::Layout& L, const int32_t* slot_table, const int32_t* offsets,
                           const int2* tiles, const int32_t* tiles_n, int max_tiles, const int32_t* row_token,
@@ -1096,7 +1096,7 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
     return launch_prefill_mx_q2(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,
                                 row_w, D, F, k, limit, ws + wo.mx, y, s);
   }
-  if (is_aff(KIND) && MT == 64 && prefill_mx_aff_supported(aff_bits(KIND), aff_group(KIND), D, F) &&
+  if (is_aff(KIND) && MT == 64 && prefill_mx_aff_supported(aff_bits(KIND), aff_group(KIND), D, F, L) &&
       !small_tiles_requested() && !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
     // 2-bit g64, 3- and 4-bit g64 / g128 prefill on the block-scaled matrix cores
     hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, prefill_mx_mt(), tiles, tiles_n, zeros);

@@ -43,11 +43,11 @@ __device__ __forceinline__ f32x16_t mfma32_plane(const i32x8_t& a, const i32x8_t
 template <int NP>
 struct P4Chunk {
   uint4 codes[NP][2];   // per (matrix, weight block) pair and half of the chunk: the lane's two runs
-  uint32_t sb[NP][2];   // scale | bias << 16 of the group of each half
 };
 
 // Codes of half h of chunk c for lane half kh: runs at elements 64 h + 16 kh and + 32,
-// 2 BITS bytes each, loaded as whole words as in p3_issue_aff.
+// 2 BITS bytes each, loaded as whole words as in p3_issue_aff.  (The scales and biases
+// come in groups of eight, p4_kernel.)
 template <int AK, int NM, int NF>
 __device__ __forceinline__ void p4_issue(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
                                          const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
@@ -77,16 +77,6 @@ __device__ __forceinline__ void p4_issue(uint8_t* stage, const uint8_t* (&asrc)[
         }
       }
     }
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int h = 0; h < GPC; ++h) {
-        const int si = (nrow[f] * groups + min(c * GPC + h, groups - 1)) * 2;
-        out.sb[m * NF + f][h] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
-                                ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
-      }
 }
 
 // One chunk: per token block and group (half) h, the two plane instructions of every
@@ -94,8 +84,8 @@ __device__ __forceinline__ void p4_issue(uint8_t* stage, const uint8_t* (&asrc)[
 // token blocks run one after the other, so one block's tiles are live at a time.
 template <int AK, int NP>
 __device__ __forceinline__ void p4_compute(const uint8_t* ab, const uint8_t* sbuf, int sbs, const float* sxs,
-                                           const P4Chunk<NP>& ch, int c, int lane, int ntb, int groups, bool f16,
-                                           f32x16_t (&acc)[NP][P4_TB]) {
+                                           const P4Chunk<NP>& ch, const uint32_t (&sw)[NP], const uint32_t (&bw)[NP],
+                                           int c, int lane, int ntb, int groups, bool f16, f32x16_t (&acc)[NP][P4_TB]) {
   static_assert(ak_group(AK) == 64, "one group per instruction");
   const int r32 = lane & 31, kh = lane >> 5;
   const int nh = min(2, groups - 2 * c);   // the chunk's groups inside the row
@@ -105,8 +95,8 @@ __device__ __forceinline__ void p4_compute(const uint8_t* ab, const uint8_t* sbu
   for (int p = 0; p < NP; ++p)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      sc[p][h] = scale_bits_to_f32((uint16_t)(ch.sb[p][h] & 0xFFFFu), f16);
-      bi[p][h] = scale_bits_to_f32((uint16_t)(ch.sb[p][h] >> 16), f16);
+      sc[p][h] = scale_bits_to_f32((uint16_t)(sw[p] >> (16 * h)), f16);
+      bi[p][h] = scale_bits_to_f32((uint16_t)(bw[p] >> (16 * h)), f16);
       b[p][h] = aff_code_bytes<ak_bits(AK)>(ch.codes[p][h], kh);
     }
 #pragma unroll
@@ -218,20 +208,50 @@ __global__ void __launch_bounds__(P3_THREADS) p4_kernel(MxArgs g, int slices) {
       boff[m] = (int)g.L.off[tq[m] + 2];
     }
     const int nch = g.kch;
+    // Scales and biases, eight groups (four chunks) per 16-byte load: lanes kh = 0 the
+    // scale row, kh = 1 the bias row, exchanged across the wave's halves per chunk.  One
+    // line of each row then serves 16 chunks from 4 loads (a load per chunk and row kept
+    // the rows' lines resident for the whole K loop, more than L2 holds).  A last group
+    // of eight past the row reads what follows it in the record (the host checks that
+    // something does); those groups are never used.
+    const int nq = (groups + 7) / 8;
+    uint4 sg[2][NP];
+    auto load_sg = [&](int q, uint4(&dst)[NP]) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          dst[m * NF + f] =
+              *reinterpret_cast<const uint4*>(base + (kh ? boff[m] : soff[m]) + (nrow[f] * groups + 8 * q) * 2);
+    };
+    load_sg(0, sg[0]);
     P4Chunk<NP> ring[P3_STAGES];
     p4_issue<AK, NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kh, wave, row_bytes, groups, ring[0]);
-    for (int c0 = 0; c0 < nch; c0 += 2) {
+    for (int c0 = 0; c0 < nch; c0 += 8) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < 8; ++u) {
         const int c = c0 + u;
-        // this wave's loads of chunk c have landed (the last scale load is consumed
-        // here), then every wave's; the first barrier also publishes the staged sums
-        asm volatile("" ::"v"(ring[u].sb[NP - 1][GPC - 1]) : "memory");
+        // this wave's loads of chunk c have landed (the last code load is consumed here;
+        // the scale group, issued before it, first), then every wave's; the first barrier
+        // also publishes the staged sums
+        asm volatile("" ::"v"(ring[u % 2].codes[NP - 1][1].w) : "memory");
         lds_sync();
-        p4_issue<AK, NM, NF>(abuf + (1 - u) * P3_ABYTES, asrc, base, woff, soff, boff, nrow, min(c + 1, nch - 1), kh,
-                             wave, row_bytes, groups, ring[1 - u]);
-        if (c < nch)
-          p4_compute<AK, NP>(abuf + u * P3_ABYTES, sbuf, sbs, sxs, ring[u], c, lane, ntb, groups, g.L.f16, acc);
+        if ((u + 1) % 4 == 0) load_sg(min((c + 1) / 4, nq - 1), sg[((u + 1) / 4) % 2]);
+        p4_issue<AK, NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
+                             min(c + 1, nch - 1), kh, wave, row_bytes, groups, ring[(u + 1) % 2]);
+        if (c < nch) {
+          uint32_t sw[NP], bw[NP];
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const uint4& v = sg[(u / 4) % 2][p];
+            const uint32_t mine = (u % 4) == 0 ? v.x : (u % 4) == 1 ? v.y : (u % 4) == 2 ? v.z : v.w;
+            const uint32_t other = (uint32_t)__shfl_xor((int)mine, 32, 64);
+            sw[p] = kh ? other : mine;
+            bw[p] = kh ? mine : other;
+          }
+          p4_compute<AK, NP>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], sw, bw, c, lane, ntb, groups,
+                             g.L.f16, acc);
+        }
       }
     }
     tile::wait_vmem();

@@ -755,10 +755,19 @@ int launch_prefill_mx_q2(const uint16_t* x, int T, const uint8_t* pool, const de
 
 // The other affine widths the kernels take: 2-bit codes in groups of 64, 3- and 4-bit
 // codes in groups of 64 or 128 (groups of 32 would need four instructions per plane
-// and chunk), in the shapes of the FP4 envelope with F a multiple of 64.
-bool prefill_mx_aff_supported(int bits, int group, int D, int F) {
+// and chunk), in the shapes of the FP4 envelope with F a multiple of 64.  Groups of 64
+// read scales and biases eight groups at a time: where a row's group count is not a
+// multiple of eight, the last load of the tensor's last row reads up to 16 bytes past
+// the tensor, which must still lie inside the slot record.
+bool prefill_mx_aff_supported(int bits, int group, int D, int F, const decode::Layout& L) {
   const bool kind = (bits == 2 && group == 64) || ((bits == 3 || bits == 4) && (group == 64 || group == 128));
-  return kind && D % 128 == 0 && D >= 512 && D <= 8192 && F % 64 == 0 && F >= 512 && F <= 8192;
+  if (!(kind && D % 128 == 0 && D >= 512 && D <= 8192 && F % 64 == 0 && F >= 512 && F <= 8192)) return false;
+  if (group != 64) return true;
+  auto room = [&](int t, int64_t rows, int groups) {
+    return groups % 8 == 0 || L.off[t] + rows * groups * 2 + 16 <= L.record_bytes;
+  };
+  const int gd = D / 64, gf = (F + 63) / 64;
+  return room(1, F, gd) && room(2, F, gd) && room(7, F, gd) && room(8, F, gd) && room(4, D, gf) && room(5, D, gf);
 }
 
 int launch_prefill_mx_aff(int bits, int group, const uint16_t* x, int T, const uint8_t* pool,
