@@ -67,7 +67,7 @@ int launch_prefill_mx(const uint16_t* x, int T, const uint8_t* pool, const decod
                       const int32_t* slot_table, const int32_t* offsets, const int2* tiles, const int32_t* tiles_n,
                       int max_tiles, const int32_t* row_token, const int32_t* row_slot, const float* row_w, int D,
                       int F, int k, float limit, uint8_t* ws, uint16_t* y, hipStream_t s);
-bool prefill_mx_q2_supported(int D, int F);
+bool prefill_mx_q2_supported(int D, int F, const decode::Layout& L);
 int launch_prefill_mx_q2(const uint16_t* x, int T, const uint8_t* pool, const decode::Layout& L,
                          const int32_t* slot_table, const int32_t* offsets, const int2* tiles,
                          const int32_t* tiles_n, int max_tiles, const int32_t* row_token, const int32_t* row_slot,
@@ -1087,7 +1087,7 @@ int launch_grouped(const uint16_t* x, const uint8_t* pool, const cachalot_expert
     return launch_prefill_mx(x, T, pool, L, slot_table, offsets, tiles, tiles_n, max_tiles, row_token, row_slot,
                              row_w, D, F, k, limit, ws + wo.mx, y, s);
   }
-  if (KIND == KIND_Q2 && MT == 64 && prefill_mx_q2_supported(D, F) && !small_tiles_requested() &&
+  if (KIND == KIND_Q2 && MT == 64 && prefill_mx_q2_supported(D, F, L) && !small_tiles_requested() &&
       !prefill_bf16_requested() && max_tiles <= (1 << 20)) {
     // 2-bit g128 prefill on the block-scaled matrix cores (prefill_mx.hip)
     hipLaunchKernelGGL(tile_list_kernel, dim3(1), dim3(1024), 0, s, offsets, E, prefill_mx_mt(), tiles, tiles_n, zeros);

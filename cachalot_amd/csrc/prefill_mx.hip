@@ -167,7 +167,6 @@ __global__ void __launch_bounds__(256) x_planes_rows_kernel(const uint16_t* __re
 template <int NM, int NF>
 struct P3Chunk {
   uint4 codes[NM][NF];
-  uint32_t sb[NM][NF][2];   // affine: the weight row's scale | bias << 16 bits per group of the chunk
 };
 
 template <int NM, int NF>
@@ -184,14 +183,13 @@ __device__ __forceinline__ void p3_issue(uint8_t* stage, const uint8_t* (&asrc)[
       out.codes[m][f] = *reinterpret_cast<const uint4*>(wrow[m][f] + min(c * 64 + kg * 16, row_bytes - 16));
 }
 
-// 2-bit: block kg of the chunk's group (32 codes, 8 bytes) and the group's scale and
-// bias, per (matrix, fragment); rows as 32-bit offsets from the slot record (a
-// uniform base), so no 64-bit address per row stays live.
+// 2-bit: block kg of the chunk's group (32 codes, 8 bytes) per (matrix, fragment);
+// rows as 32-bit offsets from the slot record (a uniform base), so no 64-bit address
+// per row stays live.  (The groups' scales and biases come eight at a time, p3_kernel.)
 template <int NM, int NF>
 __device__ __forceinline__ void p3_issue_q2(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
-                                            const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
-                                            const int (&nrow)[NF], int c, int kg, int wave, int row_bytes, int kch,
-                                            P3Chunk<NM, NF>& out) {
+                                            const int (&woff)[NM], const int (&nrow)[NF], int c, int kg, int wave,
+                                            int row_bytes, P3Chunk<NM, NF>& out) {
 #pragma unroll
   for (int q = 0; q < P3_ASLOTS; ++q)
     tile::lds_load16_untracked(asrc[q] + (size_t)c * P3_ROWB, stage + (P3_ASLOTS * wave + q) * 1024);
@@ -201,9 +199,6 @@ __device__ __forceinline__ void p3_issue_q2(uint8_t* stage, const uint8_t* (&asr
     for (int f = 0; f < NF; ++f) {
       const uint2 v = *reinterpret_cast<const uint2*>(base + woff[m] + nrow[f] * row_bytes + c * 32 + kg * 8);
       out.codes[m][f] = make_uint4(v.x, v.y, 0u, 0u);
-      const int si = (nrow[f] * kch + c) * 2;
-      out.sb[m][f][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
-                     ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
     }
 }
 
@@ -263,8 +258,8 @@ __device__ __forceinline__ void p3_compute(const uint8_t* ab, const uint8_t* sbu
 // into zeroed tiles, then the group formula folded into the fp32 accumulators.
 template <int NM, int NF>
 __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* sbuf, int sbs, const float* sxs,
-                                              const P3Chunk<NM, NF>& ch, int c, int i, int kg, int ntb, bool f16,
-                                              float (&acc)[NM][NF][P3_TB][4]) {
+                                              const P3Chunk<NM, NF>& ch, const uint32_t (&sbw)[NM][NF], int c, int i,
+                                              int kg, int ntb, bool f16, float (&acc)[NM][NF][P3_TB][4]) {
   i32x8_t b[NM][NF];
   float sc[NM][NF], bi[NM][NF];
 #pragma unroll
@@ -274,8 +269,8 @@ __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* 
       const uint4 w = ch.codes[m][f];
       b[m][f] = i32x8_t{(int)q2_nibbles(w.x & 0xFFFFu), (int)q2_nibbles(w.x >> 16), (int)q2_nibbles(w.y & 0xFFFFu),
                         (int)q2_nibbles(w.y >> 16), 0, 0, 0, 0};
-      sc[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f][0] & 0xFFFFu), f16);
-      bi[m][f] = scale_bits_to_f32((uint16_t)(ch.sb[m][f][0] >> 16), f16);
+      sc[m][f] = scale_bits_to_f32((uint16_t)(sbw[m][f] & 0xFFFFu), f16);
+      bi[m][f] = scale_bits_to_f32((uint16_t)(sbw[m][f] >> 16), f16);
     }
 #pragma unroll
   for (int tb = 0; tb < P3_TB; ++tb) {
@@ -315,16 +310,15 @@ __device__ __forceinline__ void p3_compute_q2(const uint8_t* ab, const uint8_t* 
 // the A planes' order; the matching codes are the two runs of 16 codes at those
 // elements, 2 BITS bytes each: run 0 at byte 2 BITS kg of the row's chunk, run 1 at
 // 8 BITS + 2 BITS kg.  Each run is loaded as whole words (3-bit: the 8 bytes from the
-// 4-byte boundary below it) into codes[m][f] (run 0: x / y, run 1: z / w); with the
-// group's scale and bias (sb) per group of the chunk.  Loads past the row (the half
-// of a last chunk that holds no group, for K not a whole number of chunks) read the
-// row's last words instead; their group is skipped.
+// 4-byte boundary below it) into codes[m][f] (run 0: x / y, run 1: z / w).  Groups
+// of 128 only here (one per chunk; the rows hold whole groups); groups of 64 run on
+// prefill_affine_mx.hip's kernels.
 template <int AK, int NM, int NF>
 __device__ __forceinline__ void p3_issue_aff(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
-                                             const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
-                                             const int (&nrow)[NF], int c, int kg, int wave, int row_bytes,
-                                             int groups, P3Chunk<NM, NF>& out) {
-  constexpr int BITS = ak_bits(AK), GPC = ak_gpc(AK), CB = 16 * BITS;
+                                             const int (&woff)[NM], const int (&nrow)[NF], int c, int kg, int wave,
+                                             int row_bytes, P3Chunk<NM, NF>& out) {
+  static_assert(ak_group(AK) == 128, "one group per chunk");
+  constexpr int BITS = ak_bits(AK), CB = 16 * BITS;
   constexpr int LB = BITS == 2 ? 4 : 8;   // bytes per run load
 #pragma unroll
   for (int q = 0; q < P3_ASLOTS; ++q)
@@ -345,34 +339,19 @@ __device__ __forceinline__ void p3_issue_aff(uint8_t* stage, const uint8_t* (&as
         out.codes[m][f] = make_uint4(a.x, a.y, b.x, b.y);
       }
     }
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int h = 0; h < GPC; ++h) {
-        const int si = (nrow[f] * groups + min(c * GPC + h, groups - 1)) * 2;
-        out.sb[m][f][h] = (uint32_t)*reinterpret_cast<const uint16_t*>(base + soff[m] + si) |
-                          ((uint32_t)*reinterpret_cast<const uint16_t*>(base + boff[m] + si) << 16);
-      }
 }
 
-// Affine chunk with fp8 codes: per token block, per group h of the chunk, the two
-// plane instructions into a zeroed tile, then the group formula folded in.  With two
-// groups per chunk (G = 64) both instructions take the whole operand and the B scale
-// keeps one group: 2^9 on the group's two blocks (lane groups 2h, 2h + 1), 2^-127 (E8M0
-// 0) on the other's, whose terms then lie below 2^-120 of the result's scale.
+// Affine chunk with fp8 codes (groups of 128): per token block, the two plane
+// instructions into a zeroed tile, then the group formula folded in.
 template <int AK, int NM, int NF>
 __device__ __forceinline__ void p3_compute_aff(const uint8_t* ab, const uint8_t* sbuf, int sbs, const float* sxs,
-                                               const P3Chunk<NM, NF>& ch, int c, int i, int kg, int ntb, int groups,
-                                               bool f16, float (&acc)[NM][NF][P3_TB][4]) {
-  constexpr int GPC = ak_gpc(AK);
+                                               const P3Chunk<NM, NF>& ch, const uint32_t (&sbw)[NM][NF], int c, int i,
+                                               int kg, int ntb, bool f16, float (&acc)[NM][NF][P3_TB][4]) {
   i32x8_t b[NM][NF];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
     for (int f = 0; f < NF; ++f) b[m][f] = aff_code_bytes<ak_bits(AK)>(ch.codes[m][f], kg);
-  const int nh = min(GPC, groups - c * GPC);   // the chunk's groups inside the row
 #pragma unroll
   for (int tb = 0; tb < P3_TB; ++tb) {
     if (tb >= ntb) break;
@@ -385,31 +364,27 @@ __device__ __forceinline__ void p3_compute_aff(const uint8_t* ab, const uint8_t*
     const uint32_t sa = *reinterpret_cast<const uint16_t*>(sbuf + row * sbs + (4 * c + kg) * 2);
     const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
     const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+    f32x4_t d[NM][NF];
 #pragma unroll
-    for (int h = 0; h < GPC; ++h) {
-      if (h >= nh) break;
-      const uint32_t bsc = GPC == 1 || (kg >> 1) == h ? E8M0_2P9 : 0u;
-      f32x4_t d[NM][NF];
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int m = 0; m < NM; ++m)
+      for (int f = 0; f < NF; ++f)
+        d[m][f] = mfma_plane<0, true>(ahi, b[m][f], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, sa, E8M0_2P9);
 #pragma unroll
-        for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<0, true>(ahi, b[m][f], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, sa, bsc);
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int m = 0; m < NM; ++m)
+      for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<1, true>(alo, b[m][f], d[m][f], sa, E8M0_2P9);
+    const float4 sx = *reinterpret_cast<const float4*>(sxs + c * P3_MT + tb * 16 + 4 * kg);
+    const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) d[m][f] = mfma_plane<1, true>(alo, b[m][f], d[m][f], sa, bsc);
-      const float4 sx = *reinterpret_cast<const float4*>(sxs + (c * GPC + h) * P3_MT + tb * 16 + 4 * kg);
-      const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int m = 0; m < NM; ++m)
+      for (int f = 0; f < NF; ++f) {
+        const float sc = scale_bits_to_f32((uint16_t)(sbw[m][f] & 0xFFFFu), f16);
+        const float bi = scale_bits_to_f32((uint16_t)(sbw[m][f] >> 16), f16);
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
-          const float sc = scale_bits_to_f32((uint16_t)(ch.sb[m][f][h] & 0xFFFFu), f16);
-          const float bi = scale_bits_to_f32((uint16_t)(ch.sb[m][f][h] >> 16), f16);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = fmaf(sc, d[m][f][r], fmaf(bi, sxv[r], acc[m][f][tb][r]));
-        }
-    }
+        for (int r = 0; r < 4; ++r) acc[m][f][tb][r] = fmaf(sc, d[m][f][r], fmaf(bi, sxv[r], acc[m][f][tb][r]));
+      }
   }
 }
 
@@ -486,14 +461,12 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
     const uint8_t* base = g.pool + (int64_t)slot * g.L.record_bytes;
     const int tq[2] = {NM == 2 ? 0 : 3, 6};   // w1, w3 (gate/up) or w2 (down)
     const uint8_t* wrow[NM][NF];
-    int woff[NM], soff[NM], boff[NM], nrow[NF];   // 2-bit: offsets in the record (< 2^31: one expert)
+    int woff[NM], nrow[NF];   // affine: offsets in the record (< 2^31: one expert)
 #pragma unroll
     for (int f = 0; f < NF; ++f) nrow[f] = min(nw0 + 16 * f + i, g.N - 1);   // rows past N: clamped (discarded)
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       woff[m] = (int)g.L.off[tq[m]];
-      soff[m] = (int)g.L.off[tq[m] + 1];
-      boff[m] = (int)g.L.off[tq[m] + 2];
 #pragma unroll
       for (int f = 0; f < NF; ++f) wrow[m][f] = base + g.L.off[tq[m]] + (int64_t)nrow[f] * row_bytes;
     }
@@ -506,15 +479,30 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
     const uint8_t* sgp = base + g.L.off[tq[pm] + 1] + (int64_t)min(nw0 + 16 * pf + i, g.N - 1) * blocks;
     const int ngrp = (blocks + 15) / 16;
     const int nch = g.kch;
+    // Affine scales and biases: lane (i, p) holds eight groups (chunks 8q .. 8q + 7) of
+    // its pair's row, the scale row in sgs and the bias row in sgb (one 16-byte load
+    // each, issued with chunk 8q's loads); each chunk's scale | bias << 16 goes to the
+    // lanes by one shuffle per pair.  Loads per chunk and row kept the scale and bias
+    // lines in L2 through the whole K loop.  A last group of eight past the row reads
+    // what follows the tensor in the record (the host checks that something does).
+    const int arow = min(nw0 + 16 * pf + i, g.N - 1);
+    const uint8_t* sgs_p = base + g.L.off[tq[pm] + 1] + (int64_t)arow * groups * 2;
+    const uint8_t* sgb_p = base + g.L.off[tq[pm] + 2] + (int64_t)arow * groups * 2;
+    const int nq = (groups + 7) / 8;
+    uint4 sgs, sgb;
+    if constexpr (Q2) {
+      sgs = *reinterpret_cast<const uint4*>(sgs_p);
+      sgb = *reinterpret_cast<const uint4*>(sgb_p);
+    }
     P3Chunk<NM, NF> ring[P3_STAGES];
     uint4 sgrp[2];
     // every issue is unconditional (a chunk past the end re-reads the last one into a
     // stage nothing reads again), so each wait is for exactly the loads it needs
     if constexpr (!Q2) sgrp[0] = *reinterpret_cast<const uint4*>(sgp);
     if constexpr (ak_bytes(AK))
-      p3_issue_aff<AK, NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kg, wave, row_bytes, groups, ring[0]);
+      p3_issue_aff<AK, NM, NF>(abuf, asrc, base, woff, nrow, 0, kg, wave, row_bytes, ring[0]);
     else if constexpr (Q2)
-      p3_issue_q2<NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kg, wave, row_bytes, nch, ring[0]);
+      p3_issue_q2<NM, NF>(abuf, asrc, base, woff, nrow, 0, kg, wave, row_bytes, ring[0]);
     else p3_issue<NM, NF>(abuf, asrc, wrow, 0, kg, wave, row_bytes, ring[0]);
     // eight chunks per trip: A stage and code ring index u % 2, scale group buffer (u / 4) % 2
     for (int c0 = 0; c0 < nch; c0 += 8) {
@@ -523,30 +511,46 @@ __global__ void __launch_bounds__(P3_THREADS) p3_kernel(MxArgs g, int slices) {
         const int c = c0 + u;
         // this wave's loads of chunk c have landed (its last code load is consumed
         // here; its earlier direct-to-LDS loads complete first), then every wave's
-        // (2-bit: the pair's bias is the last load of a chunk; the first barrier also
-        // publishes the chunk sums stored above)
-        if constexpr (Q2) asm volatile("" ::"v"(ring[u % 2].sb[NM - 1][NF - 1][GPC - 1]) : "memory");
+        // (affine: the first barrier also publishes the group sums stored above)
+        if constexpr (Q2 && ak_bits(AK) == 2) asm volatile("" ::"v"(ring[u % 2].codes[NM - 1][NF - 1].y) : "memory");
         else asm volatile("" ::"v"(ring[u % 2].codes[NM - 1][NF - 1].w) : "memory");
         lds_sync();
+        uint32_t sbw[NM][NF];
+        if constexpr (Q2) {
+          const int J = u >> 1, sh = 16 * (u & 1);
+          const uint32_t ws = J == 0 ? sgs.x : J == 1 ? sgs.y : J == 2 ? sgs.z : sgs.w;
+          const uint32_t wb = J == 0 ? sgb.x : J == 1 ? sgb.y : J == 2 ? sgb.z : sgb.w;
+          const uint32_t mine = ((ws >> sh) & 0xFFFFu) | (((wb >> sh) & 0xFFFFu) << 16);
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+              sbw[m][f] = (uint32_t)__shfl((int)mine, 16 * (m * NF + f) + i, 64);
+          if (u == 7) {   // the next eight groups, into the registers just read
+            const int q = min(c / 8 + 1, nq - 1);
+            sgs = *reinterpret_cast<const uint4*>(sgs_p + 16 * q);
+            sgb = *reinterpret_cast<const uint4*>(sgb_p + 16 * q);
+          }
+        }
         if constexpr (!Q2)
           if ((u + 1) % 4 == 0)   // the scale group of chunk c + 1
             sgrp[((u + 1) / 4) % 2] = *reinterpret_cast<const uint4*>(sgp + 16 * min((c + 1) / 4, ngrp - 1));
         if constexpr (ak_bytes(AK))
-          p3_issue_aff<AK, NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
-                                   min(c + 1, nch - 1), kg, wave, row_bytes, groups, ring[(u + 1) % 2]);
+          p3_issue_aff<AK, NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, nrow, min(c + 1, nch - 1), kg,
+                                   wave, row_bytes, ring[(u + 1) % 2]);
         else if constexpr (Q2)
-          p3_issue_q2<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
-                              min(c + 1, nch - 1), kg, wave, row_bytes, nch, ring[(u + 1) % 2]);
+          p3_issue_q2<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, nrow, min(c + 1, nch - 1), kg, wave,
+                              row_bytes, ring[(u + 1) % 2]);
         else
           p3_issue<NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, wrow, min(c + 1, nch - 1), kg, wave, row_bytes,
                            ring[(u + 1) % 2]);
         if (c < nch) {
           if constexpr (ak_bytes(AK)) {
-            p3_compute_aff<AK, NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], c, i, kg, ntb, groups,
+            p3_compute_aff<AK, NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], sbw, c, i, kg, ntb,
                                        g.L.f16, acc);
           } else if constexpr (Q2) {
-            p3_compute_q2<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], c, i, kg, ntb, g.L.f16,
-                                  acc);
+            p3_compute_q2<NM, NF>(abuf + (u % 2) * P3_ABYTES, sbuf, sbs, sxs, ring[u % 2], sbw, c, i, kg, ntb,
+                                  g.L.f16, acc);
           } else {
             uint32_t bs[NM][NF];
             p3_scales<NM, NF>(sgrp[(u / 4) % 2], u % 4, c, i, kg, blocks, bs);
@@ -673,10 +677,22 @@ bool prefill_mx_supported(int D, int F, const decode::Layout& L) {
   return room(1, F, D / 32) && room(7, F, D / 32) && room(4, D, F / 32);
 }
 
+// Affine scales and biases are read eight groups at a time: where a row's group count
+// is not a multiple of eight, the last load of the tensor's last row reads up to 16
+// bytes past the tensor, which must still lie inside the slot record.
+static bool affine_scale_room(int group, int D, int F, const decode::Layout& L) {
+  auto room = [&](int t, int64_t rows, int groups) {
+    return groups % 8 == 0 || L.off[t] + rows * groups * 2 + 16 <= L.record_bytes;
+  };
+  const int gd = (D + group - 1) / group, gf = (F + group - 1) / group;
+  return room(1, F, gd) && room(2, F, gd) && room(7, F, gd) && room(8, F, gd) && room(4, D, gf) && room(5, D, gf);
+}
+
 // 2-bit g128 banks: any shape of the FP4 envelope (the rows' groups are padded to whole
-// chunks in the bank; scales and biases are read one per chunk).
-bool prefill_mx_q2_supported(int D, int F) {
-  return D % 128 == 0 && D >= 512 && D <= 8192 && F % 32 == 0 && F >= 512 && F <= 8192;
+// chunks in the bank).
+bool prefill_mx_q2_supported(int D, int F, const decode::Layout& L) {
+  return D % 128 == 0 && D >= 512 && D <= 8192 && F % 32 == 0 && F >= 512 && F <= 8192 &&
+         affine_scale_room(128, D, F, L);
 }
 
 namespace {
@@ -715,8 +731,9 @@ int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layou
   const size_t lds_dn = (size_t)P3_STAGES * P3_ABYTES + (size_t)P3_MT * (sbh + 16) +
                         (Q2 ? (size_t)P3_MT * fch * GPC * 4 : 0);
   // affine fp8 codes in groups of 64: the 32 x 32 x 64 kernels (prefill_affine_mx.hip)
-  if constexpr (ak_bytes(AK) && ak_group(AK) == 64)
+  if constexpr (ak_bytes(AK) && ak_group(AK) == 64) {
     return launch_prefill_affine_g64(AK, gu, s_gu, lds_gu, dn, s_dn, lds_dn, tiles8, s);
+  } else {
   auto kgu = p3_kernel<AK, 2, 2>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kgu), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds_gu) != hipSuccess)
@@ -730,6 +747,7 @@ int launch_p3(const uint16_t* x, int T, const uint8_t* pool, const decode::Layou
     return fail(CACHALOT_EHIP, "prefill (block-scaled): cannot grant %zu bytes of LDS", lds_dn);
   hipLaunchKernelGGL(kdn, dim3(s_dn * tiles8), dim3(P3_THREADS), lds_dn, s, dn, s_dn);
   return check_launch("p3_kernel<1,4>");
+  }
 }
 
 }  // namespace
@@ -755,19 +773,11 @@ int launch_prefill_mx_q2(const uint16_t* x, int T, const uint8_t* pool, const de
 
 // The other affine widths the kernels take: 2-bit codes in groups of 64, 3- and 4-bit
 // codes in groups of 64 or 128 (groups of 32 would need four instructions per plane
-// and chunk), in the shapes of the FP4 envelope with F a multiple of 64.  Groups of 64
-// read scales and biases eight groups at a time: where a row's group count is not a
-// multiple of eight, the last load of the tensor's last row reads up to 16 bytes past
-// the tensor, which must still lie inside the slot record.
+// and chunk), in the shapes of the FP4 envelope with F a multiple of 64.
 bool prefill_mx_aff_supported(int bits, int group, int D, int F, const decode::Layout& L) {
   const bool kind = (bits == 2 && group == 64) || ((bits == 3 || bits == 4) && (group == 64 || group == 128));
-  if (!(kind && D % 128 == 0 && D >= 512 && D <= 8192 && F % 64 == 0 && F >= 512 && F <= 8192)) return false;
-  if (group != 64) return true;
-  auto room = [&](int t, int64_t rows, int groups) {
-    return groups % 8 == 0 || L.off[t] + rows * groups * 2 + 16 <= L.record_bytes;
-  };
-  const int gd = D / 64, gf = (F + 63) / 64;
-  return room(1, F, gd) && room(2, F, gd) && room(7, F, gd) && room(8, F, gd) && room(4, D, gf) && room(5, D, gf);
+  return kind && D % 128 == 0 && D >= 512 && D <= 8192 && F % 64 == 0 && F >= 512 && F <= 8192 &&
+         affine_scale_room(group, D, F, L);
 }
 
 int launch_prefill_mx_aff(int bits, int group, const uint16_t* x, int T, const uint8_t* pool,
