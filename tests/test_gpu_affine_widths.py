@@ -8,8 +8,9 @@ tool writes bits 2/3/4 x groups 32/64/128 (build_affine_bank.py:266-267).
   (helpers.term_flips), routed = the route-order sum bit for bit,
   out = bf16(routed + addend) bit for bit; the device-routed layer with ids
   bit-exact;
-* grouped (prefill / batched) rows against the oracle on the bf16-MFMA grouped kernels and
-  the VALU kernels, dropped ids giving zeros.
+* grouped (prefill / batched) rows against the oracle on the block-scaled prefill kernels,
+  the bf16-MFMA grouped kernels and the VALU kernels, dropped ids giving zeros; a small
+  layer shape whose K and group counts are ragged on the block-scaled kernels.
 """
 from __future__ import annotations
 
@@ -209,3 +210,38 @@ def test_affine_decode_other_shapes(cuda, bits, group, sd, d, f, k):
     terms = _decode_terms(cuda, store, 0, x, idx, w)
     _check_decode(f"affine {bits}-bit g{group} D={d} F={f} k={k}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
                   _np(routed), _f32(out), terms, bf16_bits_to_f32(ab))
+
+
+SMALL_PREFILL = [(2, 128, "float16"), (2, 64, "bfloat16"), (3, 64, "float16"), (4, 128, "bfloat16")]
+
+
+@pytest.mark.parametrize("bits,group,sd", SMALL_PREFILL)
+def test_affine_prefill_small_shape(cuda, bits, group, sd, monkeypatch):
+    """D = 640, F = 576 on the block-scaled prefill kernels (the 2-bit g128 fp4 path, the 16 x 16 x 128
+    fp8-code kernels for groups of 128, the 32 x 32 x 64 kernels for groups of 64): x is five 128-element
+    chunks, h four and a half (the last chunk half past F), the rows' group counts (10 / 9 for groups of
+    64, 5 for groups of 128) are not multiples of the eight groups a scale load covers, and the weight
+    slices run past F and D.  48 tokens x top-6 over 8 experts (64-row tiles, some experts over 64
+    rows), three dropped ids; terms against the oracle, the combine bit for bit."""
+    from cachalot_amd.moe_prefill import grouped_experts
+
+    monkeypatch.setenv("CACHALOT_AFFINE_VALU", "0")
+    monkeypatch.setenv("CACHALOT_PREFILL_BF16", "0")
+    D, F, E, k, t = 640, 576, 8, 6, 48
+    fmt = _fmt(bits, group, sd, d=D, f=F)
+    store = make_store(fmt, n_layers=1, n_experts=E)
+    rng = np.random.default_rng(11 + bits + group)
+    idx = np.stack([rng.choice(E, size=k, replace=False) for _ in range(t)]).astype(np.int32)
+    drops = [(0, 2), (t // 2, k - 1), (t - 1, 0)]
+    for (r, c), v in zip(drops, (-1, E + 1, 1 << 28)):
+        idx[r, c] = v
+    w = rng.dirichlet(np.ones(k), size=t).astype(np.float32)
+    xb = osynth.activations(SEED, 3400, t, D)
+    ab = osynth.activations(SEED, 3401, t, D)
+    routed, out, y = grouped_experts(_bf16(xb, cuda), torch.from_numpy(idx).to(cuda), torch.from_numpy(w).to(cuda),
+                                     store.pool, store.layer_table(0), addend=_bf16(ab, cuda), want_routed=True,
+                                     want_terms=True)
+    yf = _f32(y)
+    assert not any(yf[r, c].any() for r, c in drops)
+    _grouped_check(f"prefill {bits}-bit g{group} {sd} D={D} F={F}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
+                   _np(routed), _f32(out), yf, E, addend=bf16_bits_to_f32(ab))
