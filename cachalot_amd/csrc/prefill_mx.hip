@@ -33,21 +33,25 @@
 // down: NM = 1, NF = 4 -> 256 rows of W2).  K runs in chunks of 128: the A planes
 // of the chunk through a two-stage LDS ring filled by direct-to-LDS loads
 // (16-byte slots XOR-swizzled by row, so the operand reads hit distinct banks),
-// the wave's codes and B scales one chunk ahead in registers.  The tile's A
-// scales sit in LDS for the whole K loop.  Three workgroups fit a CU (49 KiB of
-// LDS, 96 VGPRs + 64 AGPRs each): measured 3.51 ms per config-3 layer against
-// 3.64 with a three-stage ring (two chunks ahead), which left room for two.  Workgroups
-// go to the XCDs round-robin by launch index; the mapping gives every slice of
-// one tile to one XCD, so the tile's A rows are fetched into that XCD's L2 once.
+// the wave's codes one chunk ahead in registers, the B scales 32 bytes (eight
+// chunks) per lane and load, one trip of eight chunks ahead.  The tile's A scales sit
+// in LDS for the whole K loop.  Three workgroups fit a CU (49 KiB of LDS, ~100 VGPRs +
+// 64 AGPRs each): measured 3.51 ms per config-3 layer against 3.64 with a three-stage
+// ring (two chunks ahead), which left room for two.  Workgroups go to the XCDs
+// round-robin by launch index; the mapping gives every slice of one tile to one XCD,
+// so the tile's A rows are fetched into that XCD's L2 once.
 //
-// 2-bit affine g128 banks (Q2 = true) run the same kernels: a 128-code group is one
-// K chunk, its codes q go in as the fp4 operand (E2M1 of q / 2 with B scale 2, spread
-// into natural nibble order), and the group formula s * sum(x q) + b * sum(x) is
-// applied per chunk: each chunk's two plane instructions accumulate into a zeroed
-// tile, which is folded into the fp32 accumulators with the weight row's scale and
-// bias and the token row's chunk sum of x (or h).  The chunk sums come from the plane
-// writers (x_planes_rows_kernel; the gate/up epilogue for h, whose workgroup holds one
-// whole 128-column chunk of h).
+// Affine banks (AK != AK_FP4) run the same kernels with the group formula
+// s * sum(x q) + b * sum(x) applied per 128-code group, one group per K chunk: each
+// chunk's two plane instructions accumulate into a zeroed tile, folded into fp32
+// accumulators in VGPRs as acc = fma(s, tile, fma(b, sum x, acc)) with the weight
+// row's scale and bias and the token row's group sum of x (or h).  2-bit g128 codes go
+// in as the fp4 operand (E2M1 of q / 2 with B scale 2, spread into natural nibble
+// order); 3- and 4-bit g128 codes as fp8 bytes (prefill_mx.h).  The scales and biases
+// come eight groups per 16-byte load, each chunk's pair shuffled to the lanes.  The
+// group sums come from the plane writers (x_planes_rows_kernel; the gate/up epilogue
+// for h, whose workgroup holds one whole 128-column chunk of h).  Groups of 64 run on
+// prefill_affine_mx.hip's 32 x 32 x 64 kernels over the same planes.
 #include <type_traits>
 
 #include "decode_common.h"
