@@ -31,7 +31,9 @@
 // The grouped kernels also take the other affine widths (aff_kind<BITS, G>: 3- and
 // 4-bit codes, groups of 32 / 64 / 128, 2-bit codes in groups of 32 / 64), with the
 // codes read per step and the group formula applied per group (see chunk_mma_aff).
-// FP4 and 2-bit g128 prefill go to the block-scaled kernels of prefill_mx.hip.
+// FP4, 2-bit g128 and (2-bit g64, 3- / 4-bit g64 / g128) affine prefill go to the
+// block-scaled kernels of prefill_mx.hip and prefill_affine_mx.hip; these kernels take
+// groups of 32, the other shapes and CACHALOT_PREFILL_BF16=1.
 #include "decode_common.h"
 #include "mfma_tile.h"
 #include "permute_small.h"
