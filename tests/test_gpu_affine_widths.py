@@ -245,3 +245,45 @@ def test_affine_prefill_small_shape(cuda, bits, group, sd, monkeypatch):
     assert not any(yf[r, c].any() for r, c in drops)
     _grouped_check(f"prefill {bits}-bit g{group} {sd} D={D} F={F}", fmt, 0, bf16_bits_to_f32(xb), idx, w,
                    _np(routed), _f32(out), yf, E, addend=bf16_bits_to_f32(ab))
+
+
+@pytest.mark.parametrize("bits,group", [(2, 128), (3, 64)])
+def test_affine_prefill_config3_routing(cuda, bits, group, monkeypatch):
+    """Config 3's routing (4096 tokens, D 4096, F 2880, 384 experts, top-6, the Zipf router bias)
+    over the 2-bit g128 and oQ3e (3-bit g64) banks with fp16 scales, on the block-scaled prefill
+    kernels: 192 sampled rows of each of the three heaviest experts (hundreds to thousands of rows,
+    many 64-row tiles) and every route of 16 random tokens against the oracle; the combine of all
+    tokens bit for bit over the GPU's terms.  (The router itself is checked bit for bit at this
+    shape by test_gpu_workloads.test_config3_prefill_workload.)"""
+    from cachalot_amd import synth
+    from cachalot_amd.moe_prefill import grouped_experts
+    from cachalot_amd.router import route_topk_rows
+
+    monkeypatch.setenv("CACHALOT_AFFINE_VALU", "0")
+    monkeypatch.setenv("CACHALOT_PREFILL_BF16", "0")
+    D, F, E, K, T = 4096, 2880, 384, 6, 4096
+    fmt = _fmt(bits, group, "float16", d=D, f=F)
+    store = make_store(fmt, n_layers=1, n_experts=E)
+    w, b = synth.router_weights(SEED + 3, 0, E, D, cuda)
+    b = b + torch.tensor(synth.zipf_bias(E, seed=SEED), dtype=torch.float32, device=cuda)
+    x = synth.activations(SEED + 3, 0, T, D, cuda)
+    idx, wt, _ = route_topk_rows(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+    oi, ow = _np(idx), _np(wt)
+    counts = np.bincount(oi.reshape(-1), minlength=E)
+    heavy = np.argsort(counts, kind="stable")[-3:]
+    assert counts[heavy].min() > 256, counts[heavy]
+    routed, out, y = grouped_experts(x, idx, wt, store.pool, store.layer_table(0), want_routed=True, want_terms=True)
+    rng = np.random.default_rng(9 + bits)
+    rows_of = {int(e): np.sort(rng.choice(int(counts[e]), size=192, replace=False)) for e in heavy}
+    sample = {}
+    for tk in rng.choice(T, size=16, replace=False):
+        for s in range(K):
+            sample.setdefault(int(oi[tk, s]), []).append((int(tk), s))
+    for e, pairs in sample.items():
+        if e in rows_of:
+            continue
+        want = set(pairs)
+        rows = np.argwhere(oi == e)
+        rows_of[e] = np.asarray([i for i, (a, c) in enumerate(rows.tolist()) if (a, c) in want])
+    _grouped_check(f"config3 routing prefill {bits}-bit g{group}", fmt, 0, _f32(x), oi, ow, _np(routed), _f32(out),
+                   _f32(y), E, rows_of=rows_of)
