@@ -50,10 +50,9 @@ struct P4Chunk {
 // come in groups of eight, p4_kernel.)
 template <int AK, int NM, int NF>
 __device__ __forceinline__ void p4_issue(uint8_t* stage, const uint8_t* (&asrc)[P3_ASLOTS], const uint8_t* base,
-                                         const int (&woff)[NM], const int (&soff)[NM], const int (&boff)[NM],
-                                         const int (&nrow)[NF], int c, int kh, int wave, int row_bytes, int groups,
-                                         P4Chunk<NM * NF>& out) {
-  constexpr int BITS = ak_bits(AK), GPC = ak_gpc(AK), CB = 16 * BITS;
+                                         const int (&woff)[NM], const int (&nrow)[NF], int c, int kh, int wave,
+                                         int row_bytes, P4Chunk<NM * NF>& out) {
+  constexpr int BITS = ak_bits(AK), CB = 16 * BITS;
   constexpr int LB = BITS == 2 ? 4 : 8;
 #pragma unroll
   for (int q = 0; q < P3_ASLOTS; ++q)
@@ -226,7 +225,7 @@ __global__ void __launch_bounds__(P3_THREADS) p4_kernel(MxArgs g, int slices) {
     };
     load_sg(0, sg[0]);
     P4Chunk<NP> ring[P3_STAGES];
-    p4_issue<AK, NM, NF>(abuf, asrc, base, woff, soff, boff, nrow, 0, kh, wave, row_bytes, groups, ring[0]);
+    p4_issue<AK, NM, NF>(abuf, asrc, base, woff, nrow, 0, kh, wave, row_bytes, ring[0]);
     for (int c0 = 0; c0 < nch; c0 += 8) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
@@ -237,8 +236,8 @@ __global__ void __launch_bounds__(P3_THREADS) p4_kernel(MxArgs g, int slices) {
         asm volatile("" ::"v"(ring[u % 2].codes[NP - 1][1].w) : "memory");
         lds_sync();
         if ((u + 1) % 4 == 0) load_sg(min((c + 1) / 4, nq - 1), sg[((u + 1) / 4) % 2]);
-        p4_issue<AK, NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, soff, boff, nrow,
-                             min(c + 1, nch - 1), kh, wave, row_bytes, groups, ring[(u + 1) % 2]);
+        p4_issue<AK, NM, NF>(abuf + ((u + 1) % 2) * P3_ABYTES, asrc, base, woff, nrow, min(c + 1, nch - 1), kh, wave,
+                             row_bytes, ring[(u + 1) % 2]);
         if (c < nch) {
           uint32_t sw[NP], bw[NP];
 #pragma unroll
