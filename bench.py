@@ -438,8 +438,14 @@ def prefill_affine(args, dev, log_fn, fmt, label, note):
     torch.cuda.synchronize()
     ms = a.elapsed_time(e) / reps
     tflops = 2.0 * T * K * 3 * D * F / (ms * 1e-3) / 1e12
+    idx, _, _ = route_topk_rows(x, w, b, topk=K, route_scale=1.0, score_fn="sigmoid")
+    touched = int((torch.bincount(idx.reshape(-1).long(), minlength=E) > 0).sum())
+    # HBM floor: every touched expert's weights once, x read once, out written once
+    floor_ms = (touched * fmt.algorithmic_bytes + 2 * T * D * 2) / (HBM_PEAK_GBPS * 1e9) * 1e3
     res = {"ms_per_layer": round(ms, 3), "tflops": round(tflops, 1), "frac_bf16_mfma_peak": round(tflops / 2500.0, 4),
-           "expert_bytes": fmt.algorithmic_bytes, "note": note}
+           "expert_bytes": fmt.algorithmic_bytes, "experts_touched": touched,
+           "weight_GBps": round(touched * fmt.algorithmic_bytes / (ms * 1e-3) / 1e9, 1),
+           "hbm_floor_ms": round(floor_ms, 4), "frac_attainable": round(floor_ms / ms, 4), "note": note}
     log_fn(f"{label}: {ms:.3f} ms/layer, {tflops:.1f} TFLOP/s")
     del store
     torch.cuda.empty_cache()
