@@ -736,8 +736,9 @@ def layer_with_shared(args, store, gates, log_fn):
 
 
 def stream_ceiling(dev) -> dict:
-    """Plain streaming reads (cachalot_stream_read) of 24, 60 and 288 MB, each from 8 rotating buffers
-    (the 256 MB MALL holds none of them between reads): the HBM read ceiling at the decode's sizes."""
+    """Plain streaming reads (cachalot_stream_read) of 20, 24, 40, 60 and 288 MB, each from 8 rotating
+    buffers (the 256 MB MALL holds none of them between reads): the HBM read ceiling at the decode's
+    sizes (20 / 40 MB: the down and gate/up kernels' expert bytes, 60 MB: both)."""
     import torch
 
     from cachalot_amd import _lib
@@ -746,7 +747,7 @@ def stream_ceiling(dev) -> dict:
     out = {}
     sink = torch.zeros(65536, dtype=torch.int32, device=dev)
     stream = _lib.stream_handle(dev)
-    for mb in (24, 60, 288):
+    for mb in (20, 24, 40, 60, 288):
         nbytes = mb * 1000 * 1000 // 16 * 16
         bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(8 if mb < 288 else 2)]
         best = None
@@ -1035,6 +1036,11 @@ def main() -> int:
     result["config4_stack"] = stack
     result["stream_ceiling"] = ceiling
     result["roofline"]["frac_of_stream_ceiling"] = round(achieved / ceiling["60MB"]["GBps"], 4)
+    # the two kernels read 40 MB (gate/up) and 20 MB (down) one after the other: the sum of
+    # plain reads of those sizes is the ceiling of a two-launch form
+    split_us = ceiling["40MB"]["us"] + ceiling["20MB"]["us"]
+    result["roofline"]["split_stream_ceiling_us"] = round(split_us, 2)
+    result["roofline"]["frac_of_split_stream_ceiling"] = round(split_us / us_kernel, 4)
     if not args.no_extra:
         result["config0_fp4_decode"] = fp4_decode_config0(args, dev, log)
         result["affine_widths"] = affine_width_decodes(args, dev, log)
