@@ -92,20 +92,29 @@ __device__ __forceinline__ void load_words(const uint8_t* p, uint32_t (&w)[W]) {
   }
 }
 
-// Nibble registers of codes (8 t .. 8 t + 7) in natural order -> the even codes of a
-// pair (lo, hi) of such registers, then the odd ones, as the plane blocks order a
-// 16-code piece: even(lo, hi) nibbles = codes 0, 2, 4, 6 of lo, then of hi.
-__device__ __forceinline__ uint32_t even_nibbles(uint32_t lo, uint32_t hi) {
-  uint32_t a = lo & 0x0F0F0F0Fu, b = hi & 0x0F0F0F0Fu;
-  a |= a >> 4;   // byte 0 = codes 0 | 2 << 4, byte 2 = codes 4 | 6 << 4
-  b |= b >> 4;
-  return __builtin_amdgcn_perm(b, a, 0x06040200u);   // bytes a0, a2, b0, b2
-}
-__device__ __forceinline__ uint32_t odd_nibbles(uint32_t lo, uint32_t hi) {
-  return even_nibbles(lo >> 4, hi >> 4);
+// 3- and 4-bit codes go to the matrix cores in natural order (nibble j of B word t =
+// code 8 t + j of the lane's 32), so the kernels put their LDS copy of the plane blocks
+// in natural order too: a piece's 16 bytes hold its even elements, then its odd ones
+// (the order the 2-bit spread yields), and each wave re-orders the 16-byte runs it
+// copied itself once they have landed.  Run r of `bytes` copied by copy_to_lds_untracked
+// with (part, parts); only the data runs (the first 256 bytes of a block) move.
+__device__ __forceinline__ void planes_natural_own(uint8_t* planes, int bytes, int part, int parts, int lane) {
+  asm volatile("" ::: "memory");   // after the caller's wait for the copies
+  for (int c = part * 1024 + 16 * lane; c < bytes; c += parts * 1024) {
+    if (c % PB_BYTES >= PB_SCALE) continue;
+    uint4* p = reinterpret_cast<uint4*>(planes + c);
+    const uint4 v = *p;   // bytes 0..7: elements 0, 2, .., 14; bytes 8..15: 1, 3, .., 15
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05010400u);   // elements 0, 1, 2, 3
+    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07030602u);
+    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05010400u);
+    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07030602u);
+    *p = o;
+  }
 }
 
 // B operands of step s of a group whose words are w: `lo` (and for 3 / 4 bits `hi`).
+// 2-bit codes in the planes' piece order, 3- and 4-bit codes in natural order.
 template <int BITS, int W>
 __device__ __forceinline__ void step_operands(const uint32_t (&w)[W], int s, i32x8_t& lo, i32x8_t& hi) {
   if constexpr (BITS == 2) {
@@ -122,12 +131,10 @@ __device__ __forceinline__ void step_operands(const uint32_t (&w)[W], int s, i32
       n[2] = mx::spread3(__builtin_amdgcn_alignbit(w2, w1, 16) & 0xFFFFFFu);
       n[3] = mx::spread3(w2 >> 8);
     }
-    const uint32_t p[4] = {even_nibbles(n[0], n[1]), odd_nibbles(n[0], n[1]), even_nibbles(n[2], n[3]),
-                           odd_nibbles(n[2], n[3])};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      lo[t] = (int)(p[t] & 0x33333333u);
-      hi[t] = (int)((p[t] >> 2) & 0x33333333u);
+      lo[t] = (int)(n[t] & 0x33333333u);
+      hi[t] = (int)((n[t] >> 2) & 0x33333333u);
       lo[t + 4] = 0;
       hi[t + 4] = 0;
     }
@@ -225,6 +232,7 @@ __global__ void __launch_bounds__(AG_THREADS) amx_gate_up_kernel(const uint8_t* 
   } else {
     copy_to_lds_untracked(xplanes, s.planes, GT * PB_BYTES, wave < rw ? wave : wave - 1, AG_WAVES - 1, lane);
     tile::wait_vmem();
+    if constexpr (BITS != 2) planes_natural_own(s.planes, GT * PB_BYTES, wave < rw ? wave : wave - 1, AG_WAVES - 1, lane);
   }
   lds_sync();
   const int slot = __builtin_amdgcn_readfirstlane(s.slot);
@@ -391,6 +399,7 @@ __global__ void __launch_bounds__(AD_THREADS) amx_down_kernel(const uint8_t* __r
   }
   // the copies (issued first) have landed; the codes stay in flight
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(MAXM * Gm::LDI));
+  if constexpr (BITS != 2) planes_natural_own(s.planes, k * GKB * PB_BYTES, wave, AD_WAVES, lane);
   lds_sync();
 
   // ---- 1. items
