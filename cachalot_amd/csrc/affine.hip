@@ -56,7 +56,6 @@ namespace aff {
 using namespace decode;
 
 constexpr int THREADS = 256;
-constexpr int WAVES = THREADS / 64;
 constexpr int TB = 4;            // token rows per grouped tile
 constexpr int MAX_K = 8192;      // D, F (padded) <= MAX_K
 

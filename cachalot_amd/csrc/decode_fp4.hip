@@ -40,7 +40,6 @@ constexpr int MAX_D = 8192;
 constexpr int MAX_KF = 24576;                    // k * F staged by the down kernel
 constexpr int ZERO_BYTES = 64;                   // 4 steps x 16 bytes
 constexpr int GU_ZERO = MAX_D * 2;
-constexpr int DN_ZERO = MAX_KF * 4;
 
 // Copy `bytes` (a multiple of 16) into LDS with untracked direct-to-LDS loads, 1 KiB
 // chunks c = part, part + parts, ... (tile::lds_load16_untracked); the caller waits.

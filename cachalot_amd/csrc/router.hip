@@ -53,7 +53,7 @@ __device__ __forceinline__ void route_tail(const float* __restrict__ scores, con
   else
     wave_topk<16, true>(scores, tail.bias, tail.E, tail.k, tail.order, top_i, top_v, tail.slot_table, top_s);
   if (threadIdx.x == 0) normalise_weights(top_v, tail.k, tail.route_scale, tail.norm, w);
-  if (threadIdx.x < tail.k) {
+  if ((int)threadIdx.x < tail.k) {
     tail.ws_slots[threadIdx.x] = top_s[threadIdx.x];
     tail.ws_w[threadIdx.x] = w[threadIdx.x];
     if (tail.idx_out) tail.idx_out[threadIdx.x] = top_i[threadIdx.x];
